@@ -1,0 +1,228 @@
+/* libtopos_hip — the MI355X (gfx950) execution backend for topos.
+ *
+ * A plain C ABI: no C++ or torch types cross it, only pointers, sizes and
+ * integer codes. The topos side binds it at run time (dlopen), exactly as its
+ * CUDA rung binds libcudart/libcublas (src/backend/cuda/kernels/context.rs:217-288),
+ * so a build without the library or a machine without a GPU is a status answer,
+ * never a build failure.
+ *
+ * Three faces:
+ *   - the manifest and status (src/backend/manifest.rs:16-37, backend.rs:128-177);
+ *   - the offered task face, host buffers in and out, synchronous — the bodies of
+ *     `Task::offer` arms for GemmTask<f32> and MapTask<f32>
+ *     (src/backend/task.rs:57-115);
+ *   - the device face: the same kernels on HBM-resident buffers, enqueued on a
+ *     caller stream (what the plan executor and the benchmark drive);
+ *   - the plan face: a device program (the lowered `Plan` columns,
+ *     src/engine/plan.rs:311-347) executed from one pre-sized HBM arena.
+ *
+ * Degrade to slow, never to wrong (src/backend/cuda/kernels/mod.rs:94-121):
+ * any runtime HIP failure poisons the library; every later offer declines
+ * (TOPOS_HIP_DECLINED) and topos computes on its reference path.
+ */
+#ifndef TOPOS_HIP_H
+#define TOPOS_HIP_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TOPOS_HIP_ABI_VERSION 1
+
+/* ---- status codes ---- */
+enum {
+  TOPOS_HIP_OK = 0,
+  /* The task was not served (outside the kernels' mapping, below the cost
+   * threshold, or the backend is unavailable/poisoned): the caller computes on
+   * the reference path. The `None` of `Task::offer`. */
+  TOPOS_HIP_DECLINED = 1,
+  /* Setup: no HIP device is visible (SetupError::NoDevice; tests skip). */
+  TOPOS_HIP_NO_DEVICE = 2,
+  /* Setup: any other one-time setup failure (SetupError::Failed; tests fail). */
+  TOPOS_HIP_SETUP_FAILED = 3,
+  /* Disabled after a runtime error (BackendUnavailable::Poisoned). */
+  TOPOS_HIP_POISONED = 4,
+  /* The call violates its contract (a GemmTask whose slice does not span its
+   * matrix, an unknown operation, a malformed program): the reference panics
+   * here. Does not poison. */
+  TOPOS_HIP_INVALID_ARGUMENT = 5,
+  /* A HIP call failed during this call; the library is now poisoned. */
+  TOPOS_HIP_RUNTIME_ERROR = 6,
+  /* A device-face request the kernels do not cover (device face only; the task
+   * face answers DECLINED instead). */
+  TOPOS_HIP_UNSUPPORTED = 7
+};
+
+/* ---- the vocabulary mirrored from src/backend ---- */
+enum { TOPOS_HIP_EXACT = 0, TOPOS_HIP_FAST = 1 };              /* Numerics (numerics.rs:24-42) */
+enum { TOPOS_HIP_BIT_IDENTICAL = 0, TOPOS_HIP_ENVELOPE = 1 };  /* Fidelity (coverage.rs:13-33) */
+enum {                                                         /* Formula (formula.rs:24-37) */
+  TOPOS_HIP_FORMULA_GEMM = 0,
+  TOPOS_HIP_FORMULA_MAP = 1,
+  TOPOS_HIP_FORMULA_WINDOW_PRODUCT = 2,
+  TOPOS_HIP_FORMULA_REDUCE_WINDOW = 3,
+  TOPOS_HIP_FORMULA_BATCH_NORM_TRAINING = 4,
+  TOPOS_HIP_FORMULA_BATCH_NORM_INFERENCE = 5
+};
+enum { TOPOS_HIP_PRECISION_F32 = 1u, TOPOS_HIP_PRECISION_F64 = 2u }; /* Precision bits */
+enum {                                                         /* MapOperation (elementary.rs:13-22) */
+  TOPOS_HIP_MAP_EXP = 0,
+  TOPOS_HIP_MAP_LN = 1,
+  TOPOS_HIP_MAP_SQRT = 2,
+  TOPOS_HIP_MAP_TANH = 3
+};
+
+/* ---- manifest and status ---- */
+
+/* ABI version of the loaded library; a binding refuses a mismatch. */
+int topos_hip_abi_version(void);
+/* Build facts only, no device probe (Manifest::compiled, manifest.rs:30-32). */
+int topos_hip_compiled(void);
+/* The coverage cell for one formula (Manifest::coverage, manifest.rs:22-28).
+ * Returns 1 and fills `fidelity` and `precisions` (TOPOS_HIP_PRECISION_* bits)
+ * when a kernel serves the formula, 0 for Coverage::Absent. */
+int topos_hip_coverage(int formula, int *fidelity, unsigned *precisions);
+/* Forces the lazy one-time setup (Manifest::status, manifest.rs:34-36; the
+ * OnceLock of src/backend/cuda/kernels/mod.rs:36-68). Returns TOPOS_HIP_OK,
+ * TOPOS_HIP_NO_DEVICE, TOPOS_HIP_SETUP_FAILED or TOPOS_HIP_POISONED. */
+int topos_hip_status(void);
+/* The reason held for the last non-OK status (setup error or poison message),
+ * or "" — valid for the life of the process. */
+const char *topos_hip_status_reason(void);
+/* Static text for a status code. */
+const char *topos_hip_status_string(int code);
+
+/* ---- offered task face (host buffers, synchronous) ---- */
+
+/* One dense f32 product, the GemmTask of src/payload/gemm.rs:40-125:
+ * element (i, j) of `a` is a[i * a_row_stride + j * a_col_stride] (m x k),
+ * of `b` is b[i * b_row_stride + j * b_col_stride] (k x n); `a_len`/`b_len`
+ * are the slice lengths, which must span the matrices (gemm.rs:57-89).
+ * On TOPOS_HIP_OK, `product` holds the contiguous row-major [m, n] product:
+ * bit-identical to gemm::multiply under TOPOS_HIP_EXACT, within the envelope
+ * |c - exact| <= 1e-5 * sum_k |a_ik * b_kj| under TOPOS_HIP_FAST.
+ * TOPOS_HIP_DECLINED: compute on the reference path (GEMV shapes, below the
+ * cost threshold, extents beyond i32, or the backend unavailable/poisoned).
+ * Replaces the `Backend::Cuda => cuda::gemm_f32(self)` arm of
+ * src/backend/task.rs:63-75 (the Hip arm beside it). */
+int topos_hip_gemm_f32(const float *a, size_t a_len, size_t a_row_stride, size_t a_col_stride,
+                       const float *b, size_t b_len, size_t b_row_stride, size_t b_col_stride,
+                       size_t m, size_t k, size_t n, int numerics, float *product);
+
+/* One whole-buffer transcendental, the MapTask of src/backend/task.rs:36-54:
+ * `out[i] = op(elements[i])` bit-identical to the host libm under either
+ * posture. TOPOS_HIP_DECLINED below the size threshold or when unavailable.
+ * Replaces the `Backend::Metal => metal::map_f32(..)` arm of task.rs:103-115. */
+int topos_hip_map_f32(int operation, const float *elements, size_t count, int numerics, float *out);
+
+/* ---- device face (HBM-resident buffers, asynchronous on `stream`) ----
+ * `stream` is a hipStream_t (NULL: the null stream). Pointers are device
+ * addresses. Returns TOPOS_HIP_OK once the work is enqueued. */
+
+/* The same product as topos_hip_gemm_f32 with device operands; the product is
+ * row-major with leading dimension `ldc` >= n. Operand strides may be any
+ * non-negative values (stride 0 broadcasts). */
+int topos_hip_gemm_f32_device(const float *a, int64_t a_row_stride, int64_t a_col_stride,
+                              const float *b, int64_t b_row_stride, int64_t b_col_stride,
+                              int64_t m, int64_t k, int64_t n, int numerics, float *product,
+                              int64_t ldc, void *stream);
+
+/* Elementwise unary map over `count` contiguous elements (MapOperation). */
+int topos_hip_map_f32_device(int operation, const float *x, int64_t count, float *y, void *stream);
+
+/* Row reductions over the last axis of a contiguous [rows, columns] buffer,
+ * the Tensorial reductions and fused rules of src/payload/tensor.rs:1055-1124,
+ * src/function/log_softmax.rs:51-60 and src/function/log_sum_exp.rs:53-61.
+ * Sum-type reductions are bit-identical (ascending, first-term seeded) under
+ * TOPOS_HIP_EXACT and tree-ordered under TOPOS_HIP_FAST; max is bit-identical
+ * under both. */
+enum {
+  TOPOS_HIP_ROWS_SUM = 0,         /* out[rows]          sum_along(1) */
+  TOPOS_HIP_ROWS_MAX = 1,         /* out[rows]          max_along(1) */
+  TOPOS_HIP_ROWS_LOG_SOFTMAX = 2, /* out[rows, columns] log_softmax(1) */
+  TOPOS_HIP_ROWS_SOFTMAX = 3,     /* out[rows, columns] log_softmax(1).exp() */
+  TOPOS_HIP_ROWS_LOG_SUM_EXP = 4  /* out[rows]          logsumexp(1) */
+};
+int topos_hip_rows_f32_device(int reduction, const float *x, int64_t rows, int64_t columns,
+                              int numerics, float *out, void *stream);
+
+/* LayerNorm over the last axis (src/neural/layer_norm.rs:100-132): mean and
+ * biased variance by sum / count, (x - mean) / sqrt(var + epsilon), then
+ * * scale[j] + shift[j]. */
+int topos_hip_layer_norm_f32_device(const float *x, int64_t rows, int64_t columns,
+                                    const float *scale, const float *shift, float epsilon,
+                                    int numerics, float *out, void *stream);
+
+/* ---- generated elementwise/broadcast chains ----
+ * A chain is a straight-line program of f32 elementwise operations over
+ * `n_inputs` strided views of one logical shape; each output is written
+ * contiguous row-major. It is compiled once (hipRTC, gfx950) into a kernel of
+ * its own; every operation rounds to f32 exactly as the interpreter's
+ * materialized intermediates do (no contraction, no fast math). */
+enum {
+  TOPOS_HIP_CHAIN_NEG = 0,
+  TOPOS_HIP_CHAIN_EXP = 1,
+  TOPOS_HIP_CHAIN_LN = 2,
+  TOPOS_HIP_CHAIN_SQRT = 3,
+  TOPOS_HIP_CHAIN_TANH = 4,
+  TOPOS_HIP_CHAIN_ADD = 16,
+  TOPOS_HIP_CHAIN_SUB = 17,
+  TOPOS_HIP_CHAIN_MUL = 18,
+  TOPOS_HIP_CHAIN_DIV = 19,
+  TOPOS_HIP_CHAIN_MAX = 20,  /* f32::max */
+  TOPOS_HIP_CHAIN_STEP = 21  /* x >= y ? 1 : 0 */
+};
+#define TOPOS_HIP_MAX_RANK 4
+/* A strided view of `rank` axes (the Layout of src/payload/layout.rs:23-31):
+ * element (i0..) lives at offset + sum i_d * strides[d], in elements. */
+typedef struct {
+  int32_t rank;
+  int64_t shape[TOPOS_HIP_MAX_RANK];
+  int64_t strides[TOPOS_HIP_MAX_RANK];
+  int64_t offset;
+} topos_hip_layout;
+/* Operand references: value >= 0 names an earlier instruction's result,
+ * value < 0 names input (-value - 1). */
+typedef struct {
+  int32_t op;
+  int32_t left;
+  int32_t right; /* ignored by unary operations */
+} topos_hip_chain_step;
+typedef struct {
+  int32_t rank;
+  int64_t shape[TOPOS_HIP_MAX_RANK];      /* the logical shape of every view */
+  int32_t n_inputs;
+  const topos_hip_layout *inputs;         /* [n_inputs], each over `shape` */
+  int32_t n_steps;
+  const topos_hip_chain_step *steps;      /* [n_steps] */
+  int32_t n_outputs;
+  const int32_t *outputs;                 /* [n_outputs] step or input references */
+} topos_hip_chain_desc;
+typedef struct topos_hip_chain topos_hip_chain;
+/* Generates and compiles (or fetches from the process cache) the chain's
+ * kernel. */
+int topos_hip_chain_create(const topos_hip_chain_desc *desc, topos_hip_chain **chain);
+/* inputs[i] is the base pointer the i-th layout's offset and strides address;
+ * outputs[o] receives volume(shape) contiguous elements. */
+int topos_hip_chain_launch(const topos_hip_chain *chain, const float *const *inputs,
+                           float *const *outputs, void *stream);
+/* The generated HIP source (for inspection and tests); valid while the chain
+ * lives. */
+const char *topos_hip_chain_source(const topos_hip_chain *chain);
+void topos_hip_chain_destroy(topos_hip_chain *chain);
+
+/* ---- test surface ---- */
+
+/* Installs a fake device runtime before first use (Api::fake of
+ * src/backend/cuda/kernels/context.rs:101-162): setup succeeds without a GPU,
+ * device memory is host memory, kernels are not run, and the device call
+ * numbered `fail_after_calls` (0-based) fails, which must poison the library.
+ * Returns TOPOS_HIP_INVALID_ARGUMENT once the real runtime is initialised. */
+int topos_hip_fake_runtime(int fail_after_calls);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,102 @@
+"""ctypes binding of libtopos_hip.so (include/topos_hip.h).
+
+The library is built in-tree by ``python -m poorgrad_amd.build``. Importing
+this module without it raises ImportError: there is no fallback path.
+"""
+from __future__ import annotations
+
+import ctypes
+from ctypes import POINTER, c_char_p, c_float, c_int, c_int32, c_int64, c_size_t, c_uint, c_void_p
+from pathlib import Path
+
+LIBRARY_PATH = Path(__file__).resolve().parent / "libtopos_hip.so"
+
+if not LIBRARY_PATH.exists():
+    raise ImportError(f"{LIBRARY_PATH} is not built; run `python -m poorgrad_amd.build` "
+                      "(the HIP backend has no CPU fallback)")
+
+lib = ctypes.CDLL(str(LIBRARY_PATH))
+
+# ---- status codes and vocabulary (mirrors include/topos_hip.h) ----
+OK, DECLINED, NO_DEVICE, SETUP_FAILED, POISONED, INVALID_ARGUMENT, RUNTIME_ERROR, UNSUPPORTED = range(8)
+EXACT, FAST = 0, 1
+BIT_IDENTICAL, ENVELOPE = 0, 1
+FORMULA_GEMM, FORMULA_MAP, FORMULA_WINDOW_PRODUCT, FORMULA_REDUCE_WINDOW = 0, 1, 2, 3
+FORMULA_BATCH_NORM_TRAINING, FORMULA_BATCH_NORM_INFERENCE = 4, 5
+PRECISION_F32, PRECISION_F64 = 1, 2
+MAP_EXP, MAP_LN, MAP_SQRT, MAP_TANH = 0, 1, 2, 3
+ROWS_SUM, ROWS_MAX, ROWS_LOG_SOFTMAX, ROWS_SOFTMAX, ROWS_LOG_SUM_EXP = 0, 1, 2, 3, 4
+CHAIN_NEG, CHAIN_EXP, CHAIN_LN, CHAIN_SQRT, CHAIN_TANH = 0, 1, 2, 3, 4
+CHAIN_ADD, CHAIN_SUB, CHAIN_MUL, CHAIN_DIV, CHAIN_MAX, CHAIN_STEP = 16, 17, 18, 19, 20, 21
+MAX_RANK = 4
+
+FLOAT_P = POINTER(c_float)
+
+
+class Layout(ctypes.Structure):
+    _fields_ = [("rank", c_int32), ("shape", c_int64 * MAX_RANK), ("strides", c_int64 * MAX_RANK),
+                ("offset", c_int64)]
+
+
+class ChainStep(ctypes.Structure):
+    _fields_ = [("op", c_int32), ("left", c_int32), ("right", c_int32)]
+
+
+class ChainDesc(ctypes.Structure):
+    _fields_ = [("rank", c_int32), ("shape", c_int64 * MAX_RANK), ("n_inputs", c_int32),
+                ("inputs", POINTER(Layout)), ("n_steps", c_int32), ("steps", POINTER(ChainStep)),
+                ("n_outputs", c_int32), ("outputs", POINTER(c_int32))]
+
+
+# Every symbol the header declares, with its prototype. The CPU tests check
+# that each one resolves.
+PROTOTYPES = {
+    "topos_hip_abi_version": (c_int, []),
+    "topos_hip_compiled": (c_int, []),
+    "topos_hip_coverage": (c_int, [c_int, POINTER(c_int), POINTER(c_uint)]),
+    "topos_hip_status": (c_int, []),
+    "topos_hip_status_reason": (c_char_p, []),
+    "topos_hip_status_string": (c_char_p, [c_int]),
+    "topos_hip_gemm_f32": (c_int, [FLOAT_P, c_size_t, c_size_t, c_size_t, FLOAT_P, c_size_t, c_size_t,
+                                   c_size_t, c_size_t, c_size_t, c_size_t, c_int, FLOAT_P]),
+    "topos_hip_map_f32": (c_int, [c_int, FLOAT_P, c_size_t, c_int, FLOAT_P]),
+    "topos_hip_gemm_f32_device": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_int64, c_int64, c_int64,
+                                          c_int64, c_int64, c_int, c_void_p, c_int64, c_void_p]),
+    "topos_hip_map_f32_device": (c_int, [c_int, c_void_p, c_int64, c_void_p, c_void_p]),
+    "topos_hip_rows_f32_device": (c_int, [c_int, c_void_p, c_int64, c_int64, c_int, c_void_p, c_void_p]),
+    "topos_hip_layer_norm_f32_device": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_float,
+                                                c_int, c_void_p, c_void_p]),
+    "topos_hip_chain_create": (c_int, [POINTER(ChainDesc), POINTER(c_void_p)]),
+    "topos_hip_chain_launch": (c_int, [c_void_p, POINTER(c_void_p), POINTER(c_void_p), c_void_p]),
+    "topos_hip_chain_source": (c_char_p, [c_void_p]),
+    "topos_hip_chain_destroy": (None, [c_void_p]),
+    "topos_hip_fake_runtime": (c_int, [c_int]),
+}
+
+for _name, (_restype, _argtypes) in PROTOTYPES.items():
+    _function = getattr(lib, _name)
+    _function.restype = _restype
+    _function.argtypes = _argtypes
+
+
+class HipError(RuntimeError):
+    """A non-OK status from the library, carrying the code."""
+
+    def __init__(self, code: int, what: str):
+        reason = lib.topos_hip_status_reason().decode()
+        text = lib.topos_hip_status_string(code).decode()
+        super().__init__(f"{what}: {text}" + (f" ({reason})" if reason else ""))
+        self.code = code
+
+
+def checked(code: int, what: str) -> None:
+    if code != OK:
+        raise HipError(code, what)
+
+
+def status() -> int:
+    return lib.topos_hip_status()
+
+
+def status_reason() -> str:
+    return lib.topos_hip_status_reason().decode()

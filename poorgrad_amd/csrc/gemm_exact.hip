@@ -1,0 +1,146 @@
+// Exact-posture GEMM: bit-identical to the reference slice path,
+// src/payload/gemm.rs:140-211.
+//
+// Every output element is one independent accumulator over ascending k,
+// seeded with the first term a[i,0]*b[0,j] (never a zero: 0 + -0 would lose
+// the sign of an all negative-zero sum, src/payload/tests/gemm_tests.rs:130-139),
+// then acc = RN(acc + RN(a[i,s] * b[s,j])) for s = 1..k-1: a separately rounded
+// multiply and add, never a fused multiply-add, never a split of k. That is
+// VALU work (two instructions per term) and the kernel is shaped for it:
+// 128x128 output tiles per 256-lane workgroup, 8x8 accumulators per lane,
+// operands staged k-major through LDS so each lane reads its eight rows and
+// eight columns as two 128-bit LDS loads each.
+#pragma clang fp contract(off)
+#include "backend.hpp"
+
+namespace topos_hip {
+namespace {
+
+constexpr int kTileM = 128;
+constexpr int kTileN = 128;
+constexpr int kTileK = 8;
+constexpr int kThreads = 256;
+
+// Loads a kTileK x kTileM slab of the left operand (rows m0.., inner k0..)
+// into lds[k][m]. `unit_inner` picks the lane mapping that reads contiguous
+// memory: along k when the column stride is one, along m otherwise.
+template <bool kUnitInner>
+__device__ inline void stage_left(float (*lds)[kTileM + 4], const float *__restrict__ a, int64_t rs,
+                                  int64_t cs, int64_t m, int64_t k, int64_t m0, int64_t k0) {
+  const int t = threadIdx.x;
+#pragma unroll
+  for (int e = 0; e < (kTileM * kTileK) / kThreads; ++e) {
+    const int flat = e * kThreads + t;
+    int mm, kk;
+    if (kUnitInner) {
+      kk = flat % kTileK;
+      mm = flat / kTileK;
+    } else {
+      mm = flat % kTileM;
+      kk = flat / kTileM;
+    }
+    const int64_t gm = m0 + mm, gk = k0 + kk;
+    lds[kk][mm] = (gm < m && gk < k) ? a[gm * rs + gk * cs] : 0.0f;
+  }
+}
+
+// Loads a kTileK x kTileN slab of the right operand (inner k0.., columns n0..)
+// into lds[k][n].
+template <bool kUnitInner>
+__device__ inline void stage_right(float (*lds)[kTileN + 4], const float *__restrict__ b, int64_t rs,
+                                   int64_t cs, int64_t k, int64_t n, int64_t k0, int64_t n0) {
+  const int t = threadIdx.x;
+#pragma unroll
+  for (int e = 0; e < (kTileN * kTileK) / kThreads; ++e) {
+    const int flat = e * kThreads + t;
+    int nn, kk;
+    if (kUnitInner) {
+      kk = flat % kTileK;
+      nn = flat / kTileK;
+    } else {
+      nn = flat % kTileN;
+      kk = flat / kTileN;
+    }
+    const int64_t gk = k0 + kk, gn = n0 + nn;
+    lds[kk][nn] = (gk < k && gn < n) ? b[gk * rs + gn * cs] : 0.0f;
+  }
+}
+
+template <bool kLeftUnitInner, bool kRightUnitInner>
+__global__ __launch_bounds__(kThreads) void gemm_exact_kernel(
+    const float *__restrict__ a, int64_t a_rs, int64_t a_cs, const float *__restrict__ b,
+    int64_t b_rs, int64_t b_cs, int64_t m, int64_t k, int64_t n, float *__restrict__ c, int64_t ldc) {
+  __shared__ float left[kTileK][kTileM + 4];
+  __shared__ float right[kTileK][kTileN + 4];
+  const int64_t m0 = (int64_t)blockIdx.y * kTileM;
+  const int64_t n0 = (int64_t)blockIdx.x * kTileN;
+  const int tx = threadIdx.x % 16;
+  const int ty = threadIdx.x / 16;
+  // Lane (tx, ty) owns rows ty*4 + {0..3} and 64 + ty*4 + {0..3}, and the
+  // same pattern of columns, so each lane's LDS reads are two float4s.
+  float acc[8][8];
+
+  for (int64_t k0 = 0; k0 < k; k0 += kTileK) {
+    __syncthreads();
+    stage_left<kLeftUnitInner>(left, a, a_rs, a_cs, m, k, m0, k0);
+    stage_right<kRightUnitInner>(right, b, b_rs, b_cs, k, n, k0, n0);
+    __syncthreads();
+    const int steps = (k - k0) < kTileK ? (int)(k - k0) : kTileK;
+    for (int s = 0; s < steps; ++s) {
+      const float4 a_lo = *reinterpret_cast<const float4 *>(&left[s][ty * 4]);
+      const float4 a_hi = *reinterpret_cast<const float4 *>(&left[s][64 + ty * 4]);
+      const float4 b_lo = *reinterpret_cast<const float4 *>(&right[s][tx * 4]);
+      const float4 b_hi = *reinterpret_cast<const float4 *>(&right[s][64 + tx * 4]);
+      const float av[8] = {a_lo.x, a_lo.y, a_lo.z, a_lo.w, a_hi.x, a_hi.y, a_hi.z, a_hi.w};
+      const float bv[8] = {b_lo.x, b_lo.y, b_lo.z, b_lo.w, b_hi.x, b_hi.y, b_hi.z, b_hi.w};
+      if (k0 == 0 && s == 0) {
+        // The seed: the first term itself (gemm.rs:151-160).
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+#pragma unroll
+          for (int j = 0; j < 8; ++j) acc[i][j] = __fmul_rn(av[i], bv[j]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+#pragma unroll
+          for (int j = 0; j < 8; ++j) acc[i][j] = __fadd_rn(acc[i][j], __fmul_rn(av[i], bv[j]));
+      }
+    }
+  }
+
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int64_t row = m0 + (i < 4 ? ty * 4 + i : 64 + ty * 4 + (i - 4));
+    if (row >= m) continue;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int64_t col = n0 + (j < 4 ? tx * 4 + j : 64 + tx * 4 + (j - 4));
+      if (col < n) c[row * ldc + col] = acc[i][j];
+    }
+  }
+}
+
+}  // namespace
+
+void launch_gemm_exact(const float *a, int64_t a_rs, int64_t a_cs, const float *b, int64_t b_rs,
+                       int64_t b_cs, int64_t m, int64_t k, int64_t n, float *c, int64_t ldc,
+                       hipStream_t stream) {
+  const int64_t grid_n = (n + kTileN - 1) / kTileN;
+  const int64_t grid_m = (m + kTileM - 1) / kTileM;
+  if (grid_m > 65535 || grid_n > 0x7fffffff)
+    throw Unsupported{"exact gemm: product too tall for one launch"};
+  const dim3 grid((unsigned)grid_n, (unsigned)grid_m);
+  const bool left_unit = a_cs == 1;
+  const bool right_unit = b_rs == 1 && b_cs != 1;
+  if (left_unit && right_unit)
+    gemm_exact_kernel<true, true><<<grid, kThreads, 0, stream>>>(a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc);
+  else if (left_unit)
+    gemm_exact_kernel<true, false><<<grid, kThreads, 0, stream>>>(a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc);
+  else if (right_unit)
+    gemm_exact_kernel<false, true><<<grid, kThreads, 0, stream>>>(a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc);
+  else
+    gemm_exact_kernel<false, false><<<grid, kThreads, 0, stream>>>(a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc);
+  check_launch("gemm_exact_kernel launch");
+}
+
+}  // namespace topos_hip

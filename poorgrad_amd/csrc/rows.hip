@@ -1,0 +1,275 @@
+// Row reductions over the last axis of a contiguous [rows, columns] buffer:
+// sum_along / max_along (src/payload/tensor.rs:1073-1124), LogSumExp
+// (src/function/log_sum_exp.rs:53-61), LogSoftmax (src/function/log_softmax.rs:51-60),
+// softmax = log_softmax.exp (src/graph/composite.rs:43-45) and LayerNorm
+// (src/neural/layer_norm.rs:100-132).
+//
+// Exact posture: each row's fold is one lane's sequential chain, seeded with
+// the row's first value and ascending in column order — the interpreter's
+// accumulation order, so the bits match. A 256-lane workgroup owns kRows rows;
+// all four waves stream coalesced 128-column slabs of those rows, apply the
+// pass's elementwise transform (exp(x - peak), (x - mean)^2, ...) — the
+// expensive part, spread over every SIMD — and park the values in LDS, where
+// wave 0's lane r folds row r in order. Elementwise output passes are plain
+// coalesced row-major sweeps using the per-row statistics.
+//
+// Fast posture: one wave per row, each lane folds a strided share and the
+// wave combines by butterfly shuffles (reassociated: envelope fidelity). The
+// max fold is order-independent under f32::max (NaN loses; +-0 ties are the
+// only order-visible case), so both postures use the same maxima.
+#pragma clang fp contract(off)
+#include "backend.hpp"
+#include "faithful_math.h"
+
+namespace topos_hip {
+namespace {
+
+using topos_faithful::exp_f32;
+using topos_faithful::ln_f32;
+using topos_faithful::max_f32;
+
+constexpr int kThreads = 256;
+constexpr int kSlab = 128;  // columns per staged slab
+
+enum Transform { kIdentity, kShiftedExp, kCentredSquare };
+enum Fold { kSum, kMax };
+
+// One exact pass over the kRows x columns block: lane r of wave 0 returns the
+// ordered fold of T(x[r, c], stat[r]) over c = 0..columns-1.
+template <int kRows, Transform kT, Fold kF, bool kVector>
+__device__ float exact_fold(const float *__restrict__ x, int64_t rows, int64_t columns, int64_t row0,
+                            const float *stat, float (*slab)[kSlab + 1]) {
+  constexpr int kQuads = kRows * (kSlab / 4) / kThreads;  // float4s per lane per slab
+  const int t = threadIdx.x;
+  float acc = 0.0f;
+  for (int64_t c0 = 0; c0 < columns; c0 += kSlab) {
+    const int width = (columns - c0) < kSlab ? (int)(columns - c0) : kSlab;
+    float v[kQuads][4];
+#pragma unroll
+    for (int e = 0; e < kQuads; ++e) {
+      const int q = t + kThreads * e;
+      const int r = q / (kSlab / 4);
+      const int cq = (q % (kSlab / 4)) * 4;
+      const int64_t row = row0 + r;
+      if (kVector && row < rows && cq + 3 < width) {
+        const float4 w = *reinterpret_cast<const float4 *>(x + row * columns + c0 + cq);
+        v[e][0] = w.x; v[e][1] = w.y; v[e][2] = w.z; v[e][3] = w.w;
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          v[e][i] = (row < rows && cq + i < width) ? x[row * columns + c0 + cq + i] : 0.0f;
+      }
+    }
+    __syncthreads();  // wave 0 is done folding the previous slab
+#pragma unroll
+    for (int e = 0; e < kQuads; ++e) {
+      const int q = t + kThreads * e;
+      const int r = q / (kSlab / 4);
+      const int cq = (q % (kSlab / 4)) * 4;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float value = v[e][i];
+        if (kT == kShiftedExp) value = exp_f32(value - stat[r]);
+        if (kT == kCentredSquare) {
+          const float centred = value - stat[r];
+          value = centred * centred;
+        }
+        slab[r][cq + i] = value;
+      }
+    }
+    __syncthreads();
+    if (t < kRows) {
+      int j = 0;
+      if (c0 == 0) {
+        acc = slab[t][0];  // the seed: the row's first value
+        j = 1;
+      }
+      for (; j < width; ++j) {
+        const float value = slab[t][j];
+        acc = (kF == kSum) ? acc + value : max_f32(acc, value);
+      }
+    }
+  }
+  return acc;
+}
+
+// Coalesced elementwise output pass over the block's rows.
+template <int kReduction, int kRows>
+__device__ void exact_write(const float *__restrict__ x, int64_t rows, int64_t columns, int64_t row0,
+                            const float *first, const float *second, const float *scale,
+                            const float *shift, float *__restrict__ out) {
+  const int64_t block_rows = (rows - row0) < kRows ? (rows - row0) : kRows;
+  const int64_t total = block_rows * columns;
+  for (int64_t i = threadIdx.x; i < total; i += kThreads) {
+    const int r = (int)(i / columns);
+    const int64_t c = i % columns;
+    const int64_t at = (row0 + r) * columns + c;
+    const float value = x[at];
+    float result;
+    if (kReduction == TOPOS_HIP_ROWS_LOG_SOFTMAX || kReduction == TOPOS_HIP_ROWS_SOFTMAX) {
+      result = (value - first[r]) - second[r];  // shifted - normalizer
+      if (kReduction == TOPOS_HIP_ROWS_SOFTMAX) result = exp_f32(result);
+    } else {  // layer norm: (x - mean) / deviation * scale + shift
+      const float normalized = (value - first[r]) / second[r];
+      result = normalized * scale[c] + shift[c];
+    }
+    out[at] = result;
+  }
+}
+
+constexpr int kLayerNorm = 100;
+
+template <int kReduction, int kRows, bool kVector>
+__global__ __launch_bounds__(kThreads) void rows_exact_kernel(const float *__restrict__ x, int64_t rows,
+                                                              int64_t columns, const float *scale,
+                                                              const float *shift, float epsilon,
+                                                              float *__restrict__ out) {
+  __shared__ float slab[kRows][kSlab + 1];
+  __shared__ float first[kRows];
+  __shared__ float second[kRows];
+  const int64_t row0 = (int64_t)blockIdx.x * kRows;
+  const int t = threadIdx.x;
+  const bool owner = t < kRows && row0 + t < rows;
+
+  if (kReduction == TOPOS_HIP_ROWS_SUM || kReduction == TOPOS_HIP_ROWS_MAX) {
+    const float acc = exact_fold<kRows, kIdentity, kReduction == TOPOS_HIP_ROWS_SUM ? kSum : kMax, kVector>(
+        x, rows, columns, row0, nullptr, slab);
+    if (owner) out[row0 + t] = acc;
+    return;
+  }
+  if (kReduction == kLayerNorm) {
+    const float count = (float)columns;  // counted(shape, extent) as f32
+    const float total = exact_fold<kRows, kIdentity, kSum, kVector>(x, rows, columns, row0, nullptr, slab);
+    if (t < kRows) first[t] = total / count;  // mean
+    __syncthreads();
+    const float power = exact_fold<kRows, kCentredSquare, kSum, kVector>(x, rows, columns, row0, first, slab);
+    if (t < kRows) second[t] = __builtin_sqrtf(power / count + epsilon);  // deviation
+    __syncthreads();
+    exact_write<kLayerNorm, kRows>(x, rows, columns, row0, first, second, scale, shift, out);
+    return;
+  }
+  // LogSumExp, LogSoftmax, softmax: peak, then the shifted exponential sum.
+  const float peak = exact_fold<kRows, kIdentity, kMax, kVector>(x, rows, columns, row0, nullptr, slab);
+  if (t < kRows) first[t] = peak;
+  __syncthreads();
+  const float total = exact_fold<kRows, kShiftedExp, kSum, kVector>(x, rows, columns, row0, first, slab);
+  if (kReduction == TOPOS_HIP_ROWS_LOG_SUM_EXP) {
+    if (owner) out[row0 + t] = peak + ln_f32(total);
+    return;
+  }
+  if (t < kRows) second[t] = ln_f32(total);  // normalizer
+  __syncthreads();
+  exact_write<kReduction, kRows>(x, rows, columns, row0, first, second, nullptr, nullptr, out);
+}
+
+// ---- fast posture: one wave per row ----
+
+__device__ inline float wave_sum(float value) {
+#pragma unroll
+  for (int offset = 32; offset >= 1; offset /= 2) value += __shfl_xor(value, offset, 64);
+  return value;
+}
+
+__device__ inline float wave_max(float value) {
+#pragma unroll
+  for (int offset = 32; offset >= 1; offset /= 2) value = max_f32(value, __shfl_xor(value, offset, 64));
+  return value;
+}
+
+template <int kReduction>
+__global__ __launch_bounds__(kThreads) void rows_fast_kernel(const float *__restrict__ x, int64_t rows,
+                                                             int64_t columns, const float *scale,
+                                                             const float *shift, float epsilon,
+                                                             float *__restrict__ out) {
+  const int lane = threadIdx.x % 64;
+  const int64_t row = (int64_t)blockIdx.x * (kThreads / 64) + threadIdx.x / 64;
+  if (row >= rows) return;
+  const float *src = x + row * columns;
+  if (kReduction == TOPOS_HIP_ROWS_MAX) {
+    float peak = src[0];
+    for (int64_t c = lane; c < columns; c += 64) peak = max_f32(peak, src[c]);
+    peak = wave_max(peak);
+    if (lane == 0) out[row] = peak;
+    return;
+  }
+  if (kReduction == TOPOS_HIP_ROWS_SUM) {
+    float total = 0.0f;
+    for (int64_t c = lane; c < columns; c += 64) total += src[c];
+    total = wave_sum(total);
+    if (lane == 0) out[row] = total;
+    return;
+  }
+  if (kReduction == kLayerNorm) {
+    float total = 0.0f;
+    for (int64_t c = lane; c < columns; c += 64) total += src[c];
+    const float mean = wave_sum(total) / (float)columns;
+    float power = 0.0f;
+    for (int64_t c = lane; c < columns; c += 64) {
+      const float centred = src[c] - mean;
+      power += centred * centred;
+    }
+    const float deviation = __builtin_sqrtf(wave_sum(power) / (float)columns + epsilon);
+    for (int64_t c = lane; c < columns; c += 64)
+      out[row * columns + c] = ((src[c] - mean) / deviation) * scale[c] + shift[c];
+    return;
+  }
+  float peak = src[0];
+  for (int64_t c = lane; c < columns; c += 64) peak = max_f32(peak, src[c]);
+  peak = wave_max(peak);
+  float total = 0.0f;
+  for (int64_t c = lane; c < columns; c += 64) total += exp_f32(src[c] - peak);
+  total = wave_sum(total);
+  if (kReduction == TOPOS_HIP_ROWS_LOG_SUM_EXP) {
+    if (lane == 0) out[row] = peak + ln_f32(total);
+    return;
+  }
+  const float normalizer = ln_f32(total);
+  for (int64_t c = lane; c < columns; c += 64) {
+    float result = (src[c] - peak) - normalizer;
+    if (kReduction == TOPOS_HIP_ROWS_SOFTMAX) result = exp_f32(result);
+    out[row * columns + c] = result;
+  }
+}
+
+template <int kReduction>
+void launch_one(const float *x, int64_t rows, int64_t columns, int numerics, const float *scale,
+                const float *shift, float epsilon, float *out, hipStream_t stream) {
+  if (numerics == TOPOS_HIP_FAST) {
+    const int64_t blocks = (rows + 3) / 4;
+    rows_fast_kernel<kReduction><<<(unsigned)blocks, kThreads, 0, stream>>>(x, rows, columns, scale, shift, epsilon, out);
+  } else {
+    constexpr int kRows = 64;
+    const int64_t blocks = (rows + kRows - 1) / kRows;
+    const bool vector = reinterpret_cast<uintptr_t>(x) % 16 == 0 && columns % 4 == 0;
+    if (vector)
+      rows_exact_kernel<kReduction, kRows, true><<<(unsigned)blocks, kThreads, 0, stream>>>(x, rows, columns, scale, shift, epsilon, out);
+    else
+      rows_exact_kernel<kReduction, kRows, false><<<(unsigned)blocks, kThreads, 0, stream>>>(x, rows, columns, scale, shift, epsilon, out);
+  }
+  check_launch("row reduction launch");
+}
+
+}  // namespace
+
+void launch_rows(int reduction, const float *x, int64_t rows, int64_t columns, int numerics,
+                 float *out, hipStream_t stream) {
+  if (rows <= 0 || columns <= 0) throw InvalidArgument{"row reduction needs a non-empty operand"};
+  if (rows > 0x7fffffffLL * 4) throw Unsupported{"row reduction: too many rows for one launch"};
+  switch (reduction) {
+    case TOPOS_HIP_ROWS_SUM: launch_one<TOPOS_HIP_ROWS_SUM>(x, rows, columns, numerics, nullptr, nullptr, 0.0f, out, stream); break;
+    case TOPOS_HIP_ROWS_MAX: launch_one<TOPOS_HIP_ROWS_MAX>(x, rows, columns, numerics, nullptr, nullptr, 0.0f, out, stream); break;
+    case TOPOS_HIP_ROWS_LOG_SOFTMAX: launch_one<TOPOS_HIP_ROWS_LOG_SOFTMAX>(x, rows, columns, numerics, nullptr, nullptr, 0.0f, out, stream); break;
+    case TOPOS_HIP_ROWS_SOFTMAX: launch_one<TOPOS_HIP_ROWS_SOFTMAX>(x, rows, columns, numerics, nullptr, nullptr, 0.0f, out, stream); break;
+    case TOPOS_HIP_ROWS_LOG_SUM_EXP: launch_one<TOPOS_HIP_ROWS_LOG_SUM_EXP>(x, rows, columns, numerics, nullptr, nullptr, 0.0f, out, stream); break;
+    default: throw InvalidArgument{"unknown row reduction"};
+  }
+}
+
+void launch_layer_norm(const float *x, int64_t rows, int64_t columns, const float *scale,
+                       const float *shift, float epsilon, int numerics, float *out,
+                       hipStream_t stream) {
+  if (rows <= 0 || columns <= 0) throw InvalidArgument{"layer norm needs a non-empty operand"};
+  launch_one<kLayerNorm>(x, rows, columns, numerics, scale, shift, epsilon, out, stream);
+}
+
+}  // namespace topos_hip

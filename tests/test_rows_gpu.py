@@ -1,0 +1,123 @@
+"""Row reductions and fused rules on the GPU against the oracle:
+bit-identical in the exact posture (ascending, first-term seeded), within a
+stated envelope in the fast posture."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from poorgrad_amd import device
+from tests.conftest import banner
+from tests.gpu_util import assert_bitwise, to_device
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [(1, 1), (3, 5), (64, 10), (65, 129), (257, 1000), (128, 4096), (63, 4099), (2, 50257)]
+
+
+def sample(rows, columns, seed):
+    return oracle.Generator(seed).normal(rows * columns, 3.0).reshape(rows, columns)
+
+
+def expected_rows(kind, x):
+    from poorgrad_amd import _native as n
+
+    if kind == n.ROWS_SUM:
+        return oracle.sum_along(x, 1)
+    if kind == n.ROWS_MAX:
+        return oracle.max_along(x, 1)
+    if kind == n.ROWS_LOG_SOFTMAX:
+        return oracle.log_softmax_rows(x)
+    if kind == n.ROWS_SOFTMAX:
+        return oracle.softmax_rows(x)
+    return oracle.log_sum_exp_rows(x)
+
+
+KINDS = ["sum", "max", "log_softmax", "softmax", "log_sum_exp"]
+
+
+def kind_code(name):
+    from poorgrad_amd import _native as n
+
+    return {"sum": n.ROWS_SUM, "max": n.ROWS_MAX, "log_softmax": n.ROWS_LOG_SOFTMAX,
+            "softmax": n.ROWS_SOFTMAX, "log_sum_exp": n.ROWS_LOG_SUM_EXP}[name]
+
+
+@pytest.mark.parametrize("kind", KINDS)
+@pytest.mark.parametrize("rows, columns", SHAPES)
+def test_exact_rows_bit_identical(hip, kind, rows, columns):
+    banner(f"exact rows {kind} {rows}x{columns}")
+    x = sample(rows, columns, rows * 31 + columns)
+    got = device.rows(kind_code(kind), to_device(x), hip.EXACT)
+    torch.cuda.synchronize()
+    assert_bitwise(got, expected_rows(kind_code(kind), x), f"{kind} {rows}x{columns}")
+
+
+@pytest.mark.parametrize("kind", KINDS)
+@pytest.mark.parametrize("rows, columns", SHAPES)
+def test_fast_rows_within_envelope(hip, kind, rows, columns):
+    banner(f"fast rows {kind} {rows}x{columns}")
+    x = sample(rows, columns, rows * 17 + columns)
+    got = device.rows(kind_code(kind), to_device(x), hip.FAST).cpu().numpy().astype(np.float64)
+    want = expected_rows(kind_code(kind), x).astype(np.float64)
+    if kind == "max":
+        assert_bitwise(got.astype(np.float32), want.astype(np.float32), "fast max")
+        return
+    # Reassociated sums: a sum's error is bounded by 2 * columns * eps * sum|x|;
+    # a log-sum's by 2 * columns * eps absolutely (the relative error of the
+    # sum), and softmax's relatively.
+    eps = 2.0**-24
+    if kind == "sum":
+        bound = 2 * columns * eps * np.abs(x.astype(np.float64)).sum(axis=1)
+        assert (np.abs(got - want) <= bound + 1e-30).all()
+    elif kind == "softmax":
+        assert (np.abs(got - want) <= 4 * columns * eps * np.abs(want) + 1e-37).all()
+    else:
+        assert (np.abs(got - want) <= 4 * columns * eps * (1 + np.abs(want))).all()
+
+
+def test_exact_rows_special_values(hip):
+    banner("exact rows special values")
+    x = np.array([[-0.0, -0.0, -0.0, -0.0],
+                  [0.0, -0.0, 0.0, -0.0],
+                  [np.nan, 1.0, 2.0, np.nan],
+                  [np.inf, 1.0, -np.inf, 0.0],
+                  [-np.inf, -np.inf, -np.inf, -np.inf],
+                  [1e38, 1e38, 1e38, -1e38]], dtype=np.float32)
+    for kind in KINDS:
+        got = device.rows(kind_code(kind), to_device(x), hip.EXACT)
+        torch.cuda.synchronize()
+        assert_bitwise(got, expected_rows(kind_code(kind), x), f"special {kind}")
+
+
+@pytest.mark.parametrize("rows, columns", [(3, 5), (64, 768), (257, 1000), (96, 4096)])
+def test_layer_norm_exact_and_fast(hip, rows, columns):
+    banner(f"layer norm {rows}x{columns}")
+    g = oracle.Generator(rows + columns)
+    x = g.normal(rows * columns, 1.0).reshape(rows, columns)
+    scale, shift = g.normal(columns, 1.0), g.normal(columns, 1.0)
+    want = oracle.layer_norm_rows(x, scale, shift, 1e-5)
+    got = device.layer_norm(to_device(x), to_device(scale), to_device(shift), 1e-5, hip.EXACT)
+    torch.cuda.synchronize()
+    assert_bitwise(got, want, "exact layer norm")
+    fast = device.layer_norm(to_device(x), to_device(scale), to_device(shift), 1e-5, hip.FAST).cpu().numpy()
+    assert np.allclose(fast, want, rtol=1e-4, atol=1e-4 * np.abs(scale).max())
+
+
+def test_full_size_row_softmax_sampled(hip):
+    """The chain config's [16384, 4096] row softmax: sampled rows against the
+    oracle, and every row a probability vector."""
+    banner("row softmax 16384x4096 sampled")
+    x = torch.randn(16384, 4096, generator=torch.Generator().manual_seed(11)).cuda()
+    for numerics in (hip.EXACT, hip.FAST):
+        out = device.rows(kind_code("softmax"), x, numerics)
+        torch.cuda.synchronize()
+        picks = [0, 1, 4095, 8191, 16382, 16383]
+        host = x[picks].cpu().numpy()
+        want = oracle.softmax_rows(host)
+        if numerics == hip.EXACT:
+            assert_bitwise(out[picks], want, "row softmax sample")
+        else:
+            assert np.allclose(out[picks].cpu().numpy(), want, rtol=1e-5, atol=1e-9)
+        sums = out.sum(dim=1, dtype=torch.float64)
+        assert torch.allclose(sums, torch.ones_like(sums), atol=1e-4)
