@@ -213,6 +213,145 @@ int topos_hip_chain_launch(const topos_hip_chain *chain, const float *const *inp
 const char *topos_hip_chain_source(const topos_hip_chain *chain);
 void topos_hip_chain_destroy(topos_hip_chain *chain);
 
+/* ---- the plan face: device programs ----
+ *
+ * A device program is a topos forward plan lowered to a node table: the
+ * plan's columns functions()/operands()/shapes()/readable()
+ * (src/engine/plan.rs:311-347) in recording order, one record per node, plus
+ * the leaf payloads. The library plays Plan::forward (plan.rs:514-641) on one
+ * GPU: it recomputes reachability and liveness from the readable set, keeps
+ * every view (transpose, permute, narrow, broadcasts, view-legal reshapes) as
+ * a layout over its source's storage, fuses elementwise trees into generated
+ * kernels, and places every materialised value at an offset of one
+ * pre-sized HBM arena. Under TOPOS_HIP_EXACT every readable value is
+ * bit-identical to the interpreter's (src/engine/run.rs:417-526); under
+ * TOPOS_HIP_FAST products and row reductions meet the envelope instead.
+ *
+ * The producer is the plan consumer a `Backend::Hip` member adds beside
+ * emit_stablehlo (src/emission/lower.rs:103-177).
+ */
+
+/* Node kinds: the Function variants (src/function/function.rs:26-59). */
+enum {
+  TOPOS_HIP_OP_LEAF = 0,           /* leaf: payload leaf_index */
+  TOPOS_HIP_OP_PARAMETER = 1,      /* slot */
+  TOPOS_HIP_OP_INPUT = 2,          /* slot */
+  TOPOS_HIP_OP_ADD = 3,
+  TOPOS_HIP_OP_SUB = 4,
+  TOPOS_HIP_OP_MUL = 5,
+  TOPOS_HIP_OP_DIV = 6,
+  TOPOS_HIP_OP_NEG = 7,
+  TOPOS_HIP_OP_TANH = 8,
+  TOPOS_HIP_OP_EXP = 9,
+  TOPOS_HIP_OP_LN = 10,
+  TOPOS_HIP_OP_MATMUL = 11,
+  TOPOS_HIP_OP_TRANSPOSE = 12,
+  TOPOS_HIP_OP_SUM = 13,
+  TOPOS_HIP_OP_SUM_ALONG = 14,     /* axis = params[0] */
+  TOPOS_HIP_OP_BROADCAST = 15,     /* [operand, like] */
+  TOPOS_HIP_OP_BROADCAST_ALONG = 16, /* [operand, like], axis = params[0] */
+  TOPOS_HIP_OP_RESHAPE = 17,       /* to the node's shape */
+  TOPOS_HIP_OP_PERMUTE = 18,       /* order = params[0..rank) */
+  TOPOS_HIP_OP_NARROW = 19,        /* axis, start, len = params[0..3) */
+  TOPOS_HIP_OP_PAD = 20,           /* axis, start, full_extent = params[0..3) */
+  TOPOS_HIP_OP_UNFOLD = 21,        /* not served: the program is refused */
+  TOPOS_HIP_OP_FOLD = 22,          /* not served: the program is refused */
+  TOPOS_HIP_OP_GATHER = 23,        /* [table, selection] */
+  TOPOS_HIP_OP_SCATTER = 24,       /* [gradient, selection], rows = params[0] */
+  TOPOS_HIP_OP_LOG_SOFTMAX = 25,   /* axis = params[0] */
+  TOPOS_HIP_OP_LOG_SUM_EXP = 26,   /* axis = params[0] */
+  TOPOS_HIP_OP_SQRT = 27,
+  TOPOS_HIP_OP_POWF = 28,          /* served for constant operands only */
+  TOPOS_HIP_OP_MAXIMUM = 29,
+  TOPOS_HIP_OP_RELU = 30,
+  TOPOS_HIP_OP_STEP = 31
+};
+
+#define TOPOS_HIP_NODE_READABLE 1u /* a root or an observed value (plan.rs:150-158) */
+/* An input fed with a Tensor::selection payload (src/payload/tensor.rs:312-342):
+ * the node's shape is [rows, vocab] and params[0] holds the bits of its f32
+ * `one`; bind it with topos_hip_program_bind_selection. */
+#define TOPOS_HIP_NODE_SELECTION 2u
+
+typedef struct {
+  int32_t op;        /* TOPOS_HIP_OP_* */
+  int32_t rank;      /* 0..TOPOS_HIP_MAX_RANK */
+  int64_t shape[TOPOS_HIP_MAX_RANK]; /* the recorded shape (plan.shapes()) */
+  int32_t operands[2];               /* earlier node indices; -1 where unused */
+  int64_t params[TOPOS_HIP_MAX_RANK]; /* the variant's own parameters, as listed above */
+  int32_t slot;      /* parameter/input slot, or the leaf payload's index */
+  uint32_t flags;    /* TOPOS_HIP_NODE_* */
+} topos_hip_node;
+
+/* Leaf payloads (the Storage variants of src/payload/storage.rs:36-51). */
+enum {
+  TOPOS_HIP_LEAF_CONSTANT = 0,  /* `value` everywhere (Storage::Constant) */
+  TOPOS_HIP_LEAF_DENSE = 1,     /* `count` row-major floats from leaf_data[offset] */
+  TOPOS_HIP_LEAF_SELECTION = 2  /* `count` rows; row r selects leaf_indices[offset + r];
+                                   `value` is the selection's one, its zero is +0 */
+};
+typedef struct {
+  int32_t kind;
+  float value;
+  int64_t offset;
+  int64_t count;
+} topos_hip_leaf;
+
+typedef struct topos_hip_program topos_hip_program;
+
+/* Validates and plans the program (shape inference per node, views, fusion
+ * groups, launch order, arena offsets) and compiles its generated kernels.
+ * TOPOS_HIP_UNSUPPORTED names a node outside the kernels (Unfold, Fold, Powf
+ * of non-constant operands); TOPOS_HIP_INVALID_ARGUMENT a malformed table. */
+int topos_hip_program_create(const topos_hip_node *nodes, int64_t n_nodes, const topos_hip_leaf *leaves,
+                             int64_t n_leaves, const float *leaf_data, int64_t leaf_data_len,
+                             const int32_t *leaf_indices, int64_t leaf_indices_len, int numerics,
+                             topos_hip_program **program);
+/* Bytes of the program's HBM arena (liveness-packed), and the number of
+ * kernel launches one run enqueues. */
+int topos_hip_program_info(const topos_hip_program *program, uint64_t *arena_bytes, int64_t *launches,
+                           int64_t *fused_groups);
+/* Binds a parameter or dense input slot to caller-owned device memory
+ * holding the slot's recorded shape, row-major. The binding holds until
+ * rebound; parameters stay resident across runs. */
+int topos_hip_program_bind(topos_hip_program *program, int is_input, int32_t slot, const float *device);
+/* Binds a selection input slot (Tensor::selection, src/payload/tensor.rs:312-342):
+ * `rows` host indices, each below the recorded vocabulary, copied to the
+ * device together with their row-sorted order (for the ordered scatter). */
+int topos_hip_program_bind_selection(topos_hip_program *program, int32_t slot, const int32_t *indices,
+                                     int64_t rows, float one);
+/* Enqueues one forward run on `stream` (the arena is reserved on first use). */
+int topos_hip_program_run(topos_hip_program *program, void *stream);
+/* The device address of a readable node's value after a run: contiguous
+ * row-major, volume(shape) floats, valid until the next run. */
+int topos_hip_program_output(const topos_hip_program *program, int64_t node, const float **device);
+/* Copies a readable node's value to host memory (`count` = its volume) and
+ * waits for it: the synchronous read-out of Run::value. */
+int topos_hip_program_read(const topos_hip_program *program, int64_t node, float *host, int64_t count);
+/* The reason the last program call on this thread was refused
+ * (TOPOS_HIP_INVALID_ARGUMENT / TOPOS_HIP_UNSUPPORTED), or "". */
+const char *topos_hip_last_refusal(void);
+/* Describes the launch plan (one line per launch) for inspection and tests. */
+const char *topos_hip_program_describe(const topos_hip_program *program);
+void topos_hip_program_destroy(topos_hip_program *program);
+
+/* ---- device-resident optimizer steps (src/neural/optimizer.rs:40-51,
+ * src/neural/adam.rs:62-171) over `count` floats, in place ---- */
+
+/* Sgd::step: parameter - gradient * rate. */
+int topos_hip_sgd_step_f32(float *parameter, const float *gradient, int64_t count, float rate,
+                           void *stream);
+/* One AdamW parameter update with the moment buffers `first`/`second`
+ * (updated in place; zero-filled before the first step stands for the
+ * optimizer's absent moments, whose Constant-zero scaling gives the same
+ * bits). `first_correction`/`second_correction` are 1 - beta^t as the
+ * optimizer computes them in f32; `decay` applies when `decayed` != 0 (the
+ * rank >= 2 policy of AdamW::step). */
+int topos_hip_adamw_step_f32(float *parameter, const float *gradient, float *first, float *second,
+                             int64_t count, float beta1, float beta2, float first_share,
+                             float second_share, float first_correction, float second_correction,
+                             float epsilon, float rate, float decay, int decayed, void *stream);
+
 /* ---- test surface ---- */
 
 /* Installs a fake device runtime before first use (Api::fake of

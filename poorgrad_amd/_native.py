@@ -15,6 +15,15 @@ if not LIBRARY_PATH.exists():
     raise ImportError(f"{LIBRARY_PATH} is not built; run `python -m poorgrad_amd.build` "
                       "(the HIP backend has no CPU fallback)")
 
+# One HIP runtime per process. torch carries its own libamdhip64.so.7; the
+# library binds to whichever copy of that soname is loaded first, so load
+# torch's first. Loading /opt/rocm's first leaves torch a second runtime that
+# cannot see the device.
+try:
+    import torch  # noqa: F401
+except ImportError:  # the C ABI itself needs no torch
+    pass
+
 lib = ctypes.CDLL(str(LIBRARY_PATH))
 
 # ---- status codes and vocabulary (mirrors include/topos_hip.h) ----
@@ -48,6 +57,20 @@ class ChainDesc(ctypes.Structure):
                 ("n_outputs", c_int32), ("outputs", POINTER(c_int32))]
 
 
+NODE_READABLE, NODE_SELECTION = 1, 2
+LEAF_CONSTANT, LEAF_DENSE, LEAF_SELECTION = 0, 1, 2
+INT32_P = POINTER(c_int32)
+
+
+class Node(ctypes.Structure):
+    _fields_ = [("op", c_int32), ("rank", c_int32), ("shape", c_int64 * MAX_RANK), ("operands", c_int32 * 2),
+                ("params", c_int64 * MAX_RANK), ("slot", c_int32), ("flags", ctypes.c_uint32)]
+
+
+class Leaf(ctypes.Structure):
+    _fields_ = [("kind", c_int32), ("value", c_float), ("offset", c_int64), ("count", c_int64)]
+
+
 # Every symbol the header declares, with its prototype. The CPU tests check
 # that each one resolves.
 PROTOTYPES = {
@@ -71,6 +94,20 @@ PROTOTYPES = {
     "topos_hip_chain_source": (c_char_p, [c_void_p]),
     "topos_hip_chain_destroy": (None, [c_void_p]),
     "topos_hip_fake_runtime": (c_int, [c_int]),
+    "topos_hip_program_create": (c_int, [POINTER(Node), c_int64, POINTER(Leaf), c_int64, FLOAT_P, c_int64,
+                                         INT32_P, c_int64, c_int, POINTER(c_void_p)]),
+    "topos_hip_program_info": (c_int, [c_void_p, POINTER(ctypes.c_uint64), POINTER(c_int64), POINTER(c_int64)]),
+    "topos_hip_program_bind": (c_int, [c_void_p, c_int, c_int32, c_void_p]),
+    "topos_hip_program_bind_selection": (c_int, [c_void_p, c_int32, INT32_P, c_int64, c_float]),
+    "topos_hip_program_run": (c_int, [c_void_p, c_void_p]),
+    "topos_hip_program_output": (c_int, [c_void_p, c_int64, POINTER(c_void_p)]),
+    "topos_hip_program_read": (c_int, [c_void_p, c_int64, FLOAT_P, c_int64]),
+    "topos_hip_last_refusal": (c_char_p, []),
+    "topos_hip_program_describe": (c_char_p, [c_void_p]),
+    "topos_hip_program_destroy": (None, [c_void_p]),
+    "topos_hip_sgd_step_f32": (c_int, [c_void_p, c_void_p, c_int64, c_float, c_void_p]),
+    "topos_hip_adamw_step_f32": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_float, c_float, c_float,
+                                         c_float, c_float, c_float, c_float, c_float, c_float, c_int, c_void_p]),
 }
 
 for _name, (_restype, _argtypes) in PROTOTYPES.items():

@@ -83,26 +83,6 @@ struct Borrowed {
   Borrowed &operator=(const Borrowed &) = delete;
 };
 
-// Runs `body`, mapping the library's exceptions to status codes; a runtime
-// failure poisons the library for good.
-template <class Body>
-int guarded(Body body) {
-  try {
-    body();
-    return TOPOS_HIP_OK;
-  } catch (const InvalidArgument &e) {
-    return TOPOS_HIP_INVALID_ARGUMENT;
-  } catch (const Unsupported &e) {
-    return TOPOS_HIP_UNSUPPORTED;
-  } catch (const RuntimeFailure &e) {
-    Context::get().poison(e.message);
-    return TOPOS_HIP_RUNTIME_ERROR;
-  } catch (const std::bad_alloc &) {
-    Context::get().poison("host allocation failed");
-    return TOPOS_HIP_RUNTIME_ERROR;
-  }
-}
-
 bool fits_i32(size_t value) { return value <= 0x7fffffffu; }
 
 // Enqueues the product with the posture's kernel: the matrix cores under
@@ -285,16 +265,11 @@ int topos_hip_chain_create(const topos_hip_chain_desc *desc, topos_hip_chain **c
 
 int topos_hip_chain_launch(const topos_hip_chain *chain, const float *const *inputs,
                            float *const *outputs, void *stream) {
-  if (!chain || (chain->n_inputs && !inputs) || !outputs) return TOPOS_HIP_INVALID_ARGUMENT;
+  if (!chain || !outputs) return TOPOS_HIP_INVALID_ARGUMENT;
   const int status = ready_for_device_face();
   if (status != TOPOS_HIP_OK) return status;
   return guarded([&] { launch_chain(*chain, inputs, outputs, static_cast<hipStream_t>(stream)); });
 }
 
-const char *topos_hip_chain_source(const topos_hip_chain *chain) {
-  return chain ? chain->source.c_str() : "";
-}
-
-void topos_hip_chain_destroy(topos_hip_chain *chain) { delete chain; }
 
 }  // extern "C"

@@ -12,19 +12,6 @@
 
 #include "../../include/topos_hip.h"
 
-// A compiled chain kernel (topos_hip_chain_create).
-struct topos_hip_chain {
-  std::string source;
-  hipModule_t module = nullptr;
-  hipFunction_t function = nullptr;
-  int n_inputs = 0;
-  int n_outputs = 0;
-  int64_t volume = 0;
-  bool quads = false;             // innermost extent % 4 == 0: quad path legal
-  std::vector<bool> vector_in;    // input may use 16-byte loads (given alignment)
-  std::vector<int64_t> in_offset;
-};
-
 namespace topos_hip {
 
 // The device calls the library makes outside kernel launches, as a table so a
@@ -93,6 +80,30 @@ class Context {
   std::mutex task_lock_;
 };
 
+// Runs `body`, mapping the library's exceptions to status codes; a runtime
+// failure poisons the library for good.
+template <class Body>
+int guarded(Body body) {
+  try {
+    body();
+    return TOPOS_HIP_OK;
+  } catch (const InvalidArgument &) {
+    return TOPOS_HIP_INVALID_ARGUMENT;
+  } catch (const Unsupported &) {
+    return TOPOS_HIP_UNSUPPORTED;
+  } catch (const RuntimeFailure &e) {
+    Context::get().poison(e.message);
+    return TOPOS_HIP_RUNTIME_ERROR;
+  } catch (const std::bad_alloc &) {
+    Context::get().poison("host allocation failed");
+    return TOPOS_HIP_RUNTIME_ERROR;
+  }
+}
+
+// The message of the last InvalidArgument/Unsupported a program call raised
+// on this thread (for diagnostics; status codes stay the contract).
+std::string &last_refusal();
+
 // Throws RuntimeFailure on a HIP error, naming the call.
 void check(hipError_t status, const char *what);
 // Checks the launch status of the kernel just enqueued.
@@ -100,15 +111,38 @@ void check_launch(const char *what);
 
 // ---- kernel launchers (device face); throw on failure ----
 
+// A batch of equally shaped products: product `i` reads a + i * a_bs and
+// b + i * b_bs and writes c + i * c_bs (the batch odometer of
+// src/payload/tensor.rs:950-1006 flattened to one axis).
+struct Batch {
+  int64_t count = 1;
+  int64_t a_stride = 0, b_stride = 0, c_stride = 0;
+};
+
 // gemm_exact.hip: bit-identical to src/payload/gemm.rs:140-211.
 void launch_gemm_exact(const float *a, int64_t a_rs, int64_t a_cs, const float *b, int64_t b_rs,
                        int64_t b_cs, int64_t m, int64_t k, int64_t n, float *c, int64_t ldc,
-                       hipStream_t stream);
+                       hipStream_t stream, const Batch &batch = Batch());
 // gemm_mfma.hip: fp32 MFMA product within the stated envelope. Returns false
 // when the stride pattern is outside its loaders (caller falls back).
 bool launch_gemm_mfma(const float *a, int64_t a_rs, int64_t a_cs, const float *b, int64_t b_rs,
                       int64_t b_cs, int64_t m, int64_t k, int64_t n, float *c, int64_t ldc,
-                      hipStream_t stream);
+                      hipStream_t stream, const Batch &batch = Batch());
+
+// index.hip
+void launch_gather(const float *table, int64_t row_stride, int64_t column_stride, const int32_t *indices,
+                   int64_t rows, int64_t row_size, float *out, hipStream_t stream);
+void launch_scatter(const float *gradient, int64_t row_stride, int64_t column_stride, const int32_t *row_start,
+                    const int32_t *sources, int64_t rows, int64_t row_size, float *out, hipStream_t stream);
+void launch_one_hot(const int32_t *indices, int64_t rows, int64_t vocab, float one, float *out, hipStream_t stream);
+void launch_scan(const int32_t *counts, int64_t chunks, int64_t *offsets, hipStream_t stream);
+void launch_ordered_fold(const float *compacted, const int64_t *offsets, int64_t chunks, const int32_t *positive_zero,
+                         float *out, hipStream_t stream);
+void launch_sgd(float *parameter, const float *gradient, int64_t count, float rate, hipStream_t stream);
+void launch_adamw(float *parameter, const float *gradient, float *first, float *second, int64_t count, float beta1,
+                  float beta2, float first_share, float second_share, float first_correction,
+                  float second_correction, float epsilon, float rate, float decay, int decayed,
+                  hipStream_t stream);
 
 // map.hip: host-libm-faithful unary maps over contiguous buffers.
 void launch_map(int operation, const float *x, int64_t count, float *y, hipStream_t stream);

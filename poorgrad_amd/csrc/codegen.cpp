@@ -1,0 +1,614 @@
+// Generated kernels (codegen.hpp): HIP source per expression, compiled by
+// hipRTC for gfx950 and cached per process by source text.
+//
+// Shapes, strides and offsets are compile-time constants of the generated
+// source, so coordinate arithmetic is division by constants and every
+// address is a fused integer expression. The same faithful_math.h text the
+// prebuilt kernels compile is embedded, so a generated exp is the library's
+// exp bit for bit.
+#include "codegen.hpp"
+
+#include <hip/hiprtc.h>
+
+#include <algorithm>
+#include <atomic>
+#include <map>
+#include <mutex>
+#include <sstream>
+#include <thread>
+
+#include "faithful_math_text.h"  // kFaithfulMathText: faithful_math.h as a string
+
+namespace topos_hip {
+
+namespace {
+
+std::mutex cache_lock;
+// Source text -> compiled kernel (loaded or not).
+std::map<std::string, Kernel> &cache() {
+  static auto *compiled = new std::map<std::string, Kernel>();
+  return *compiled;
+}
+
+const char *unary_pattern(int op) {
+  switch (op) {
+    case TOPOS_HIP_CHAIN_NEG: return "(-%a)";
+    case TOPOS_HIP_CHAIN_EXP: return "topos_faithful::exp_f32(%a)";
+    case TOPOS_HIP_CHAIN_LN: return "topos_faithful::ln_f32(%a)";
+    case TOPOS_HIP_CHAIN_SQRT: return "__builtin_sqrtf(%a)";
+    case TOPOS_HIP_CHAIN_TANH: return "topos_faithful::tanh_f32(%a)";
+  }
+  return nullptr;
+}
+
+const char *binary_pattern(int op) {
+  switch (op) {
+    case TOPOS_HIP_CHAIN_ADD: return "(%a + %b)";
+    case TOPOS_HIP_CHAIN_SUB: return "(%a - %b)";
+    case TOPOS_HIP_CHAIN_MUL: return "(%a * %b)";
+    case TOPOS_HIP_CHAIN_DIV: return "(%a / %b)";
+    case TOPOS_HIP_CHAIN_MAX: return "topos_faithful::max_f32(%a, %b)";
+    case TOPOS_HIP_CHAIN_STEP: return "topos_faithful::step_f32(%a, %b)";
+  }
+  return nullptr;
+}
+
+std::string substitute(const char *pattern, const std::string &a, const std::string &b) {
+  std::string out;
+  for (const char *p = pattern; *p; ++p) {
+    if (p[0] == '%' && p[1] == 'a') {
+      out += a;
+      ++p;
+    } else if (p[0] == '%' && p[1] == 'b') {
+      out += b;
+      ++p;
+    } else {
+      out += *p;
+    }
+  }
+  return out;
+}
+
+std::string ll(int64_t v) { return std::to_string(v) + "LL"; }
+
+std::string float_literal(float v) {
+  // Exact: the bit pattern reinterpreted.
+  return "__builtin_bit_cast(float, " + std::to_string(__builtin_bit_cast(uint32_t, v)) + "u)";
+}
+
+std::string ref(int value, const std::string &lane) {
+  if (value < 0) return "in" + std::to_string(-value - 1) + "_" + lane;
+  return "s" + std::to_string(value) + "_" + lane;
+}
+
+void validate(const Expr &e) {
+  if (e.rank < 0 || e.rank > kMaxRank) throw InvalidArgument{"expression rank out of range"};
+  for (int d = 0; d < e.rank; ++d)
+    if (e.shape[d] <= 0) throw InvalidArgument{"expression shape must be non-empty"};
+  if (e.outputs.empty()) throw InvalidArgument{"expression without results"};
+  const int n_inputs = (int)e.inputs.size();
+  auto check_ref = [&](int v, int step) {
+    if (v < 0 ? (-v - 1) >= n_inputs : v >= step) throw InvalidArgument{"expression operand reference"};
+  };
+  for (size_t s = 0; s < e.steps.size(); ++s) {
+    const ExprStep &st = e.steps[s];
+    if (!is_unary(st.op) && !is_binary(st.op)) throw InvalidArgument{"unknown expression operation"};
+    check_ref(st.left, (int)s);
+    if (is_binary(st.op)) check_ref(st.right, (int)s);
+  }
+  for (int o : e.outputs) check_ref(o, (int)e.steps.size());
+  for (const ExprInput &in : e.inputs) {
+    if (in.kind == ExprInput::kSelection && e.rank != 2)
+      throw InvalidArgument{"a selection input needs a rank-2 expression"};
+    if (in.kind == ExprInput::kPadded && (in.pad_axis < 0 || in.pad_axis >= e.rank || in.pad_len <= 0))
+      throw InvalidArgument{"padded input window"};
+  }
+}
+
+// Input i may use 16-byte loads along the innermost axis: unit inner stride
+// and every quad start 16-byte aligned relative to the base pointer.
+bool vector_input(const Expr &e, const ExprInput &in) {
+  if (e.rank == 0 || in.kind == ExprInput::kSelection || in.kind == ExprInput::kLiteral) return false;
+  const int inner = e.rank - 1;
+  if (in.strides[inner] != 1 || in.offset % 4 != 0) return false;
+  for (int d = 0; d < inner; ++d)
+    if (in.strides[d] % 4 != 0) return false;
+  if (in.kind == ExprInput::kPadded && in.pad_axis == inner && (in.pad_start % 4 != 0 || in.pad_len % 4 != 0))
+    return false;
+  return true;
+}
+
+std::string pointer_type(const ExprInput &in) {
+  return in.kind == ExprInput::kSelection ? "const int* __restrict__" : "const float* __restrict__";
+}
+
+// Address of input `in` at coordinates `c` (names), the pad axis shifted.
+std::string address(const Expr &e, const ExprInput &in, const std::vector<std::string> &c) {
+  std::string a = ll(in.offset);
+  for (int d = 0; d < e.rank; ++d) {
+    if (in.strides[d] == 0) continue;
+    std::string coord = c[d];
+    if (in.kind == ExprInput::kPadded && d == in.pad_axis) coord = "(" + coord + " - " + ll(in.pad_start) + ")";
+    a += " + " + coord + " * " + ll(in.strides[d]);
+  }
+  return a;
+}
+
+std::string window_test(const ExprInput &in, const std::string &coord) {
+  return "(" + coord + " >= " + ll(in.pad_start) + " && " + coord + " < " + ll(in.pad_start + in.pad_len) + ")";
+}
+
+// Scalar value of input i at coordinates c.
+std::string scalar_value(const Expr &e, int i, const std::vector<std::string> &c) {
+  const ExprInput &in = e.inputs[i];
+  const std::string p = "p" + std::to_string(i);
+  if (in.kind == ExprInput::kLiteral) return float_literal(in.one);
+  if (in.kind == ExprInput::kSelection)
+    return "(" + p + "[" + c[0] + "] == (int)(" + c[1] + ") ? " + float_literal(in.one) + " : 0.0f)";
+  const std::string load = p + "[" + address(e, in, c) + "]";
+  if (in.kind == ExprInput::kPadded) return "(" + window_test(in, c[in.pad_axis]) + " ? " + load + " : 0.0f)";
+  return load;
+}
+
+void emit_steps(std::ostringstream &s, const Expr &e, const std::vector<std::string> &lanes) {
+  for (size_t k = 0; k < e.steps.size(); ++k) {
+    const ExprStep &x = e.steps[k];
+    for (const std::string &lane : lanes) {
+      const std::string a = ref(x.left, lane);
+      const std::string expr = is_unary(x.op) ? substitute(unary_pattern(x.op), a, "")
+                                              : substitute(binary_pattern(x.op), a, ref(x.right, lane));
+      s << "      const float s" << k << "_" << lane << " = " << expr << ";\n";
+    }
+  }
+}
+
+// Coordinates of flat index `flat` over `shape[0..rank)`, named c<d>_<tag>.
+void emit_coordinates(std::ostringstream &s, int rank, const int64_t *shape, const std::string &flat,
+                      const std::string &tag, std::vector<std::string> &names) {
+  names.assign(rank, "");
+  std::string rem = flat;
+  for (int d = rank - 1; d >= 0; --d) {
+    const std::string name = "c" + std::to_string(d) + "_" + tag;
+    names[d] = name;
+    if (d == 0) {
+      s << "      const long long " << name << " = " << rem << ";\n";
+    } else {
+      s << "      const long long " << name << " = (" << rem << ") % " << ll(shape[d]) << ";\n";
+      const std::string next = "r" + std::to_string(d) + "_" + tag;
+      s << "      const long long " << next << " = (" << rem << ") / " << ll(shape[d]) << ";\n";
+      rem = next;
+    }
+  }
+}
+
+std::string preamble() {
+  std::string s = "#pragma clang fp contract(off)\n";
+  s += kFaithfulMathText;
+  s += "\n";
+  return s;
+}
+
+std::string signature(const Expr &e, const std::string &tail) {
+  std::ostringstream s;
+  s << "extern \"C\" __global__ __launch_bounds__(256) void topos_gen(";
+  for (size_t i = 0; i < e.inputs.size(); ++i) s << pointer_type(e.inputs[i]) << " p" << i << ", ";
+  s << tail << ")";
+  return s.str();
+}
+
+std::vector<char> rtc_compile(const std::string &source) {
+  hiprtcProgram program;
+  if (hiprtcCreateProgram(&program, source.c_str(), "topos_gen.hip", 0, nullptr, nullptr) != HIPRTC_SUCCESS)
+    throw RuntimeFailure{"hiprtcCreateProgram failed"};
+  const char *options[] = {"--offload-arch=gfx950", "-O3", "-ffp-contract=off",
+                           "-fno-gpu-flush-denormals-to-zero", "-fhip-fp32-correctly-rounded-divide-sqrt",
+                           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"};
+  const hiprtcResult built = hiprtcCompileProgram(program, (int)(sizeof(options) / sizeof(options[0])), options);
+  if (built != HIPRTC_SUCCESS) {
+    size_t size = 0;
+    hiprtcGetProgramLogSize(program, &size);
+    std::string log(size, '\0');
+    if (size) hiprtcGetProgramLog(program, &log[0]);
+    hiprtcDestroyProgram(&program);
+    throw RuntimeFailure{"generated kernel failed to compile: " + log};
+  }
+  size_t code_size = 0;
+  hiprtcGetCodeSize(program, &code_size);
+  std::vector<char> code(code_size);
+  hiprtcGetCode(program, code.data());
+  hiprtcDestroyProgram(&program);
+  return code;
+}
+
+Generated make(const std::string &source) {
+  auto g = std::make_shared<Kernel>();
+  g->source = source;
+  return g;
+}
+
+bool pointers_aligned(const Expr &e, const void *const *inputs) {
+  for (size_t i = 0; i < e.inputs.size(); ++i)
+    if (vector_input(e, e.inputs[i]) && reinterpret_cast<uintptr_t>(inputs[i]) % 16 != 0) return false;
+  return true;
+}
+
+void launch(const Generated &g, unsigned blocks, std::vector<void *> &arguments, hipStream_t stream) {
+  if (!g || !g->loaded) throw RuntimeFailure{"generated kernel was not loaded"};
+  check(hipModuleLaunchKernel(g->function, blocks, 1, 1, 256, 1, 1, 0, stream, arguments.data(), nullptr),
+        "hipModuleLaunchKernel(generated)");
+}
+
+}  // namespace
+
+void compile_kernels(const std::vector<Generated> &kernels, bool load) {
+  // Distinct sources that still need work.
+  std::vector<std::string> todo;
+  {
+    std::lock_guard<std::mutex> guard(cache_lock);
+    std::map<std::string, bool> seen;
+    for (const Generated &g : kernels) {
+      if (!g || seen.count(g->source)) continue;
+      seen[g->source] = true;
+      auto it = cache().find(g->source);
+      if (it == cache().end() || (load && !it->second.loaded)) todo.push_back(g->source);
+    }
+  }
+  // hipRTC in parallel; each thread compiles its share.
+  std::vector<std::vector<char>> codes(todo.size());
+  std::vector<std::string> failures(todo.size());
+  const unsigned hardware = std::max(1u, std::thread::hardware_concurrency());
+  const size_t workers = std::min<size_t>(todo.size(), std::min(16u, hardware));
+  std::vector<std::thread> threads;
+  std::atomic<size_t> next{0};
+  for (size_t w = 0; w < workers; ++w)
+    threads.emplace_back([&] {
+      for (size_t i = next++; i < todo.size(); i = next++) {
+        try {
+          codes[i] = rtc_compile(todo[i]);
+        } catch (const RuntimeFailure &e) {
+          failures[i] = e.message;
+        }
+      }
+    });
+  for (std::thread &t : threads) t.join();
+  for (size_t i = 0; i < todo.size(); ++i)
+    if (!failures[i].empty()) throw RuntimeFailure{failures[i]};
+  // Load on the calling thread, then publish.
+  std::lock_guard<std::mutex> guard(cache_lock);
+  for (size_t i = 0; i < todo.size(); ++i) {
+    Kernel k;
+    k.source = todo[i];
+    if (load) {
+      hipModule_t module;
+      check(hipModuleLoadData(&module, codes[i].data()), "hipModuleLoadData(generated)");
+      check(hipModuleGetFunction(&k.function, module, "topos_gen"), "hipModuleGetFunction(generated)");
+      k.loaded = true;
+    }
+    cache()[todo[i]] = k;
+  }
+  for (const Generated &g : kernels) {
+    if (!g) continue;
+    const Kernel &k = cache().at(g->source);
+    g->function = k.function;
+    g->loaded = k.loaded;
+  }
+}
+
+bool is_unary(int op) { return unary_pattern(op) != nullptr; }
+bool is_binary(int op) { return binary_pattern(op) != nullptr; }
+
+// ---- chain ----
+
+Generated generate_chain(const Expr &e) {
+  validate(e);
+  std::ostringstream s;
+  s << preamble();
+  std::string tail;
+  for (size_t o = 0; o < e.outputs.size(); ++o) tail += "float* __restrict__ q" + std::to_string(o) + ", ";
+  tail += "int vector_ok";
+  s << signature(e, tail) << " {\n";
+  const int64_t volume = e.volume();
+  s << "  const long long volume = " << ll(volume) << ";\n";
+  s << "  const long long stride = (long long)gridDim.x * 1024;\n";
+  s << "  for (long long base = ((long long)blockIdx.x * 256 + threadIdx.x) * 4; base < volume; base += stride) {\n";
+  const bool quads = e.rank > 0 && e.shape[e.rank - 1] % 4 == 0;
+  const std::vector<std::string> lanes = {"0", "1", "2", "3"};
+  if (quads) {
+    const int inner = e.rank - 1;
+    s << "    {\n";
+    std::vector<std::string> c;
+    emit_coordinates(s, e.rank, e.shape, "base", "q", c);
+    for (size_t i = 0; i < e.inputs.size(); ++i) {
+      const ExprInput &in = e.inputs[i];
+      const std::string p = "p" + std::to_string(i), v = "in" + std::to_string(i) + "_";
+      if (in.kind == ExprInput::kLiteral) {
+        for (int j = 0; j < 4; ++j) s << "      const float " << v << j << " = " << float_literal(in.one) << ";\n";
+        continue;
+      }
+      if (in.kind == ExprInput::kSelection) {
+        s << "      const int sel" << i << " = " << p << "[" << c[0] << "];\n";
+        for (int j = 0; j < 4; ++j)
+          s << "      const float " << v << j << " = (sel" << i << " == (int)(" << c[1] << " + " << j << ")) ? "
+            << float_literal(in.one) << " : 0.0f;\n";
+        continue;
+      }
+      const bool padded = in.kind == ExprInput::kPadded;
+      const bool inner_window = padded && in.pad_axis == inner;
+      // A window test that holds for the whole quad: on an outer axis, or an
+      // inner window whose bounds are multiples of four.
+      const bool quad_window = padded && (!inner_window || (in.pad_start % 4 == 0 && in.pad_len % 4 == 0));
+      const std::string a = "a" + std::to_string(i);
+      s << "      const long long " << a << " = " << address(e, in, c) << ";\n";
+      if (!padded || quad_window) {
+        const std::string inside = padded ? window_test(in, c[in.pad_axis]) : "true";
+        s << "      float " << v << "0 = 0.0f, " << v << "1 = 0.0f, " << v << "2 = 0.0f, " << v << "3 = 0.0f;\n";
+        s << "      if (" << inside << ") {\n";
+        if (in.strides[inner] == 0) {
+          s << "        " << v << "0 = " << p << "[" << a << "]; " << v << "1 = " << v << "0; " << v << "2 = " << v
+            << "0; " << v << "3 = " << v << "0;\n";
+        } else if (vector_input(e, in)) {
+          s << "        if (vector_ok) { const float4 w = *(const float4*)(" << p << " + " << a << "); " << v
+            << "0 = w.x; " << v << "1 = w.y; " << v << "2 = w.z; " << v << "3 = w.w; }\n";
+          s << "        else { ";
+          for (int j = 0; j < 4; ++j) s << v << j << " = " << p << "[" << a << " + " << j << "]; ";
+          s << "}\n";
+        } else {
+          for (int j = 0; j < 4; ++j)
+            s << "        " << v << j << " = " << p << "[" << a << " + " << ll(j * in.strides[inner]) << "];\n";
+        }
+        s << "      }\n";
+      } else {
+        for (int j = 0; j < 4; ++j) {
+          const std::string cj = "(" + c[inner] + " + " + std::to_string(j) + ")";
+          s << "      const float " << v << j << " = " << window_test(in, cj) << " ? " << p << "[" << a << " + "
+            << ll(j * in.strides[inner]) << "] : 0.0f;\n";
+        }
+      }
+    }
+    emit_steps(s, e, lanes);
+    for (size_t o = 0; o < e.outputs.size(); ++o) {
+      s << "      if (vector_ok) *(float4*)(q" << o << " + base) = make_float4(";
+      for (int j = 0; j < 4; ++j) s << (j ? ", " : "") << ref(e.outputs[o], lanes[j]);
+      s << ");\n      else {";
+      for (int j = 0; j < 4; ++j) s << " q" << o << "[base + " << j << "] = " << ref(e.outputs[o], lanes[j]) << ";";
+      s << " }\n";
+    }
+    s << "    }\n";
+  } else {
+    s << "    for (int j = 0; j < 4 && base + j < volume; ++j) {\n";
+    s << "      const long long f = base + j;\n";
+    std::vector<std::string> c;
+    if (e.rank > 0) emit_coordinates(s, e.rank, e.shape, "f", "g", c);
+    for (size_t i = 0; i < e.inputs.size(); ++i)
+      s << "      const float in" << i << "_g = " << scalar_value(e, (int)i, c) << ";\n";
+    emit_steps(s, e, {"g"});
+    for (size_t o = 0; o < e.outputs.size(); ++o) s << "      q" << o << "[f] = " << ref(e.outputs[o], "g") << ";\n";
+    s << "    }\n";
+  }
+  s << "  }\n}\n";
+  return make(s.str());
+}
+
+void launch_generated_chain(const Generated &g, const Expr &e, const void *const *inputs, float *const *outputs,
+                            hipStream_t stream) {
+  int vector_ok = pointers_aligned(e, inputs) ? 1 : 0;
+  for (size_t o = 0; o < e.outputs.size(); ++o)
+    if (reinterpret_cast<uintptr_t>(outputs[o]) % 16 != 0) vector_ok = 0;
+  std::vector<const void *> pointers;
+  for (size_t i = 0; i < e.inputs.size(); ++i) pointers.push_back(inputs[i]);
+  for (size_t o = 0; o < e.outputs.size(); ++o) pointers.push_back(outputs[o]);
+  std::vector<void *> arguments;
+  for (auto &p : pointers) arguments.push_back(&p);
+  arguments.push_back(&vector_ok);
+  int64_t blocks = (e.volume() + 1023) / 1024;
+  if (blocks < 1) blocks = 1;
+  if (blocks > 256 * 16) blocks = 256 * 16;
+  launch(g, (unsigned)blocks, arguments, stream);
+}
+
+// ---- fold ----
+
+Generated generate_fold(const Expr &e, int axis, FoldKind kind) {
+  validate(e);
+  if (axis < 0 || axis >= e.rank) throw InvalidArgument{"fold axis out of range"};
+  std::ostringstream s;
+  s << preamble();
+  s << signature(e, "float* __restrict__ out") << " {\n";
+  // Remaining axes, in order, name the output coordinates.
+  std::vector<int64_t> rest;
+  std::vector<int> rest_axes;
+  for (int d = 0; d < e.rank; ++d)
+    if (d != axis) {
+      rest.push_back(e.shape[d]);
+      rest_axes.push_back(d);
+    }
+  int64_t outputs = 1;
+  for (int64_t x : rest) outputs *= x;
+  const int64_t extent = e.shape[axis];
+  s << "  const long long o = (long long)blockIdx.x * 256 + threadIdx.x;\n";
+  s << "  if (o >= " << ll(outputs) << ") return;\n";
+  std::vector<std::string> rc;
+  if (!rest.empty()) emit_coordinates(s, (int)rest.size(), rest.data(), "o", "o", rc);
+  std::vector<std::string> c(e.rank);
+  for (size_t k = 0; k < rest_axes.size(); ++k) c[rest_axes[k]] = rc[k];
+  c[axis] = "k";
+  // Per-input base address with the fold coordinate at zero, and its stride.
+  std::vector<std::string> zero = c;
+  zero[axis] = "0LL";
+  const bool inner_axis = axis == e.rank - 1;
+  bool quads = inner_axis && extent % 4 == 0 && extent >= 4;
+  for (const ExprInput &in : e.inputs)
+    if (in.kind == ExprInput::kPadded && in.pad_axis == axis && (in.pad_start % 4 || in.pad_len % 4)) quads = false;
+  for (size_t i = 0; i < e.inputs.size(); ++i) {
+    const ExprInput &in = e.inputs[i];
+    if (in.kind == ExprInput::kLiteral) continue;
+    if (in.kind == ExprInput::kSelection) {
+      // Folding along the vocabulary: the row, hence its index, is fixed.
+      if (axis == 1) s << "  const int sel" << i << " = p" << i << "[" << c[0] << "];\n";
+      continue;
+    }
+    std::string base = ll(in.offset);
+    for (int d = 0; d < e.rank; ++d) {
+      if (d == axis || in.strides[d] == 0) continue;
+      std::string coord = c[d];
+      if (in.kind == ExprInput::kPadded && d == in.pad_axis) coord = "(" + coord + " - " + ll(in.pad_start) + ")";
+      base += " + " + coord + " * " + ll(in.strides[d]);
+    }
+    if (in.kind == ExprInput::kPadded && in.pad_axis == axis) base += " - " + ll(in.pad_start * in.strides[axis]);
+    s << "  const float* __restrict__ b" << i << " = p" << i << " + (" << base << ");\n";
+    if (in.kind == ExprInput::kPadded && in.pad_axis != axis)
+      s << "  const bool w" << i << " = " << window_test(in, c[in.pad_axis]) << ";\n";
+  }
+  // The value of input i at fold coordinate `k` (+j).
+  auto value = [&](int i, const std::string &k) -> std::string {
+    const ExprInput &in = e.inputs[i];
+    if (in.kind == ExprInput::kLiteral) return float_literal(in.one);
+    if (in.kind == ExprInput::kSelection) {
+      if (axis == 0)  // folding over rows: each step reads its row's index
+        return "(p" + std::to_string(i) + "[" + k + "] == (int)(" + c[1] + ") ? " + float_literal(in.one) + " : 0.0f)";
+      return "(sel" + std::to_string(i) + " == (int)(" + k + ") ? " + float_literal(in.one) + " : 0.0f)";
+    }
+    const std::string load = "b" + std::to_string(i) + "[(" + k + ") * " + ll(in.strides[axis]) + "]";
+    if (in.kind == ExprInput::kPadded) {
+      if (in.pad_axis == axis) return "(" + window_test(in, k) + " ? " + load + " : 0.0f)";
+      return "(w" + std::to_string(i) + " ? " + load + " : 0.0f)";
+    }
+    return load;
+  };
+  auto combine = [&](const std::string &acc, const std::string &v) {
+    return kind == kFoldSum ? acc + " + " + v : "topos_faithful::max_f32(" + acc + ", " + v + ")";
+  };
+  const std::string result = ref(e.outputs[0], "x");
+  auto element = [&](const std::string &k) {
+    for (size_t i = 0; i < e.inputs.size(); ++i) s << "      const float in" << i << "_x = " << value((int)i, k) << ";\n";
+    emit_steps(s, e, {"x"});
+  };
+  s << "  float acc;\n";
+  s << "  {\n    const long long k = 0;\n";
+  element("k");
+  s << "    acc = " << result << ";\n  }\n";
+  if (quads) {
+    // Steps 1..3 of the first quad, then whole quads: the loads of a quad
+    // are independent of the fold, so they issue together.
+    s << "  for (long long k = 1; k < 4; ++k) {\n";
+    element("k");
+    s << "    acc = " << combine("acc", result) << ";\n  }\n";
+    s << "  #pragma unroll 2\n";
+    s << "  for (long long k4 = 4; k4 < " << ll(extent) << "; k4 += 4) {\n";
+    for (int j = 0; j < 4; ++j) {
+      s << "    float r" << j << ";\n    {\n      const long long k = k4 + " << j << ";\n";
+      element("k");
+      s << "      r" << j << " = " << result << ";\n    }\n";
+    }
+    for (int j = 0; j < 4; ++j) s << "    acc = " << combine("acc", "r" + std::to_string(j)) << ";\n";
+    s << "  }\n";
+  } else {
+    s << "  for (long long k = 1; k < " << ll(extent) << "; ++k) {\n";
+    element("k");
+    s << "    acc = " << combine("acc", result) << ";\n  }\n";
+  }
+  s << "  out[o] = acc;\n}\n";
+  return make(s.str());
+}
+
+void launch_generated_fold(const Generated &g, const Expr &e, int axis, const void *const *inputs, float *out,
+                           hipStream_t stream) {
+  int64_t outputs = 1;
+  for (int d = 0; d < e.rank; ++d)
+    if (d != axis) outputs *= e.shape[d];
+  std::vector<const void *> pointers;
+  for (size_t i = 0; i < e.inputs.size(); ++i) pointers.push_back(inputs[i]);
+  pointers.push_back(out);
+  std::vector<void *> arguments;
+  for (auto &p : pointers) arguments.push_back(&p);
+  const int64_t blocks = (outputs + 255) / 256;
+  if (blocks > 0x7fffffff) throw Unsupported{"fold: too many outputs for one launch"};
+  launch(g, (unsigned)blocks, arguments, stream);
+}
+
+// ---- exact whole-tensor sum over a large operand ----
+
+namespace {
+
+// Emits the odometer walk over one chunk's flat range, calling `body` with
+// the value of the expression at the current element as `v`.
+void emit_chunk_walk(std::ostringstream &s, const Expr &e, const std::string &body) {
+  const int64_t volume = e.volume();
+  s << "  const long long chunk = (long long)blockIdx.x * 256 + threadIdx.x;\n";
+  s << "  const long long first = chunk * " << ll(kSumChunk) << ";\n";
+  s << "  if (first >= " << ll(volume) << ") return;\n";
+  s << "  const long long count = " << ll(volume) << " - first < " << ll(kSumChunk) << " ? " << ll(volume)
+    << " - first : " << ll(kSumChunk) << ";\n";
+  std::vector<std::string> start;
+  emit_coordinates(s, e.rank, e.shape, "first", "f", start);
+  std::vector<std::string> c(e.rank);
+  for (int d = 0; d < e.rank; ++d) {
+    c[d] = "c" + std::to_string(d);
+    s << "  long long " << c[d] << " = " << start[d] << ";\n";
+  }
+  s << "  for (long long i = 0; i < count; ++i) {\n";
+  for (size_t i = 0; i < e.inputs.size(); ++i)
+    s << "      const float in" << i << "_x = " << scalar_value(e, (int)i, c) << ";\n";
+  emit_steps(s, e, {"x"});
+  s << "    const float v = " << ref(e.outputs[0], "x") << ";\n";
+  s << body;
+  // Advance the odometer.
+  if (e.rank > 0) {
+    s << "    ++" << c[e.rank - 1] << ";\n";
+    for (int d = e.rank - 1; d > 0; --d)
+      s << "    if (" << c[d] << " == " << ll(e.shape[d]) << ") { " << c[d] << " = 0; ++" << c[d - 1] << "; }\n";
+  }
+  s << "  }\n";
+}
+
+}  // namespace
+
+Generated generate_sum_count(const Expr &e) {
+  validate(e);
+  std::ostringstream s;
+  s << preamble();
+  s << signature(e, "int* __restrict__ counts, int* __restrict__ positive_zero") << " {\n";
+  s << "  int nonzero = 0, plus_zero = 0;\n";
+  // A term is "zero" only when it compares equal to zero; NaN counts as a term.
+  emit_chunk_walk(s, e, "    if (v == 0.0f) { if (!__builtin_signbit(v)) plus_zero = 1; } else { ++nonzero; }\n");
+  s << "  counts[chunk] = nonzero;\n  positive_zero[chunk] = plus_zero;\n}\n";
+  return make(s.str());
+}
+
+Generated generate_sum_compact(const Expr &e) {
+  validate(e);
+  std::ostringstream s;
+  s << preamble();
+  s << signature(e, "const long long* __restrict__ offsets, float* __restrict__ compacted") << " {\n";
+  s << "  long long at = 0;\n";
+  s << "  float* __restrict__ dst = nullptr;\n";
+  s << "  { const long long chunk0 = (long long)blockIdx.x * 256 + threadIdx.x;\n";
+  s << "    if (chunk0 * " << ll(kSumChunk) << " < " << ll(e.volume()) << ") dst = compacted + offsets[chunk0]; }\n";
+  emit_chunk_walk(s, e, "    if (!(v == 0.0f)) dst[at++] = v;\n");
+  s << "}\n";
+  return make(s.str());
+}
+
+void launch_sum_count(const Generated &g, const Expr &e, const void *const *inputs, int32_t *counts,
+                      int32_t *positive_zero, hipStream_t stream) {
+  const int64_t chunks = (e.volume() + kSumChunk - 1) / kSumChunk;
+  std::vector<const void *> pointers(inputs, inputs + e.inputs.size());
+  pointers.push_back(counts);
+  pointers.push_back(positive_zero);
+  std::vector<void *> arguments;
+  for (auto &p : pointers) arguments.push_back(&p);
+  launch(g, (unsigned)((chunks + 255) / 256), arguments, stream);
+}
+
+void launch_sum_compact(const Generated &g, const Expr &e, const void *const *inputs, const int64_t *offsets,
+                        float *compacted, hipStream_t stream) {
+  const int64_t chunks = (e.volume() + kSumChunk - 1) / kSumChunk;
+  std::vector<const void *> pointers(inputs, inputs + e.inputs.size());
+  pointers.push_back(offsets);
+  pointers.push_back(compacted);
+  std::vector<void *> arguments;
+  for (auto &p : pointers) arguments.push_back(&p);
+  launch(g, (unsigned)((chunks + 255) / 256), arguments, stream);
+}
+
+}  // namespace topos_hip

@@ -1,0 +1,108 @@
+// Generated kernels: an elementwise expression over strided views, emitted
+// as HIP source and compiled by hipRTC for gfx950 (cached per source text).
+//
+// One expression model serves three kernel shapes:
+//   - a chain: the expression's requested results written contiguous, four
+//     consecutive elements per lane (16-byte loads and stores where legal);
+//   - a fold: the expression reduced along one axis in ascending order, one
+//     lane per output, seeded with the first term (the sequential folds of
+//     src/payload/tensor.rs:1055-1124);
+//   - the two passes of an exact whole-tensor sum over a large operand (count
+//     and compact the nonzero terms), whose final ordered fold runs in
+//     index.hip.
+// Every operation rounds to f32 exactly as the interpreter's materialised
+// intermediate does: no contraction, no fast math, libm-faithful
+// transcendentals.
+#pragma once
+#include <cstdint>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "backend.hpp"
+
+namespace topos_hip {
+
+constexpr int kMaxRank = TOPOS_HIP_MAX_RANK;
+
+struct ExprInput {
+  // kLiteral: the constant `one` everywhere, embedded in the source (its
+  // pointer argument is unused).
+  enum Kind { kStrided = 0, kSelection = 1, kPadded = 2, kLiteral = 3 };
+  int kind = kStrided;
+  // kStrided / kPadded: element (c0..) lives at offset + sum c_d * strides[d]
+  // (kPadded: with the pad axis coordinate shifted by -pad_start, and +0
+  // outside the window).
+  int64_t offset = 0;
+  int64_t strides[kMaxRank] = {0, 0, 0, 0};
+  // kSelection: the expression is [rows, vocab]; the element is `one` where
+  // indices[c0] == c1, else +0.
+  float one = 1.0f;
+  // kPadded: the window [pad_start, pad_start + pad_len) along pad_axis.
+  int pad_axis = 0;
+  int64_t pad_start = 0;
+  int64_t pad_len = 0;
+};
+
+// Operand references: >= 0 an earlier step, < 0 input (-ref - 1).
+struct ExprStep {
+  int op = 0;  // TOPOS_HIP_CHAIN_*
+  int left = 0;
+  int right = 0;
+};
+
+struct Expr {
+  int rank = 0;
+  int64_t shape[kMaxRank] = {1, 1, 1, 1};
+  std::vector<ExprInput> inputs;
+  std::vector<ExprStep> steps;
+  std::vector<int> outputs;  // references; a fold reads outputs[0]
+  int64_t volume() const {
+    int64_t v = 1;
+    for (int d = 0; d < rank; ++d) v *= shape[d];
+    return v;
+  }
+};
+
+enum FoldKind { kFoldSum = 0, kFoldMax = 1 };
+
+bool is_unary(int op);
+bool is_binary(int op);
+
+// A generated kernel: its source, then (after compile_kernels) its loaded
+// function.
+struct Kernel {
+  std::string source;
+  hipFunction_t function = nullptr;
+  bool loaded = false;
+};
+using Generated = std::shared_ptr<Kernel>;
+
+// Compiles every distinct source not yet in the process cache, in parallel
+// (hipRTC, gfx950), and, when `load`, loads the modules. Kernels whose source
+// is cached share the cached module.
+void compile_kernels(const std::vector<Generated> &kernels, bool load);
+
+// Chain: outputs[o] receives volume() contiguous floats.
+Generated generate_chain(const Expr &e);
+void launch_generated_chain(const Generated &g, const Expr &e, const void *const *inputs,
+                            float *const *outputs, hipStream_t stream);
+
+// Fold along `axis`: the output is the expression's shape without that axis,
+// contiguous.
+Generated generate_fold(const Expr &e, int axis, FoldKind kind);
+void launch_generated_fold(const Generated &g, const Expr &e, int axis, const void *const *inputs,
+                           float *out, hipStream_t stream);
+
+// Whole-tensor exact sum over a large operand, in chunks of kSumChunk flat
+// elements: pass one counts each chunk's nonzero terms (and whether the
+// chunk holds a +0), pass two writes them compacted in order.
+constexpr int64_t kSumChunk = 1024;
+Generated generate_sum_count(const Expr &e);
+Generated generate_sum_compact(const Expr &e);
+void launch_sum_count(const Generated &g, const Expr &e, const void *const *inputs, int32_t *counts,
+                      int32_t *positive_zero, hipStream_t stream);
+void launch_sum_compact(const Generated &g, const Expr &e, const void *const *inputs,
+                        const int64_t *offsets, float *compacted, hipStream_t stream);
+
+}  // namespace topos_hip

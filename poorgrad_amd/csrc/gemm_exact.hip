@@ -69,8 +69,12 @@ __device__ inline void stage_right(float (*lds)[kTileN + 4], const float *__rest
 template <bool kLeftUnitInner, bool kRightUnitInner>
 __global__ __launch_bounds__(kThreads) void gemm_exact_kernel(
     const float *__restrict__ a, int64_t a_rs, int64_t a_cs, const float *__restrict__ b,
-    int64_t b_rs, int64_t b_cs, int64_t m, int64_t k, int64_t n, float *__restrict__ c, int64_t ldc) {
+    int64_t b_rs, int64_t b_cs, int64_t m, int64_t k, int64_t n, float *__restrict__ c, int64_t ldc,
+    int64_t a_bs, int64_t b_bs, int64_t c_bs) {
   __shared__ float left[kTileK][kTileM + 4];
+  a += (int64_t)blockIdx.z * a_bs;
+  b += (int64_t)blockIdx.z * b_bs;
+  c += (int64_t)blockIdx.z * c_bs;
   __shared__ float right[kTileK][kTileN + 4];
   const int64_t m0 = (int64_t)blockIdx.y * kTileM;
   const int64_t n0 = (int64_t)blockIdx.x * kTileN;
@@ -124,22 +128,23 @@ __global__ __launch_bounds__(kThreads) void gemm_exact_kernel(
 
 void launch_gemm_exact(const float *a, int64_t a_rs, int64_t a_cs, const float *b, int64_t b_rs,
                        int64_t b_cs, int64_t m, int64_t k, int64_t n, float *c, int64_t ldc,
-                       hipStream_t stream) {
+                       hipStream_t stream, const Batch &batch) {
   const int64_t grid_n = (n + kTileN - 1) / kTileN;
   const int64_t grid_m = (m + kTileM - 1) / kTileM;
-  if (grid_m > 65535 || grid_n > 0x7fffffff)
+  if (grid_m > 65535 || grid_n > 0x7fffffff || batch.count > 65535 || batch.count < 1)
     throw Unsupported{"exact gemm: product too tall for one launch"};
-  const dim3 grid((unsigned)grid_n, (unsigned)grid_m);
+  const dim3 grid((unsigned)grid_n, (unsigned)grid_m, (unsigned)batch.count);
+  const int64_t a_bs = batch.a_stride, b_bs = batch.b_stride, c_bs = batch.c_stride;
   const bool left_unit = a_cs == 1;
   const bool right_unit = b_rs == 1 && b_cs != 1;
   if (left_unit && right_unit)
-    gemm_exact_kernel<true, true><<<grid, kThreads, 0, stream>>>(a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc);
+    gemm_exact_kernel<true, true><<<grid, kThreads, 0, stream>>>(a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, a_bs, b_bs, c_bs);
   else if (left_unit)
-    gemm_exact_kernel<true, false><<<grid, kThreads, 0, stream>>>(a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc);
+    gemm_exact_kernel<true, false><<<grid, kThreads, 0, stream>>>(a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, a_bs, b_bs, c_bs);
   else if (right_unit)
-    gemm_exact_kernel<false, true><<<grid, kThreads, 0, stream>>>(a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc);
+    gemm_exact_kernel<false, true><<<grid, kThreads, 0, stream>>>(a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, a_bs, b_bs, c_bs);
   else
-    gemm_exact_kernel<false, false><<<grid, kThreads, 0, stream>>>(a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc);
+    gemm_exact_kernel<false, false><<<grid, kThreads, 0, stream>>>(a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, a_bs, b_bs, c_bs);
   check_launch("gemm_exact_kernel launch");
 }
 

@@ -105,9 +105,12 @@ template <bool kLeftInnerK, bool kRightInnerK, bool kVector>
 __global__ __launch_bounds__(kThreads) void gemm_mfma_kernel(
     const float *__restrict__ a, int64_t a_rs, int64_t a_cs, const float *__restrict__ b,
     int64_t b_rs, int64_t b_cs, int64_t m, int64_t k, int64_t n, float *__restrict__ c, int64_t ldc,
-    int grid_m, int grid_n) {
+    int grid_m, int grid_n, int64_t a_bs, int64_t b_bs, int64_t c_bs) {
   __shared__ float left[2][kTileK][kTileM + kPad];
   __shared__ float right[2][kTileK][kTileN + kPad];
+  a += (int64_t)blockIdx.y * a_bs;
+  b += (int64_t)blockIdx.y * b_bs;
+  c += (int64_t)blockIdx.y * c_bs;
 
   // Workgroups are dealt to the eight XCDs round-robin; renumber so each XCD
   // receives a contiguous run of tiles, then walk tiles in groups of kGroupM
@@ -192,18 +195,20 @@ __global__ __launch_bounds__(kThreads) void gemm_mfma_kernel(
 template <bool kL, bool kR>
 void dispatch_vector(bool vector, dim3 grid, hipStream_t stream, const float *a, int64_t a_rs,
                      int64_t a_cs, const float *b, int64_t b_rs, int64_t b_cs, int64_t m, int64_t k,
-                     int64_t n, float *c, int64_t ldc, int gm, int gn) {
+                     int64_t n, float *c, int64_t ldc, int gm, int gn, const Batch &batch) {
   if (vector)
-    gemm_mfma_kernel<kL, kR, true><<<grid, kThreads, 0, stream>>>(a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, gm, gn);
+    gemm_mfma_kernel<kL, kR, true><<<grid, kThreads, 0, stream>>>(a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, gm, gn,
+                                                                  batch.a_stride, batch.b_stride, batch.c_stride);
   else
-    gemm_mfma_kernel<kL, kR, false><<<grid, kThreads, 0, stream>>>(a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, gm, gn);
+    gemm_mfma_kernel<kL, kR, false><<<grid, kThreads, 0, stream>>>(a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, gm, gn,
+                                                                   batch.a_stride, batch.b_stride, batch.c_stride);
 }
 
 }  // namespace
 
 bool launch_gemm_mfma(const float *a, int64_t a_rs, int64_t a_cs, const float *b, int64_t b_rs,
                       int64_t b_cs, int64_t m, int64_t k, int64_t n, float *c, int64_t ldc,
-                      hipStream_t stream) {
+                      hipStream_t stream, const Batch &batch) {
   // Orientation: each operand needs a unit stride along k or along its outer
   // axis; an extent-1 axis leaves its stride unused (any value serves).
   const bool left_inner_k = a_cs == 1 || m == 1;
@@ -219,20 +224,21 @@ bool launch_gemm_mfma(const float *a, int64_t a_rs, int64_t a_cs, const float *b
   const int64_t right_lead = rk ? b_cs : b_rs;
   const bool vector = (reinterpret_cast<uintptr_t>(a) % 16 == 0) &&
                       (reinterpret_cast<uintptr_t>(b) % 16 == 0) && (left_lead % 4 == 0) &&
+                      (batch.count == 1 || (batch.a_stride % 4 == 0 && batch.b_stride % 4 == 0)) &&
                       (right_lead % 4 == 0) && (lk ? a_cs == 1 : a_rs == 1) &&
                       (rk ? b_rs == 1 : b_cs == 1);
   const int64_t gm = (m + kTileM - 1) / kTileM;
   const int64_t gn = (n + kTileN - 1) / kTileN;
-  if (gm * gn > 0x7fffffff) throw Unsupported{"mfma gemm: grid too large"};
-  const dim3 grid((unsigned)(gm * gn));
+  if (gm * gn > 0x7fffffff || batch.count > 65535 || batch.count < 1) throw Unsupported{"mfma gemm: grid too large"};
+  const dim3 grid((unsigned)(gm * gn), (unsigned)batch.count);
   if (lk && rk)
-    dispatch_vector<true, true>(vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, (int)gm, (int)gn);
+    dispatch_vector<true, true>(vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, (int)gm, (int)gn, batch);
   else if (lk)
-    dispatch_vector<true, false>(vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, (int)gm, (int)gn);
+    dispatch_vector<true, false>(vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, (int)gm, (int)gn, batch);
   else if (rk)
-    dispatch_vector<false, true>(vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, (int)gm, (int)gn);
+    dispatch_vector<false, true>(vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, (int)gm, (int)gn, batch);
   else
-    dispatch_vector<false, false>(vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, (int)gm, (int)gn);
+    dispatch_vector<false, false>(vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, (int)gm, (int)gn, batch);
   check_launch("gemm_mfma_kernel launch");
   return true;
 }

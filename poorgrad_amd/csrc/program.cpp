@@ -1,0 +1,1576 @@
+// The plan face: a topos forward plan, lowered to a node table, executed on
+// one GPU from one pre-sized HBM arena.
+//
+// Planning restates what Plan::new and Plan::forward decide
+// (src/engine/plan.rs:143-283, 514-641) and adds the device's own choices:
+//
+//   reachability  wanted = the ancestor closure of the readable nodes;
+//   values        every node's value is a storage plus a layout
+//                 (src/payload/layout.rs:23-335): a view (transpose, permute,
+//                 narrow, broadcast, broadcast_along, view-legal reshape) is a
+//                 new layout over its operand's storage and launches nothing;
+//                 a Constant payload is a layout of zero strides over one
+//                 element (host-known constants are folded at plan time with
+//                 the same f32 operations); a Selection is an index buffer;
+//   fusion        an elementwise node whose only consumer is another
+//                 elementwise node, or a sum, is not materialised: the
+//                 consumer's generated kernel recomputes it in registers (the
+//                 interpreter's per-node rounding is kept, so the bits do not
+//                 change); a pad consumed by one elementwise node becomes a
+//                 windowed input of that node's kernel;
+//   launches      one per materialised elementwise tree (a generated chain),
+//                 per reduction (a generated fold, the row kernels, or the
+//                 exact compacted whole-tensor sum), per product (the GEMM
+//                 kernels, batched over leading axes), per gather/scatter;
+//   liveness      a storage lives from the launch that writes it to the last
+//                 launch that reads it (readable values to the end of the
+//                 run); arena offsets are assigned first-fit over those
+//                 intervals.
+#include <algorithm>
+#include <array>
+#include <climits>
+#include <cmath>
+#include <cstring>
+#include <functional>
+#include <map>
+#include <memory>
+#include <sstream>
+#include <vector>
+
+#include "codegen.hpp"
+#include "faithful_math.h"
+
+namespace topos_hip {
+
+std::string &last_refusal() {
+  static thread_local std::string message;
+  return message;
+}
+
+namespace {
+
+struct Layout {
+  int rank = 0;
+  int64_t shape[kMaxRank] = {1, 1, 1, 1};
+  int64_t strides[kMaxRank] = {0, 0, 0, 0};
+  int64_t offset = 0;
+  int64_t volume() const {
+    int64_t v = 1;
+    for (int d = 0; d < rank; ++d) v *= shape[d];
+    return v;
+  }
+};
+
+Layout contiguous(int rank, const int64_t *shape, int64_t offset = 0) {
+  Layout l;
+  l.rank = rank;
+  l.offset = offset;
+  int64_t running = 1;
+  for (int d = rank - 1; d >= 0; --d) {
+    l.shape[d] = shape[d];
+    l.strides[d] = running;
+    running *= shape[d];
+  }
+  return l;
+}
+
+Layout constant_layout(int rank, const int64_t *shape, int64_t offset) {
+  Layout l;
+  l.rank = rank;
+  l.offset = offset;
+  for (int d = 0; d < rank; ++d) l.shape[d] = shape[d];
+  return l;
+}
+
+// Layout::is_contiguous (layout.rs): extent-1 axes may hold any stride.
+bool is_contiguous(const Layout &l) {
+  int64_t expected = 1;
+  for (int d = l.rank - 1; d >= 0; --d) {
+    if (l.shape[d] != 1 && l.strides[d] != expected) return false;
+    expected *= l.shape[d];
+  }
+  return true;
+}
+
+// Layout::reshape (layout.rs): a contiguous layout takes any shape; else the
+// unit-axis view when only extent-1 axes move; else None.
+bool reshape_view(const Layout &from, int rank, const int64_t *shape, Layout &out) {
+  if (is_contiguous(from)) {
+    out = contiguous(rank, shape, from.offset);
+    return true;
+  }
+  std::vector<std::pair<int64_t, int64_t>> source;
+  for (int d = 0; d < from.rank; ++d)
+    if (from.shape[d] != 1) source.push_back({from.shape[d], from.strides[d]});
+  size_t next = 0;
+  Layout l;
+  l.rank = rank;
+  l.offset = from.offset;
+  for (int d = 0; d < rank; ++d) {
+    l.shape[d] = shape[d];
+    if (shape[d] == 1) {
+      l.strides[d] = 0;
+      continue;
+    }
+    if (next >= source.size() || source[next].first != shape[d]) return false;
+    l.strides[d] = source[next].second;
+    ++next;
+  }
+  if (next != source.size()) return false;
+  out = l;
+  return true;
+}
+
+enum class StorageKind { kArena, kParameter, kInput, kLeaf, kPool, kSelectionInput, kSelectionLeaf };
+
+struct Storage {
+  StorageKind kind = StorageKind::kArena;
+  int64_t index = -1;  // slot, leaf index or pool index
+  int64_t bytes = 0;   // arena storages
+  int64_t offset = -1; // arena byte offset
+  int first = INT_MAX;
+  int last = -1;
+  bool pinned = false;
+  // selections
+  int64_t rows = 0, vocab = 0;
+  float one = 1.0f;
+};
+
+struct Value {
+  enum Kind { kNone, kDense, kSelection, kInline, kPadInline } kind = kNone;
+  int storage = -1;
+  Layout layout;
+  bool constant = false;
+  bool host_known = false;
+  float host_value = 0.0f;
+};
+
+// Device buffers of a bound selection: its indices and their row-sorted
+// order (CSR over the vocabulary) for the ordered scatter.
+struct SelectionBuffers {
+  int32_t *indices = nullptr;
+  int32_t *row_start = nullptr;
+  int32_t *sources = nullptr;
+  int64_t rows = 0, vocab = 0;
+};
+
+bool is_elementwise(int op) {
+  switch (op) {
+    case TOPOS_HIP_OP_ADD: case TOPOS_HIP_OP_SUB: case TOPOS_HIP_OP_MUL: case TOPOS_HIP_OP_DIV:
+    case TOPOS_HIP_OP_NEG: case TOPOS_HIP_OP_TANH: case TOPOS_HIP_OP_EXP: case TOPOS_HIP_OP_LN:
+    case TOPOS_HIP_OP_SQRT: case TOPOS_HIP_OP_POWF: case TOPOS_HIP_OP_MAXIMUM: case TOPOS_HIP_OP_RELU:
+    case TOPOS_HIP_OP_STEP:
+      return true;
+  }
+  return false;
+}
+
+int arity(int op) {
+  switch (op) {
+    case TOPOS_HIP_OP_LEAF: case TOPOS_HIP_OP_PARAMETER: case TOPOS_HIP_OP_INPUT: return 0;
+    case TOPOS_HIP_OP_ADD: case TOPOS_HIP_OP_SUB: case TOPOS_HIP_OP_MUL: case TOPOS_HIP_OP_DIV:
+    case TOPOS_HIP_OP_MATMUL: case TOPOS_HIP_OP_BROADCAST: case TOPOS_HIP_OP_BROADCAST_ALONG:
+    case TOPOS_HIP_OP_GATHER: case TOPOS_HIP_OP_SCATTER: case TOPOS_HIP_OP_POWF: case TOPOS_HIP_OP_MAXIMUM:
+    case TOPOS_HIP_OP_STEP:
+      return 2;
+  }
+  return 1;
+}
+
+const char *op_name(int op) {
+  static const char *names[] = {"Leaf", "Parameter", "Input", "Add", "Sub", "Mul", "Div", "Neg", "Tanh", "Exp",
+                                "Ln", "MatMul", "Transpose", "Sum", "SumAlong", "Broadcast", "BroadcastAlong",
+                                "Reshape", "Permute", "Narrow", "Pad", "Unfold", "Fold", "Gather", "Scatter",
+                                "LogSoftmax", "LogSumExp", "Sqrt", "Powf", "Maximum", "Relu", "Step"};
+  return op >= 0 && op <= TOPOS_HIP_OP_STEP ? names[op] : "?";
+}
+
+// f32 arithmetic of one elementwise node on host-known constants: the same
+// operations the kernels and the interpreter perform.
+float fold_scalar(int op, float a, float b) {
+  using namespace topos_faithful;
+  switch (op) {
+    case TOPOS_HIP_OP_ADD: return a + b;
+    case TOPOS_HIP_OP_SUB: return a - b;
+    case TOPOS_HIP_OP_MUL: return a * b;
+    case TOPOS_HIP_OP_DIV: return a / b;
+    case TOPOS_HIP_OP_NEG: return -a;
+    case TOPOS_HIP_OP_TANH: return tanh_f32(a);
+    case TOPOS_HIP_OP_EXP: return exp_f32(a);
+    case TOPOS_HIP_OP_LN: return ln_f32(a);
+    case TOPOS_HIP_OP_SQRT: return std::sqrt(a);
+    case TOPOS_HIP_OP_POWF: return powf(a, b);
+    case TOPOS_HIP_OP_MAXIMUM: return max_f32(a, b);
+    case TOPOS_HIP_OP_RELU: return max_f32(a, 0.0f);
+    case TOPOS_HIP_OP_STEP: return step_f32(a, b);
+  }
+  throw InvalidArgument{"not an elementwise operation"};
+}
+
+// The sequential sum of `count` copies of `value` (tensor.rs:1055-1093 over a
+// Constant payload); stops once further terms cannot change the total.
+float fold_repeated(float value, int64_t count) {
+  float acc = value;
+  for (int64_t i = 1; i < count; ++i) {
+    const float next = acc + value;
+    if (next == acc || next != next) {
+      acc = next;
+      break;
+    }
+    acc = next;
+  }
+  return acc;
+}
+
+int chain_op(int op) {
+  switch (op) {
+    case TOPOS_HIP_OP_ADD: return TOPOS_HIP_CHAIN_ADD;
+    case TOPOS_HIP_OP_SUB: return TOPOS_HIP_CHAIN_SUB;
+    case TOPOS_HIP_OP_MUL: return TOPOS_HIP_CHAIN_MUL;
+    case TOPOS_HIP_OP_DIV: return TOPOS_HIP_CHAIN_DIV;
+    case TOPOS_HIP_OP_NEG: return TOPOS_HIP_CHAIN_NEG;
+    case TOPOS_HIP_OP_TANH: return TOPOS_HIP_CHAIN_TANH;
+    case TOPOS_HIP_OP_EXP: return TOPOS_HIP_CHAIN_EXP;
+    case TOPOS_HIP_OP_LN: return TOPOS_HIP_CHAIN_LN;
+    case TOPOS_HIP_OP_SQRT: return TOPOS_HIP_CHAIN_SQRT;
+    case TOPOS_HIP_OP_MAXIMUM: return TOPOS_HIP_CHAIN_MAX;
+    case TOPOS_HIP_OP_STEP: return TOPOS_HIP_CHAIN_STEP;
+  }
+  throw Unsupported{std::string("no device kernel computes ") + op_name(op) + " of a non-constant operand"};
+}
+
+}  // namespace
+
+}  // namespace topos_hip
+
+using namespace topos_hip;
+
+struct topos_hip_program {
+  // ---- the program ----
+  std::vector<topos_hip_node> nodes;
+  std::vector<topos_hip_leaf> leaves;
+  std::vector<float> leaf_data;
+  std::vector<int32_t> leaf_indices;
+  int numerics = TOPOS_HIP_EXACT;
+  bool device = true;  // false under the fake runtime: plan and compile only
+
+  // ---- the plan ----
+  std::vector<bool> wanted, readable;
+  std::vector<std::vector<int>> consumers;
+  std::vector<Value> values;
+  std::vector<Storage> storages;
+  std::vector<float> pool;  // host-known constants, in device order
+  std::map<int64_t, int> parameter_storage, input_storage, leaf_storage;
+  struct Exec {
+    topos_hip_program *program;
+    hipStream_t stream;
+  };
+  struct Launch {
+    std::string what;
+    std::vector<int> reads, writes;
+    std::function<void(const Exec &)> run;
+  };
+  std::vector<Launch> launches;
+  std::vector<Generated> pending;  // generated kernels, compiled together after planning
+  std::map<int64_t, int> output_storage;  // readable node -> storage holding it contiguous
+  std::map<int64_t, int64_t> output_offset;
+  uint64_t arena_bytes = 0;
+  int64_t fused_groups = 0;
+  std::string description;
+
+  // ---- device state ----
+  char *arena = nullptr;
+  float *constants = nullptr;  // pool then leaf data
+  int64_t leaf_data_offset = 0;
+  std::map<int64_t, const float *> parameters, inputs;
+  std::map<int64_t, SelectionBuffers> selection_inputs;
+  std::map<int64_t, SelectionBuffers> selection_leaves;
+  std::vector<void *> allocations;
+
+  ~topos_hip_program() {
+    if (!device) return;
+    for (void *p : allocations) hipFree(p);
+    for (auto &kv : selection_inputs) {
+      hipFree(kv.second.indices);
+      hipFree(kv.second.row_start);
+      hipFree(kv.second.sources);
+    }
+  }
+
+  // ================= planning =================
+
+  const topos_hip_node &node(int64_t i) const { return nodes[i]; }
+
+  [[noreturn]] void refuse(int64_t i, const std::string &why) const {
+    throw InvalidArgument{"node " + std::to_string(i) + " (" + op_name(nodes[i].op) + "): " + why};
+  }
+
+  static bool same_shape(const topos_hip_node &a, const topos_hip_node &b) {
+    if (a.rank != b.rank) return false;
+    for (int d = 0; d < a.rank; ++d)
+      if (a.shape[d] != b.shape[d]) return false;
+    return true;
+  }
+
+  static int64_t volume_of(const topos_hip_node &n) {
+    int64_t v = 1;
+    for (int d = 0; d < n.rank; ++d) v *= n.shape[d];
+    return v;
+  }
+
+  // Checks the table: operand references, arities, and each recorded shape
+  // against the shape the variant infers (Function::infer_shape,
+  // src/function/function.rs:386-431).
+  void validate() {
+    const int64_t n = (int64_t)nodes.size();
+    for (int64_t i = 0; i < n; ++i) {
+      const topos_hip_node &x = nodes[i];
+      if (x.op < 0 || x.op > TOPOS_HIP_OP_STEP) refuse(i, "unknown operation");
+      if (x.rank < 0 || x.rank > kMaxRank) refuse(i, "rank beyond the library's four axes");
+      for (int d = 0; d < x.rank; ++d)
+        if (x.shape[d] <= 0) refuse(i, "empty axis");
+      const int k = arity(x.op);
+      for (int j = 0; j < 2; ++j) {
+        if (j < k && (x.operands[j] < 0 || x.operands[j] >= i)) refuse(i, "operand must name an earlier node");
+        if (j >= k && x.operands[j] != -1) refuse(i, "unused operand slot must be -1");
+      }
+      const topos_hip_node *a = k > 0 ? &nodes[x.operands[0]] : nullptr;
+      const topos_hip_node *b = k > 1 ? &nodes[x.operands[1]] : nullptr;
+      auto expect = [&](bool ok, const char *what) {
+        if (!ok) refuse(i, what);
+      };
+      switch (x.op) {
+        case TOPOS_HIP_OP_LEAF: {
+          expect(x.slot >= 0 && x.slot < (int64_t)leaves.size(), "leaf payload index");
+          const topos_hip_leaf &leaf = leaves[x.slot];
+          if (leaf.kind == TOPOS_HIP_LEAF_DENSE)
+            expect(leaf.offset >= 0 && leaf.count == volume_of(x) &&
+                       leaf.offset + leaf.count <= (int64_t)leaf_data.size(),
+                   "dense leaf payload span");
+          else if (leaf.kind == TOPOS_HIP_LEAF_SELECTION) {
+            expect(x.rank == 2 && leaf.count == x.shape[0] && leaf.offset >= 0 &&
+                       leaf.offset + leaf.count <= (int64_t)leaf_indices.size(),
+                   "selection leaf payload span");
+            for (int64_t r = 0; r < leaf.count; ++r)
+              expect(leaf_indices[leaf.offset + r] >= 0 && leaf_indices[leaf.offset + r] < x.shape[1],
+                     "selection index out of vocabulary");
+          } else
+            expect(leaf.kind == TOPOS_HIP_LEAF_CONSTANT, "leaf payload kind");
+          break;
+        }
+        case TOPOS_HIP_OP_PARAMETER:
+        case TOPOS_HIP_OP_INPUT:
+          expect(x.slot >= 0, "slot");
+          if (x.flags & TOPOS_HIP_NODE_SELECTION) expect(x.op == TOPOS_HIP_OP_INPUT && x.rank == 2, "selection input shape");
+          break;
+        case TOPOS_HIP_OP_ADD: case TOPOS_HIP_OP_SUB: case TOPOS_HIP_OP_MUL: case TOPOS_HIP_OP_DIV:
+        case TOPOS_HIP_OP_POWF: case TOPOS_HIP_OP_MAXIMUM: case TOPOS_HIP_OP_STEP:
+          expect(same_shape(*a, *b) && same_shape(x, *a), "elementwise operands and result share one shape");
+          break;
+        case TOPOS_HIP_OP_NEG: case TOPOS_HIP_OP_TANH: case TOPOS_HIP_OP_EXP: case TOPOS_HIP_OP_LN:
+        case TOPOS_HIP_OP_SQRT: case TOPOS_HIP_OP_RELU: case TOPOS_HIP_OP_LOG_SOFTMAX:
+          expect(same_shape(x, *a), "the result keeps the operand's shape");
+          if (x.op == TOPOS_HIP_OP_LOG_SOFTMAX) expect(x.params[0] >= 0 && x.params[0] < a->rank, "axis");
+          break;
+        case TOPOS_HIP_OP_MATMUL: {
+          expect(a->rank >= 2 && a->rank == b->rank && x.rank == a->rank, "matmul ranks");
+          const int s = a->rank - 2;
+          for (int d = 0; d < s; ++d) expect(a->shape[d] == b->shape[d] && x.shape[d] == a->shape[d], "batch axes");
+          expect(a->shape[s + 1] == b->shape[s] && x.shape[s] == a->shape[s] && x.shape[s + 1] == b->shape[s + 1],
+                 "matmul inner dimensions");
+          break;
+        }
+        case TOPOS_HIP_OP_TRANSPOSE:
+          if (a->rank < 2) {
+            expect(same_shape(x, *a), "transpose below rank 2 is the identity");
+          } else {
+            expect(a->rank == 2 && x.rank == 2 && x.shape[0] == a->shape[1] && x.shape[1] == a->shape[0],
+                   "transpose supports rank 2");
+          }
+          break;
+        case TOPOS_HIP_OP_SUM:
+          expect(x.rank == 0, "sum is a scalar");
+          break;
+        case TOPOS_HIP_OP_SUM_ALONG: case TOPOS_HIP_OP_LOG_SUM_EXP: {
+          const int64_t axis = x.params[0];
+          expect(axis >= 0 && axis < a->rank && x.rank == a->rank - 1, "axis");
+          for (int d = 0, e = 0; d < a->rank; ++d)
+            if (d != axis) expect(x.shape[e++] == a->shape[d], "the result drops the axis");
+          break;
+        }
+        case TOPOS_HIP_OP_BROADCAST:
+          expect(volume_of(*a) == 1 && same_shape(x, *b), "broadcast spreads one element over the like shape");
+          break;
+        case TOPOS_HIP_OP_BROADCAST_ALONG: {
+          const int64_t axis = x.params[0];
+          expect(same_shape(x, *b) && axis >= 0 && axis < b->rank && a->rank == b->rank - 1, "broadcast_along");
+          for (int d = 0, e = 0; d < b->rank; ++d)
+            if (d != axis) expect(a->shape[e++] == b->shape[d], "broadcast_along needs the remaining shape");
+          break;
+        }
+        case TOPOS_HIP_OP_RESHAPE:
+          expect(volume_of(x) == volume_of(*a), "reshape keeps the volume");
+          break;
+        case TOPOS_HIP_OP_PERMUTE: {
+          expect(x.rank == a->rank, "permute rank");
+          bool seen[kMaxRank] = {false, false, false, false};
+          for (int d = 0; d < x.rank; ++d) {
+            const int64_t o = x.params[d];
+            expect(o >= 0 && o < a->rank && !seen[o], "permute order");
+            seen[o] = true;
+            expect(x.shape[d] == a->shape[o], "permuted shape");
+          }
+          break;
+        }
+        case TOPOS_HIP_OP_NARROW: {
+          const int64_t axis = x.params[0], start = x.params[1], len = x.params[2];
+          expect(axis >= 0 && axis < a->rank && x.rank == a->rank && len > 0 && start >= 0 &&
+                     start + len <= a->shape[axis],
+                 "narrow window");
+          for (int d = 0; d < x.rank; ++d) expect(x.shape[d] == (d == axis ? len : a->shape[d]), "narrowed shape");
+          break;
+        }
+        case TOPOS_HIP_OP_PAD: {
+          const int64_t axis = x.params[0], start = x.params[1], full = x.params[2];
+          expect(axis >= 0 && axis < a->rank && x.rank == a->rank && start >= 0 && start + a->shape[axis] <= full,
+                 "pad window");
+          for (int d = 0; d < x.rank; ++d) expect(x.shape[d] == (d == axis ? full : a->shape[d]), "padded shape");
+          break;
+        }
+        case TOPOS_HIP_OP_GATHER:
+          expect(b->rank == 2 && a->rank >= 1 && b->shape[1] == a->shape[0] && x.rank == a->rank &&
+                     x.shape[0] == b->shape[0],
+                 "gather shapes");
+          for (int d = 1; d < x.rank; ++d) expect(x.shape[d] == a->shape[d], "gathered rows");
+          break;
+        case TOPOS_HIP_OP_SCATTER:
+          expect(b->rank == 2 && a->rank >= 1 && a->shape[0] == b->shape[0] && x.params[0] == b->shape[1] &&
+                     x.rank == a->rank && x.shape[0] == x.params[0],
+                 "scatter shapes");
+          for (int d = 1; d < x.rank; ++d) expect(x.shape[d] == a->shape[d], "scattered rows");
+          break;
+        case TOPOS_HIP_OP_UNFOLD:
+        case TOPOS_HIP_OP_FOLD:
+          break;  // refused when reached (only if wanted)
+      }
+    }
+  }
+
+  // Operand links whose values are read. The `like` operand of Broadcast and
+  // BroadcastAlong contributes its shape only (recorded, hence known), so a
+  // node reached only that way needs no computation: skipping it changes no
+  // readable value.
+  static int value_links(int op) {
+    return (op == TOPOS_HIP_OP_BROADCAST || op == TOPOS_HIP_OP_BROADCAST_ALONG) ? 1 : arity(op);
+  }
+
+  // Plan::new's reachability (src/engine/plan.rs:150-172) over value links.
+  void mark_wanted() {
+    const int64_t n = (int64_t)nodes.size();
+    wanted.assign(n, false);
+    readable.assign(n, false);
+    for (int64_t i = 0; i < n; ++i)
+      if (nodes[i].flags & TOPOS_HIP_NODE_READABLE) wanted[i] = readable[i] = true;
+    for (int64_t i = n - 1; i >= 0; --i) {
+      if (!wanted[i]) continue;
+      for (int j = 0; j < value_links(nodes[i].op); ++j) wanted[nodes[i].operands[j]] = true;
+    }
+    consumers.assign(n, {});
+    for (int64_t i = 0; i < n; ++i) {
+      if (!wanted[i]) continue;
+      for (int j = 0; j < value_links(nodes[i].op); ++j) {
+        auto &c = consumers[nodes[i].operands[j]];
+        if (c.empty() || c.back() != i) c.push_back((int)i);
+      }
+    }
+  }
+
+  // ---- storages ----
+
+  int new_storage(StorageKind kind, int64_t index = -1, int64_t bytes = 0) {
+    Storage s;
+    s.kind = kind;
+    s.index = index;
+    s.bytes = bytes;
+    storages.push_back(s);
+    return (int)storages.size() - 1;
+  }
+  int arena_storage(int64_t bytes) { return new_storage(StorageKind::kArena, -1, std::max<int64_t>(bytes, 4)); }
+
+  int pool_constant(float v) {
+    pool.push_back(v);
+    return new_storage(StorageKind::kPool, (int64_t)pool.size() - 1);
+  }
+
+  Value dense_value(int storage, const Layout &layout) {
+    Value v;
+    v.kind = Value::kDense;
+    v.storage = storage;
+    v.layout = layout;
+    return v;
+  }
+
+  Value host_constant(const topos_hip_node &x, float value) {
+    Value v = dense_value(pool_constant(value), constant_layout(x.rank, x.shape, 0));
+    v.constant = true;
+    v.host_known = true;
+    v.host_value = value;
+    return v;
+  }
+
+  // A value that reads as `source` in the layout `layout` (views keep the
+  // constant flags: a view of a Constant is a Constant).
+  Value view_of(const Value &source, const Layout &layout) {
+    Value v = source;
+    v.layout = layout;
+    return v;
+  }
+
+  // ---- launches ----
+
+  int add_launch(const std::string &what, std::vector<int> reads, std::vector<int> writes,
+                 std::function<void(const Exec &)> run) {
+    Launch l{what, std::move(reads), std::move(writes), std::move(run)};
+    launches.push_back(std::move(l));
+    return (int)launches.size() - 1;
+  }
+
+  // Pointer resolution at run time.
+  char *base(int storage_id) const {
+    const Storage &s = storages[storage_id];
+    switch (s.kind) {
+      case StorageKind::kArena: return arena + s.offset;
+      case StorageKind::kParameter: {
+        auto it = parameters.find(s.index);
+        if (it == parameters.end()) throw InvalidArgument{"parameter slot " + std::to_string(s.index) + " is not bound"};
+        return (char *)it->second;
+      }
+      case StorageKind::kInput: {
+        auto it = inputs.find(s.index);
+        if (it == inputs.end()) throw InvalidArgument{"input slot " + std::to_string(s.index) + " is not bound"};
+        return (char *)it->second;
+      }
+      case StorageKind::kPool: return (char *)(constants + s.index);
+      case StorageKind::kLeaf: return (char *)(constants + leaf_data_offset + s.index);
+      case StorageKind::kSelectionInput: {
+        auto it = selection_inputs.find(s.index);
+        if (it == selection_inputs.end())
+          throw InvalidArgument{"selection input slot " + std::to_string(s.index) + " is not bound"};
+        return (char *)it->second.indices;
+      }
+      case StorageKind::kSelectionLeaf: return (char *)selection_leaves.at(s.index).indices;
+    }
+    return nullptr;
+  }
+
+  const SelectionBuffers &selection_buffers(int storage_id) const {
+    const Storage &s = storages[storage_id];
+    if (s.kind == StorageKind::kSelectionInput) {
+      auto it = selection_inputs.find(s.index);
+      if (it == selection_inputs.end())
+        throw InvalidArgument{"selection input slot " + std::to_string(s.index) + " is not bound"};
+      return it->second;
+    }
+    return selection_leaves.at(s.index);
+  }
+
+  // ---- expressions ----
+
+  bool is_inline(int64_t i) const { return values[i].kind == Value::kInline; }
+
+  // Appends node `i`'s expression (its inlined subtree) to `e`, returning its
+  // reference. `memo` maps nodes to references, `inputs_of` maps leaf nodes to
+  // input positions, `storage_of` lists each input's storage.
+  int expr_of(int64_t i, Expr &e, std::map<int64_t, int> &memo, std::vector<int> &storage_of,
+              int64_t compute_root = -1) {
+    auto found = memo.find(i);
+    if (found != memo.end()) return found->second;
+    const topos_hip_node &x = nodes[i];
+    const Value &v = values[i];
+    int result;
+    if (v.kind == Value::kInline || i == compute_root) {
+      // An elementwise node computed in registers.
+      const int a = expr_of(x.operands[0], e, memo, storage_of);
+      int b = 0;
+      int op;
+      if (x.op == TOPOS_HIP_OP_RELU) {
+        ExprInput zero;
+        zero.kind = ExprInput::kLiteral;
+        zero.one = 0.0f;  // zero_like of an f32 element: +0
+        e.inputs.push_back(zero);
+        storage_of.push_back(-1);
+        b = -(int)e.inputs.size();
+        op = TOPOS_HIP_CHAIN_MAX;
+      } else {
+        op = chain_op(x.op);
+        if (is_binary(op)) b = expr_of(x.operands[1], e, memo, storage_of);
+      }
+      e.steps.push_back(ExprStep{op, a, b});
+      result = (int)e.steps.size() - 1;
+    } else {
+      ExprInput in;
+      int storage = v.storage;
+      if (v.kind == Value::kDense && v.host_known) {
+        in.kind = ExprInput::kLiteral;
+        in.one = v.host_value;
+        storage = -1;
+      } else if (v.kind == Value::kDense) {
+        in.kind = ExprInput::kStrided;
+        in.offset = v.layout.offset;
+        for (int d = 0; d < e.rank; ++d) in.strides[d] = v.layout.strides[d];
+      } else if (v.kind == Value::kSelection) {
+        in.kind = ExprInput::kSelection;
+        in.one = storages[v.storage].one;
+      } else if (v.kind == Value::kPadInline) {
+        const Value &src = values[x.operands[0]];
+        if (src.kind != Value::kDense) throw RuntimeFailure{"padded input of a non-dense value"};
+        // (A window of a host-known constant reads its pool element through
+        // zero strides.)
+        in.kind = ExprInput::kPadded;
+        in.offset = src.layout.offset;
+        for (int d = 0; d < e.rank; ++d) in.strides[d] = src.layout.strides[d];
+        in.pad_axis = (int)x.params[0];
+        in.pad_start = x.params[1];
+        in.pad_len = nodes[x.operands[0]].shape[x.params[0]];
+        storage = src.storage;
+      } else {
+        throw RuntimeFailure{"expression leaf without a value"};
+      }
+      e.inputs.push_back(in);
+      storage_of.push_back(storage);
+      result = -(int)e.inputs.size();
+    }
+    memo[i] = result;
+    return result;
+  }
+
+  Expr expression_for(int64_t root, std::vector<int> &storage_of) {
+    Expr e;
+    const topos_hip_node &x = nodes[root];
+    e.rank = x.rank;
+    for (int d = 0; d < x.rank; ++d) e.shape[d] = x.shape[d];
+    std::map<int64_t, int> memo;
+    e.outputs.push_back(expr_of(root, e, memo, storage_of, root));
+    return e;
+  }
+
+  std::vector<const void *> pointers_for(const std::vector<int> &storage_of) const {
+    std::vector<const void *> p(storage_of.size(), nullptr);
+    for (size_t i = 0; i < storage_of.size(); ++i)
+      if (storage_of[i] >= 0) p[i] = base(storage_of[i]);
+    return p;
+  }
+
+  static std::vector<int> real(const std::vector<int> &storage_of) {
+    std::vector<int> r;
+    for (int s : storage_of)
+      if (s >= 0) r.push_back(s);
+    return r;
+  }
+
+  std::string describe_expr(const Expr &e) const {
+    std::ostringstream s;
+    s << "[";
+    for (int d = 0; d < e.rank; ++d) s << (d ? "," : "") << e.shape[d];
+    s << "] " << e.inputs.size() << " inputs, " << e.steps.size() << " steps";
+    return s.str();
+  }
+
+  // A generated chain computing node `root` (and its inlined subtree) into a
+  // fresh contiguous arena buffer.
+  Value emit_chain(int64_t root) {
+    std::vector<int> storage_of;
+    Expr e = expression_for(root, storage_of);
+    const int out = arena_storage(e.volume() * 4);
+    Generated g = generate_chain(e);
+    pending.push_back(g);
+    ++fused_groups;
+    add_launch(std::string("chain ") + op_name(nodes[root].op) + " " + describe_expr(e), real(storage_of), {out},
+               [this, e, g, storage_of, out](const Exec &x) {
+                 auto p = pointers_for(storage_of);
+                 float *q = (float *)base(out);
+                 launch_generated_chain(g, e, p.data(), &q, x.stream);
+               });
+    const topos_hip_node &n = nodes[root];
+    return dense_value(out, contiguous(n.rank, n.shape));
+  }
+
+  // Copies any dense/constant value into a fresh contiguous buffer.
+  Value materialize(int64_t i) {
+    const Value &v = values[i];
+    const topos_hip_node &n = nodes[i];
+    if (v.kind == Value::kSelection) {
+      const int out = arena_storage(volume_of(n) * 4);
+      const int sel = v.storage;
+      const float one = storages[sel].one;
+      const int64_t rows = n.shape[0], vocab = n.shape[1];
+      add_launch("one-hot " + std::to_string(rows) + "x" + std::to_string(vocab), {sel}, {out},
+                 [this, sel, out, rows, vocab, one](const Exec &x) {
+                   launch_one_hot((const int32_t *)base(sel), rows, vocab, one, (float *)base(out), x.stream);
+                 });
+      return dense_value(out, contiguous(n.rank, n.shape));
+    }
+    if (v.kind != Value::kDense) throw RuntimeFailure{"materialising a value without storage"};
+    Expr e;
+    e.rank = n.rank;
+    for (int d = 0; d < n.rank; ++d) e.shape[d] = n.shape[d];
+    ExprInput in;
+    std::vector<int> storage_of;
+    if (v.host_known) {
+      in.kind = ExprInput::kLiteral;
+      in.one = v.host_value;
+      storage_of.push_back(-1);
+    } else {
+      in.offset = v.layout.offset;
+      for (int d = 0; d < n.rank; ++d) in.strides[d] = v.layout.strides[d];
+      storage_of.push_back(v.storage);
+    }
+    e.inputs.push_back(in);
+    e.outputs.push_back(-1);
+    const int out = arena_storage(e.volume() * 4);
+    Generated g = generate_chain(e);
+    pending.push_back(g);
+    add_launch("copy " + describe_expr(e), real(storage_of), {out}, [this, e, g, storage_of, out](const Exec &x) {
+      auto p = pointers_for(storage_of);
+      float *q = (float *)base(out);
+      launch_generated_chain(g, e, p.data(), &q, x.stream);
+    });
+    return dense_value(out, contiguous(n.rank, n.shape));
+  }
+
+  // Makes node i's value usable as a strided dense operand.
+  const Value &dense_operand(int64_t i) {
+    if (values[i].kind == Value::kSelection) values[i] = materialize(i);
+    return values[i];
+  }
+
+  // ---- the node loop ----
+
+  bool inline_candidate(int64_t i) const {
+    if (readable[i] || consumers[i].size() != 1) return false;
+    const topos_hip_node &c = nodes[consumers[i][0]];
+    return is_elementwise(c.op) || c.op == TOPOS_HIP_OP_SUM_ALONG || c.op == TOPOS_HIP_OP_SUM;
+  }
+
+  void plan_node(int64_t i) {
+    const topos_hip_node &x = nodes[i];
+    Value &out = values[i];
+    switch (x.op) {
+      case TOPOS_HIP_OP_LEAF: {
+        const topos_hip_leaf &leaf = leaves[x.slot];
+        if (leaf.kind == TOPOS_HIP_LEAF_CONSTANT) {
+          out = host_constant(x, leaf.value);
+        } else if (leaf.kind == TOPOS_HIP_LEAF_DENSE) {
+          out = dense_value(new_storage(StorageKind::kLeaf, leaf.offset), contiguous(x.rank, x.shape));
+        } else {
+          const int s = new_storage(StorageKind::kSelectionLeaf, x.slot);
+          storages[s].rows = x.shape[0];
+          storages[s].vocab = x.shape[1];
+          storages[s].one = leaf.value;
+          out.kind = Value::kSelection;
+          out.storage = s;
+        }
+        return;
+      }
+      case TOPOS_HIP_OP_PARAMETER: {
+        auto it = parameter_storage.find(x.slot);
+        const int s = it != parameter_storage.end() ? it->second
+                                                    : (parameter_storage[x.slot] = new_storage(StorageKind::kParameter, x.slot));
+        out = dense_value(s, contiguous(x.rank, x.shape));
+        return;
+      }
+      case TOPOS_HIP_OP_INPUT: {
+        if (x.flags & TOPOS_HIP_NODE_SELECTION) {
+          const int s = new_storage(StorageKind::kSelectionInput, x.slot);
+          storages[s].rows = x.shape[0];
+          storages[s].vocab = x.shape[1];
+          storages[s].one = __builtin_bit_cast(float, (uint32_t)x.params[0]);
+          out.kind = Value::kSelection;
+          out.storage = s;
+          return;
+        }
+        auto it = input_storage.find(x.slot);
+        const int s = it != input_storage.end() ? it->second
+                                                : (input_storage[x.slot] = new_storage(StorageKind::kInput, x.slot));
+        out = dense_value(s, contiguous(x.rank, x.shape));
+        return;
+      }
+      case TOPOS_HIP_OP_TRANSPOSE: {
+        const Value &a = dense_operand(x.operands[0]);
+        Layout l = a.layout;
+        if (l.rank == 2) {
+          std::swap(l.shape[0], l.shape[1]);
+          std::swap(l.strides[0], l.strides[1]);
+        }
+        out = view_of(a, l);
+        return;
+      }
+      case TOPOS_HIP_OP_PERMUTE: {
+        const Value &a = dense_operand(x.operands[0]);
+        Layout l = a.layout;
+        for (int d = 0; d < x.rank; ++d) {
+          l.shape[d] = a.layout.shape[x.params[d]];
+          l.strides[d] = a.layout.strides[x.params[d]];
+        }
+        out = view_of(a, l);
+        return;
+      }
+      case TOPOS_HIP_OP_NARROW: {
+        const Value &a = dense_operand(x.operands[0]);
+        Layout l = a.layout;
+        const int axis = (int)x.params[0];
+        l.shape[axis] = x.params[2];
+        l.offset += x.params[1] * l.strides[axis];
+        out = view_of(a, l);
+        return;
+      }
+      case TOPOS_HIP_OP_BROADCAST: {
+        const Value &a = dense_operand(x.operands[0]);
+        out = view_of(a, constant_layout(x.rank, x.shape, a.layout.offset));
+        out.constant = true;
+        return;
+      }
+      case TOPOS_HIP_OP_BROADCAST_ALONG: {
+        const Value &a = dense_operand(x.operands[0]);
+        const int axis = (int)x.params[0];
+        Layout l;
+        l.rank = x.rank;
+        l.offset = a.layout.offset;
+        for (int d = 0, e = 0; d < x.rank; ++d) {
+          l.shape[d] = x.shape[d];
+          l.strides[d] = d == axis ? 0 : a.layout.strides[e++];
+        }
+        out = view_of(a, l);
+        return;
+      }
+      case TOPOS_HIP_OP_RESHAPE: {
+        const Value &a = dense_operand(x.operands[0]);
+        if (a.constant) {
+          out = view_of(a, constant_layout(x.rank, x.shape, a.layout.offset));
+          return;
+        }
+        Layout l;
+        if (reshape_view(a.layout, x.rank, x.shape, l)) {
+          out = view_of(a, l);
+          return;
+        }
+        // Not a view (layout.rs reshape answers None): the interpreter copies
+        // the elements out in logical order.
+        Value copied = materialize(x.operands[0]);
+        out = view_of(copied, contiguous(x.rank, x.shape));
+        return;
+      }
+      case TOPOS_HIP_OP_UNFOLD:
+      case TOPOS_HIP_OP_FOLD:
+        throw Unsupported{std::string("node ") + std::to_string(i) + ": " + op_name(x.op) +
+                          " (the window patterns) has no device kernel"};
+      default:
+        break;
+    }
+    if (is_elementwise(x.op)) {
+      plan_elementwise(i);
+      return;
+    }
+    switch (x.op) {
+      case TOPOS_HIP_OP_PAD: plan_pad(i); return;
+      case TOPOS_HIP_OP_MATMUL: plan_matmul(i); return;
+      case TOPOS_HIP_OP_SUM_ALONG: plan_sum_along(i); return;
+      case TOPOS_HIP_OP_SUM: plan_sum(i); return;
+      case TOPOS_HIP_OP_LOG_SOFTMAX:
+      case TOPOS_HIP_OP_LOG_SUM_EXP: plan_rows(i); return;
+      case TOPOS_HIP_OP_GATHER: plan_gather(i); return;
+      case TOPOS_HIP_OP_SCATTER: plan_scatter(i); return;
+    }
+    refuse(i, "no plan for this operation");
+  }
+
+  void plan_elementwise(int64_t i) {
+    const topos_hip_node &x = nodes[i];
+    const int k = arity(x.op);
+    bool all_constant = true, all_known = true;
+    for (int j = 0; j < k; ++j) {
+      const Value &a = values[x.operands[j]];
+      if (!(a.kind == Value::kDense && a.constant)) all_constant = false;
+      if (!(a.kind == Value::kDense && a.host_known)) all_known = false;
+    }
+    if (all_known) {
+      const float a = values[x.operands[0]].host_value;
+      const float b = k > 1 ? values[x.operands[1]].host_value : 0.0f;
+      values[i] = host_constant(x, fold_scalar(x.op, a, b));
+      return;
+    }
+    if (x.op == TOPOS_HIP_OP_POWF)
+      throw Unsupported{"node " + std::to_string(i) + ": Powf is served for host-known constant operands only"};
+    if (all_constant) {
+      // A Constant payload computed at run time: one element, rank 0.
+      Expr e;
+      e.rank = 0;
+      std::vector<int> storage_of;
+      std::map<int64_t, int> memo;
+      int refs[2] = {0, 0};
+      for (int j = 0; j < k; ++j) {
+        const Value &a = values[x.operands[j]];
+        ExprInput in;
+        if (a.host_known) {
+          in.kind = ExprInput::kLiteral;
+          in.one = a.host_value;
+          storage_of.push_back(-1);
+        } else {
+          in.offset = a.layout.offset;
+          storage_of.push_back(a.storage);
+        }
+        e.inputs.push_back(in);
+        refs[j] = -(int)e.inputs.size();
+      }
+      if (x.op == TOPOS_HIP_OP_RELU) {
+        ExprInput zero;
+        zero.kind = ExprInput::kLiteral;
+        zero.one = 0.0f;
+        e.inputs.push_back(zero);
+        storage_of.push_back(-1);
+        e.steps.push_back(ExprStep{TOPOS_HIP_CHAIN_MAX, refs[0], -(int)e.inputs.size()});
+      } else {
+        e.steps.push_back(ExprStep{chain_op(x.op), refs[0], refs[1]});
+      }
+      e.outputs.push_back(0);
+      const int out = arena_storage(4);
+      Generated g = generate_chain(e);
+      pending.push_back(g);
+    pending.push_back(g);
+      add_launch(std::string("scalar ") + op_name(x.op), real(storage_of), {out},
+                 [this, e, g, storage_of, out](const Exec &ex) {
+                   auto p = pointers_for(storage_of);
+                   float *q = (float *)base(out);
+                   launch_generated_chain(g, e, p.data(), &q, ex.stream);
+                 });
+      values[i] = dense_value(out, constant_layout(x.rank, x.shape, 0));
+      values[i].constant = true;
+      return;
+    }
+    if (inline_candidate(i)) {
+      values[i].kind = Value::kInline;
+      return;
+    }
+    values[i].kind = Value::kNone;  // the root of its own expression
+    values[i] = emit_chain(i);
+  }
+
+  void plan_pad(int64_t i) {
+    const topos_hip_node &x = nodes[i];
+    dense_operand(x.operands[0]);
+    if (!readable[i] && consumers[i].size() == 1 && is_elementwise(nodes[consumers[i][0]].op)) {
+      values[i].kind = Value::kPadInline;
+      return;
+    }
+    // Materialised: a chain whose one input is the padded window.
+    values[i].kind = Value::kPadInline;
+    std::vector<int> storage_of;
+    Expr e;
+    e.rank = x.rank;
+    for (int d = 0; d < x.rank; ++d) e.shape[d] = x.shape[d];
+    std::map<int64_t, int> memo;
+    e.outputs.push_back(expr_of(i, e, memo, storage_of));
+    const int out = arena_storage(e.volume() * 4);
+    Generated g = generate_chain(e);
+    pending.push_back(g);
+    add_launch("pad " + describe_expr(e), real(storage_of), {out}, [this, e, g, storage_of, out](const Exec &ex) {
+      auto p = pointers_for(storage_of);
+      float *q = (float *)base(out);
+      launch_generated_chain(g, e, p.data(), &q, ex.stream);
+    });
+    values[i] = dense_value(out, contiguous(x.rank, x.shape));
+  }
+
+  // Flattens the batch axes of a rank >= 3 operand to one stride when the
+  // layout allows it.
+  static bool batch_stride(const Layout &l, int batch_axes, int64_t &stride) {
+    if (batch_axes == 0) {
+      stride = 0;
+      return true;
+    }
+    for (int d = 0; d + 1 < batch_axes; ++d)
+      if (l.shape[d + 1] != 1 && l.strides[d] != l.shape[d + 1] * l.strides[d + 1]) return false;
+    stride = l.strides[batch_axes - 1];
+    return true;
+  }
+
+  void plan_matmul(int64_t i) {
+    const topos_hip_node &x = nodes[i];
+    const Value a = dense_operand(x.operands[0]);
+    const Value b = dense_operand(x.operands[1]);
+    const int r = x.rank, s = r - 2;
+    const int64_t m = x.shape[s], n = x.shape[s + 1], k = nodes[x.operands[0]].shape[s + 1];
+    int64_t batches = 1;
+    for (int d = 0; d < s; ++d) batches *= x.shape[d];
+    const int out = arena_storage(batches * m * n * 4);
+    Batch batch;
+    batch.count = batches;
+    batch.c_stride = m * n;
+    bool flat = batch_stride(a.layout, s, batch.a_stride) && batch_stride(b.layout, s, batch.b_stride);
+    // Per-launch offsets when the batch axes do not flatten: one product per
+    // batch index, each at its own operand offsets.
+    std::vector<std::array<int64_t, 3>> parts;
+    if (flat) {
+      parts.push_back({a.layout.offset, b.layout.offset, 0});
+    } else {
+      for (int64_t q = 0; q < batches; ++q) {
+        int64_t rem = q, ao = a.layout.offset, bo = b.layout.offset;
+        for (int d = s - 1; d >= 0; --d) {
+          const int64_t c = rem % x.shape[d];
+          rem /= x.shape[d];
+          ao += c * a.layout.strides[d];
+          bo += c * b.layout.strides[d];
+        }
+        parts.push_back({ao, bo, q * m * n});
+      }
+      batch = Batch();
+      batch.c_stride = m * n;
+    }
+    const int64_t ars = a.layout.strides[s], acs = a.layout.strides[s + 1];
+    const int64_t brs = b.layout.strides[s], bcs = b.layout.strides[s + 1];
+    const int numerics_ = numerics;
+    std::ostringstream what;
+    what << "gemm " << (numerics == TOPOS_HIP_FAST ? "mfma" : "exact") << " " << batches << "x(" << m << "," << n
+         << "," << k << ") a[" << ars << "," << acs << "] b[" << brs << "," << bcs << "]";
+    add_launch(what.str(), {a.storage, b.storage}, {out},
+               [this, a, b, out, parts, batch, m, n, k, ars, acs, brs, bcs, numerics_](const Exec &ex) {
+                 const float *pa = (const float *)base(a.storage);
+                 const float *pb = (const float *)base(b.storage);
+                 float *pc = (float *)base(out);
+                 for (const auto &part : parts) {
+                   const float *qa = pa + part[0], *qb = pb + part[1];
+                   float *qc = pc + part[2];
+                   if (numerics_ == TOPOS_HIP_FAST &&
+                       launch_gemm_mfma(qa, ars, acs, qb, brs, bcs, m, k, n, qc, n, ex.stream, batch))
+                     continue;
+                   launch_gemm_exact(qa, ars, acs, qb, brs, bcs, m, k, n, qc, n, ex.stream, batch);
+                 }
+               });
+    values[i] = dense_value(out, contiguous(x.rank, x.shape));
+  }
+
+  // The expression a reduction folds: the operand's inlined tree, or the
+  // operand's value read through its layout.
+  Expr reduction_expression(int64_t operand, std::vector<int> &storage_of) {
+    const topos_hip_node &a = nodes[operand];
+    Expr e;
+    e.rank = a.rank;
+    for (int d = 0; d < a.rank; ++d) e.shape[d] = a.shape[d];
+    std::map<int64_t, int> memo;
+    e.outputs.push_back(expr_of(operand, e, memo, storage_of));
+    return e;
+  }
+
+  void plan_sum_along(int64_t i) {
+    const topos_hip_node &x = nodes[i];
+    const int64_t operand = x.operands[0];
+    const int axis = (int)x.params[0];
+    const Value &a = values[operand];
+    if (a.kind == Value::kDense && a.host_known) {
+      values[i] = host_constant(x, fold_repeated(a.host_value, nodes[operand].shape[axis]));
+      return;
+    }
+    std::vector<int> storage_of;
+    Expr e = reduction_expression(operand, storage_of);
+    const int out = arena_storage(volume_of(x) * 4);
+    Generated g = generate_fold(e, axis, kFoldSum);
+    pending.push_back(g);
+    ++fused_groups;
+    add_launch("fold sum axis " + std::to_string(axis) + " " + describe_expr(e), real(storage_of), {out},
+               [this, e, g, storage_of, out, axis](const Exec &ex) {
+                 auto p = pointers_for(storage_of);
+                 launch_generated_fold(g, e, axis, p.data(), (float *)base(out), ex.stream);
+               });
+    values[i] = dense_value(out, contiguous(x.rank, x.shape));
+  }
+
+  void plan_sum(int64_t i) {
+    const topos_hip_node &x = nodes[i];
+    const int64_t operand = x.operands[0];
+    const Value &a = values[operand];
+    if (a.kind == Value::kDense && a.host_known) {
+      values[i] = host_constant(x, fold_repeated(a.host_value, volume_of(nodes[operand])));
+      return;
+    }
+    std::vector<int> storage_of;
+    Expr e = reduction_expression(operand, storage_of);
+    const int64_t volume = e.volume();
+    const int64_t chunks = (volume + kSumChunk - 1) / kSumChunk;
+    const int out = arena_storage(4);
+    const int counts = arena_storage(chunks * 4);
+    const int flags = arena_storage(chunks * 4);
+    const int offsets = arena_storage((chunks + 1) * 8);
+    const int compacted = arena_storage(volume * 4);
+    Generated count = generate_sum_count(e);
+    Generated compact = generate_sum_compact(e);
+    pending.push_back(count);
+    pending.push_back(compact);
+    ++fused_groups;
+    std::vector<int> reads = real(storage_of);
+    add_launch("sum (ordered, compacted) " + describe_expr(e), reads, {out, counts, flags, offsets, compacted},
+               [this, e, count, compact, storage_of, out, counts, flags, offsets, compacted, chunks](const Exec &ex) {
+                 auto p = pointers_for(storage_of);
+                 launch_sum_count(count, e, p.data(), (int32_t *)base(counts), (int32_t *)base(flags), ex.stream);
+                 launch_scan((const int32_t *)base(counts), chunks, (int64_t *)base(offsets), ex.stream);
+                 launch_sum_compact(compact, e, p.data(), (const int64_t *)base(offsets), (float *)base(compacted),
+                                    ex.stream);
+                 launch_ordered_fold((const float *)base(compacted), (const int64_t *)base(offsets), chunks,
+                                     (const int32_t *)base(flags), (float *)base(out), ex.stream);
+               });
+    Value v = dense_value(out, constant_layout(0, x.shape, 0));
+    v.constant = true;
+    values[i] = v;
+  }
+
+  // LogSoftmax / LogSumExp along `axis`: the row kernels over a contiguous
+  // [rows, extent] operand (permuted into place when the axis is not last).
+  void plan_rows(int64_t i) {
+    const topos_hip_node &x = nodes[i];
+    const int64_t operand = x.operands[0];
+    const topos_hip_node &a = nodes[operand];
+    const int axis = (int)x.params[0];
+    Value v = dense_operand(operand);
+    const bool last = axis == a.rank - 1;
+    bool direct = v.kind == Value::kDense && !v.constant && last && is_contiguous(v.layout);
+    int source = v.storage;
+    int64_t source_offset = v.layout.offset;
+    int order[kMaxRank];
+    for (int d = 0, e = 0; d < a.rank; ++d)
+      if (d != axis) order[e++] = d;
+    order[a.rank - 1] = axis;
+    if (!direct) {
+      // Copy the operand with the axis moved last.
+      Expr e;
+      e.rank = a.rank;
+      ExprInput in;
+      std::vector<int> storage_of;
+      for (int d = 0; d < a.rank; ++d) {
+        e.shape[d] = a.shape[order[d]];
+        in.strides[d] = v.layout.strides[order[d]];
+      }
+      if (v.host_known) {
+        in.kind = ExprInput::kLiteral;
+        in.one = v.host_value;
+        storage_of.push_back(-1);
+      } else {
+        in.offset = v.layout.offset;
+        storage_of.push_back(v.storage);
+      }
+      e.inputs.push_back(in);
+      e.outputs.push_back(-1);
+      const int copy = arena_storage(e.volume() * 4);
+      Generated g = generate_chain(e);
+      pending.push_back(g);
+    pending.push_back(g);
+      add_launch("copy (axis last) " + describe_expr(e), real(storage_of), {copy},
+                 [this, e, g, storage_of, copy](const Exec &ex) {
+                   auto p = pointers_for(storage_of);
+                   float *q = (float *)base(copy);
+                   launch_generated_chain(g, e, p.data(), &q, ex.stream);
+                 });
+      source = copy;
+      source_offset = 0;
+    }
+    const int64_t extent = a.shape[axis];
+    const int64_t rows = volume_of(a) / extent;
+    const bool full = x.op == TOPOS_HIP_OP_LOG_SOFTMAX;
+    const int out = arena_storage((full ? volume_of(a) : rows) * 4);
+    const int kind = full ? TOPOS_HIP_ROWS_LOG_SOFTMAX : TOPOS_HIP_ROWS_LOG_SUM_EXP;
+    const int numerics_ = numerics;
+    add_launch(std::string(full ? "log_softmax " : "log_sum_exp ") + std::to_string(rows) + "x" +
+                   std::to_string(extent),
+               {source}, {out}, [this, source, source_offset, out, rows, extent, kind, numerics_](const Exec &ex) {
+                 launch_rows(kind, (const float *)base(source) + source_offset, rows, extent, numerics_,
+                             (float *)base(out), ex.stream);
+               });
+    if (!full) {
+      values[i] = dense_value(out, contiguous(x.rank, x.shape));
+      return;
+    }
+    // The result in the permuted order, viewed back in the node's axes.
+    int64_t permuted_shape[kMaxRank];
+    for (int d = 0; d < a.rank; ++d) permuted_shape[d] = a.shape[order[d]];
+    const Layout p = contiguous(a.rank, permuted_shape);
+    Layout l;
+    l.rank = a.rank;
+    for (int d = 0; d < a.rank; ++d) {
+      l.shape[order[d]] = permuted_shape[d];
+      l.strides[order[d]] = p.strides[d];
+    }
+    values[i] = dense_value(out, l);
+  }
+
+  // A [rows, row_size] reading of a rank >= 1 layout (row = axis 0).
+  static bool as_rows(const Layout &l, int64_t &row_stride, int64_t &column_stride) {
+    row_stride = l.strides[0];
+    if (l.rank == 1) {
+      column_stride = 0;
+      return true;
+    }
+    for (int d = 1; d + 1 < l.rank; ++d)
+      if (l.shape[d + 1] != 1 && l.strides[d] != l.shape[d + 1] * l.strides[d + 1]) return false;
+    column_stride = l.strides[l.rank - 1];
+    return true;
+  }
+
+  void plan_gather(int64_t i) {
+    const topos_hip_node &x = nodes[i];
+    Value t = dense_operand(x.operands[0]);
+    const Value &sel = values[x.operands[1]];
+    if (sel.kind != Value::kSelection) refuse(i, "gather needs a selection (Tensor::selection) operand");
+    int64_t rs, cs;
+    if (!as_rows(t.layout, rs, cs)) {
+      t = materialize(x.operands[0]);
+      as_rows(t.layout, rs, cs);
+    }
+    const int64_t rows = x.shape[0], row_size = volume_of(x) / rows;
+    const int out = arena_storage(volume_of(x) * 4);
+    const int table = t.storage, selection = sel.storage;
+    const int64_t offset = t.layout.offset;
+    add_launch("gather " + std::to_string(rows) + "x" + std::to_string(row_size), {table, selection}, {out},
+               [this, table, selection, out, offset, rs, cs, rows, row_size](const Exec &ex) {
+                 launch_gather((const float *)base(table) + offset, rs, cs, (const int32_t *)base(selection), rows,
+                               row_size, (float *)base(out), ex.stream);
+               });
+    values[i] = dense_value(out, contiguous(x.rank, x.shape));
+  }
+
+  void plan_scatter(int64_t i) {
+    const topos_hip_node &x = nodes[i];
+    Value g = dense_operand(x.operands[0]);
+    const Value &sel = values[x.operands[1]];
+    if (sel.kind != Value::kSelection) refuse(i, "scatter needs a selection (Tensor::selection) operand");
+    int64_t rs, cs;
+    if (!as_rows(g.layout, rs, cs)) {
+      g = materialize(x.operands[0]);
+      as_rows(g.layout, rs, cs);
+    }
+    const int64_t rows = x.shape[0], row_size = volume_of(x) / rows;
+    const int out = arena_storage(volume_of(x) * 4);
+    const int gradient = g.storage, selection = sel.storage;
+    const int64_t offset = g.layout.offset;
+    add_launch("scatter " + std::to_string(rows) + "x" + std::to_string(row_size), {gradient, selection}, {out},
+               [this, gradient, selection, out, offset, rs, cs, rows, row_size](const Exec &ex) {
+                 const SelectionBuffers &b = selection_buffers(selection);
+                 launch_scatter((const float *)base(gradient) + offset, rs, cs, b.row_start, b.sources, rows,
+                                row_size, (float *)base(out), ex.stream);
+               });
+    values[i] = dense_value(out, contiguous(x.rank, x.shape));
+  }
+
+  // Every readable node ends in a contiguous buffer the caller can read.
+  void finish_readables() {
+    for (int64_t i = 0; i < (int64_t)nodes.size(); ++i) {
+      if (!readable[i]) continue;
+      const Value &v = values[i];
+      const topos_hip_node &x = nodes[i];
+      const bool in_place = v.kind == Value::kDense && !v.constant && is_contiguous(v.layout) &&
+                            (storages[v.storage].kind != StorageKind::kArena ||
+                             (v.layout.offset == 0 && storages[v.storage].bytes == volume_of(x) * 4)) &&
+                            storages[v.storage].kind != StorageKind::kPool;
+      const bool scalar_buffer = v.kind == Value::kDense && v.constant && !v.host_known && volume_of(x) == 1 &&
+                                 storages[v.storage].kind == StorageKind::kArena;
+      if (in_place || scalar_buffer) {
+        output_storage[i] = v.storage;
+        output_offset[i] = v.layout.offset;
+      } else {
+        const Value copied = materialize(i);
+        output_storage[i] = copied.storage;
+        output_offset[i] = 0;
+      }
+      storages[output_storage[i]].pinned = true;
+    }
+  }
+
+  // First-fit offsets over the storages' live intervals.
+  void assign_arena() {
+    for (size_t l = 0; l < launches.size(); ++l) {
+      for (int s : launches[l].writes) storages[s].first = std::min(storages[s].first, (int)l);
+      for (int s : launches[l].reads) storages[s].last = std::max(storages[s].last, (int)l);
+      for (int s : launches[l].writes) storages[s].last = std::max(storages[s].last, (int)l);
+    }
+    std::vector<std::vector<int>> born(launches.size()), dies(launches.size());
+    for (size_t s = 0; s < storages.size(); ++s) {
+      Storage &st = storages[s];
+      if (st.kind != StorageKind::kArena || st.first == INT_MAX) continue;
+      born[st.first].push_back((int)s);
+      if (!st.pinned) dies[st.last].push_back((int)s);
+    }
+    std::map<int64_t, int64_t> free_blocks;  // offset -> bytes
+    int64_t top = 0;
+    auto round = [](int64_t b) { return (b + 255) / 256 * 256; };
+    for (size_t l = 0; l < launches.size(); ++l) {
+      for (int s : born[l]) {
+        const int64_t need = round(storages[s].bytes);
+        auto fit = free_blocks.end();
+        for (auto it = free_blocks.begin(); it != free_blocks.end(); ++it)
+          if (it->second >= need) {
+            fit = it;
+            break;
+          }
+        if (fit != free_blocks.end()) {
+          storages[s].offset = fit->first;
+          const int64_t rest = fit->second - need, at = fit->first + need;
+          free_blocks.erase(fit);
+          if (rest > 0) free_blocks[at] = rest;
+        } else if (!free_blocks.empty() && std::prev(free_blocks.end())->first + std::prev(free_blocks.end())->second == top) {
+          // Grow the last free block at the top.
+          auto last = std::prev(free_blocks.end());
+          storages[s].offset = last->first;
+          top = last->first + need;
+          free_blocks.erase(last);
+        } else {
+          storages[s].offset = top;
+          top += need;
+        }
+      }
+      for (int s : dies[l]) {
+        int64_t at = storages[s].offset, size = round(storages[s].bytes);
+        auto next = free_blocks.lower_bound(at);
+        if (next != free_blocks.end() && at + size == next->first) {
+          size += next->second;
+          next = free_blocks.erase(next);
+        }
+        if (next != free_blocks.begin()) {
+          auto prev = std::prev(next);
+          if (prev->first + prev->second == at) {
+            at = prev->first;
+            size += prev->second;
+            free_blocks.erase(prev);
+          }
+        }
+        free_blocks[at] = size;
+      }
+    }
+    arena_bytes = (uint64_t)std::max<int64_t>(top, 256);
+  }
+
+  void describe() {
+    std::ostringstream s;
+    s << "arena " << arena_bytes << " bytes, " << launches.size() << " launches, " << fused_groups
+      << " generated kernels\n";
+    for (size_t l = 0; l < launches.size(); ++l) s << l << ": " << launches[l].what << "\n";
+    description = s.str();
+  }
+
+  void plan() {
+    validate();
+    mark_wanted();
+    values.assign(nodes.size(), Value());
+    for (int64_t i = 0; i < (int64_t)nodes.size(); ++i)
+      if (wanted[i]) plan_node(i);
+    finish_readables();
+    assign_arena();
+    compile_kernels(pending, device);
+    describe();
+  }
+
+  // ================= device state =================
+
+  void upload_constants() {
+    // The pool, then every dense leaf payload, in one allocation.
+    std::vector<float> all(pool);
+    leaf_data_offset = (int64_t)all.size();
+    all.insert(all.end(), leaf_data.begin(), leaf_data.end());
+    if (all.empty()) all.push_back(0.0f);
+    void *p = nullptr;
+    check(hipMalloc(&p, all.size() * 4), "hipMalloc(constants)");
+    allocations.push_back(p);
+    constants = (float *)p;
+    check(hipMemcpy(constants, all.data(), all.size() * 4, hipMemcpyHostToDevice), "hipMemcpy(constants)");
+    for (const Storage &s : storages)
+      if (s.kind == StorageKind::kSelectionLeaf && !selection_leaves.count(s.index)) {
+        const topos_hip_leaf &leaf = leaves[s.index];
+        selection_leaves[s.index] = upload_selection(&leaf_indices[leaf.offset], s.rows, s.vocab, true);
+      }
+  }
+
+  // Copies a selection's indices and its row-sorted order to the device.
+  SelectionBuffers upload_selection(const int32_t *indices, int64_t rows, int64_t vocab, bool track) {
+    std::vector<int32_t> row_start(vocab + 1, 0), sources(rows);
+    for (int64_t r = 0; r < rows; ++r) ++row_start[indices[r] + 1];
+    for (int64_t v = 0; v < vocab; ++v) row_start[v + 1] += row_start[v];
+    std::vector<int32_t> cursor(row_start.begin(), row_start.end() - 1);
+    for (int64_t r = 0; r < rows; ++r) sources[cursor[indices[r]]++] = (int32_t)r;  // ascending source order
+    SelectionBuffers b;
+    b.rows = rows;
+    b.vocab = vocab;
+    void *p = nullptr;
+    check(hipMalloc(&p, rows * 4), "hipMalloc(selection)");
+    b.indices = (int32_t *)p;
+    check(hipMalloc(&p, (vocab + 1) * 4), "hipMalloc(selection rows)");
+    b.row_start = (int32_t *)p;
+    check(hipMalloc(&p, std::max<int64_t>(rows, 1) * 4), "hipMalloc(selection sources)");
+    b.sources = (int32_t *)p;
+    if (track) {
+      allocations.push_back(b.indices);
+      allocations.push_back(b.row_start);
+      allocations.push_back(b.sources);
+    }
+    check(hipMemcpy(b.indices, indices, rows * 4, hipMemcpyHostToDevice), "hipMemcpy(selection)");
+    check(hipMemcpy(b.row_start, row_start.data(), (vocab + 1) * 4, hipMemcpyHostToDevice), "hipMemcpy(rows)");
+    check(hipMemcpy(b.sources, sources.data(), rows * 4, hipMemcpyHostToDevice), "hipMemcpy(sources)");
+    return b;
+  }
+
+  void run(hipStream_t stream) {
+    if (!device) throw InvalidArgument{"the fake runtime plans programs but does not run them"};
+    if (!arena) {
+      void *p = nullptr;
+      check(hipMalloc(&p, arena_bytes), "hipMalloc(arena)");
+      allocations.push_back(p);
+      arena = (char *)p;
+    }
+    // Every binding must be present before anything is enqueued.
+    for (const Storage &s : storages) {
+      if (s.first == INT_MAX && s.last < 0) continue;
+      if (s.kind == StorageKind::kParameter && !parameters.count(s.index))
+        throw InvalidArgument{"parameter slot " + std::to_string(s.index) + " is not bound"};
+      if (s.kind == StorageKind::kInput && !inputs.count(s.index))
+        throw InvalidArgument{"input slot " + std::to_string(s.index) + " is not bound"};
+      if (s.kind == StorageKind::kSelectionInput && !selection_inputs.count(s.index))
+        throw InvalidArgument{"selection input slot " + std::to_string(s.index) + " is not bound"};
+    }
+    const Exec ex{this, stream};
+    for (const Launch &l : launches) l.run(ex);
+  }
+};
+
+extern "C" {
+
+int topos_hip_program_create(const topos_hip_node *nodes, int64_t n_nodes, const topos_hip_leaf *leaves,
+                             int64_t n_leaves, const float *leaf_data, int64_t leaf_data_len,
+                             const int32_t *leaf_indices, int64_t leaf_indices_len, int numerics,
+                             topos_hip_program **program) {
+  if (!program || n_nodes <= 0 || !nodes || (n_leaves > 0 && !leaves) || (leaf_data_len > 0 && !leaf_data) ||
+      (leaf_indices_len > 0 && !leaf_indices) || n_leaves < 0 || leaf_data_len < 0 || leaf_indices_len < 0)
+    return TOPOS_HIP_INVALID_ARGUMENT;
+  if (numerics != TOPOS_HIP_EXACT && numerics != TOPOS_HIP_FAST) return TOPOS_HIP_INVALID_ARGUMENT;
+  *program = nullptr;
+  const int status = Context::get().status();
+  if (status != TOPOS_HIP_OK) return status;
+  auto p = std::make_unique<topos_hip_program>();
+  p->nodes.assign(nodes, nodes + n_nodes);
+  p->leaves.assign(leaves, leaves + n_leaves);
+  p->leaf_data.assign(leaf_data, leaf_data + leaf_data_len);
+  p->leaf_indices.assign(leaf_indices, leaf_indices + leaf_indices_len);
+  p->numerics = numerics;
+  p->device = Context::get().runtime().launches_kernels;
+  last_refusal().clear();
+  const int code = guarded([&] {
+    try {
+      p->plan();
+    } catch (const InvalidArgument &e) {
+      last_refusal() = e.message;
+      throw;
+    } catch (const Unsupported &e) {
+      last_refusal() = e.message;
+      throw;
+    }
+    if (p->device) p->upload_constants();
+  });
+  if (code == TOPOS_HIP_OK) *program = p.release();
+  return code;
+}
+
+int topos_hip_program_info(const topos_hip_program *program, uint64_t *arena_bytes, int64_t *launches,
+                           int64_t *fused_groups) {
+  if (!program) return TOPOS_HIP_INVALID_ARGUMENT;
+  if (arena_bytes) *arena_bytes = program->arena_bytes;
+  if (launches) *launches = (int64_t)program->launches.size();
+  if (fused_groups) *fused_groups = program->fused_groups;
+  return TOPOS_HIP_OK;
+}
+
+int topos_hip_program_bind(topos_hip_program *program, int is_input, int32_t slot, const float *device) {
+  if (!program || !device || slot < 0) return TOPOS_HIP_INVALID_ARGUMENT;
+  (is_input ? program->inputs : program->parameters)[slot] = device;
+  return TOPOS_HIP_OK;
+}
+
+int topos_hip_program_bind_selection(topos_hip_program *program, int32_t slot, const int32_t *indices, int64_t rows,
+                                     float one) {
+  if (!program || !indices || rows <= 0) return TOPOS_HIP_INVALID_ARGUMENT;
+  const Storage *declared = nullptr;
+  for (const Storage &s : program->storages)
+    if (s.kind == StorageKind::kSelectionInput && s.index == slot) declared = &s;
+  if (!declared) return TOPOS_HIP_INVALID_ARGUMENT;
+  if (declared->rows != rows || __builtin_bit_cast(uint32_t, declared->one) != __builtin_bit_cast(uint32_t, one))
+    return TOPOS_HIP_INVALID_ARGUMENT;
+  for (int64_t r = 0; r < rows; ++r)
+    if (indices[r] < 0 || indices[r] >= declared->vocab) return TOPOS_HIP_INVALID_ARGUMENT;
+  if (!program->device) return TOPOS_HIP_OK;
+  const int64_t vocab = declared->vocab;
+  return guarded([&] {
+    auto old = program->selection_inputs.find(slot);
+    if (old != program->selection_inputs.end()) {
+      check(hipDeviceSynchronize(), "hipDeviceSynchronize(rebind selection)");
+      hipFree(old->second.indices);
+      hipFree(old->second.row_start);
+      hipFree(old->second.sources);
+      program->selection_inputs.erase(old);
+    }
+    program->selection_inputs[slot] = program->upload_selection(indices, rows, vocab, false);
+  });
+}
+
+int topos_hip_program_run(topos_hip_program *program, void *stream) {
+  if (!program) return TOPOS_HIP_INVALID_ARGUMENT;
+  const int status = Context::get().status();
+  if (status != TOPOS_HIP_OK) return status;
+  return guarded([&] { program->run(static_cast<hipStream_t>(stream)); });
+}
+
+int topos_hip_program_output(const topos_hip_program *program, int64_t node, const float **device) {
+  if (!program || !device) return TOPOS_HIP_INVALID_ARGUMENT;
+  auto it = program->output_storage.find(node);
+  if (it == program->output_storage.end()) return TOPOS_HIP_INVALID_ARGUMENT;
+  if (!program->device || (program->storages[it->second].kind == StorageKind::kArena && !program->arena))
+    return TOPOS_HIP_INVALID_ARGUMENT;
+  int code = guarded([&] {
+    *device = (const float *)program->base(it->second) + program->output_offset.at(node);
+  });
+  return code;
+}
+
+int topos_hip_program_read(const topos_hip_program *program, int64_t node, float *host, int64_t count) {
+  if (!program || !host || node < 0 || node >= (int64_t)program->nodes.size()) return TOPOS_HIP_INVALID_ARGUMENT;
+  if (count != topos_hip_program::volume_of(program->nodes[node])) return TOPOS_HIP_INVALID_ARGUMENT;
+  const float *device = nullptr;
+  const int code = topos_hip_program_output(program, node, &device);
+  if (code != TOPOS_HIP_OK) return code;
+  return guarded([&] {
+    check(hipDeviceSynchronize(), "hipDeviceSynchronize(read)");
+    check(hipMemcpy(host, device, count * 4, hipMemcpyDeviceToHost), "hipMemcpy(read)");
+  });
+}
+
+const char *topos_hip_last_refusal(void) { return last_refusal().c_str(); }
+
+const char *topos_hip_program_describe(const topos_hip_program *program) {
+  return program ? program->description.c_str() : "";
+}
+
+void topos_hip_program_destroy(topos_hip_program *program) { delete program; }
+
+int topos_hip_sgd_step_f32(float *parameter, const float *gradient, int64_t count, float rate, void *stream) {
+  if (!parameter || !gradient || count < 0) return TOPOS_HIP_INVALID_ARGUMENT;
+  const int status = Context::get().status();
+  if (status != TOPOS_HIP_OK) return status;
+  return guarded([&] { launch_sgd(parameter, gradient, count, rate, static_cast<hipStream_t>(stream)); });
+}
+
+int topos_hip_adamw_step_f32(float *parameter, const float *gradient, float *first, float *second, int64_t count,
+                             float beta1, float beta2, float first_share, float second_share, float first_correction,
+                             float second_correction, float epsilon, float rate, float decay, int decayed,
+                             void *stream) {
+  if (!parameter || !gradient || !first || !second || count < 0) return TOPOS_HIP_INVALID_ARGUMENT;
+  const int status = Context::get().status();
+  if (status != TOPOS_HIP_OK) return status;
+  return guarded([&] {
+    launch_adamw(parameter, gradient, first, second, count, beta1, beta2, first_share, second_share, first_correction,
+                 second_correction, epsilon, rate, decay, decayed, static_cast<hipStream_t>(stream));
+  });
+}
+
+}  // extern "C"

@@ -1,0 +1,126 @@
+"""A device program: a recorded plan executed by libtopos_hip on one GPU.
+
+torch supplies the device memory of parameters and dense inputs (bound by
+address) and the stream; planning, the arena and every kernel are the
+library's.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Sequence
+
+import numpy as np
+
+from . import _native as n
+from .topos import ProgramTable, Tape, Value
+
+
+class DeviceProgram:
+    """topos_hip_program_*: create once, bind, run many times."""
+
+    def __init__(self, tape: Tape, roots: Sequence[Value], observe: Sequence[Value] = (), numerics: int = n.EXACT):
+        self.tape = tape
+        self.table: ProgramTable = tape.program(roots, observe)
+        self.numerics = numerics
+        self.handle = self.table.create(numerics)
+        self._held = {}  # keeps bound tensors alive
+
+    @property
+    def describe(self) -> str:
+        return n.lib.topos_hip_program_describe(self.handle).decode()
+
+    @property
+    def info(self) -> dict:
+        arena, launches, groups = ctypes.c_uint64(), ctypes.c_int64(), ctypes.c_int64()
+        n.checked(n.lib.topos_hip_program_info(self.handle, ctypes.byref(arena), ctypes.byref(launches),
+                                               ctypes.byref(groups)), "program info")
+        return {"arena_bytes": arena.value, "launches": launches.value, "generated_kernels": groups.value}
+
+    def bind_parameter(self, slot: int, tensor) -> None:
+        self._bind(0, slot, tensor)
+
+    def bind_input(self, slot: int, tensor) -> None:
+        self._bind(1, slot, tensor)
+
+    def _bind(self, is_input: int, slot: int, tensor) -> None:
+        import torch
+
+        if tensor.dtype != torch.float32 or not tensor.is_cuda or not tensor.is_contiguous():
+            raise TypeError("bind a contiguous float32 device tensor")
+        shapes = self.tape.input_shapes if is_input else self.tape.parameter_shapes
+        if tuple(tensor.shape) != tuple(shapes[slot]):
+            raise ValueError(f"slot {slot} records shape {shapes[slot]}, got {tuple(tensor.shape)}")
+        n.checked(n.lib.topos_hip_program_bind(self.handle, is_input, slot, tensor.data_ptr()), "program bind")
+        self._held[(is_input, slot)] = tensor
+
+    def bind_selection(self, slot: int, indices: np.ndarray, one: float = 1.0) -> None:
+        indices = np.ascontiguousarray(indices, dtype=np.int32)
+        n.checked(n.lib.topos_hip_program_bind_selection(self.handle, slot, indices.ctypes.data_as(n.INT32_P),
+                                                         indices.size, one),
+                  "program bind selection")
+
+    def run(self) -> None:
+        import torch
+
+        n.checked(n.lib.topos_hip_program_run(self.handle, torch.cuda.current_stream().cuda_stream), "program run")
+
+    def pointer(self, value: Value) -> int:
+        """Device address of a readable value after a run (contiguous f32)."""
+        p = ctypes.c_void_p()
+        n.checked(n.lib.topos_hip_program_output(self.handle, value.id, ctypes.byref(p)), "program output")
+        return p.value
+
+    def read(self, value: Value) -> np.ndarray:
+        out = np.empty(value.shape, dtype=np.float32)
+        n.checked(n.lib.topos_hip_program_read(self.handle, value.id, out.ctypes.data_as(n.FLOAT_P), out.size),
+                  "program read")
+        return out
+
+    def __del__(self):
+        handle = getattr(self, "handle", None)
+        if handle:
+            n.lib.topos_hip_program_destroy(handle)
+            self.handle = None
+
+
+def sgd_step(parameter, gradient_pointer: int, rate: float) -> None:
+    """Sgd::step on one device-resident parameter (src/neural/optimizer.rs:40-51)."""
+    import torch
+
+    n.checked(n.lib.topos_hip_sgd_step_f32(parameter.data_ptr(), gradient_pointer, parameter.numel(), rate,
+                                           torch.cuda.current_stream().cuda_stream), "sgd step")
+
+
+class AdamW:
+    """AdamW over device-resident parameters (src/neural/adam.rs:62-171): the
+    optimizer's scalar bookkeeping in f32 on the host, the per-element update
+    on the device. Moments start at zero, the device stand-in for the absent
+    moments whose Constant-zero scaling gives the same bits."""
+
+    def __init__(self, parameters, beta1=0.9, beta2=0.999, epsilon=1e-8, decay=0.01):
+        import torch
+
+        f = np.float32
+        self.beta1, self.beta2, self.epsilon, self.decay = f(beta1), f(beta2), f(epsilon), f(decay)
+        self.first_share = f(1) - self.beta1
+        self.second_share = f(1) - self.beta2
+        self.beta1_power, self.beta2_power = f(1), f(1)
+        self.moments = [(torch.zeros_like(p), torch.zeros_like(p)) for p in parameters]
+
+    def step(self, parameters, gradient_pointers, rate: float) -> None:
+        import torch
+
+        f = np.float32
+        self.beta1_power = f(self.beta1_power * self.beta1)
+        self.beta2_power = f(self.beta2_power * self.beta2)
+        first_correction = f(1) - self.beta1_power
+        second_correction = f(1) - self.beta2_power
+        stream = torch.cuda.current_stream().cuda_stream
+        for p, g, (m, v) in zip(parameters, gradient_pointers, self.moments):
+            decayed = 1 if p.dim() >= 2 else 0  # AdamW::step's rank >= 2 policy
+            n.checked(n.lib.topos_hip_adamw_step_f32(p.data_ptr(), g, m.data_ptr(), v.data_ptr(), p.numel(),
+                                                     float(self.beta1), float(self.beta2), float(self.first_share),
+                                                     float(self.second_share), float(first_correction),
+                                                     float(second_correction), float(self.epsilon), rate,
+                                                     float(self.decay), decayed, stream),
+                      "adamw step")

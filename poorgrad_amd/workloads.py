@@ -1,0 +1,200 @@
+"""The benchmark configurations recorded as train steps on the topos surface
+(poorgrad_amd.topos), plus their synthetic data.
+
+* ``mlp``: the MNIST-shaped step of BASELINE configs[0] — 784 -> 128 -> 10,
+  ReLU, softmax cross-entropy, Kaiming-uniform weights, zero biases.
+* ``gpt2``: the GPT-2-small step of configs[3] — pre-LayerNorm blocks, causal
+  softmax attention batched as rank-3 products over (batch x heads), GELU MLP
+  of 4x width, tied embeddings, cross-entropy over the vocabulary — with any
+  dimensions (the parity tests record the same graph at a small size).
+
+Both use the recorded-gradients route (src/graph/tape.rs:335-411;
+examples/makemore/mlp_compiled.rs:142-204): one forward program reads the
+loss and every parameter's gradient. The recipes follow the reference's
+facades and examples (src/neural/{linear,layer_norm,loss}.rs,
+examples/gpt2/model.rs:60-199); targets and token ids are Tensor::selection
+payloads.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+
+import numpy as np
+
+from .topos import Constant, Dense, Selection, Tape, Value, cross_entropy, layer_norm, linear
+
+# ---- synthetic data: src/neural/init.rs:45-102, vectorized ----
+
+_GOLDEN = np.uint64(0x9E3779B97F4A7C15)
+
+
+def _splitmix(seed: int, count: int, skip: int = 0) -> np.ndarray:
+    """Outputs skip+1 .. skip+count of splitmix64 from `seed` (init.rs:50-56)."""
+    with np.errstate(over="ignore"):
+        steps = np.arange(skip + 1, skip + count + 1, dtype=np.uint64)
+        z = np.uint64(seed) + steps * _GOLDEN
+        z = (z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+        z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+        return z ^ (z >> np.uint64(31))
+
+
+def unit(seed: int, count: int, skip: int = 0) -> np.ndarray:
+    """unit() draws in [0, 1) (init.rs:58-60), as f64."""
+    return (_splitmix(seed, count, skip) >> np.uint64(11)).astype(np.float64) / float(1 << 53)
+
+
+def uniform(seed: int, scale: float, shape) -> np.ndarray:
+    """init::uniform (init.rs:88-91): (unit * 2 - 1) * scale, rounded to f32."""
+    count = int(np.prod(shape))
+    return ((unit(seed, count) * 2.0 - 1.0) * scale).astype(np.float32).reshape(shape)
+
+
+def normal(seed: int, deviation: float, shape) -> np.ndarray:
+    """init::normal (init.rs:93-102): Box-Muller on consecutive draw pairs.
+    (numpy's f64 log/cos may differ from the C library's in the last bit, so
+    this is the reference's generator up to that rounding: synthetic data.)"""
+    count = int(np.prod(shape))
+    u = unit(seed, 2 * count)
+    radius = np.sqrt(-2.0 * np.log(1.0 - u[0::2]))
+    angle = 2.0 * math.pi * u[1::2]
+    return (radius * np.cos(angle) * deviation).astype(np.float32).reshape(shape)
+
+
+def labels(seed: int, count: int, classes: int) -> np.ndarray:
+    """Uniform class indices: splitmix64 outputs modulo the class count."""
+    return (_splitmix(seed, count) % np.uint64(classes)).astype(np.int32)
+
+
+@dataclass
+class Workload:
+    """A recorded train step: parameters (slot order), their initial values,
+    feeds, and the loss and gradients the program reads."""
+    tape: Tape
+    parameters: list
+    initial: list
+    loss: Value
+    gradients: list
+    dense_inputs: dict = field(default_factory=dict)      # slot -> array
+    selection_inputs: dict = field(default_factory=dict)  # slot -> (indices, one)
+    config: dict = field(default_factory=dict)
+
+    @property
+    def roots(self) -> list:
+        return [self.loss] + list(self.gradients)
+
+    def parameter_count(self) -> int:
+        return int(sum(a.size for a in self.initial))
+
+
+def mlp(batch: int = 64, sizes=(784, 128, 10), weight_seeds=(7, 8), input_seed: int = 11,
+        label_seed: int = 13) -> Workload:
+    """Linear -> ReLU -> Linear, cross_entropy over
+    one-hot targets; inputs U[0,1), Kaiming-uniform weights
+    U(-sqrt(6/fan_in), +sqrt(6/fan_in)), zero biases."""
+    tape = Tape()
+    params, initial = [], []
+    for (fan_in, fan_out), seed in zip(zip(sizes[:-1], sizes[1:]), weight_seeds):
+        w = tape.parameter((fan_in, fan_out))
+        b = tape.parameter((fan_out,))
+        params += [w, b]
+        initial += [uniform(seed, math.sqrt(6.0 / fan_in), (fan_in, fan_out)), np.zeros(fan_out, np.float32)]
+    x = tape.input((batch, sizes[0]))
+    targets = tape.selection_input(batch, sizes[-1])
+    h = x
+    for layer in range(len(sizes) - 1):
+        h = linear(h, params[2 * layer], params[2 * layer + 1])
+        if layer < len(sizes) - 2:
+            h = h.relu()
+    loss = cross_entropy(h, targets)
+    gradients = tape.differentiate(loss, params)
+    feeds = unit(input_seed, batch * sizes[0]).astype(np.float32).reshape(batch, sizes[0])
+    return Workload(tape, params, initial, loss, gradients, dense_inputs={x.node.slot: feeds},
+                    selection_inputs={targets.node.slot: (labels(label_seed, batch, sizes[-1]), 1.0)},
+                    config={"model": "mlp", "sizes": list(sizes), "batch": batch})
+
+
+def _gelu(x: Value, half: Value, one: Value, root: Value, coefficient: Value) -> Value:
+    """examples/gpt2/model.rs:85-98: 0.5 x (1 + tanh(0.7978846 (x + 0.044715 x^3)))."""
+    cubic = x * x * x * coefficient.broadcast_like(x)
+    inner = ((x + cubic) * root.broadcast_like(x)).tanh()
+    return x * (inner + one.broadcast_like(inner)) * half.broadcast_like(x)
+
+
+def gpt2(batch: int = 8, context: int = 1024, vocab: int = 50257, width: int = 768, heads: int = 12,
+         layers: int = 12, positions: int = 1024, weight_seed: int = 7, token_seed: int = 13) -> Workload:
+    """BASELINE configs[3] (or the same graph at other dimensions): GPT-2 with
+    pre-LayerNorm blocks, causal attention, GELU MLP, tied embeddings."""
+    assert width % heads == 0 and context <= positions
+    head = width // heads
+    rows = batch * context
+    tape = Tape()
+    params, initial = [], []
+    seed = [weight_seed]
+
+    def weight(shape):
+        p = tape.parameter(shape)
+        params.append(p)
+        initial.append(normal(seed[0], 0.02, shape))
+        seed[0] += 1
+        return p
+
+    def filled(shape, value):
+        p = tape.parameter(shape)
+        params.append(p)
+        initial.append(np.full(shape, value, np.float32))
+        return p
+
+    wte = weight((vocab, width))
+    wpe = weight((positions, width))
+    blocks = []
+    for _ in range(layers):
+        blocks.append({
+            "ln1": (filled((width,), 1.0), filled((width,), 0.0)),
+            "attn": (weight((width, 3 * width)), filled((3 * width,), 0.0)),
+            "proj": (weight((width, width)), filled((width,), 0.0)),
+            "ln2": (filled((width,), 1.0), filled((width,), 0.0)),
+            "fc": (weight((width, 4 * width)), filled((4 * width,), 0.0)),
+            "out": (weight((4 * width, width)), filled((width,), 0.0)),
+        })
+    ln_f = (filled((width,), 1.0), filled((width,), 0.0))
+
+    # Leaves shared by every block (examples/gpt2/model.rs:363-388).
+    causal = np.where(np.arange(context)[None, :] <= np.arange(context)[:, None], 0.0, -np.inf).astype(np.float32)
+    mask = tape.leaf(Dense(causal))
+    scale = tape.leaf(Constant((), float(np.float32(1.0 / math.sqrt(head)))))
+    epsilon = tape.leaf(Constant((), float(np.float32(1e-5))))
+    half, one = tape.leaf(Constant((), 0.5)), tape.leaf(Constant((), 1.0))
+    root = tape.leaf(Constant((), float(np.float32(0.7978846))))
+    coefficient = tape.leaf(Constant((), float(np.float32(0.044715))))
+
+    tokens = tape.selection_input(rows, vocab)
+    targets = tape.selection_input(rows, vocab)
+    where = tape.leaf(Selection(np.tile(np.arange(context, dtype=np.int32), batch), positions))
+
+    def split_heads(fused: Value, part: int) -> Value:
+        x = fused.narrow(1, part * width, width).reshape((batch, context, heads, head))
+        return x.permute((0, 2, 1, 3)).reshape((batch * heads, context, head))
+
+    x = wte.gather(tokens) + wpe.gather(where)
+    for b in blocks:
+        h = layer_norm(x, *b["ln1"], epsilon)
+        fused = linear(h, *b["attn"])
+        q, k, v = split_heads(fused, 0), split_heads(fused, 1), split_heads(fused, 2)
+        scores = q.matmul(k.permute((0, 2, 1)))
+        weights = (scores * scale.broadcast_like(scores) + mask.broadcast_along(0, scores)).softmax(2)
+        attended = weights.matmul(v).reshape((batch, heads, context, head)).permute((0, 2, 1, 3))
+        x = x + linear(attended.reshape((rows, width)), *b["proj"])
+        h = layer_norm(x, *b["ln2"], epsilon)
+        x = x + linear(_gelu(linear(h, *b["fc"]), half, one, root, coefficient), *b["out"])
+    logits = layer_norm(x, *ln_f, epsilon).matmul(wte.transpose())
+    loss = cross_entropy(logits, targets)
+    gradients = tape.differentiate(loss, params)
+
+    stream = labels(token_seed, rows + batch, vocab).reshape(batch, context + 1)
+    token_ids = stream[:, :-1].reshape(-1)
+    next_ids = stream[:, 1:].reshape(-1)  # next-token targets
+    return Workload(tape, params, initial, loss, gradients,
+                    selection_inputs={tokens.node.slot: (token_ids, 1.0), targets.node.slot: (next_ids, 1.0)},
+                    config={"model": "gpt2", "batch": batch, "context": context, "vocab": vocab, "width": width,
+                            "heads": heads, "layers": layers})

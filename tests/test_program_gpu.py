@@ -1,0 +1,211 @@
+"""Device programs against the topos interpreter (oracle/interpreter.py) on
+the same recorded graphs and inputs: every readable value bit-identical in
+the exact posture (src/engine/tests/plan_tests.rs:9-22, :83-131 — plan equals
+interpreter bitwise), and within the stated envelope in the fast posture
+(plan_tests.rs:542-592)."""
+import math
+
+import numpy as np
+import pytest
+
+from poorgrad_amd import topos as t
+from poorgrad_amd import workloads
+from tests.conftest import banner
+from tests.gpu_util import assert_bitwise
+from tests.program_util import run_device, run_oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def check_workload(w, numerics, hip):
+    want = run_oracle(w.tape, w.roots, w.initial, w.dense_inputs, w.selection_inputs)
+    got, program = run_device(w.tape, w.roots, w.initial, w.dense_inputs, w.selection_inputs, numerics)
+    return want, got, program
+
+
+def test_mlp_train_step_exact_is_bit_identical(hip):
+    """BASELINE configs[0] at its full size: loss and all four gradients."""
+    banner("program mlp exact")
+    w = workloads.mlp()
+    want, got, program = check_workload(w, hip.EXACT, hip)
+    for r in w.roots:
+        assert_bitwise(got[r.id], want[r.id], f"mlp node {r.id}")
+    assert abs(float(want[w.loss.id]) - math.log(10)) < 0.5
+
+
+def test_mlp_train_step_fast_within_envelope(hip):
+    banner("program mlp fast")
+    w = workloads.mlp()
+    want, got, _ = check_workload(w, hip.FAST, hip)
+    # plan_tests.rs:583-590: |fast - exact| <= 1e-4 * max(|exact|, 1)
+    for r in w.roots:
+        g, e = got[r.id].astype(np.float64), want[r.id].astype(np.float64)
+        assert (np.abs(g - e) <= 1e-4 * np.maximum(np.abs(e), 1.0)).all(), f"node {r.id}"
+
+
+@pytest.mark.parametrize("layers, heads", [(1, 2), (2, 4)])
+def test_small_gpt2_train_step_exact_is_bit_identical(hip, layers, heads):
+    """The GPT-2 graph (batched causal attention, LayerNorm, GELU, tied
+    embeddings, cross-entropy, recorded gradients) at a small size."""
+    banner(f"program gpt2 small layers={layers}")
+    w = workloads.gpt2(batch=2, context=16, vocab=37, width=32, heads=heads, layers=layers, positions=24)
+    want, got, _ = check_workload(w, hip.EXACT, hip)
+    for r in w.roots:
+        assert_bitwise(got[r.id], want[r.id], f"gpt2 node {r.id} {r.shape}")
+
+
+def test_small_gpt2_fast_within_envelope(hip):
+    banner("program gpt2 small fast")
+    w = workloads.gpt2(batch=2, context=32, vocab=61, width=64, heads=4, layers=2, positions=32)
+    want, got, _ = check_workload(w, hip.FAST, hip)
+    loss_exact, loss_fast = float(want[w.loss.id]), float(got[w.loss.id])
+    assert abs(loss_fast - loss_exact) <= 1e-4 * max(abs(loss_exact), 1.0)
+    for r in w.gradients:
+        g, e = got[r.id].astype(np.float64), want[r.id].astype(np.float64)
+        scale = max(np.abs(e).max(), 1e-3)
+        assert np.abs(g - e).max() <= 1e-3 * scale, f"gradient {r.id} {r.shape}"
+
+
+def coverage_graph():
+    """One graph touching every served variant and storage kind."""
+    rng = np.random.default_rng(5)
+    tape = t.Tape()
+    a = tape.parameter((6, 8))
+    b = tape.parameter((8, 5))
+    c = tape.parameter((4, 6, 8))
+    table = tape.parameter((9, 8))
+    x = tape.input((6, 8))
+    sel = tape.selection_input(6, 9)
+    leaf = tape.leaf(t.Dense(rng.standard_normal((6, 5)).astype(np.float32)))
+    two = tape.leaf(t.Constant((), 2.0))
+    roots = []
+    y = (a * x + x.exp()).tanh() - (a / (x.abs() + two.broadcast_like(x))).sqrt()
+    roots.append(y)
+    p = y.matmul(b) + leaf
+    roots.append(p.log_softmax(0))
+    roots.append(p.log_softmax(1))
+    roots.append(p.logsumexp(0))
+    roots.append(p.logsumexp(1))
+    roots.append(p.sum())
+    roots.append(p.sum_along(0))
+    roots.append(p.transpose())  # a readable view
+    cat = t.concat([a.narrow(1, 0, 3), x.narrow(1, 3, 5)], 1)
+    roots.append(cat.maximum(y).relu() + cat.step(y))
+    roots.append(c.permute((1, 0, 2)).reshape((6, 32)))  # a reshape that copies
+    roots.append(c.reshape((24, 8)).sum_along(0))  # a reshape that views
+    roots.append(c.matmul(c.permute((0, 2, 1))))  # batched, transposed right operand
+    roots.append(c.log_softmax(1).sum_along(2))
+    g = table.gather(sel)
+    roots.append(g)
+    roots.append((g * x).scatter(sel, 9))
+    onehot_sum = (tape.value(sel.id) * g.matmul(table.transpose())).sum()
+    roots.append(onehot_sum)
+    roots.append(tape.value(sel.id).sum_along(1))
+    roots.append(two * two + two)  # a host-known constant, readable
+    roots.append(p.sum().broadcast_like(p) * p)
+    loss = (p * p).sum() + onehot_sum
+    grads = tape.differentiate(loss, [a, b, c, table])
+    roots += grads
+    params = [rng.standard_normal(s).astype(np.float32) for s in tape.parameter_shapes]
+    dense = {x.node.slot: rng.standard_normal((6, 8)).astype(np.float32)}
+    selections = {sel.node.slot: (np.array([3, 0, 3, 8, 1, 3], np.int32), 1.0)}
+    return tape, roots, params, dense, selections
+
+
+def test_every_served_variant_exact(hip):
+    banner("program coverage graph exact")
+    tape, roots, params, dense, selections = coverage_graph()
+    want = run_oracle(tape, roots, params, dense, selections)
+    got, program = run_device(tape, roots, params, dense, selections, hip.EXACT)
+    for r in roots:
+        assert_bitwise(got[r.id], want[r.id], f"node {r.id} ({t.NAMES[r.node.op]} {r.shape})")
+
+
+def test_signed_zero_seeding_survives(hip):
+    """Gradient accumulation starts from a Constant zero: 0 + c maps -0 to +0
+    (src/engine/run.rs:265,313; src/graph/tape.rs:389-393)."""
+    banner("program signed zeros")
+    tape = t.Tape()
+    w = tape.parameter((4,))
+    z = tape.input((4,))
+    loss = (w * z).sum()
+    (grad,) = tape.differentiate(loss, [w])
+    params = [np.array([1.0, -1.0, 2.0, -2.0], np.float32)]
+    dense = {z.node.slot: np.array([-0.0, 0.0, -0.0, 3.0], np.float32)}
+    want = run_oracle(tape, [loss, grad], params, dense)
+    got, _ = run_device(tape, [loss, grad], params, dense)
+    assert_bitwise(got[grad.id], want[grad.id], "grad")
+    assert_bitwise(got[loss.id], want[loss.id], "loss")
+    assert (got[grad.id].view(np.uint32)[:3] == 0).all()  # +0, not -0
+
+
+def test_large_sparse_sum_is_exact(hip):
+    """The cross-entropy alignment term (targets * logits).sum() over a wide
+    vocabulary: the ordered sum over the compacted nonzero terms equals the
+    interpreter's 1.6M-term left fold."""
+    banner("program sparse sum")
+    rng = np.random.default_rng(9)
+    rows, vocab = 64, 25013
+    tape = t.Tape()
+    logits = tape.input((rows, vocab))
+    targets = tape.selection_input(rows, vocab)
+    total = (targets * logits).sum()
+    count = targets.sum()
+    dense = {logits.node.slot: rng.standard_normal((rows, vocab)).astype(np.float32)}
+    selections = {targets.node.slot: (rng.integers(0, vocab, rows).astype(np.int32), 1.0)}
+    want = run_oracle(tape, [total, count], [], dense, selections)
+    got, _ = run_device(tape, [total, count], [], dense, selections)
+    assert_bitwise(got[total.id], want[total.id], "sparse sum")
+    assert_bitwise(got[count.id], want[count.id], "selection sum")
+
+
+def test_sgd_step_matches_the_rule(hip):
+    """Sgd::step p - g * lr⇑ (src/neural/optimizer.rs:40-51; the hand rule of
+    src/neural/tests/optimizer_tests.rs:16-37)."""
+    import torch
+
+    from poorgrad_amd.program import sgd_step
+
+    banner("sgd step")
+    rng = np.random.default_rng(2)
+    p = rng.standard_normal(1000).astype(np.float32)
+    g = rng.standard_normal(1000).astype(np.float32)
+    dp, dg = torch.from_numpy(p.copy()).cuda(), torch.from_numpy(g).cuda()
+    sgd_step(dp, dg.data_ptr(), 0.01)
+    want = p - g * np.float32(0.01)
+    assert_bitwise(dp, want, "sgd")
+
+
+def test_adamw_steps_match_the_rule(hip):
+    """AdamW (src/neural/adam.rs:62-171) over three steps, restated in numpy
+    f32 operation by operation."""
+    import torch
+
+    from poorgrad_amd.program import AdamW
+
+    banner("adamw steps")
+    rng = np.random.default_rng(3)
+    shapes = [(7, 5), (5,)]
+    params = [rng.standard_normal(s).astype(np.float32) for s in shapes]
+    device = [torch.from_numpy(p.copy()).cuda() for p in params]
+    opt = AdamW(device, beta1=0.9, beta2=0.999, epsilon=1e-8, decay=0.01)
+    f = np.float32
+    b1, b2, eps, decay, lr = f(0.9), f(0.999), f(1e-8), f(0.01), f(3e-4)
+    m = [np.zeros_like(p) for p in params]
+    v = [np.zeros_like(p) for p in params]
+    p1, p2 = f(1), f(1)
+    for step in range(3):
+        grads = [rng.standard_normal(s).astype(np.float32) for s in shapes]
+        dgrads = [torch.from_numpy(g).cuda() for g in grads]
+        opt.step(device, [g.data_ptr() for g in dgrads], float(lr))
+        p1, p2 = f(p1 * b1), f(p2 * b2)
+        c1, c2 = f(1) - p1, f(1) - p2
+        for i, g in enumerate(grads):
+            m[i] = m[i] * b1 + g * (f(1) - b1)
+            v[i] = v[i] * b2 + (g * g) * (f(1) - b2)
+            direction = (m[i] / c1) / (np.sqrt(v[i] / c2) + eps)
+            stepped = params[i] - direction * lr
+            params[i] = stepped - (params[i] * decay) * lr if params[i].ndim >= 2 else stepped
+        torch.cuda.synchronize()
+        for i in range(2):
+            assert_bitwise(device[i], params[i], f"adamw step {step} param {i}")
