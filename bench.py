@@ -1,33 +1,35 @@
 #!/usr/bin/env python3
 """Benchmark of the MI355X execution backend on BASELINE.json's configs.
 
-A step is one pass of the hot path over one batch of synthetic input already
-resident in HBM:
+The headline: one GPT-2-small train step per "step" —
+the recorded-gradients program (forward, loss, every parameter's gradient:
+12 layers, d_model 768, 12 heads, context 1024, batch 8, vocab 50257, tied
+embeddings) run by libtopos_hip from its HBM arena, then AdamW (lr 3e-4,
+betas 0.9/0.999, epsilon 1e-8, decay 0.01 on rank >= 2 parameters) on the
+device-resident parameters. Token ids are uniform over the vocabulary,
+weights N(0, 0.02): synthetic data, inputs resident before timing starts.
+``value`` is train steps/s in the fast posture (matrix-core products,
+envelope fidelity; elementwise work is bit-exact in every posture).
 
-* ``gemm_sweep`` (configs[1], the default workload): the fp32 product sweep
-  through the graph matmul, forward plus both backward products
-  (A.B, A^T.G, G.B^T, src/function/matmul.rs:71-91) for (M,N,K) in
-  {(512,512,512), (1024,4096,1024), (4096,4096,4096), (8192,768,3072)};
-  the transposed operands are stride views, never copies. ``value`` is the
-  sweep's TFLOP/s in the fast (matrix-core) posture.
-* ``chains`` are measured beside it on x:[16384,4096]:
-  SiLU + bias, LayerNorm, row sum, row max and row softmax, as GB/s of
-  algorithmic traffic (each distinct input read once, each output written
-  once) against the 8 TB/s HBM peak.
+Measured beside it, each in its own section of the JSON line:
+* ``mlp``: the 784-128-10 step with SGD lr 0.01, steps/s;
+* ``gemm_sweep``: forward A.B plus A^T.G and G.B^T for the four
+  (M,N,K), TFLOP/s per product and per sweep, fast and exact;
+* ``chains``: SiLU + bias, LayerNorm, row sum/max/softmax on
+  [16384, 4096], GB/s of algorithmic traffic.
 
-The roofline object describes the dominant kernel (the launch class that takes
-the most time in the timed region), timed with HIP events on the stream the
-library launches on. The CPU baseline times the CPU oracle (a single-threaded
-restatement of the topos interpreter's arithmetic, the reference's own
-single-threaded CPU path) on a bounded sample of the same sweep on this host.
+The roofline object describes the step's dominant kernel class (most time in
+a profiled step, HIP events around every launch on the library's stream);
+``cpu_baseline`` times the CPU oracle — a single-threaded restatement of the
+topos interpreter — on a bounded sample of the same step.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--quick]
 """
 from __future__ import annotations
 
 import argparse
 import json
-import os
+import math
 import sys
 import time
 from pathlib import Path
@@ -41,123 +43,259 @@ FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense fp32 matrix, published
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, published
 SWEEP = [(512, 512, 512), (1024, 4096, 1024), (4096, 4096, 4096), (8192, 768, 3072)]
 CHAIN_ROWS, CHAIN_COLUMNS = 16384, 4096
-# Algorithmic bytes per launch: each distinct input read once, each output
-# written once, fp32.
-CHAIN_BYTES = {
+CHAIN_BYTES = {  # each distinct input read once, each output written once, fp32
     "silu_bias": 4 * (2 * CHAIN_ROWS * CHAIN_COLUMNS + CHAIN_COLUMNS),
     "layer_norm": 4 * (2 * CHAIN_ROWS * CHAIN_COLUMNS + 2 * CHAIN_COLUMNS),
     "row_sum": 4 * (CHAIN_ROWS * CHAIN_COLUMNS + CHAIN_ROWS),
     "row_max": 4 * (CHAIN_ROWS * CHAIN_COLUMNS + CHAIN_ROWS),
     "row_softmax": 4 * (2 * CHAIN_ROWS * CHAIN_COLUMNS),
 }
+ADAMW = {"rate": 3e-4, "beta1": 0.9, "beta2": 0.999, "epsilon": 1e-8, "decay": 0.01}
+
+
+def log(message: str) -> None:
+    print(f"[bench] {message}", file=sys.stderr, flush=True)
 
 
 def parse() -> argparse.Namespace:
     p = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=30)
+    p.add_argument("--steps", type=int, default=10)
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU oracle leg")
-    p.add_argument("--no-chains", action="store_true", help="time the GEMM sweep only")
-    p.add_argument("--cpu-fraction", type=float, default=1.0 / 16,
-                   help="share of each sweep product's output rows the CPU leg computes")
+    p.add_argument("--quick", action="store_true", help="the GPT-2 step only (no side sections)")
     return p.parse_args()
 
 
-class Products:
-    """The sweep's operands in HBM and its twelve products as launch closures."""
+def matmul_flops(tape, roots) -> float:
+    """2*m*n*k (times the batch) over the products the program evaluates."""
+    from poorgrad_amd import topos as t
 
-    def __init__(self, torch, n, seed: int = 7):
-        self.torch, self.n = torch, n
-        gen = torch.Generator(device="cuda")
-        gen.manual_seed(seed)
-        self.entries = []  # (label, m, k, n, launch(numerics))
-        self.host = []     # for the CPU leg: (label, a, a_strides, b, b_strides, m, k, n) lazily
-        for (M, N, K) in SWEEP:
-            A = torch.randn(M, K, device="cuda", generator=gen)
-            B = torch.randn(K, N, device="cuda", generator=gen)
-            G = torch.randn(M, N, device="cuda", generator=gen)
-            C = torch.empty(M, N, device="cuda")
-            dA = torch.empty(K, N, device="cuda")  # A^T . G  (K x N)
-            dB = torch.empty(M, K, device="cuda")  # G . B^T  (M x K)
-            shape = f"{M}x{N}x{K}"
-            # forward: (M,N,K), A (K,1), B (N,1)
-            self._add(f"forward {shape}", A, (K, 1), B, (N, 1), M, K, N, C)
-            # A^T . G: left = A^T [K x M] strides (1, K); right = G [M x N]
-            self._add(f"a_t_g {shape}", A, (1, K), G, (N, 1), K, M, N, dA)
-            # G . B^T: left = G [M x N]; right = B^T [N x K] strides (1, N)
-            self._add(f"g_b_t {shape}", G, (N, 1), B, (1, N), M, N, K, dB)
-
-    def _add(self, label, a, a_st, b, b_st, m, k, n_, out):
-        lib, stream = self.n.lib, self.torch.cuda.current_stream().cuda_stream
-
-        def launch(numerics, a=a, b=b, out=out):
-            code = lib.topos_hip_gemm_f32_device(a.data_ptr(), a_st[0], a_st[1], b.data_ptr(), b_st[0], b_st[1],
-                                                 m, k, n_, numerics, out.data_ptr(), n_, stream)
-            if code != self.n.OK:
-                raise self.n.HipError(code, f"gemm {label}")
-
-        self.entries.append((label, m, k, n_, launch))
-        self.host.append((label, a, a_st, b, b_st, m, k, n_))
-
-    @property
-    def flops(self) -> float:
-        return sum(2.0 * m * k * n_ for _, m, k, n_, _ in self.entries)
+    wanted = [False] * len(tape.nodes)
+    for r in roots:
+        wanted[r.id] = True
+    for i in range(len(tape.nodes) - 1, -1, -1):
+        if wanted[i]:
+            node = tape.nodes[i]
+            links = node.operands[:1] if node.op in (t.BROADCAST, t.BROADCAST_ALONG) else node.operands
+            for link in links:
+                wanted[link] = True
+    total = 0.0
+    for i, node in enumerate(tape.nodes):
+        if wanted[i] and node.op == t.MATMUL:
+            k = tape.nodes[node.operands[0]].shape[-1]
+            total += 2.0 * math.prod(node.shape) * k
+    return total
 
 
-def time_launches(torch, launches, steps: int, warmup: int):
-    """Runs `steps` timed passes over `launches` (label, flops_or_bytes, fn),
-    bracketing each launch with HIP events on the current stream. Returns the
-    wall time of the timed region (s) and per-label mean launch time (s)."""
+def time_steps(torch, step, steps: int, warmup: int) -> float:
     for _ in range(warmup):
-        for _, _, fn in launches:
+        step()
+    torch.cuda.synchronize()
+    start = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    return time.perf_counter() - start
+
+
+def breakdown(profile) -> dict:
+    """Per launch kind: count, total ms, share, and achieved rate."""
+    total = sum(ms for _, ms, _, _, _ in profile)
+    kinds = {}
+    for kind, ms, flops, nbytes, _ in profile:
+        k = kinds.setdefault(kind, {"launches": 0, "ms": 0.0, "flops": 0.0, "bytes": 0.0})
+        k["launches"] += 1
+        k["ms"] += ms
+        k["flops"] += flops
+        k["bytes"] += nbytes
+    out = {}
+    for kind, k in sorted(kinds.items(), key=lambda kv: -kv[1]["ms"]):
+        entry = {"launches": k["launches"], "ms": round(k["ms"], 3), "share": round(k["ms"] / total, 4)}
+        if k["flops"]:
+            entry["TFLOP/s"] = round(k["flops"] / (k["ms"] / 1e3) / 1e12, 2)
+        entry["GB/s"] = round(k["bytes"] / (k["ms"] / 1e3) / 1e9, 1)
+        out[kind] = entry
+    return out
+
+
+def gpt2_section(torch, n, args) -> dict:
+    from poorgrad_amd import workloads
+    from poorgrad_amd.program import AdamW, DeviceProgram
+
+    log("recording the GPT-2-small train step")
+    t0 = time.perf_counter()
+    w = workloads.gpt2()
+    record_s = time.perf_counter() - t0
+    log(f"recorded {len(w.tape.nodes)} nodes in {record_s:.1f}s; planning and compiling")
+    t0 = time.perf_counter()
+    program = DeviceProgram(w.tape, w.roots, numerics=n.FAST)
+    plan_s = time.perf_counter() - t0
+    info = program.info
+    log(f"planned in {plan_s:.1f}s: {info}")
+    params = [torch.from_numpy(a).cuda() for a in w.initial]
+    for slot, p in enumerate(params):
+        program.bind_parameter(slot, p)
+    for slot, (indices, one) in w.selection_inputs.items():
+        program.bind_selection(slot, indices, one)
+    optimizer = AdamW(params, ADAMW["beta1"], ADAMW["beta2"], ADAMW["epsilon"], ADAMW["decay"])
+    program.run()
+    torch.cuda.synchronize()
+    gradients = [program.pointer(g) for g in w.gradients]
+    first_loss = float(program.read(w.loss))
+    log(f"first loss {first_loss:.5f} (ln V = {math.log(w.config['vocab']):.5f})")
+
+    def step():
+        program.run()
+        optimizer.step(params, gradients, ADAMW["rate"])
+
+    log(f"timing {args.steps} steps after {args.warmup} warmup")
+    wall = time_steps(torch, step, args.steps, args.warmup)
+    last_loss = float(program.read(w.loss))
+    log(f"{wall / args.steps * 1e3:.1f} ms/step; loss after {args.steps + args.warmup + 1} runs: {last_loss:.5f}")
+    profile = program.profile()
+    torch.cuda.synchronize()
+    flops = matmul_flops(w.tape, w.roots)
+    return {"wall": wall, "workload": w, "program": program, "profile": profile, "flops": flops,
+            "record_s": record_s, "plan_s": plan_s, "info": info, "first_loss": first_loss, "last_loss": last_loss}
+
+
+def roofline(profile) -> dict:
+    kinds = breakdown(profile)
+    dominant = next(iter(kinds))
+    launches = [p for p in profile if p[0] == dominant]
+    ms = sum(p[1] for p in launches)
+    if dominant == "gemm":
+        achieved = sum(p[2] for p in launches) / (ms / 1e3) / 1e12
+        return {"bound": "mfma", "achieved": round(achieved, 3), "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4), "traffic": None,
+                "kernel": f"gemm_mfma_kernel: the step's {len(launches)} product launches, algorithmic 2*m*n*k "
+                          f"over their event-timed duration", "ms_per_step": round(ms, 3)}
+    achieved = sum(p[3] for p in launches) / (ms / 1e3) / 1e9
+    return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "kernel": f"{dominant}: the step's {len(launches)} launches", "ms_per_step": round(ms, 3)}
+
+
+def cpu_leg(full_flops: float) -> dict:
+    """The oracle interpreter on one 64-token sequence of the same model
+    (full width, depth and vocabulary), one core; extrapolated to the full
+    step by the ratio of product flops (97% of the step's arithmetic)."""
+    import numpy as np
+
+    from oracle import interpreter
+    from poorgrad_amd import workloads
+
+    w = workloads.gpt2(batch=1, context=64)
+    inputs = [None] * len(w.tape.input_shapes)
+    for slot, (indices, one) in w.selection_inputs.items():
+        inputs[slot] = interpreter.Sel(indices, w.tape.input_shapes[slot][1], one)
+    start = time.perf_counter()
+    with np.errstate(all="ignore"):
+        interpreter.run(w.tape, w.roots, w.initial, inputs)
+    seconds = time.perf_counter() - start
+    sample_flops = matmul_flops(w.tape, w.roots)
+    step_seconds = seconds * full_flops / sample_flops
+    return {"value": round(1.0 / step_seconds, 8), "unit": "steps/s", "cores": 1, "kind": "port",
+            "sample": f"the interpreter restatement (oracle/) on the same GPT-2-small train step at batch 1, "
+                      f"context 64 ({sample_flops / 1e9:.1f} GFLOP of products, {seconds:.1f} s on one core), "
+                      f"scaled by product flops to the full step ({full_flops / 1e12:.2f} TFLOP): "
+                      f"{step_seconds / 60:.1f} min per step"}
+
+
+def mlp_section(torch, n, steps: int, warmup: int) -> dict:
+    from poorgrad_amd import workloads
+    from poorgrad_amd.program import DeviceProgram, sgd_step
+
+    w = workloads.mlp()
+    program = DeviceProgram(w.tape, w.roots, numerics=n.EXACT)
+    params = [torch.from_numpy(a).cuda() for a in w.initial]
+    for slot, p in enumerate(params):
+        program.bind_parameter(slot, p)
+    held = []
+    for slot, a in w.dense_inputs.items():
+        t = torch.from_numpy(a).cuda()
+        held.append(t)
+        program.bind_input(slot, t)
+    for slot, (indices, one) in w.selection_inputs.items():
+        program.bind_selection(slot, indices, one)
+    program.run()
+    gradients = [program.pointer(g) for g in w.gradients]
+
+    def step():
+        program.run()
+        for p, g in zip(params, gradients):
+            sgd_step(p, g, 0.01)
+
+    reps = max(20, steps * 10)
+    wall = time_steps(torch, step, reps, warmup)
+    return {"steps/s": round(reps / wall, 2), "us_per_step": round(wall / reps * 1e6, 1),
+            "launches_per_step": program.info["launches"] + len(params), "posture": "exact (bit-identical)",
+            "gflop_per_step": round(3 * matmul_flops(w.tape, [w.loss]) / 1e9, 4)}
+
+
+def event_times(torch, launches, steps: int, warmup: int) -> dict:
+    for _ in range(warmup):
+        for _, fn in launches:
             fn()
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
     marks = []
-    start = time.perf_counter()
     for _ in range(steps):
-        for label, _, fn in launches:
-            e0 = torch.cuda.Event(enable_timing=True)
-            e1 = torch.cuda.Event(enable_timing=True)
+        for label, fn in launches:
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             e0.record(stream)
             fn()
             e1.record(stream)
             marks.append((label, e0, e1))
     torch.cuda.synchronize()
-    wall = time.perf_counter() - start
     per = {}
     for label, e0, e1 in marks:
         per.setdefault(label, []).append(e0.elapsed_time(e1) / 1e3)
-    return wall, {label: sum(v) / len(v) for label, v in per.items()}
+    return {label: sum(v) / len(v) for label, v in per.items()}
 
 
-def cpu_leg(products, fraction: float) -> dict:
-    """The CPU oracle on a bounded sample: the first `fraction` of every sweep
-    product's output rows (rows are independent, bit-identical to the whole
-    product), one core."""
-    import numpy as np
+def gemm_section(torch, n, steps: int, warmup: int) -> dict:
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(7)
+    stream = torch.cuda.current_stream().cuda_stream
+    products = []
+    for (M, N, K) in SWEEP:
+        A = torch.randn(M, K, device="cuda", generator=gen)
+        B = torch.randn(K, N, device="cuda", generator=gen)
+        G = torch.randn(M, N, device="cuda", generator=gen)
+        shape = f"{M}x{N}x{K}"
+        for label, a, ast, b, bst, m, k, n_ in (
+                (f"forward {shape}", A, (K, 1), B, (N, 1), M, K, N),
+                (f"a_t_g {shape}", A, (1, K), G, (N, 1), K, M, N),
+                (f"g_b_t {shape}", G, (N, 1), B, (1, N), M, N, K)):
+            out = torch.empty(m, n_, device="cuda")
+            products.append((label, 2.0 * m * n_ * k, a, ast, b, bst, m, k, n_, out))
+    result = {}
+    for posture, numerics in (("fast", n.FAST), ("exact", n.EXACT)):
+        launches = []
+        for label, _, a, ast, b, bst, m, k, n_, out in products:
+            def fn(a=a, ast=ast, b=b, bst=bst, m=m, k=k, n_=n_, out=out):
+                n.checked(n.lib.topos_hip_gemm_f32_device(a.data_ptr(), ast[0], ast[1], b.data_ptr(), bst[0], bst[1],
+                                                          m, k, n_, numerics, out.data_ptr(), n_, stream), "gemm")
+            launches.append((label, fn))
+        reps = steps if posture == "fast" else max(1, min(steps, 3))
+        per = event_times(torch, launches, reps, 1)
+        total_flops = sum(p[1] for p in products)
+        total_s = sum(per.values())
+        result[posture] = {
+            "sweep_TFLOP/s": round(total_flops / total_s / 1e12, 2),
+            "frac_of_fp32_peak": round(total_flops / total_s / 1e12 / FP32_MFMA_PEAK_TFLOPS, 4),
+            "products": {p[0]: round(p[1] / per[p[0]] / 1e12, 2) for p in products},
+        }
+    return result
 
-    import oracle
 
-    flops, seconds = 0.0, 0.0
-    for label, a, a_st, b, b_st, m, k, n_ in products.host:
-        ah = a.cpu().numpy().ravel()
-        bh = b.cpu().numpy().ravel()
-        rows = max(1, int(round(m * fraction)))
-        t0 = time.perf_counter()
-        oracle.gemm(ah, a_st, bh, b_st, m, k, n_, rows=(0, rows))
-        seconds += time.perf_counter() - t0
-        flops += 2.0 * rows * k * n_
-        del ah, bh
-    _ = np
-    return {"value": flops / seconds / 1e12, "unit": "TFLOP/s", "cores": 1, "kind": "port",
-            "sample": f"first {fraction:.4g} of the output rows of each of the 12 sweep products "
-                      f"({flops / 1e9:.1f} GFLOP, {seconds:.1f} s), exact fixed-k-order arithmetic, "
-                      f"single thread (the reference library has no threads)"}
+def chains_section(torch, n, steps: int, warmup: int) -> dict:
+    import ctypes
 
+    from poorgrad_amd import device
 
-def chains(torch, n, device, steps: int, warmup: int) -> dict:
     gen = torch.Generator(device="cuda")
     gen.manual_seed(11)
     x = torch.randn(CHAIN_ROWS, CHAIN_COLUMNS, device="cuda", generator=gen)
@@ -168,12 +306,9 @@ def chains(torch, n, device, steps: int, warmup: int) -> dict:
     stats = torch.empty(CHAIN_ROWS, device="cuda")
     stream = torch.cuda.current_stream().cuda_stream
     lib = n.lib
-    # x / (exp(-x) + 1) + b (examples/llama/model.rs:258 plus a bias broadcast along axis 0)
     silu = device.Chain((CHAIN_ROWS, CHAIN_COLUMNS), [((CHAIN_COLUMNS, 1), 0), ((0, 1), 0), ((0, 0), 0)],
                         [(n.CHAIN_NEG, -1, 0), (n.CHAIN_EXP, 0, 0), (n.CHAIN_ADD, 1, -3), (n.CHAIN_DIV, -1, 2),
                          (n.CHAIN_ADD, 3, -2)], [4])
-    import ctypes
-
     ins = (ctypes.c_void_p * 3)(x.data_ptr(), b.data_ptr(), one.data_ptr())
     outs = (ctypes.c_void_p * 1)(y.data_ptr())
 
@@ -181,34 +316,25 @@ def chains(torch, n, device, steps: int, warmup: int) -> dict:
         n.checked(lib.topos_hip_chain_launch(silu._handle, ins, outs, stream), "silu chain")
 
     def rows(kind, out, numerics):
-        def fn():
-            n.checked(lib.topos_hip_rows_f32_device(kind, x.data_ptr(), CHAIN_ROWS, CHAIN_COLUMNS, numerics,
-                                                    out.data_ptr(), stream), "rows")
-        return fn
+        return lambda: n.checked(lib.topos_hip_rows_f32_device(kind, x.data_ptr(), CHAIN_ROWS, CHAIN_COLUMNS, numerics,
+                                                               out.data_ptr(), stream), "rows")
 
     def layer_norm(numerics):
-        def fn():
-            n.checked(lib.topos_hip_layer_norm_f32_device(x.data_ptr(), CHAIN_ROWS, CHAIN_COLUMNS, g.data_ptr(),
-                                                          b.data_ptr(), 1e-5, numerics, y.data_ptr(), stream),
-                      "layer norm")
-        return fn
+        return lambda: n.checked(lib.topos_hip_layer_norm_f32_device(x.data_ptr(), CHAIN_ROWS, CHAIN_COLUMNS,
+                                                                     g.data_ptr(), b.data_ptr(), 1e-5, numerics,
+                                                                     y.data_ptr(), stream), "layer norm")
 
-    launches = [("silu_bias", CHAIN_BYTES["silu_bias"], run_silu)]
+    launches = [("silu_bias", run_silu)]
+    bytes_of = {"silu_bias": CHAIN_BYTES["silu_bias"]}
     for posture, numerics in (("exact", n.EXACT), ("fast", n.FAST)):
-        launches += [
-            (f"layer_norm/{posture}", CHAIN_BYTES["layer_norm"], layer_norm(numerics)),
-            (f"row_sum/{posture}", CHAIN_BYTES["row_sum"], rows(n.ROWS_SUM, stats, numerics)),
-            (f"row_max/{posture}", CHAIN_BYTES["row_max"], rows(n.ROWS_MAX, stats, numerics)),
-            (f"row_softmax/{posture}", CHAIN_BYTES["row_softmax"], rows(n.ROWS_SOFTMAX, y, numerics)),
-        ]
-    _, per = time_launches(torch, launches, steps, warmup)
-    out = {}
-    for label, nbytes, _ in launches:
-        t = per[label]
-        gbs = nbytes / t / 1e9
-        out[label] = {"us": round(t * 1e6, 2), "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
-                      "bytes": nbytes}
-    return out
+        for name, fn in (("layer_norm", layer_norm(numerics)), ("row_sum", rows(n.ROWS_SUM, stats, numerics)),
+                         ("row_max", rows(n.ROWS_MAX, stats, numerics)),
+                         ("row_softmax", rows(n.ROWS_SOFTMAX, y, numerics))):
+            launches.append((f"{name}/{posture}", fn))
+            bytes_of[f"{name}/{posture}"] = CHAIN_BYTES[name]
+    per = event_times(torch, launches, steps, warmup)
+    return {label: {"us": round(t * 1e6, 1), "GB/s": round(bytes_of[label] / t / 1e9, 1),
+                    "frac": round(bytes_of[label] / t / 1e9 / HBM_PEAK_GBS, 4)} for label, t in per.items()}
 
 
 def main() -> int:
@@ -220,60 +346,50 @@ def main() -> int:
     import torch
 
     from poorgrad_amd import _native as n
-    from poorgrad_amd import device
 
     if n.status() != n.OK:
         print(f"HIP backend unavailable: {n.status_reason()}", file=sys.stderr)
         return 1
-    products = Products(torch, n)
-    fast = [(label, 2.0 * m * k * n_, (lambda fn=fn: fn(n.FAST))) for label, m, k, n_, fn in products.entries]
-    exact = [(label, 2.0 * m * k * n_, (lambda fn=fn: fn(n.EXACT))) for label, m, k, n_, fn in products.entries]
-    print(f"[bench] gemm sweep fast: {args.steps} steps after {args.warmup} warmup", file=sys.stderr, flush=True)
-    wall, per = time_launches(torch, fast, args.steps, args.warmup)
-    sweep_flops = products.flops
-    value = sweep_flops * args.steps / wall / 1e12
-    # Dominant launch class: the most time in the timed region.
-    label, flops, _ = max(fast, key=lambda e: per[e[0]])
-    achieved = flops / per[label] / 1e12
-    per_product = {lab: {"us": round(per[lab] * 1e6, 1), "TFLOP/s": round(f / per[lab] / 1e12, 2)}
-                   for lab, f, _ in fast}
-    print("[bench] gemm sweep exact", file=sys.stderr, flush=True)
-    exact_steps = max(1, min(args.steps, 5))
-    exact_wall, exact_per = time_launches(torch, exact, exact_steps, 1)
-    exact_value = sweep_flops * exact_steps / exact_wall / 1e12
-    chain_results = None
-    if not args.no_chains:
-        print("[bench] chains", file=sys.stderr, flush=True)
-        chain_results = chains(torch, n, device, args.steps, args.warmup)
-    cpu = None
-    if not args.no_cpu_baseline:
-        print("[bench] cpu baseline (oracle, one core)", file=sys.stderr, flush=True)
-        cpu = cpu_leg(products, args.cpu_fraction)
+    g = gpt2_section(torch, n, args)
+    ms_per_step = g["wall"] / args.steps * 1e3
     line = {
         "metric": METRIC,
-        "value": round(value, 3),
-        "unit": "TFLOP/s",
+        "value": round(args.steps / g["wall"], 4),
+        "unit": "steps/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(wall / args.steps * 1e3, 4),
+        "ms_per_step": round(ms_per_step, 2),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic",
-        "config": {"workload": "gemm_sweep (BASELINE configs[1]): forward A.B plus A^T.G and G.B^T as stride "
-                               "views, fast (matrix-core) posture, A,B,G ~ N(0,1)",
-                   "shapes_mnk": SWEEP, "products_per_step": len(fast), "gflop_per_step": round(sweep_flops / 1e9, 3)},
-        "roofline": {"bound": "mfma", "achieved": round(achieved, 3), "peak": FP32_MFMA_PEAK_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4), "traffic": None,
-                     "kernel": f"gemm_mfma_kernel ({label})", "us_per_launch": round(per[label] * 1e6, 2)},
-        "cpu_baseline": cpu,
-        "gemm_products": per_product,
-        "exact_sweep": {"TFLOP/s": round(exact_value, 3), "frac_of_fp32_peak": round(exact_value / FP32_MFMA_PEAK_TFLOPS, 4),
-                        "per_product_us": {lab: round(t * 1e6, 1) for lab, t in exact_per.items()}},
-        "chains": chain_results,
+        "data": "synthetic: token ids uniform over the vocabulary (splitmix64 seed 13), weights N(0, 0.02)",
+        "config": {"workload": "gpt2_small_train_step (BASELINE configs[3]): recorded-gradients program + AdamW "
+                               "on device, fast posture",
+                   "layers": 12, "d_model": 768, "heads": 12, "context": 1024, "batch": 8, "vocab": 50257,
+                   "optimizer": dict(ADAMW), "tflop_per_step_products": round(g["flops"] / 1e12, 3),
+                   "nodes": len(g["workload"].tape.nodes), "launches_per_step": g["info"]["launches"],
+                   "arena_gib": round(g["info"]["arena_bytes"] / 2**30, 2),
+                   "plan_s": round(g["plan_s"], 1)},
+        "roofline": roofline(g["profile"]),
+        "cpu_baseline": None,
+        "step_breakdown": breakdown(g["profile"]),
+        "products_TFLOP/s": round(g["flops"] / (ms_per_step / 1e3) / 1e12, 2),
+        "loss": {"first": g["first_loss"], "after_steps": g["last_loss"]},
     }
+    full_flops = g["flops"]
+    del g
+    if not args.quick:
+        log("mlp step (configs[0])")
+        line["mlp"] = mlp_section(torch, n, args.steps, args.warmup)
+        log("gemm sweep (configs[1])")
+        line["gemm_sweep"] = gemm_section(torch, n, args.steps, args.warmup)
+        log("chains (configs[2])")
+        line["chains"] = chains_section(torch, n, args.steps, args.warmup)
+    if not args.no_cpu_baseline:
+        log("cpu baseline: the oracle interpreter on one core")
+        line["cpu_baseline"] = cpu_leg(full_flops)
     print(json.dumps(line), flush=True)
     return 0
 

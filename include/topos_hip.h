@@ -322,6 +322,16 @@ int topos_hip_program_bind_selection(topos_hip_program *program, int32_t slot, c
                                      int64_t rows, float one);
 /* Enqueues one forward run on `stream` (the arena is reserved on first use). */
 int topos_hip_program_run(topos_hip_program *program, void *stream);
+/* One run with a HIP event pair around every launch, waited for;
+ * `milliseconds[l]` receives launch l's duration (an array of `launches`
+ * floats, topos_hip_program_info). For measurement, not for the hot loop. */
+int topos_hip_program_run_profiled(topos_hip_program *program, void *stream, float *milliseconds);
+/* Launch l's kind ("gemm", "chain", "fold", "sum", "rows", "gather",
+ * "scatter", "copy", "pad", "scalar", "one-hot") and its algorithmic work: flops
+ * for products, and bytes (each distinct input element read once, each
+ * output written once) for everything. */
+int topos_hip_program_launch(const topos_hip_program *program, int64_t launch, const char **kind, double *flops,
+                             double *bytes);
 /* The device address of a readable node's value after a run: contiguous
  * row-major, volume(shape) floats, valid until the next run. */
 int topos_hip_program_output(const topos_hip_program *program, int64_t node, const float **device);

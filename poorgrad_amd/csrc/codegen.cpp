@@ -413,7 +413,7 @@ Generated generate_fold(const Expr &e, int axis, FoldKind kind) {
   if (axis < 0 || axis >= e.rank) throw InvalidArgument{"fold axis out of range"};
   std::ostringstream s;
   s << preamble();
-  s << signature(e, "float* __restrict__ out") << " {\n";
+  s << signature(e, "float* __restrict__ out, int vector_ok") << " {\n";
   // Remaining axes, in order, name the output coordinates.
   std::vector<int64_t> rest;
   std::vector<int> rest_axes;
@@ -478,34 +478,70 @@ Generated generate_fold(const Expr &e, int axis, FoldKind kind) {
   auto combine = [&](const std::string &acc, const std::string &v) {
     return kind == kFoldSum ? acc + " + " + v : "topos_faithful::max_f32(" + acc + ", " + v + ")";
   };
-  const std::string result = ref(e.outputs[0], "x");
-  auto element = [&](const std::string &k) {
-    for (size_t i = 0; i < e.inputs.size(); ++i) s << "      const float in" << i << "_x = " << value((int)i, k) << ";\n";
-    emit_steps(s, e, {"x"});
+  // element(k, lane): every input's value at fold coordinate k, then the
+  // expression, as lane-suffixed registers.
+  auto element = [&](const std::string &k, const std::string &lane) {
+    for (size_t i = 0; i < e.inputs.size(); ++i)
+      s << "      const float in" << i << "_" << lane << " = " << value((int)i, k) << ";\n";
+    emit_steps(s, e, {lane});
+  };
+  // A quad of consecutive fold coordinates k4..k4+3 (k4 % 4 == 0) along the
+  // innermost axis: 16-byte loads for unit-stride inputs when aligned.
+  auto quad = [&](const std::string &k4) {
+    for (size_t i = 0; i < e.inputs.size(); ++i) {
+      const ExprInput &in = e.inputs[i];
+      const std::string v = "in" + std::to_string(i) + "_q";
+      const bool unit = (in.kind == ExprInput::kStrided || in.kind == ExprInput::kPadded) && in.strides[axis] == 1 &&
+                        vector_input(e, in);
+      if (unit) {
+        const std::string b = "b" + std::to_string(i);
+        std::string inside = "true";
+        if (in.kind == ExprInput::kPadded)
+          inside = in.pad_axis == axis ? window_test(in, k4) : "w" + std::to_string(i);
+        s << "      float " << v << "0 = 0.0f, " << v << "1 = 0.0f, " << v << "2 = 0.0f, " << v << "3 = 0.0f;\n";
+        s << "      if (" << inside << ") {\n";
+        s << "        if (vector_ok) { const float4 w = *(const float4*)(" << b << " + " << k4 << "); " << v << "0 = w.x; "
+          << v << "1 = w.y; " << v << "2 = w.z; " << v << "3 = w.w; }\n";
+        s << "        else { ";
+        for (int j = 0; j < 4; ++j) s << v << j << " = " << b << "[" << k4 << " + " << j << "]; ";
+        s << "}\n      }\n";
+      } else {
+        for (int j = 0; j < 4; ++j)
+          s << "      const float " << v << j << " = " << value((int)i, k4 + " + " + std::to_string(j)) << ";\n";
+      }
+    }
+    emit_steps(s, e, {"q0", "q1", "q2", "q3"});
   };
   s << "  float acc;\n";
-  s << "  {\n    const long long k = 0;\n";
-  element("k");
-  s << "    acc = " << result << ";\n  }\n";
   if (quads) {
-    // Steps 1..3 of the first quad, then whole quads: the loads of a quad
-    // are independent of the fold, so they issue together.
-    s << "  for (long long k = 1; k < 4; ++k) {\n";
-    element("k");
-    s << "    acc = " << combine("acc", result) << ";\n  }\n";
+    s << "  {\n";
+    quad("0LL");
+    s << "    acc = " << ref(e.outputs[0], "q0") << ";\n";
+    for (int j = 1; j < 4; ++j) s << "    acc = " << combine("acc", ref(e.outputs[0], "q" + std::to_string(j))) << ";\n";
+    s << "  }\n";
     s << "  #pragma unroll 2\n";
     s << "  for (long long k4 = 4; k4 < " << ll(extent) << "; k4 += 4) {\n";
-    for (int j = 0; j < 4; ++j) {
-      s << "    float r" << j << ";\n    {\n      const long long k = k4 + " << j << ";\n";
-      element("k");
-      s << "      r" << j << " = " << result << ";\n    }\n";
-    }
-    for (int j = 0; j < 4; ++j) s << "    acc = " << combine("acc", "r" + std::to_string(j)) << ";\n";
+    quad("k4");
+    for (int j = 0; j < 4; ++j) s << "    acc = " << combine("acc", ref(e.outputs[0], "q" + std::to_string(j))) << ";\n";
     s << "  }\n";
   } else {
-    s << "  for (long long k = 1; k < " << ll(extent) << "; ++k) {\n";
-    element("k");
-    s << "    acc = " << combine("acc", result) << ";\n  }\n";
+    // The first term seeds; then blocks of eight whose loads all issue
+    // before the eight ordered additions.
+    s << "  {\n    const long long k = 0;\n";
+    element("k", "x");
+    s << "    acc = " << ref(e.outputs[0], "x") << ";\n  }\n";
+    s << "  long long k8 = 1;\n  float r0, r1, r2, r3, r4, r5, r6, r7;\n";
+    s << "  for (; k8 + 8 <= " << ll(extent) << "; k8 += 8) {\n";
+    for (int j = 0; j < 8; ++j) {
+      s << "    {\n      const long long k = k8 + " << j << ";\n";
+      element("k", "u" + std::to_string(j));
+      s << "      r" << j << " = " << ref(e.outputs[0], "u" + std::to_string(j)) << ";\n    }\n";
+    }
+    for (int j = 0; j < 8; ++j) s << "    acc = " << combine("acc", "r" + std::to_string(j)) << ";\n";
+    s << "  }\n";
+    s << "  for (long long k = k8; k < " << ll(extent) << "; ++k) {\n";
+    element("k", "x");
+    s << "    acc = " << combine("acc", ref(e.outputs[0], "x")) << ";\n  }\n";
   }
   s << "  out[o] = acc;\n}\n";
   return make(s.str());
@@ -519,8 +555,10 @@ void launch_generated_fold(const Generated &g, const Expr &e, int axis, const vo
   std::vector<const void *> pointers;
   for (size_t i = 0; i < e.inputs.size(); ++i) pointers.push_back(inputs[i]);
   pointers.push_back(out);
+  int vector_ok = pointers_aligned(e, inputs) ? 1 : 0;
   std::vector<void *> arguments;
   for (auto &p : pointers) arguments.push_back(&p);
+  arguments.push_back(&vector_ok);
   const int64_t blocks = (outputs + 255) / 256;
   if (blocks > 0x7fffffff) throw Unsupported{"fold: too many outputs for one launch"};
   launch(g, (unsigned)blocks, arguments, stream);

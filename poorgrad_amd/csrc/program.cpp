@@ -269,6 +269,8 @@ struct topos_hip_program {
     std::string what;
     std::vector<int> reads, writes;
     std::function<void(const Exec &)> run;
+    std::string kind;
+    double flops = 0, bytes = 0;
   };
   std::vector<Launch> launches;
   std::vector<Generated> pending;  // generated kernels, compiled together after planning
@@ -531,8 +533,27 @@ struct topos_hip_program {
   int add_launch(const std::string &what, std::vector<int> reads, std::vector<int> writes,
                  std::function<void(const Exec &)> run) {
     Launch l{what, std::move(reads), std::move(writes), std::move(run)};
+    l.kind = what.substr(0, what.find(' '));
     launches.push_back(std::move(l));
     return (int)launches.size() - 1;
+  }
+
+  // Algorithmic bytes of the last launch: each distinct element of a
+  // non-literal input read once (a stride-0 axis adds no elements), each
+  // output element written once.
+  static double distinct_elements(const Expr &e, const ExprInput &in) {
+    if (in.kind == ExprInput::kLiteral) return 0;
+    if (in.kind == ExprInput::kSelection) return (double)e.shape[0];  // the indices
+    double v = 1;
+    for (int d = 0; d < e.rank; ++d)
+      if (in.strides[d] != 0) v *= (double)(in.kind == ExprInput::kPadded && d == in.pad_axis ? in.pad_len : e.shape[d]);
+    return v;
+  }
+  void account(const Expr &e, double outputs, double flops = 0) {
+    double reads = 0;
+    for (const ExprInput &in : e.inputs) reads += distinct_elements(e, in);
+    launches.back().bytes = 4.0 * (reads + outputs);
+    launches.back().flops = flops;
   }
 
   // Pointer resolution at run time.
@@ -691,6 +712,7 @@ struct topos_hip_program {
                  float *q = (float *)base(out);
                  launch_generated_chain(g, e, p.data(), &q, x.stream);
                });
+    account(e, (double)e.volume());
     const topos_hip_node &n = nodes[root];
     return dense_value(out, contiguous(n.rank, n.shape));
   }
@@ -735,6 +757,7 @@ struct topos_hip_program {
       float *q = (float *)base(out);
       launch_generated_chain(g, e, p.data(), &q, x.stream);
     });
+    account(e, (double)e.volume());
     return dense_value(out, contiguous(n.rank, n.shape));
   }
 
@@ -978,6 +1001,7 @@ struct topos_hip_program {
       float *q = (float *)base(out);
       launch_generated_chain(g, e, p.data(), &q, ex.stream);
     });
+    account(e, (double)e.volume());
     values[i] = dense_value(out, contiguous(x.rank, x.shape));
   }
 
@@ -1046,6 +1070,8 @@ struct topos_hip_program {
                    launch_gemm_exact(qa, ars, acs, qb, brs, bcs, m, k, n, qc, n, ex.stream, batch);
                  }
                });
+    launches.back().flops = 2.0 * (double)batches * m * n * k;
+    launches.back().bytes = 4.0 * (double)batches * ((double)m * k + (double)k * n + (double)m * n);
     values[i] = dense_value(out, contiguous(x.rank, x.shape));
   }
 
@@ -1081,6 +1107,7 @@ struct topos_hip_program {
                  auto p = pointers_for(storage_of);
                  launch_generated_fold(g, e, axis, p.data(), (float *)base(out), ex.stream);
                });
+    account(e, (double)volume_of(x));
     values[i] = dense_value(out, contiguous(x.rank, x.shape));
   }
 
@@ -1117,6 +1144,7 @@ struct topos_hip_program {
                  launch_ordered_fold((const float *)base(compacted), (const int64_t *)base(offsets), chunks,
                                      (const int32_t *)base(flags), (float *)base(out), ex.stream);
                });
+    account(e, 1.0);
     Value v = dense_value(out, constant_layout(0, x.shape, 0));
     v.constant = true;
     values[i] = v;
@@ -1168,6 +1196,7 @@ struct topos_hip_program {
                    float *q = (float *)base(copy);
                    launch_generated_chain(g, e, p.data(), &q, ex.stream);
                  });
+      account(e, (double)e.volume());
       source = copy;
       source_offset = 0;
     }
@@ -1183,6 +1212,8 @@ struct topos_hip_program {
                  launch_rows(kind, (const float *)base(source) + source_offset, rows, extent, numerics_,
                              (float *)base(out), ex.stream);
                });
+    launches.back().kind = "rows";
+    launches.back().bytes = 4.0 * ((double)rows * extent + (full ? (double)rows * extent : (double)rows));
     if (!full) {
       values[i] = dense_value(out, contiguous(x.rank, x.shape));
       return;
@@ -1232,6 +1263,7 @@ struct topos_hip_program {
                  launch_gather((const float *)base(table) + offset, rs, cs, (const int32_t *)base(selection), rows,
                                row_size, (float *)base(out), ex.stream);
                });
+    launches.back().bytes = 4.0 * (2.0 * rows * row_size + rows);
     values[i] = dense_value(out, contiguous(x.rank, x.shape));
   }
 
@@ -1255,6 +1287,7 @@ struct topos_hip_program {
                  launch_scatter((const float *)base(gradient) + offset, rs, cs, b.row_start, b.sources, rows,
                                 row_size, (float *)base(out), ex.stream);
                });
+    launches.back().bytes = 4.0 * ((double)nodes[x.operands[0]].shape[0] * row_size + (double)rows * row_size);
     values[i] = dense_value(out, contiguous(x.rank, x.shape));
   }
 
@@ -1413,7 +1446,7 @@ struct topos_hip_program {
     return b;
   }
 
-  void run(hipStream_t stream) {
+  void run(hipStream_t stream, float *milliseconds = nullptr) {
     if (!device) throw InvalidArgument{"the fake runtime plans programs but does not run them"};
     if (!arena) {
       void *p = nullptr;
@@ -1432,7 +1465,21 @@ struct topos_hip_program {
         throw InvalidArgument{"selection input slot " + std::to_string(s.index) + " is not bound"};
     }
     const Exec ex{this, stream};
-    for (const Launch &l : launches) l.run(ex);
+    if (!milliseconds) {
+      for (const Launch &l : launches) l.run(ex);
+      return;
+    }
+    std::vector<hipEvent_t> events(launches.size() + 1);
+    for (hipEvent_t &e : events) check(hipEventCreate(&e), "hipEventCreate");
+    check(hipEventRecord(events[0], stream), "hipEventRecord");
+    for (size_t l = 0; l < launches.size(); ++l) {
+      launches[l].run(ex);
+      check(hipEventRecord(events[l + 1], stream), "hipEventRecord");
+    }
+    check(hipEventSynchronize(events.back()), "hipEventSynchronize");
+    for (size_t l = 0; l < launches.size(); ++l)
+      check(hipEventElapsedTime(&milliseconds[l], events[l], events[l + 1]), "hipEventElapsedTime");
+    for (hipEvent_t &e : events) hipEventDestroy(e);
   }
 };
 
@@ -1519,6 +1566,23 @@ int topos_hip_program_run(topos_hip_program *program, void *stream) {
   const int status = Context::get().status();
   if (status != TOPOS_HIP_OK) return status;
   return guarded([&] { program->run(static_cast<hipStream_t>(stream)); });
+}
+
+int topos_hip_program_run_profiled(topos_hip_program *program, void *stream, float *milliseconds) {
+  if (!program || !milliseconds) return TOPOS_HIP_INVALID_ARGUMENT;
+  const int status = Context::get().status();
+  if (status != TOPOS_HIP_OK) return status;
+  return guarded([&] { program->run(static_cast<hipStream_t>(stream), milliseconds); });
+}
+
+int topos_hip_program_launch(const topos_hip_program *program, int64_t launch, const char **kind, double *flops,
+                             double *bytes) {
+  if (!program || launch < 0 || launch >= (int64_t)program->launches.size()) return TOPOS_HIP_INVALID_ARGUMENT;
+  const auto &l = program->launches[launch];
+  if (kind) *kind = l.kind.c_str();
+  if (flops) *flops = l.flops;
+  if (bytes) *bytes = l.bytes;
+  return TOPOS_HIP_OK;
 }
 
 int topos_hip_program_output(const topos_hip_program *program, int64_t node, const float **device) {

@@ -64,6 +64,25 @@ class DeviceProgram:
 
         n.checked(n.lib.topos_hip_program_run(self.handle, torch.cuda.current_stream().cuda_stream), "program run")
 
+    def profile(self) -> list:
+        """One run with HIP events around every launch: per launch
+        (kind, milliseconds, flops, bytes, description)."""
+        import torch
+
+        count = self.info["launches"]
+        ms = (ctypes.c_float * count)()
+        n.checked(n.lib.topos_hip_program_run_profiled(self.handle, torch.cuda.current_stream().cuda_stream, ms),
+                  "program profiled run")
+        lines = self.describe.splitlines()[1:]
+        out = []
+        for i in range(count):
+            kind, flops, nbytes = ctypes.c_char_p(), ctypes.c_double(), ctypes.c_double()
+            n.checked(n.lib.topos_hip_program_launch(self.handle, i, ctypes.byref(kind), ctypes.byref(flops),
+                                                     ctypes.byref(nbytes)), "program launch")
+            what = lines[i].split(": ", 1)[1] if i < len(lines) else ""
+            out.append((kind.value.decode(), float(ms[i]), flops.value, nbytes.value, what))
+        return out
+
     def pointer(self, value: Value) -> int:
         """Device address of a readable value after a run (contiguous f32)."""
         p = ctypes.c_void_p()
@@ -78,7 +97,7 @@ class DeviceProgram:
 
     def __del__(self):
         handle = getattr(self, "handle", None)
-        if handle:
+        if handle and n is not None and getattr(n, "lib", None) is not None:
             n.lib.topos_hip_program_destroy(handle)
             self.handle = None
 
