@@ -64,6 +64,7 @@ def parse() -> argparse.Namespace:
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU oracle leg")
     p.add_argument("--quick", action="store_true", help="the GPT-2 step only (no side sections)")
+    p.add_argument("--profile-out", help="write the profiled step's launches (one line each) to this file")
     return p.parse_args()
 
 
@@ -379,6 +380,11 @@ def main() -> int:
         "loss": {"first": g["first_loss"], "after_steps": g["last_loss"]},
     }
     full_flops = g["flops"]
+    if args.profile_out:
+        with open(args.profile_out, "w") as f:
+            for i, (kind, ms, flops, nbytes, what) in enumerate(g["profile"]):
+                rate = f"{flops / ms / 1e9:.1f} TFLOP/s" if flops else f"{nbytes / ms / 1e6:.0f} GB/s"
+                f.write(f"{i}\t{kind}\t{ms * 1e3:.1f} us\t{rate}\t{what}\n")
     del g
     if not args.quick:
         log("mlp step (configs[0])")

@@ -96,8 +96,12 @@ void enqueue_gemm(const float *a, int64_t a_rs, int64_t a_cs, const float *b, in
     context.tick("gemm launch");
     return;
   }
-  if (numerics == TOPOS_HIP_FAST && launch_gemm_mfma(a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, stream))
-    return;
+  if (numerics == TOPOS_HIP_FAST) {
+    const int splits = mfma_splits(m, n, k, 1);
+    const int64_t floats = splits > 1 ? (int64_t)splits * m * n : 0;
+    float *workspace = floats ? context.workspace(floats) : nullptr;
+    if (launch_gemm_mfma(a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, stream, Batch(), workspace, floats)) return;
+  }
   launch_gemm_exact(a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, stream);
 }
 

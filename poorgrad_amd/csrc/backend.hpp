@@ -59,6 +59,11 @@ class Context {
   // RuntimeFailure when the countdown reaches the failing call.
   void tick(const char *what);
 
+  // A grow-only device buffer of at least `floats` floats for the device
+  // face's split products. Calls that use it are ordered on one stream;
+  // device-face calls on different streams must not overlap while using it.
+  float *workspace(int64_t floats);
+
   int device_count() const { return device_count_; }
   int architecture_major() const { return arch_major_; }
   std::mutex &task_lock() { return task_lock_; }
@@ -78,6 +83,9 @@ class Context {
   int device_count_ = 0;
   int arch_major_ = 0;
   std::mutex task_lock_;
+  std::mutex workspace_lock_;
+  float *workspace_ = nullptr;
+  int64_t workspace_floats_ = 0;
 };
 
 // Runs `body`, mapping the library's exceptions to status codes; a runtime
@@ -125,9 +133,15 @@ void launch_gemm_exact(const float *a, int64_t a_rs, int64_t a_cs, const float *
                        hipStream_t stream, const Batch &batch = Batch());
 // gemm_mfma.hip: fp32 MFMA product within the stated envelope. Returns false
 // when the stride pattern is outside its loaders (caller falls back).
+// With a workspace of at least mfma_splits(m, n, k, count) * count * m * n
+// floats, a product with too few output tiles to fill the chip is split
+// along k into that many partial products, reduced in a fixed order
+// (deterministic; envelope fidelity like the unsplit kernel).
+int mfma_splits(int64_t m, int64_t n, int64_t k, int64_t batches);
 bool launch_gemm_mfma(const float *a, int64_t a_rs, int64_t a_cs, const float *b, int64_t b_rs,
                       int64_t b_cs, int64_t m, int64_t k, int64_t n, float *c, int64_t ldc,
-                      hipStream_t stream, const Batch &batch = Batch());
+                      hipStream_t stream, const Batch &batch = Batch(), float *workspace = nullptr,
+                      int64_t workspace_floats = 0);
 
 // index.hip
 void launch_gather(const float *table, int64_t row_stride, int64_t column_stride, const int32_t *indices,

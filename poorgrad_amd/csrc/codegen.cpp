@@ -184,7 +184,20 @@ void emit_coordinates(std::ostringstream &s, int rank, const int64_t *shape, con
 std::string preamble() {
   std::string s = "#pragma clang fp contract(off)\n";
   s += kFaithfulMathText;
-  s += "\n";
+  // A barrier that orders LDS traffic only. __syncthreads() also waits for
+  // every outstanding global load (a workgroup-scope fence), which would
+  // stall the loads a fold keeps in flight across its barriers. Waiting for
+  // lgkmcnt(0) (this lane's LDS reads and writes have completed; vmcnt and
+  // expcnt left at their maxima: simm16 0xC07F on gfx9-family targets), then
+  // s_barrier, gives every LDS write before the barrier to every LDS read
+  // after it. The signal fences keep the compiler from moving memory
+  // operations across.
+  s += "\n__device__ __forceinline__ void topos_lds_barrier() {\n"
+       "  __atomic_signal_fence(__ATOMIC_SEQ_CST);\n"
+       "  __builtin_amdgcn_s_waitcnt(0xC07F);\n"
+       "  __builtin_amdgcn_s_barrier();\n"
+       "  __atomic_signal_fence(__ATOMIC_SEQ_CST);\n"
+       "}\n";
   return s;
 }
 
@@ -408,13 +421,32 @@ void launch_generated_chain(const Generated &g, const Expr &e, const void *const
 
 // ---- fold ----
 
+namespace {
+
+// Outputs per fold workgroup: 64 when that still gives 256 workgroups,
+// else 16 (more workgroups, each pulling a narrower band).
+int64_t fold_width(int64_t outputs) { return outputs / 64 >= 256 ? 64 : 16; }
+
+}  // namespace
+
 Generated generate_fold(const Expr &e, int axis, FoldKind kind) {
+  // A workgroup owns W consecutive outputs (W = 16 or 64). Per tile of
+  // H = 4096 / W fold steps, all 256 lanes evaluate the expression at 16
+  // (output, step) points each and park the values in LDS; lane j < W then
+  // folds output j over the tile in ascending step order. The next tile's
+  // loads are issued before the fold of the current one, so they are in
+  // flight while it runs.
+  //   column form (the fold axis is not the innermost): a lane's output is
+  //     lane % W and its steps lane / W + (256 / W) i — consecutive lanes read
+  //     consecutive outputs, contiguous when the innermost axis is;
+  //   row form (the fold axis is the innermost): a lane's step is lane % H
+  //     and its outputs lane / H + (256 / H) i — consecutive lanes read along
+  //     a row.
   validate(e);
   if (axis < 0 || axis >= e.rank) throw InvalidArgument{"fold axis out of range"};
   std::ostringstream s;
   s << preamble();
   s << signature(e, "float* __restrict__ out, int vector_ok") << " {\n";
-  // Remaining axes, in order, name the output coordinates.
   std::vector<int64_t> rest;
   std::vector<int> rest_axes;
   for (int d = 0; d < e.rank; ++d)
@@ -425,125 +457,93 @@ Generated generate_fold(const Expr &e, int axis, FoldKind kind) {
   int64_t outputs = 1;
   for (int64_t x : rest) outputs *= x;
   const int64_t extent = e.shape[axis];
-  s << "  const long long o = (long long)blockIdx.x * 256 + threadIdx.x;\n";
-  s << "  if (o >= " << ll(outputs) << ") return;\n";
-  std::vector<std::string> rc;
-  if (!rest.empty()) emit_coordinates(s, (int)rest.size(), rest.data(), "o", "o", rc);
-  std::vector<std::string> c(e.rank);
-  for (size_t k = 0; k < rest_axes.size(); ++k) c[rest_axes[k]] = rc[k];
-  c[axis] = "k";
-  // Per-input base address with the fold coordinate at zero, and its stride.
-  std::vector<std::string> zero = c;
-  zero[axis] = "0LL";
-  const bool inner_axis = axis == e.rank - 1;
-  bool quads = inner_axis && extent % 4 == 0 && extent >= 4;
-  for (const ExprInput &in : e.inputs)
-    if (in.kind == ExprInput::kPadded && in.pad_axis == axis && (in.pad_start % 4 || in.pad_len % 4)) quads = false;
-  for (size_t i = 0; i < e.inputs.size(); ++i) {
-    const ExprInput &in = e.inputs[i];
-    if (in.kind == ExprInput::kLiteral) continue;
-    if (in.kind == ExprInput::kSelection) {
-      // Folding along the vocabulary: the row, hence its index, is fixed.
-      if (axis == 1) s << "  const int sel" << i << " = p" << i << "[" << c[0] << "];\n";
-      continue;
-    }
-    std::string base = ll(in.offset);
-    for (int d = 0; d < e.rank; ++d) {
-      if (d == axis || in.strides[d] == 0) continue;
-      std::string coord = c[d];
-      if (in.kind == ExprInput::kPadded && d == in.pad_axis) coord = "(" + coord + " - " + ll(in.pad_start) + ")";
-      base += " + " + coord + " * " + ll(in.strides[d]);
-    }
-    if (in.kind == ExprInput::kPadded && in.pad_axis == axis) base += " - " + ll(in.pad_start * in.strides[axis]);
-    s << "  const float* __restrict__ b" << i << " = p" << i << " + (" << base << ");\n";
-    if (in.kind == ExprInput::kPadded && in.pad_axis != axis)
-      s << "  const bool w" << i << " = " << window_test(in, c[in.pad_axis]) << ";\n";
-  }
-  // The value of input i at fold coordinate `k` (+j).
-  auto value = [&](int i, const std::string &k) -> std::string {
-    const ExprInput &in = e.inputs[i];
-    if (in.kind == ExprInput::kLiteral) return float_literal(in.one);
-    if (in.kind == ExprInput::kSelection) {
-      if (axis == 0)  // folding over rows: each step reads its row's index
-        return "(p" + std::to_string(i) + "[" + k + "] == (int)(" + c[1] + ") ? " + float_literal(in.one) + " : 0.0f)";
-      return "(sel" + std::to_string(i) + " == (int)(" + k + ") ? " + float_literal(in.one) + " : 0.0f)";
-    }
-    const std::string load = "b" + std::to_string(i) + "[(" + k + ") * " + ll(in.strides[axis]) + "]";
-    if (in.kind == ExprInput::kPadded) {
-      if (in.pad_axis == axis) return "(" + window_test(in, k) + " ? " + load + " : 0.0f)";
-      return "(w" + std::to_string(i) + " ? " + load + " : 0.0f)";
-    }
-    return load;
-  };
-  auto combine = [&](const std::string &acc, const std::string &v) {
-    return kind == kFoldSum ? acc + " + " + v : "topos_faithful::max_f32(" + acc + ", " + v + ")";
-  };
-  // element(k, lane): every input's value at fold coordinate k, then the
-  // expression, as lane-suffixed registers.
-  auto element = [&](const std::string &k, const std::string &lane) {
+  const bool row_form = axis == e.rank - 1;
+  const int W = (int)fold_width(outputs), H = 4096 / W;
+  s << "  __shared__ float tile[" << W << "][" << H + 1 << "];\n";
+  s << "  const int t = threadIdx.x;\n";
+  s << "  const long long first_output = (long long)blockIdx.x * " << W << ";\n";
+  int counter = 0;
+  // The value of the expression at (output o, step k), as register `name`.
+  auto point = [&](const std::string &o, const std::string &k, const std::string &name) {
+    const std::string tag = "p" + std::to_string(counter++);
+    s << "    float " << name << " = 0.0f;\n";
+    s << "    if (" << o << " < " << ll(outputs) << " && " << k << " < " << ll(extent) << ") {\n";
+    std::vector<std::string> rc;
+    if (!rest.empty()) emit_coordinates(s, (int)rest.size(), rest.data(), o, tag, rc);
+    std::vector<std::string> c(e.rank);
+    for (size_t q = 0; q < rest_axes.size(); ++q) c[rest_axes[q]] = rc[q];
+    c[axis] = "(" + k + ")";
     for (size_t i = 0; i < e.inputs.size(); ++i)
-      s << "      const float in" << i << "_" << lane << " = " << value((int)i, k) << ";\n";
-    emit_steps(s, e, {lane});
+      s << "      const float in" << i << "_" << tag << " = " << scalar_value(e, (int)i, c) << ";\n";
+    emit_steps(s, e, {tag});
+    s << "      " << name << " = " << ref(e.outputs[0], tag) << ";\n    }\n";
   };
-  // A quad of consecutive fold coordinates k4..k4+3 (k4 % 4 == 0) along the
-  // innermost axis: 16-byte loads for unit-stride inputs when aligned.
-  auto quad = [&](const std::string &k4) {
-    for (size_t i = 0; i < e.inputs.size(); ++i) {
-      const ExprInput &in = e.inputs[i];
-      const std::string v = "in" + std::to_string(i) + "_q";
-      const bool unit = (in.kind == ExprInput::kStrided || in.kind == ExprInput::kPadded) && in.strides[axis] == 1 &&
-                        vector_input(e, in);
-      if (unit) {
-        const std::string b = "b" + std::to_string(i);
-        std::string inside = "true";
-        if (in.kind == ExprInput::kPadded)
-          inside = in.pad_axis == axis ? window_test(in, k4) : "w" + std::to_string(i);
-        s << "      float " << v << "0 = 0.0f, " << v << "1 = 0.0f, " << v << "2 = 0.0f, " << v << "3 = 0.0f;\n";
-        s << "      if (" << inside << ") {\n";
-        s << "        if (vector_ok) { const float4 w = *(const float4*)(" << b << " + " << k4 << "); " << v << "0 = w.x; "
-          << v << "1 = w.y; " << v << "2 = w.z; " << v << "3 = w.w; }\n";
-        s << "        else { ";
-        for (int j = 0; j < 4; ++j) s << v << j << " = " << b << "[" << k4 << " + " << j << "]; ";
-        s << "}\n      }\n";
-      } else {
-        for (int j = 0; j < 4; ++j)
-          s << "      const float " << v << j << " = " << value((int)i, k4 + " + " + std::to_string(j)) << ";\n";
-      }
+  // Point i of this lane, at tile start k0: its (output, local output, step, local step).
+  auto coords = [&](int i, const std::string &k0, std::string &o, std::string &lo, std::string &k,
+                    std::string &lk) {
+    if (row_form) {
+      lo = "(t / " + std::to_string(H) + " + " + std::to_string((256 / H) * i) + ")";
+      lk = "(t % " + std::to_string(H) + ")";
+    } else {
+      lo = "(t % " + std::to_string(W) + ")";
+      lk = "(t / " + std::to_string(W) + " + " + std::to_string((256 / W) * i) + ")";
     }
-    emit_steps(s, e, {"q0", "q1", "q2", "q3"});
+    o = "(first_output + " + lo + ")";
+    k = "(" + k0 + " + " + lk + ")";
   };
-  s << "  float acc;\n";
-  if (quads) {
-    s << "  {\n";
-    quad("0LL");
-    s << "    acc = " << ref(e.outputs[0], "q0") << ";\n";
-    for (int j = 1; j < 4; ++j) s << "    acc = " << combine("acc", ref(e.outputs[0], "q" + std::to_string(j))) << ";\n";
-    s << "  }\n";
-    s << "  #pragma unroll 2\n";
-    s << "  for (long long k4 = 4; k4 < " << ll(extent) << "; k4 += 4) {\n";
-    quad("k4");
-    for (int j = 0; j < 4; ++j) s << "    acc = " << combine("acc", ref(e.outputs[0], "q" + std::to_string(j))) << ";\n";
-    s << "  }\n";
-  } else {
-    // The first term seeds; then blocks of eight whose loads all issue
-    // before the eight ordered additions.
-    s << "  {\n    const long long k = 0;\n";
-    element("k", "x");
-    s << "    acc = " << ref(e.outputs[0], "x") << ";\n  }\n";
-    s << "  long long k8 = 1;\n  float r0, r1, r2, r3, r4, r5, r6, r7;\n";
-    s << "  for (; k8 + 8 <= " << ll(extent) << "; k8 += 8) {\n";
-    for (int j = 0; j < 8; ++j) {
-      s << "    {\n      const long long k = k8 + " << j << ";\n";
-      element("k", "u" + std::to_string(j));
-      s << "      r" << j << " = " << ref(e.outputs[0], "u" + std::to_string(j)) << ";\n    }\n";
+  auto load = [&](const std::string &k0, const std::string &prefix) {
+    for (int i = 0; i < 16; ++i) {
+      std::string o, lo, k, lk;
+      coords(i, k0, o, lo, k, lk);
+      point(o, k, prefix + std::to_string(i));
     }
-    for (int j = 0; j < 8; ++j) s << "    acc = " << combine("acc", "r" + std::to_string(j)) << ";\n";
-    s << "  }\n";
-    s << "  for (long long k = k8; k < " << ll(extent) << "; ++k) {\n";
-    element("k", "x");
-    s << "    acc = " << combine("acc", ref(e.outputs[0], "x")) << ";\n  }\n";
+  };
+  auto store = [&](const std::string &prefix) {
+    for (int i = 0; i < 16; ++i) {
+      std::string o, lo, k, lk;
+      coords(i, "0", o, lo, k, lk);
+      s << "    tile[" << lo << "][" << lk << "] = " << prefix << i << ";\n";
+    }
+  };
+  const std::string combine = kind == kFoldSum ? "acc + x" : "topos_faithful::max_f32(acc, x)";
+  s << "  float acc = 0.0f;\n";
+  s << "  {\n";
+  load("0LL", "v");
+  s << "    topos_lds_barrier();\n";
+  store("v");
+  s << "  }\n";
+  s << "  for (long long k0 = 0; k0 < " << ll(extent) << "; k0 += " << H << ") {\n";
+  s << "    topos_lds_barrier();\n";
+  s << "    {\n";
+  load("k0 + " + std::to_string(H), "w");  // the next tile, in flight during this fold
+  // Lanes j < W fold: on a full tile the LDS reads of each group of 64 issue
+  // before its ordered additions.
+  s << "    if (t < " << W << ") {\n";
+  s << "      const int steps = " << ll(extent) << " - k0 < " << H << " ? (int)(" << ll(extent) << " - k0) : " << H
+    << ";\n";
+  s << "      if (steps == " << H << ") {\n";
+  for (int g = 0; g < H / 64; ++g) {
+    s << "        {\n          float r[64];\n";
+    s << "          #pragma unroll\n          for (int j = 0; j < 64; ++j) r[j] = tile[t][" << 64 * g << " + j];\n";
+    if (g == 0)
+      s << "          if (k0 == 0) { acc = r[0]; } else { const float x = r[0]; acc = " << combine << "; }\n";
+    else
+      s << "          { const float x = r[0]; acc = " << combine << "; }\n";
+    s << "          #pragma unroll\n          for (int q = 1; q < 64; ++q) { const float x = r[q]; acc = " << combine
+      << "; }\n        }\n";
   }
-  s << "  out[o] = acc;\n}\n";
+  s << "      } else {\n";
+  s << "        int j = 0;\n";
+  s << "        if (k0 == 0) { acc = tile[t][0]; j = 1; }\n";
+  s << "        for (; j < steps; ++j) { const float x = tile[t][j]; acc = " << combine << "; }\n";
+  s << "      }\n";
+  s << "    }\n";
+  s << "    topos_lds_barrier();\n";
+  store("w");
+  s << "    }\n";
+  s << "  }\n";
+  s << "  if (t < " << W << " && first_output + t < " << ll(outputs) << ") out[first_output + t] = acc;\n";
+  s << "}\n";
   return make(s.str());
 }
 
@@ -559,7 +559,8 @@ void launch_generated_fold(const Generated &g, const Expr &e, int axis, const vo
   std::vector<void *> arguments;
   for (auto &p : pointers) arguments.push_back(&p);
   arguments.push_back(&vector_ok);
-  const int64_t blocks = (outputs + 255) / 256;
+  const int64_t width = fold_width(outputs);
+  const int64_t blocks = (outputs + width - 1) / width;
   if (blocks > 0x7fffffff) throw Unsupported{"fold: too many outputs for one launch"};
   launch(g, (unsigned)blocks, arguments, stream);
 }
@@ -568,36 +569,24 @@ void launch_generated_fold(const Generated &g, const Expr &e, int axis, const vo
 
 namespace {
 
-// Emits the odometer walk over one chunk's flat range, calling `body` with
-// the value of the expression at the current element as `v`.
-void emit_chunk_walk(std::ostringstream &s, const Expr &e, const std::string &body) {
-  const int64_t volume = e.volume();
-  s << "  const long long chunk = (long long)blockIdx.x * 256 + threadIdx.x;\n";
-  s << "  const long long first = chunk * " << ll(kSumChunk) << ";\n";
-  s << "  if (first >= " << ll(volume) << ") return;\n";
-  s << "  const long long count = " << ll(volume) << " - first < " << ll(kSumChunk) << " ? " << ll(volume)
-    << " - first : " << ll(kSumChunk) << ";\n";
-  std::vector<std::string> start;
-  emit_coordinates(s, e.rank, e.shape, "first", "f", start);
-  std::vector<std::string> c(e.rank);
-  for (int d = 0; d < e.rank; ++d) {
-    c[d] = "c" + std::to_string(d);
-    s << "  long long " << c[d] << " = " << start[d] << ";\n";
-  }
-  s << "  for (long long i = 0; i < count; ++i) {\n";
+// Emits the evaluation of the expression at flat element `f` (logical
+// row-major order) into `v`, guarded by f < volume.
+void emit_flat_value(std::ostringstream &s, const Expr &e, const std::string &f, const std::string &tag) {
+  s << "      float v = 0.0f;\n";
+  s << "      const bool live = " << f << " < " << ll(e.volume()) << ";\n";
+  s << "      if (live) {\n";
+  std::vector<std::string> c;
+  if (e.rank > 0) emit_coordinates(s, e.rank, e.shape, f, tag, c);
   for (size_t i = 0; i < e.inputs.size(); ++i)
-    s << "      const float in" << i << "_x = " << scalar_value(e, (int)i, c) << ";\n";
-  emit_steps(s, e, {"x"});
-  s << "    const float v = " << ref(e.outputs[0], "x") << ";\n";
-  s << body;
-  // Advance the odometer.
-  if (e.rank > 0) {
-    s << "    ++" << c[e.rank - 1] << ";\n";
-    for (int d = e.rank - 1; d > 0; --d)
-      s << "    if (" << c[d] << " == " << ll(e.shape[d]) << ") { " << c[d] << " = 0; ++" << c[d - 1] << "; }\n";
-  }
-  s << "  }\n";
+    s << "      const float in" << i << "_" << tag << " = " << scalar_value(e, (int)i, c) << ";\n";
+  emit_steps(s, e, {tag});
+  s << "      v = " << ref(e.outputs[0], tag) << ";\n      }\n";
 }
+
+// A chunk is kSumChunk consecutive elements, kSumChunk / 256 rounds of 256
+// consecutive elements, one per lane in order: wave 0 holds the first 64 of
+// a round, wave 1 the next 64, ...
+constexpr int kRounds = (int)(kSumChunk / 256);
 
 }  // namespace
 
@@ -606,10 +595,23 @@ Generated generate_sum_count(const Expr &e) {
   std::ostringstream s;
   s << preamble();
   s << signature(e, "int* __restrict__ counts, int* __restrict__ positive_zero") << " {\n";
+  s << "  __shared__ int wave_counts[4];\n  __shared__ int wave_plus[4];\n";
+  s << "  const long long chunk = blockIdx.x;\n";
   s << "  int nonzero = 0, plus_zero = 0;\n";
-  // A term is "zero" only when it compares equal to zero; NaN counts as a term.
-  emit_chunk_walk(s, e, "    if (v == 0.0f) { if (!__builtin_signbit(v)) plus_zero = 1; } else { ++nonzero; }\n");
-  s << "  counts[chunk] = nonzero;\n  positive_zero[chunk] = plus_zero;\n}\n";
+  s << "  for (int round = 0; round < " << kRounds << "; ++round) {\n";
+  s << "    const long long f = chunk * " << ll(kSumChunk) << " + round * 256 + threadIdx.x;\n    {\n";
+  emit_flat_value(s, e, "f", "x");
+  // A term is zero only when it compares equal to zero; NaN counts as a term.
+  s << "      if (live) { if (v == 0.0f) { if (!__builtin_signbit(v)) plus_zero = 1; } else { ++nonzero; } }\n";
+  s << "    }\n  }\n";
+  // Lane totals -> the chunk's count (integers: any order is exact).
+  s << "  for (int off = 32; off >= 1; off >>= 1) { nonzero += __shfl_xor(nonzero, off, 64); "
+       "plus_zero |= __shfl_xor(plus_zero, off, 64); }\n";
+  s << "  if ((threadIdx.x & 63) == 0) { wave_counts[threadIdx.x >> 6] = nonzero; wave_plus[threadIdx.x >> 6] = plus_zero; }\n";
+  s << "  __syncthreads();\n";
+  s << "  if (threadIdx.x == 0) {\n";
+  s << "    counts[chunk] = wave_counts[0] + wave_counts[1] + wave_counts[2] + wave_counts[3];\n";
+  s << "    positive_zero[chunk] = wave_plus[0] | wave_plus[1] | wave_plus[2] | wave_plus[3];\n  }\n}\n";
   return make(s.str());
 }
 
@@ -618,12 +620,24 @@ Generated generate_sum_compact(const Expr &e) {
   std::ostringstream s;
   s << preamble();
   s << signature(e, "const long long* __restrict__ offsets, float* __restrict__ compacted") << " {\n";
-  s << "  long long at = 0;\n";
-  s << "  float* __restrict__ dst = nullptr;\n";
-  s << "  { const long long chunk0 = (long long)blockIdx.x * 256 + threadIdx.x;\n";
-  s << "    if (chunk0 * " << ll(kSumChunk) << " < " << ll(e.volume()) << ") dst = compacted + offsets[chunk0]; }\n";
-  emit_chunk_walk(s, e, "    if (!(v == 0.0f)) dst[at++] = v;\n");
-  s << "}\n";
+  s << "  __shared__ int wave_counts[4];\n";
+  s << "  const long long chunk = blockIdx.x;\n";
+  s << "  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;\n";
+  s << "  long long at = offsets[chunk];\n";
+  s << "  for (int round = 0; round < " << kRounds << "; ++round) {\n";
+  s << "    const long long f = chunk * " << ll(kSumChunk) << " + round * 256 + threadIdx.x;\n    {\n";
+  emit_flat_value(s, e, "f", "x");
+  s << "      const bool keep = live && !(v == 0.0f);\n";
+  s << "      const unsigned long long mask = __ballot(keep);\n";
+  s << "      const int before = __popcll(mask & ((1ull << lane) - 1ull));\n";
+  s << "      if (lane == 0) wave_counts[wave] = __popcll(mask);\n";
+  s << "      __syncthreads();\n";
+  s << "      int offset = 0;\n";
+  s << "      for (int w = 0; w < wave; ++w) offset += wave_counts[w];\n";
+  s << "      if (keep) compacted[at + offset + before] = v;\n";
+  s << "      at += wave_counts[0] + wave_counts[1] + wave_counts[2] + wave_counts[3];\n";
+  s << "      __syncthreads();\n";
+  s << "    }\n  }\n}\n";
   return make(s.str());
 }
 
@@ -635,7 +649,7 @@ void launch_sum_count(const Generated &g, const Expr &e, const void *const *inpu
   pointers.push_back(positive_zero);
   std::vector<void *> arguments;
   for (auto &p : pointers) arguments.push_back(&p);
-  launch(g, (unsigned)((chunks + 255) / 256), arguments, stream);
+  launch(g, (unsigned)chunks, arguments, stream);
 }
 
 void launch_sum_compact(const Generated &g, const Expr &e, const void *const *inputs, const int64_t *offsets,
@@ -646,7 +660,7 @@ void launch_sum_compact(const Generated &g, const Expr &e, const void *const *in
   pointers.push_back(compacted);
   std::vector<void *> arguments;
   for (auto &p : pointers) arguments.push_back(&p);
-  launch(g, (unsigned)((chunks + 255) / 256), arguments, stream);
+  launch(g, (unsigned)chunks, arguments, stream);
 }
 
 }  // namespace topos_hip

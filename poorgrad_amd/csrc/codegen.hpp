@@ -95,9 +95,10 @@ void launch_generated_fold(const Generated &g, const Expr &e, int axis, const vo
                            float *out, hipStream_t stream);
 
 // Whole-tensor exact sum over a large operand, in chunks of kSumChunk flat
-// elements: pass one counts each chunk's nonzero terms (and whether the
-// chunk holds a +0), pass two writes them compacted in order.
-constexpr int64_t kSumChunk = 1024;
+// elements (one workgroup each, lanes on consecutive elements): pass one
+// counts each chunk's nonzero terms (and whether the chunk holds a +0), pass
+// two writes them compacted in element order.
+constexpr int64_t kSumChunk = 4096;
 Generated generate_sum_count(const Expr &e);
 Generated generate_sum_compact(const Expr &e);
 void launch_sum_count(const Generated &g, const Expr &e, const void *const *inputs, int32_t *counts,

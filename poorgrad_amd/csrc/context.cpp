@@ -112,6 +112,22 @@ void Context::tick(const char *what) {
   if (left == 0) throw RuntimeFailure{std::string("fake runtime failure injected at ") + what};
 }
 
+float *Context::workspace(int64_t floats) {
+  std::lock_guard<std::mutex> guard(workspace_lock_);
+  if (floats <= workspace_floats_) return workspace_;
+  if (workspace_) {
+    check(hipDeviceSynchronize(), "hipDeviceSynchronize(workspace)");
+    runtime_.free(workspace_);
+    workspace_ = nullptr;
+    workspace_floats_ = 0;
+  }
+  void *p = nullptr;
+  check(runtime_.malloc(&p, (size_t)floats * sizeof(float)), "hipMalloc(workspace)");
+  workspace_ = static_cast<float *>(p);
+  workspace_floats_ = floats;
+  return workspace_;
+}
+
 void check(hipError_t status, const char *what) {
   if (status != hipSuccess)
     throw RuntimeFailure{std::string(what) + " failed: " + hipGetErrorString(status)};

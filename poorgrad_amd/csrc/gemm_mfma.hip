@@ -3,7 +3,8 @@
 // Envelope fidelity: the k-sum is blocked and reassociated by the matrix core,
 // so results are compared against the exact product within
 // |c - exact| <= 1e-5 * sum_k |a_ik * b_kj| (and are deterministic: the same
-// inputs give the same bits on every run, since no atomics or split-k exist).
+// inputs give the same bits on every run: no atomics, and a split along k is
+// reduced in a fixed order).
 //
 // Shape: 128x128 output tile per 256-lane workgroup (four waves in 2x2, each
 // wave a 64x64 tile = 2x2 MFMA blocks of 32x32), k staged 16 deep through LDS,
@@ -14,6 +15,8 @@
 // m-contiguous, G B^T with B k-contiguous; src/function/matmul.rs:76-91) are
 // served by the same kernel through the operand-orientation template flags, so
 // no transpose is ever materialised.
+#include <algorithm>
+
 #include "backend.hpp"
 
 namespace topos_hip {
@@ -105,12 +108,17 @@ template <bool kLeftInnerK, bool kRightInnerK, bool kVector>
 __global__ __launch_bounds__(kThreads) void gemm_mfma_kernel(
     const float *__restrict__ a, int64_t a_rs, int64_t a_cs, const float *__restrict__ b,
     int64_t b_rs, int64_t b_cs, int64_t m, int64_t k, int64_t n, float *__restrict__ c, int64_t ldc,
-    int grid_m, int grid_n, int64_t a_bs, int64_t b_bs, int64_t c_bs) {
+    int grid_m, int grid_n, int64_t a_bs, int64_t b_bs, int64_t c_bs, int64_t split_len, int64_t split_stride) {
   __shared__ float left[2][kTileK][kTileM + kPad];
   __shared__ float right[2][kTileK][kTileN + kPad];
   a += (int64_t)blockIdx.y * a_bs;
   b += (int64_t)blockIdx.y * b_bs;
   c += (int64_t)blockIdx.y * c_bs;
+  // Split k: this workgroup sums k in [k_begin, k_end) into its own partial
+  // product (the fixed-order reduction adds the partials afterwards).
+  const int64_t k_begin = (int64_t)blockIdx.z * split_len;
+  const int64_t k_end = min(k, k_begin + split_len);
+  c += (int64_t)blockIdx.z * split_stride;
 
   // Workgroups are dealt to the eight XCDs round-robin; renumber so each XCD
   // receives a contiguous run of tiles, then walk tiles in groups of kGroupM
@@ -143,19 +151,19 @@ __global__ __launch_bounds__(kThreads) void gemm_mfma_kernel(
   // Left operand: outer = m (row stride a_rs), inner = k (a_cs).
   // Right operand: outer = n (b_cs), inner = k (b_rs).
   Slab sa, sb;
-  load_slab<kLeftInnerK, kVector>(sa, a, a_rs, a_cs, m, k, m0, 0);
-  load_slab<kRightInnerK, kVector>(sb, b, b_cs, b_rs, n, k, n0, 0);
+  load_slab<kLeftInnerK, kVector>(sa, a, a_rs, a_cs, m, k_end, m0, k_begin);
+  load_slab<kRightInnerK, kVector>(sb, b, b_cs, b_rs, n, k_end, n0, k_begin);
   store_slab<kLeftInnerK>(left[0], sa);
   store_slab<kRightInnerK>(right[0], sb);
   __syncthreads();
 
-  const int64_t slabs = (k + kTileK - 1) / kTileK;
+  const int64_t slabs = (k_end - k_begin + kTileK - 1) / kTileK;
   for (int64_t s = 0; s < slabs; ++s) {
     const int cur = (int)(s & 1);
     const bool more = s + 1 < slabs;
     if (more) {
-      load_slab<kLeftInnerK, kVector>(sa, a, a_rs, a_cs, m, k, m0, (s + 1) * kTileK);
-      load_slab<kRightInnerK, kVector>(sb, b, b_cs, b_rs, n, k, n0, (s + 1) * kTileK);
+      load_slab<kLeftInnerK, kVector>(sa, a, a_rs, a_cs, m, k_end, m0, k_begin + (s + 1) * kTileK);
+      load_slab<kRightInnerK, kVector>(sb, b, b_cs, b_rs, n, k_end, n0, k_begin + (s + 1) * kTileK);
     }
 #pragma unroll
     for (int kk = 0; kk < kTileK; kk += 2) {
@@ -195,20 +203,49 @@ __global__ __launch_bounds__(kThreads) void gemm_mfma_kernel(
 template <bool kL, bool kR>
 void dispatch_vector(bool vector, dim3 grid, hipStream_t stream, const float *a, int64_t a_rs,
                      int64_t a_cs, const float *b, int64_t b_rs, int64_t b_cs, int64_t m, int64_t k,
-                     int64_t n, float *c, int64_t ldc, int gm, int gn, const Batch &batch) {
+                     int64_t n, float *c, int64_t ldc, int gm, int gn, const Batch &batch, int64_t c_bs,
+                     int64_t split_len, int64_t split_stride) {
   if (vector)
     gemm_mfma_kernel<kL, kR, true><<<grid, kThreads, 0, stream>>>(a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, gm, gn,
-                                                                  batch.a_stride, batch.b_stride, batch.c_stride);
+                                                                  batch.a_stride, batch.b_stride, c_bs, split_len,
+                                                                  split_stride);
   else
     gemm_mfma_kernel<kL, kR, false><<<grid, kThreads, 0, stream>>>(a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, gm, gn,
-                                                                   batch.a_stride, batch.b_stride, batch.c_stride);
+                                                                   batch.a_stride, batch.b_stride, c_bs, split_len,
+                                                                   split_stride);
+}
+
+// The fixed-order sum of `splits` partial products (each [count][m][n],
+// contiguous) into c: partial 0 seeds, then 1, 2, ... are added in order, so
+// the result is the same on every run.
+__global__ __launch_bounds__(256) void split_reduce_kernel(const float *__restrict__ partials, int splits,
+                                                           int64_t split_stride, int64_t m, int64_t n,
+                                                           int64_t count, float *__restrict__ c, int64_t ldc,
+                                                           int64_t c_bs) {
+  const int64_t total = count * m * n;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (int64_t)gridDim.x * blockDim.x) {
+    float acc = partials[e];
+    for (int s = 1; s < splits; ++s) acc += partials[s * split_stride + e];
+    const int64_t q = e / (m * n), r = (e / n) % m, col = e % n;
+    c[q * c_bs + r * ldc + col] = acc;
+  }
 }
 
 }  // namespace
 
+int mfma_splits(int64_t m, int64_t n, int64_t k, int64_t batches) {
+  // Enough workgroups to fill the 256 CUs twice, each split at least 256 deep.
+  const int64_t tiles = ((m + kTileM - 1) / kTileM) * ((n + kTileN - 1) / kTileN) * batches;
+  if (tiles >= 512 || k < 1024) return 1;
+  int64_t splits = (512 + tiles - 1) / tiles;
+  splits = std::min<int64_t>(splits, k / 256);
+  splits = std::min<int64_t>(splits, 16);
+  return (int)std::max<int64_t>(splits, 1);
+}
+
 bool launch_gemm_mfma(const float *a, int64_t a_rs, int64_t a_cs, const float *b, int64_t b_rs,
                       int64_t b_cs, int64_t m, int64_t k, int64_t n, float *c, int64_t ldc,
-                      hipStream_t stream, const Batch &batch) {
+                      hipStream_t stream, const Batch &batch, float *workspace, int64_t workspace_floats) {
   // Orientation: each operand needs a unit stride along k or along its outer
   // axis; an extent-1 axis leaves its stride unused (any value serves).
   const bool left_inner_k = a_cs == 1 || m == 1;
@@ -230,16 +267,37 @@ bool launch_gemm_mfma(const float *a, int64_t a_rs, int64_t a_cs, const float *b
   const int64_t gm = (m + kTileM - 1) / kTileM;
   const int64_t gn = (n + kTileN - 1) / kTileN;
   if (gm * gn > 0x7fffffff || batch.count > 65535 || batch.count < 1) throw Unsupported{"mfma gemm: grid too large"};
-  const dim3 grid((unsigned)(gm * gn), (unsigned)batch.count);
+  int splits = mfma_splits(m, n, k, batch.count);
+  const int64_t split_stride = batch.count * m * n;
+  if (splits > 1 && (!workspace || workspace_floats < splits * split_stride)) splits = 1;
+  int64_t split_len = k;
+  if (splits > 1) {
+    split_len = ((k + splits - 1) / splits + kTileK - 1) / kTileK * kTileK;
+    splits = (int)((k + split_len - 1) / split_len);
+  }
+  const dim3 grid((unsigned)(gm * gn), (unsigned)batch.count, (unsigned)splits);
+  // With splits, each partial is written contiguous ([count][m][n]) into the
+  // workspace, then reduced into c.
+  float *target = splits > 1 ? workspace : c;
+  const int64_t target_ld = splits > 1 ? n : ldc;
+  const int64_t target_bs = splits > 1 ? m * n : batch.c_stride;
   if (lk && rk)
-    dispatch_vector<true, true>(vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, (int)gm, (int)gn, batch);
+    dispatch_vector<true, true>(vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, target, target_ld, (int)gm, (int)gn, batch, target_bs, split_len, split_stride);
   else if (lk)
-    dispatch_vector<true, false>(vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, (int)gm, (int)gn, batch);
+    dispatch_vector<true, false>(vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, target, target_ld, (int)gm, (int)gn, batch, target_bs, split_len, split_stride);
   else if (rk)
-    dispatch_vector<false, true>(vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, (int)gm, (int)gn, batch);
+    dispatch_vector<false, true>(vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, target, target_ld, (int)gm, (int)gn, batch, target_bs, split_len, split_stride);
   else
-    dispatch_vector<false, false>(vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, (int)gm, (int)gn, batch);
+    dispatch_vector<false, false>(vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, target, target_ld, (int)gm, (int)gn, batch, target_bs, split_len, split_stride);
   check_launch("gemm_mfma_kernel launch");
+  if (splits > 1) {
+    const int64_t total = split_stride;
+    int64_t blocks = (total + 255) / 256;
+    if (blocks > 256 * 32) blocks = 256 * 32;
+    split_reduce_kernel<<<(unsigned)blocks, 256, 0, stream>>>(workspace, splits, split_stride, m, n, batch.count, c,
+                                                              ldc, batch.c_stride);
+    check_launch("split_reduce_kernel launch");
+  }
   return true;
 }
 

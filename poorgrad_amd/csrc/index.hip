@@ -65,6 +65,7 @@ __global__ __launch_bounds__(1024) void scan_kernel(const int32_t *__restrict__ 
   const int64_t per = (chunks + 1023) / 1024;
   const int64_t begin = t * per, end = begin + per < chunks ? begin + per : chunks;
   int64_t mine = 0;
+#pragma unroll 8
   for (int64_t c = begin; c < end; ++c) mine += counts[c];
   totals[t] = mine;
   __syncthreads();
@@ -79,6 +80,7 @@ __global__ __launch_bounds__(1024) void scan_kernel(const int32_t *__restrict__ 
   }
   __syncthreads();
   int64_t running = totals[t];
+#pragma unroll 8
   for (int64_t c = begin; c < end; ++c) {
     offsets[c] = running;
     running += counts[c];

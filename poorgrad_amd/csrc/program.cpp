@@ -131,6 +131,7 @@ struct Storage {
   int first = INT_MAX;
   int last = -1;
   bool pinned = false;
+  bool side = false;  // written on the side stream: placed in the side region
   // selections
   int64_t rows = 0, vocab = 0;
   float one = 1.0f;
@@ -271,6 +272,9 @@ struct topos_hip_program {
     std::function<void(const Exec &)> run;
     std::string kind;
     double flops = 0, bytes = 0;
+    bool side = false;     // runs on the side stream
+    int wait_for = -1;     // side launch: the main launch whose completion it awaits
+    bool signals = false;  // main launch: records its event for side launches
   };
   std::vector<Launch> launches;
   std::vector<Generated> pending;  // generated kernels, compiled together after planning
@@ -289,8 +293,18 @@ struct topos_hip_program {
   std::map<int64_t, SelectionBuffers> selection_leaves;
   std::vector<void *> allocations;
 
+  // The side stream and the events that order it after the main stream.
+  hipStream_t side_stream = nullptr;
+  std::map<int, hipEvent_t> signal_events;
+  hipEvent_t side_start = nullptr, side_done = nullptr;
+  int64_t side_launches = 0;
+
   ~topos_hip_program() {
     if (!device) return;
+    for (auto &kv : signal_events) hipEventDestroy(kv.second);
+    if (side_done) hipEventDestroy(side_done);
+    if (side_start) hipEventDestroy(side_start);
+    if (side_stream) hipStreamDestroy(side_stream);
     for (void *p : allocations) hipFree(p);
     for (auto &kv : selection_inputs) {
       hipFree(kv.second.indices);
@@ -1053,19 +1067,34 @@ struct topos_hip_program {
     const int64_t ars = a.layout.strides[s], acs = a.layout.strides[s + 1];
     const int64_t brs = b.layout.strides[s], bcs = b.layout.strides[s + 1];
     const int numerics_ = numerics;
+    // Scratch for the partial products of a split along k (fast posture).
+    int64_t workspace_floats = 0;
+    int workspace = -1;
+    if (numerics == TOPOS_HIP_FAST) {
+      const int splits = mfma_splits(m, n, k, batch.count);
+      if (splits > 1) {
+        workspace_floats = (int64_t)splits * batch.count * m * n;
+        workspace = arena_storage(workspace_floats * 4);
+      }
+    }
     std::ostringstream what;
     what << "gemm " << (numerics == TOPOS_HIP_FAST ? "mfma" : "exact") << " " << batches << "x(" << m << "," << n
          << "," << k << ") a[" << ars << "," << acs << "] b[" << brs << "," << bcs << "]";
-    add_launch(what.str(), {a.storage, b.storage}, {out},
-               [this, a, b, out, parts, batch, m, n, k, ars, acs, brs, bcs, numerics_](const Exec &ex) {
+    std::vector<int> writes = {out};
+    if (workspace >= 0) writes.push_back(workspace);
+    add_launch(what.str(), {a.storage, b.storage}, writes,
+               [this, a, b, out, parts, batch, m, n, k, ars, acs, brs, bcs, numerics_, workspace,
+                workspace_floats](const Exec &ex) {
                  const float *pa = (const float *)base(a.storage);
                  const float *pb = (const float *)base(b.storage);
                  float *pc = (float *)base(out);
+                 float *pw = workspace >= 0 ? (float *)base(workspace) : nullptr;
                  for (const auto &part : parts) {
                    const float *qa = pa + part[0], *qb = pb + part[1];
                    float *qc = pc + part[2];
                    if (numerics_ == TOPOS_HIP_FAST &&
-                       launch_gemm_mfma(qa, ars, acs, qb, brs, bcs, m, k, n, qc, n, ex.stream, batch))
+                       launch_gemm_mfma(qa, ars, acs, qb, brs, bcs, m, k, n, qc, n, ex.stream, batch, pw,
+                                        workspace_floats))
                      continue;
                    launch_gemm_exact(qa, ars, acs, qb, brs, bcs, m, k, n, qc, n, ex.stream, batch);
                  }
@@ -1325,7 +1354,7 @@ struct topos_hip_program {
     std::vector<std::vector<int>> born(launches.size()), dies(launches.size());
     for (size_t s = 0; s < storages.size(); ++s) {
       Storage &st = storages[s];
-      if (st.kind != StorageKind::kArena || st.first == INT_MAX) continue;
+      if (st.kind != StorageKind::kArena || st.first == INT_MAX || st.side) continue;
       born[st.first].push_back((int)s);
       if (!st.pinned) dies[st.last].push_back((int)s);
     }
@@ -1375,6 +1404,15 @@ struct topos_hip_program {
         free_blocks[at] = size;
       }
     }
+    // The side region: storages the side stream writes never share memory
+    // with main-stream storages. A side launch waits only for its inputs, so
+    // it may run ahead of main launches that still use memory first-fit would
+    // otherwise have handed to its outputs.
+    for (Storage &st : storages)
+      if (st.kind == StorageKind::kArena && st.side && st.first != INT_MAX) {
+        st.offset = top;
+        top += round(st.bytes);
+      }
     arena_bytes = (uint64_t)std::max<int64_t>(top, 256);
   }
 
@@ -1382,8 +1420,52 @@ struct topos_hip_program {
     std::ostringstream s;
     s << "arena " << arena_bytes << " bytes, " << launches.size() << " launches, " << fused_groups
       << " generated kernels\n";
-    for (size_t l = 0; l < launches.size(); ++l) s << l << ": " << launches[l].what << "\n";
+    for (size_t l = 0; l < launches.size(); ++l)
+      s << l << ": " << launches[l].what << (launches[l].side ? " [side]" : "") << "\n";
     description = s.str();
+  }
+
+  // Short dead-end branches run on a side stream, overlapping the main
+  // chain: a launch whose downstream is at most kSideDepth launches, all of
+  // them side launches themselves (a parameter gradient's product or fold
+  // and the zero-seeded accumulation behind it). A side launch waits for the
+  // event of its latest main-stream producer; the run ends with the main
+  // stream waiting for the side stream. Every storage a side launch touches
+  // is kept to the end of the run, so no later main launch reuses its memory
+  // while the side stream may still use it.
+  void assign_streams() {
+    const size_t count = launches.size();
+    std::vector<int> producer(storages.size(), -1);
+    for (size_t l = 0; l < count; ++l)
+      for (int s : launches[l].writes) producer[s] = (int)l;
+    std::vector<std::vector<int>> readers(count);
+    for (size_t l = 0; l < count; ++l)
+      for (int s : launches[l].reads)
+        if (producer[s] >= 0 && producer[s] != (int)l) readers[producer[s]].push_back((int)l);
+    constexpr int kSideDepth = 4;
+    std::vector<int> downstream(count, 0);  // an over-count of the launches downstream
+    for (size_t q = count; q-- > 0;) {
+      bool side = true;
+      int below = 0;
+      for (int r : readers[q]) {
+        side = side && launches[r].side;
+        below += 1 + downstream[r];
+      }
+      downstream[q] = std::min(below, 1 << 20);
+      launches[q].side = side && below <= kSideDepth;
+    }
+    for (size_t l = 0; l < count; ++l) {
+      Launch &launch = launches[l];
+      if (!launch.side) continue;
+      ++side_launches;
+      for (int s : launch.reads) {
+        storages[s].pinned = true;
+        const int p = producer[s];
+        if (p >= 0 && !launches[p].side) launch.wait_for = std::max(launch.wait_for, p);
+      }
+      for (int s : launch.writes) storages[s].pinned = storages[s].side = true;
+      if (launch.wait_for >= 0) launches[launch.wait_for].signals = true;
+    }
   }
 
   void plan() {
@@ -1393,6 +1475,7 @@ struct topos_hip_program {
     for (int64_t i = 0; i < (int64_t)nodes.size(); ++i)
       if (wanted[i]) plan_node(i);
     finish_readables();
+    assign_streams();
     assign_arena();
     compile_kernels(pending, device);
     describe();
@@ -1466,7 +1549,39 @@ struct topos_hip_program {
     }
     const Exec ex{this, stream};
     if (!milliseconds) {
-      for (const Launch &l : launches) l.run(ex);
+      if (side_launches == 0) {
+        for (const Launch &l : launches) l.run(ex);
+        return;
+      }
+      if (!side_stream) {
+        check(hipStreamCreateWithFlags(&side_stream, hipStreamNonBlocking), "hipStreamCreate(side)");
+        check(hipEventCreateWithFlags(&side_done, hipEventDisableTiming), "hipEventCreate(side)");
+        check(hipEventCreateWithFlags(&side_start, hipEventDisableTiming), "hipEventCreate(side)");
+        for (size_t l = 0; l < launches.size(); ++l)
+          if (launches[l].signals) {
+            hipEvent_t e;
+            check(hipEventCreateWithFlags(&e, hipEventDisableTiming), "hipEventCreate(signal)");
+            signal_events[(int)l] = e;
+          }
+      }
+      // The side stream first waits for everything enqueued on the main
+      // stream before this run (the caller's writes to parameters and inputs).
+      check(hipEventRecord(side_start, stream), "hipEventRecord(start)");
+      check(hipStreamWaitEvent(side_stream, side_start, 0), "hipStreamWaitEvent(start)");
+      const Exec side_ex{this, side_stream};
+      for (size_t l = 0; l < launches.size(); ++l) {
+        const Launch &launch = launches[l];
+        if (launch.side) {
+          if (launch.wait_for >= 0)
+            check(hipStreamWaitEvent(side_stream, signal_events.at(launch.wait_for), 0), "hipStreamWaitEvent");
+          launch.run(side_ex);
+        } else {
+          launch.run(ex);
+          if (launch.signals) check(hipEventRecord(signal_events.at((int)l), stream), "hipEventRecord(signal)");
+        }
+      }
+      check(hipEventRecord(side_done, side_stream), "hipEventRecord(side done)");
+      check(hipStreamWaitEvent(stream, side_done, 0), "hipStreamWaitEvent(side done)");
       return;
     }
     std::vector<hipEvent_t> events(launches.size() + 1);

@@ -209,3 +209,54 @@ def test_adamw_steps_match_the_rule(hip):
         torch.cuda.synchronize()
         for i in range(2):
             assert_bitwise(device[i], params[i], f"adamw step {step} param {i}")
+
+
+def _adamw_reference(params, grads, state, f=np.float32):
+    """AdamW::step (src/neural/adam.rs:62-171) restated in numpy f32."""
+    b1, b2, eps, decay, lr = f(0.9), f(0.999), f(1e-8), f(0.01), f(3e-4)
+    state["p1"], state["p2"] = f(state["p1"] * b1), f(state["p2"] * b2)
+    c1, c2 = f(1) - state["p1"], f(1) - state["p2"]
+    out = []
+    for i, (p, g) in enumerate(zip(params, grads)):
+        m = state["m"][i] * b1 + g * (f(1) - b1)
+        v = state["v"][i] * b2 + (g * g) * (f(1) - b2)
+        state["m"][i], state["v"][i] = m, v
+        direction = (m / c1) / (np.sqrt(v / c2) + eps)
+        stepped = p - direction * lr
+        out.append(stepped - (p * decay) * lr if p.ndim >= 2 else stepped)
+    return out
+
+
+def test_small_gpt2_adamw_steps_exact(hip):
+    """Three train steps through the device program and the device AdamW,
+    against the interpreter and the AdamW rule: every parameter bit-identical
+    after every step. Exercises the side stream (parameter-gradient branches)
+    across runs, where a scheduling race would change bits."""
+    import torch
+
+    from poorgrad_amd.program import AdamW, DeviceProgram
+
+    banner("program gpt2 small three adamw steps")
+    w = workloads.gpt2(batch=2, context=16, vocab=37, width=32, heads=4, layers=2, positions=24)
+    program = DeviceProgram(w.tape, w.roots, numerics=hip.EXACT)
+    assert "[side]" in program.describe
+    device = [torch.from_numpy(a.copy()).cuda() for a in w.initial]
+    for slot, t_ in enumerate(device):
+        program.bind_parameter(slot, t_)
+    for slot, (indices, one) in w.selection_inputs.items():
+        program.bind_selection(slot, indices, one)
+    optimizer = AdamW(device)
+    host = [a.copy() for a in w.initial]
+    state = {"p1": np.float32(1), "p2": np.float32(1), "m": [np.zeros_like(a) for a in host],
+             "v": [np.zeros_like(a) for a in host]}
+    pointers = None
+    for step in range(3):
+        want = run_oracle(w.tape, w.roots, host, {}, w.selection_inputs)
+        program.run()
+        if pointers is None:
+            pointers = [program.pointer(g) for g in w.gradients]
+        optimizer.step(device, pointers, 3e-4)
+        torch.cuda.synchronize()
+        host = _adamw_reference(host, [want[g.id] for g in w.gradients], state)
+        for i, (d, h) in enumerate(zip(device, host)):
+            assert_bitwise(d, h, f"step {step} parameter {i}")
