@@ -51,6 +51,12 @@ CHAIN_BYTES = {  # each distinct input read once, each output written once, fp32
     "row_softmax": 4 * (2 * CHAIN_ROWS * CHAIN_COLUMNS),
 }
 ADAMW = {"rate": 3e-4, "beta1": 0.9, "beta2": 0.999, "epsilon": 1e-8, "decay": 0.01}
+# HBM bytes per product launch of the step, measured with rocprofv3 --pmc
+# FETCH_SIZE and WRITE_SIZE over one step's product launches, each counter
+# scaled by what it reads for a 256 MiB copy (x2.0 and x1.0): the summary
+# profiles/gpt2_train_step_traffic.md holds the commands and the figures. A
+# counter run cannot happen inside this process, so the figure is carried.
+MEASURED_PRODUCT_TRAFFIC_BYTES = 496.1 * 2**20
 
 
 def log(message: str) -> None:
@@ -65,6 +71,9 @@ def parse() -> argparse.Namespace:
     p.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU oracle leg")
     p.add_argument("--quick", action="store_true", help="the GPT-2 step only (no side sections)")
     p.add_argument("--profile-out", help="write the profiled step's launches (one line each) to this file")
+    p.add_argument("--calibration-copy-mib", type=int, default=0,
+                   help="copy this many MiB device-to-device once before the step (a known-size kernel for "
+                        "scaling hardware byte counters)")
     return p.parse_args()
 
 
@@ -169,7 +178,9 @@ def roofline(profile) -> dict:
     if dominant == "gemm":
         achieved = sum(p[2] for p in launches) / (ms / 1e3) / 1e12
         return {"bound": "mfma", "achieved": round(achieved, 3), "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4), "traffic": None,
+                "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4),
+                "traffic": round(MEASURED_PRODUCT_TRAFFIC_BYTES),
+                "algorithmic_bytes_per_launch": round(sum(p[3] for p in launches) / len(launches)),
                 "kernel": f"gemm_mfma_kernel: the step's {len(launches)} product launches, algorithmic 2*m*n*k "
                           f"over their event-timed duration", "ms_per_step": round(ms, 3)}
     achieved = sum(p[3] for p in launches) / (ms / 1e3) / 1e9
@@ -351,6 +362,12 @@ def main() -> int:
     if n.status() != n.OK:
         print(f"HIP backend unavailable: {n.status_reason()}", file=sys.stderr)
         return 1
+    if args.calibration_copy_mib:
+        count = args.calibration_copy_mib * (1 << 20) // 4
+        source = torch.ones(count, device="cuda")
+        torch.empty_like(source).copy_(source)
+        torch.cuda.synchronize()
+        del source
     g = gpt2_section(torch, n, args)
     ms_per_step = g["wall"] / args.steps * 1e3
     line = {

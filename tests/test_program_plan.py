@@ -1,0 +1,131 @@
+"""Planning device programs without a GPU: the fake runtime
+(topos_hip_fake_runtime, the Api::fake pattern of
+src/backend/cuda/kernels/context.rs:101-162) plans and compiles every
+generated kernel for gfx950 but runs nothing. Each scenario runs in a fresh
+interpreter (the runtime choice is process-wide)."""
+import subprocess
+import sys
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent.parent
+
+PREAMBLE = r'''
+import numpy as np
+from poorgrad_amd import _native as n
+assert n.lib.topos_hip_fake_runtime(1 << 30) == n.OK
+from poorgrad_amd import topos as t, workloads
+from poorgrad_amd.program import DeviceProgram
+'''
+
+
+def run(code: str) -> str:
+    result = subprocess.run([sys.executable, "-c", PREAMBLE + code], capture_output=True, text=True, cwd=ROOT,
+                            timeout=600)
+    assert result.returncode == 0, result.stderr[-3000:]
+    return result.stdout
+
+
+def test_an_elementwise_tree_is_one_generated_kernel():
+    out = run(r'''
+tape = t.Tape()
+x = tape.input((64, 32))
+b = tape.parameter((32,))
+y = ((-x).exp() + x.one_like())
+z = x / y + b.broadcast_along(0, x)
+p = DeviceProgram(tape, [z])
+print(p.info["launches"])
+print(p.describe)
+''')
+    lines = out.splitlines()
+    assert lines[0] == "1", out
+    assert "chain Add [64,32]" in out
+
+
+def test_a_reduction_absorbs_its_elementwise_operand():
+    out = run(r'''
+tape = t.Tape()
+x = tape.input((16, 48))
+s = (x * x + x).sum_along(1)
+p = DeviceProgram(tape, [s])
+print(p.info["launches"])
+print(p.describe)
+''')
+    assert out.splitlines()[0] == "1", out
+    assert "fold sum axis 1 [16,48] 1 inputs, 2 steps" in out
+
+
+def test_views_launch_nothing():
+    out = run(r'''
+tape = t.Tape()
+a = tape.parameter((8, 6))
+v = a.transpose().narrow(0, 1, 4).reshape((4, 1, 8)).permute((2, 0, 1))   # a unit-axis reshape: a view
+s = v.sum_along(0)
+p = DeviceProgram(tape, [s])
+print(p.info["launches"])
+w = a.transpose().narrow(0, 1, 4).reshape((2, 2, 8)).sum_along(0)         # not a view: copied first
+q = DeviceProgram(tape, [w])
+print(q.info["launches"])
+''')
+    assert out.splitlines()[:2] == ["1", "2"], out
+
+
+def test_mlp_step_plans_with_side_branches_and_an_arena():
+    out = run(r'''
+w = workloads.mlp()
+for numerics in (n.EXACT, n.FAST):
+    p = DeviceProgram(w.tape, w.roots, numerics=numerics)
+    info = p.info
+    print(info["arena_bytes"] > 0, info["launches"], p.describe.count("[side]"))
+''')
+    for line in out.splitlines():
+        ok, launches, side = line.split()
+        assert ok == "True" and int(launches) > 10 and int(side) > 0, out
+
+
+def test_unserved_variants_are_refused_with_a_reason():
+    out = run(r'''
+import ctypes
+tape = t.Tape()
+x = tape.input((6,))
+tape._record(t.UNFOLD, [x.id], (2, 3), params=(0, 3, 3, 1))
+table = tape.program([t.Value(tape, 1)])
+try:
+    table.create(n.EXACT)
+except n.HipError as e:
+    print(e.code, n.lib.topos_hip_last_refusal().decode())
+''')
+    code, _, reason = out.strip().partition(" ")
+    assert int(code) == 7 and "Unfold" in reason, out  # TOPOS_HIP_UNSUPPORTED
+
+
+def test_malformed_tables_are_invalid_arguments():
+    out = run(r'''
+tape = t.Tape()
+x = tape.input((4, 4))
+y = x + x
+table = tape.program([y])
+table.nodes[1].operands[0] = 5   # a forward reference
+try:
+    table.create(n.EXACT)
+except n.HipError as e:
+    print(e.code)
+tape = t.Tape()
+s = tape.leaf(t.Selection(np.array([0, 9], np.int32), 4))   # index out of vocabulary
+table = tape.program([s])
+try:
+    table.create(n.EXACT)
+except n.HipError as e:
+    print(e.code)
+''')
+    assert out.split() == ["5", "5"], out  # TOPOS_HIP_INVALID_ARGUMENT
+
+
+def test_the_gpt2_graph_plans():
+    out = run(r'''
+w = workloads.gpt2(batch=2, context=16, vocab=37, width=32, heads=4, layers=2, positions=24)
+p = DeviceProgram(w.tape, w.roots, numerics=n.FAST)
+d = p.describe
+print(p.info["launches"], d.count("gemm mfma"), d.count("[side]"), d.count("log_softmax"))
+''')
+    launches, gemms, side, softmax = map(int, out.split())
+    assert launches > 100 and gemms > 20 and side > 10 and softmax == 2, out
