@@ -6,11 +6,18 @@
 // inputs give the same bits on every run: no atomics, and a split along k is
 // reduced in a fixed order).
 //
-// Shape: 128x128 output tile per 256-lane workgroup (four waves in 2x2, each
-// wave a 64x64 tile = 2x2 MFMA blocks of 32x32), k staged 16 deep through LDS,
-// double-buffered: the next slab's global loads are in flight while the
-// current slab feeds the matrix cores. LDS holds both operands k-major
-// ([k][m], [k][n]) so an MFMA fragment is one conflict-free 32-lane b32 read.
+// Shape: a BM x BN output tile per workgroup of 64 * (BM / 64) * (BN / 64)
+// lanes, each wave owning a 64x64 block (2x2 MFMA blocks of 32x32). Tiles are
+// 128x128, or 128x64 / 64x128 when one output extent is at most 64 (the
+// attention products with a 64-wide head), so no half-empty tiles are
+// launched. k is staged 16 deep through LDS, double-buffered: the next slab's
+// global loads are in flight while the current slab feeds the matrix cores.
+// LDS holds both operands k-major ([k][outer]) so an MFMA fragment is one
+// 32-lane b32 read; rows are padded to 148 (128-wide) or 84 (64-wide) floats,
+// 20 mod 64 banks, which measured fastest for both the fragment reads and the
+// transposing stores of k-contiguous operands. A tile wholly inside the
+// operands takes a branch-free load path (one uniform test per slab); only
+// edge tiles pay per-element bounds checks.
 // The forward product and both transposed backward products (A^T G with A
 // m-contiguous, G B^T with B k-contiguous; src/function/matmul.rs:76-91) are
 // served by the same kernel through the operand-orientation template flags, so
@@ -24,93 +31,93 @@ namespace {
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
-constexpr int kTileM = 128;
-constexpr int kTileN = 128;
 constexpr int kTileK = 16;
-constexpr int kThreads = 256;
-constexpr int kPad = 4;
+constexpr int kPad = 20;
 constexpr int kGroupM = 8;
 
-// One operand slab in registers between its global load and its LDS store:
-// two 4-vectors per lane (kTile x 128 = 512 vectors over 256 lanes).
+// One operand slab (outer extent O, kTileK deep) between its global loads and
+// its LDS store as [k][O + kPad]. Element (o, kk) of the operand lives at
+// p[o * outer_stride + kk * k_stride]. kInnerK: k is the unit-stride axis
+// (lanes step along k), else the outer axis is. kVector: 16-byte loads are
+// legal (aligned, unit stride, partner stride % 4 == 0).
+template <int O, int T, bool kInnerK, bool kVector>
 struct Slab {
-  float4 v[2];
+  static constexpr int V = O * kTileK / 4 / T;  // 4-vectors per lane
+  float4 v[V];
+
+  // The slab starting at (o0, k0) when it lies wholly inside the operand.
+  __device__ inline void load_inside(const float *__restrict__ p, int64_t outer_stride, int64_t k_stride,
+                                     int64_t o0, int64_t k0) {
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int e = 0; e < V; ++e) {
+      const int x = t + T * e;
+      const int o = kInnerK ? x / (kTileK / 4) : (x % (O / 4)) * 4;
+      const int kk = kInnerK ? (x % (kTileK / 4)) * 4 : x / (O / 4);
+      const int64_t go = o0 + o, gk = k0 + kk;
+      if (kVector) {
+        v[e] = kInnerK ? *reinterpret_cast<const float4 *>(p + go * outer_stride + gk)
+                       : *reinterpret_cast<const float4 *>(p + gk * k_stride + go);
+      } else if (kInnerK) {
+        v[e] = make_float4(p[go * outer_stride + gk * k_stride], p[go * outer_stride + (gk + 1) * k_stride],
+                           p[go * outer_stride + (gk + 2) * k_stride], p[go * outer_stride + (gk + 3) * k_stride]);
+      } else {
+        v[e] = make_float4(p[go * outer_stride + gk * k_stride], p[(go + 1) * outer_stride + gk * k_stride],
+                           p[(go + 2) * outer_stride + gk * k_stride], p[(go + 3) * outer_stride + gk * k_stride]);
+      }
+    }
+  }
+
+  // Any slab: elements outside [0, outer_extent) x [.., k_end) read as zero.
+  __device__ inline void load_edge(const float *__restrict__ p, int64_t outer_stride, int64_t k_stride,
+                                   int64_t outer_extent, int64_t k_end, int64_t o0, int64_t k0) {
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int e = 0; e < V; ++e) {
+      const int x = t + T * e;
+      const int o = kInnerK ? x / (kTileK / 4) : (x % (O / 4)) * 4;
+      const int kk = kInnerK ? (x % (kTileK / 4)) * 4 : x / (O / 4);
+      const int64_t go = o0 + o, gk = k0 + kk;
+      float w[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        if (kInnerK)
+          w[q] = (go < outer_extent && gk + q < k_end) ? p[go * outer_stride + (gk + q) * k_stride] : 0.0f;
+        else
+          w[q] = (gk < k_end && go + q < outer_extent) ? p[(go + q) * outer_stride + gk * k_stride] : 0.0f;
+      }
+      v[e] = make_float4(w[0], w[1], w[2], w[3]);
+    }
+  }
+
+  __device__ inline void store(float (*lds)[O + kPad]) const {
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int e = 0; e < V; ++e) {
+      const int x = t + T * e;
+      if (kInnerK) {
+        const int o = x / (kTileK / 4), kk = (x % (kTileK / 4)) * 4;
+        lds[kk + 0][o] = v[e].x;
+        lds[kk + 1][o] = v[e].y;
+        lds[kk + 2][o] = v[e].z;
+        lds[kk + 3][o] = v[e].w;
+      } else {
+        const int o = (x % (O / 4)) * 4, kk = x / (O / 4);
+        *reinterpret_cast<float4 *>(&lds[kk][o]) = v[e];
+      }
+    }
+  }
 };
 
-// Global -> registers for a 128 (outer) x 16 (k) slab of an operand whose
-// element (o, kk) lives at p[o * outer_stride + kk * k_stride].
-// kInnerK: k is the unit-stride axis (lanes step along k), else the outer axis
-// is. kVector: 16-byte loads are legal (aligned, unit stride, stride % 4 == 0).
-template <bool kInnerK, bool kVector>
-__device__ inline void load_slab(Slab &slab, const float *__restrict__ p, int64_t outer_stride,
-                                 int64_t k_stride, int64_t outer_extent, int64_t k_extent,
-                                 int64_t o0, int64_t k0) {
-  const int t = threadIdx.x;
-#pragma unroll
-  for (int e = 0; e < 2; ++e) {
-    int o, kk;
-    if (kInnerK) {  // 128 rows x 4 vectors along k
-      o = t / 4 + 64 * e;
-      kk = (t % 4) * 4;
-    } else {  // 16 k-rows x 32 vectors along the outer axis
-      kk = t / 32 + 8 * e;
-      o = (t % 32) * 4;
-    }
-    const int64_t go = o0 + o, gk = k0 + kk;
-    float4 value;
-    if (kInnerK) {
-      if (kVector && go < outer_extent && gk + 3 < k_extent) {
-        value = *reinterpret_cast<const float4 *>(p + go * outer_stride + gk);
-      } else {
-        float w[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          w[q] = (go < outer_extent && gk + q < k_extent) ? p[go * outer_stride + (gk + q) * k_stride] : 0.0f;
-        value = make_float4(w[0], w[1], w[2], w[3]);
-      }
-    } else {
-      if (kVector && gk < k_extent && go + 3 < outer_extent) {
-        value = *reinterpret_cast<const float4 *>(p + gk * k_stride + go);
-      } else {
-        float w[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          w[q] = (gk < k_extent && go + q < outer_extent) ? p[(go + q) * outer_stride + gk * k_stride] : 0.0f;
-        value = make_float4(w[0], w[1], w[2], w[3]);
-      }
-    }
-    slab.v[e] = value;
-  }
-}
-
-// Registers -> LDS [k][outer], matching load_slab's lane mapping.
-template <bool kInnerK>
-__device__ inline void store_slab(float (*lds)[kTileM + kPad], const Slab &slab) {
-  const int t = threadIdx.x;
-#pragma unroll
-  for (int e = 0; e < 2; ++e) {
-    if (kInnerK) {
-      const int o = t / 4 + 64 * e;
-      const int kk = (t % 4) * 4;
-      lds[kk + 0][o] = slab.v[e].x;
-      lds[kk + 1][o] = slab.v[e].y;
-      lds[kk + 2][o] = slab.v[e].z;
-      lds[kk + 3][o] = slab.v[e].w;
-    } else {
-      const int kk = t / 32 + 8 * e;
-      const int o = (t % 32) * 4;
-      *reinterpret_cast<float4 *>(&lds[kk][o]) = slab.v[e];
-    }
-  }
-}
-
-template <bool kLeftInnerK, bool kRightInnerK, bool kVector>
-__global__ __launch_bounds__(kThreads) void gemm_mfma_kernel(
+template <int BM, int BN, bool kLeftInnerK, bool kRightInnerK, bool kVector>
+__global__ __launch_bounds__(BM * BN / 64) void gemm_mfma_kernel(
     const float *__restrict__ a, int64_t a_rs, int64_t a_cs, const float *__restrict__ b,
     int64_t b_rs, int64_t b_cs, int64_t m, int64_t k, int64_t n, float *__restrict__ c, int64_t ldc,
     int grid_m, int grid_n, int64_t a_bs, int64_t b_bs, int64_t c_bs, int64_t split_len, int64_t split_stride) {
-  __shared__ float left[2][kTileK][kTileM + kPad];
-  __shared__ float right[2][kTileK][kTileN + kPad];
+  constexpr int T = BM * BN / 64;  // one 64x64 block per wave
+  constexpr int WN = BN / 64;
+  __shared__ float left[2][kTileK][BM + kPad];
+  __shared__ float right[2][kTileK][BN + kPad];
   a += (int64_t)blockIdx.y * a_bs;
   b += (int64_t)blockIdx.y * b_bs;
   c += (int64_t)blockIdx.y * c_bs;
@@ -132,13 +139,14 @@ __global__ __launch_bounds__(kThreads) void gemm_mfma_kernel(
   const int group_rows = min(grid_m - first_m, kGroupM);
   const int tile_m = first_m + (pid % in_group) % group_rows;
   const int tile_n = (pid % in_group) / group_rows;
-  const int64_t m0 = (int64_t)tile_m * kTileM;
-  const int64_t n0 = (int64_t)tile_n * kTileN;
+  const int64_t m0 = (int64_t)tile_m * BM;
+  const int64_t n0 = (int64_t)tile_n * BN;
+  const bool interior = m0 + BM <= m && n0 + BN <= n;
 
   const int lane = threadIdx.x % 64;
   const int wave = threadIdx.x / 64;
-  const int wm = (wave / 2) * 64;  // wave's row offset inside the tile
-  const int wn = (wave % 2) * 64;  // wave's column offset
+  const int wm = (wave / WN) * 64;  // wave's row offset inside the tile
+  const int wn = (wave % WN) * 64;  // wave's column offset
 
   floatx16 acc[2][2];
 #pragma unroll
@@ -150,21 +158,30 @@ __global__ __launch_bounds__(kThreads) void gemm_mfma_kernel(
 
   // Left operand: outer = m (row stride a_rs), inner = k (a_cs).
   // Right operand: outer = n (b_cs), inner = k (b_rs).
-  Slab sa, sb;
-  load_slab<kLeftInnerK, kVector>(sa, a, a_rs, a_cs, m, k_end, m0, k_begin);
-  load_slab<kRightInnerK, kVector>(sb, b, b_cs, b_rs, n, k_end, n0, k_begin);
-  store_slab<kLeftInnerK>(left[0], sa);
-  store_slab<kRightInnerK>(right[0], sb);
+  Slab<BM, T, kLeftInnerK, kVector> sa;
+  Slab<BN, T, kRightInnerK, kVector> sb;
+  // Both operands' loads for one slab. `inside` (the slab lies wholly inside
+  // both operands) is uniform and kept the outermost branch: each path is one
+  // straight run of loads, all in flight together.
+  auto load = [&](int64_t k0) {
+    if (interior && k0 + kTileK <= k_end) {
+      sa.load_inside(a, a_rs, a_cs, m0, k0);
+      sb.load_inside(b, b_cs, b_rs, n0, k0);
+    } else {
+      sa.load_edge(a, a_rs, a_cs, m, k_end, m0, k0);
+      sb.load_edge(b, b_cs, b_rs, n, k_end, n0, k0);
+    }
+  };
+  load(k_begin);
+  sa.store(left[0]);
+  sb.store(right[0]);
   __syncthreads();
 
   const int64_t slabs = (k_end - k_begin + kTileK - 1) / kTileK;
   for (int64_t s = 0; s < slabs; ++s) {
     const int cur = (int)(s & 1);
     const bool more = s + 1 < slabs;
-    if (more) {
-      load_slab<kLeftInnerK, kVector>(sa, a, a_rs, a_cs, m, k_end, m0, k_begin + (s + 1) * kTileK);
-      load_slab<kRightInnerK, kVector>(sb, b, b_cs, b_rs, n, k_end, n0, k_begin + (s + 1) * kTileK);
-    }
+    if (more) load(k_begin + (s + 1) * kTileK);
 #pragma unroll
     for (int kk = 0; kk < kTileK; kk += 2) {
       const int kr = kk + lane / 32;
@@ -178,8 +195,8 @@ __global__ __launch_bounds__(kThreads) void gemm_mfma_kernel(
       acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b1, acc[1][1], 0, 0, 0);
     }
     if (more) {
-      store_slab<kLeftInnerK>(left[cur ^ 1], sa);
-      store_slab<kRightInnerK>(right[cur ^ 1], sb);
+      sa.store(left[cur ^ 1]);
+      sb.store(right[cur ^ 1]);
     }
     __syncthreads();
   }
@@ -200,19 +217,46 @@ __global__ __launch_bounds__(kThreads) void gemm_mfma_kernel(
     }
 }
 
-template <bool kL, bool kR>
+// The tile shape for an m x n product: 128x128, or a 64-wide side when that
+// output extent is at most 64.
+struct TileShape {
+  int bm, bn;
+};
+TileShape tile_shape(int64_t m, int64_t n) {
+  if (n <= 64 && m > 64) return {128, 64};
+  if (m <= 64 && n > 64) return {64, 128};
+  return {128, 128};
+}
+
+template <int BM, int BN, bool kL, bool kR>
 void dispatch_vector(bool vector, dim3 grid, hipStream_t stream, const float *a, int64_t a_rs,
                      int64_t a_cs, const float *b, int64_t b_rs, int64_t b_cs, int64_t m, int64_t k,
                      int64_t n, float *c, int64_t ldc, int gm, int gn, const Batch &batch, int64_t c_bs,
                      int64_t split_len, int64_t split_stride) {
+  constexpr int T = BM * BN / 64;
   if (vector)
-    gemm_mfma_kernel<kL, kR, true><<<grid, kThreads, 0, stream>>>(a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, gm, gn,
-                                                                  batch.a_stride, batch.b_stride, c_bs, split_len,
-                                                                  split_stride);
+    gemm_mfma_kernel<BM, BN, kL, kR, true><<<grid, T, 0, stream>>>(a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, gm,
+                                                                   gn, batch.a_stride, batch.b_stride, c_bs,
+                                                                   split_len, split_stride);
   else
-    gemm_mfma_kernel<kL, kR, false><<<grid, kThreads, 0, stream>>>(a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, gm, gn,
-                                                                   batch.a_stride, batch.b_stride, c_bs, split_len,
-                                                                   split_stride);
+    gemm_mfma_kernel<BM, BN, kL, kR, false><<<grid, T, 0, stream>>>(a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, gm,
+                                                                    gn, batch.a_stride, batch.b_stride, c_bs,
+                                                                    split_len, split_stride);
+}
+
+template <int BM, int BN>
+void dispatch_orientation(bool lk, bool rk, bool vector, dim3 grid, hipStream_t stream, const float *a,
+                          int64_t a_rs, int64_t a_cs, const float *b, int64_t b_rs, int64_t b_cs, int64_t m,
+                          int64_t k, int64_t n, float *c, int64_t ldc, int gm, int gn, const Batch &batch,
+                          int64_t c_bs, int64_t split_len, int64_t split_stride) {
+  if (lk && rk)
+    dispatch_vector<BM, BN, true, true>(vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, gm, gn, batch, c_bs, split_len, split_stride);
+  else if (lk)
+    dispatch_vector<BM, BN, true, false>(vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, gm, gn, batch, c_bs, split_len, split_stride);
+  else if (rk)
+    dispatch_vector<BM, BN, false, true>(vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, gm, gn, batch, c_bs, split_len, split_stride);
+  else
+    dispatch_vector<BM, BN, false, false>(vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, gm, gn, batch, c_bs, split_len, split_stride);
 }
 
 // The fixed-order sum of `splits` partial products (each [count][m][n],
@@ -234,11 +278,16 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float *__restri
 }  // namespace
 
 int mfma_splits(int64_t m, int64_t n, int64_t k, int64_t batches) {
-  // Enough workgroups to fill the 256 CUs twice, each split at least 256 deep.
-  const int64_t tiles = ((m + kTileM - 1) / kTileM) * ((n + kTileN - 1) / kTileN) * batches;
-  if (tiles >= 512 || k < 1024) return 1;
-  int64_t splits = (512 + tiles - 1) / tiles;
-  splits = std::min<int64_t>(splits, k / 256);
+  // Three workgroups per CU (the kernel's occupancy) is 768 over the 256 CUs;
+  // a product with fewer tiles is split along k until it reaches that, each
+  // split at least 256 deep, and deep products are split further (up to 2048
+  // workgroups while each split stays 512 deep): measured on MI355X, the
+  // partial products' extra traffic costs less than idle CUs.
+  const TileShape shape = tile_shape(m, n);
+  const int64_t tiles = ((m + shape.bm - 1) / shape.bm) * ((n + shape.bn - 1) / shape.bn) * batches;
+  if (tiles >= 768 || k < 512) return 1;
+  int64_t splits = std::min<int64_t>((768 + tiles - 1) / tiles, k / 256);
+  while (splits * 2 * tiles <= 2048 && k / (splits * 2) >= 512) splits *= 2;
   splits = std::min<int64_t>(splits, 16);
   return (int)std::max<int64_t>(splits, 1);
 }
@@ -264,8 +313,9 @@ bool launch_gemm_mfma(const float *a, int64_t a_rs, int64_t a_cs, const float *b
                       (batch.count == 1 || (batch.a_stride % 4 == 0 && batch.b_stride % 4 == 0)) &&
                       (right_lead % 4 == 0) && (lk ? a_cs == 1 : a_rs == 1) &&
                       (rk ? b_rs == 1 : b_cs == 1);
-  const int64_t gm = (m + kTileM - 1) / kTileM;
-  const int64_t gn = (n + kTileN - 1) / kTileN;
+  const TileShape shape = tile_shape(m, n);
+  const int64_t gm = (m + shape.bm - 1) / shape.bm;
+  const int64_t gn = (n + shape.bn - 1) / shape.bn;
   if (gm * gn > 0x7fffffff || batch.count > 65535 || batch.count < 1) throw Unsupported{"mfma gemm: grid too large"};
   int splits = mfma_splits(m, n, k, batch.count);
   const int64_t split_stride = batch.count * m * n;
@@ -281,14 +331,12 @@ bool launch_gemm_mfma(const float *a, int64_t a_rs, int64_t a_cs, const float *b
   float *target = splits > 1 ? workspace : c;
   const int64_t target_ld = splits > 1 ? n : ldc;
   const int64_t target_bs = splits > 1 ? m * n : batch.c_stride;
-  if (lk && rk)
-    dispatch_vector<true, true>(vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, target, target_ld, (int)gm, (int)gn, batch, target_bs, split_len, split_stride);
-  else if (lk)
-    dispatch_vector<true, false>(vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, target, target_ld, (int)gm, (int)gn, batch, target_bs, split_len, split_stride);
-  else if (rk)
-    dispatch_vector<false, true>(vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, target, target_ld, (int)gm, (int)gn, batch, target_bs, split_len, split_stride);
+  if (shape.bn == 64)
+    dispatch_orientation<128, 64>(lk, rk, vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, target, target_ld, (int)gm, (int)gn, batch, target_bs, split_len, split_stride);
+  else if (shape.bm == 64)
+    dispatch_orientation<64, 128>(lk, rk, vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, target, target_ld, (int)gm, (int)gn, batch, target_bs, split_len, split_stride);
   else
-    dispatch_vector<false, false>(vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, target, target_ld, (int)gm, (int)gn, batch, target_bs, split_len, split_stride);
+    dispatch_orientation<128, 128>(lk, rk, vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, target, target_ld, (int)gm, (int)gn, batch, target_bs, split_len, split_stride);
   check_launch("gemm_mfma_kernel launch");
   if (splits > 1) {
     const int64_t total = split_stride;
