@@ -30,6 +30,10 @@ namespace topos_hip {
 namespace {
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
+// Four consecutive floats at any 4-byte-aligned address: gfx950 serves
+// unaligned global_load_dwordx4, so operands with odd leading dimensions (the
+// 50257-wide vocabulary products) keep 16-byte loads.
+typedef float float4u __attribute__((ext_vector_type(4), aligned(4)));
 
 constexpr int kTileK = 16;
 constexpr int kPad = 20;
@@ -38,8 +42,8 @@ constexpr int kGroupM = 8;
 // One operand slab (outer extent O, kTileK deep) between its global loads and
 // its LDS store as [k][O + kPad]. Element (o, kk) of the operand lives at
 // p[o * outer_stride + kk * k_stride]. kInnerK: k is the unit-stride axis
-// (lanes step along k), else the outer axis is. kVector: 16-byte loads are
-// legal (aligned, unit stride, partner stride % 4 == 0).
+// (lanes step along k), else the outer axis is. kVector: the axis the lanes
+// step along has unit stride, so four neighbours are one 16-byte load.
 template <int O, int T, bool kInnerK, bool kVector>
 struct Slab {
   static constexpr int V = O * kTileK / 4 / T;  // 4-vectors per lane
@@ -56,8 +60,9 @@ struct Slab {
       const int kk = kInnerK ? (x % (kTileK / 4)) * 4 : x / (O / 4);
       const int64_t go = o0 + o, gk = k0 + kk;
       if (kVector) {
-        v[e] = kInnerK ? *reinterpret_cast<const float4 *>(p + go * outer_stride + gk)
-                       : *reinterpret_cast<const float4 *>(p + gk * k_stride + go);
+        const float4u u = kInnerK ? *reinterpret_cast<const float4u *>(p + go * outer_stride + gk)
+                                  : *reinterpret_cast<const float4u *>(p + gk * k_stride + go);
+        v[e] = make_float4(u.x, u.y, u.z, u.w);
       } else if (kInnerK) {
         v[e] = make_float4(p[go * outer_stride + gk * k_stride], p[go * outer_stride + (gk + 1) * k_stride],
                            p[go * outer_stride + (gk + 2) * k_stride], p[go * outer_stride + (gk + 3) * k_stride]);
@@ -304,15 +309,9 @@ bool launch_gemm_mfma(const float *a, int64_t a_rs, int64_t a_cs, const float *b
   if (!(left_inner_k || left_outer) || !(right_inner_k || right_outer)) return false;
   const bool lk = left_inner_k && !(a_rs == 1 && a_cs != 1);
   const bool rk = right_inner_k && !(b_cs == 1 && b_rs != 1);
-  // 16-byte loads need the unit-stride axis's partner stride to keep every
-  // vector aligned, and aligned base pointers.
-  const int64_t left_lead = lk ? a_rs : a_cs;
-  const int64_t right_lead = rk ? b_cs : b_rs;
-  const bool vector = (reinterpret_cast<uintptr_t>(a) % 16 == 0) &&
-                      (reinterpret_cast<uintptr_t>(b) % 16 == 0) && (left_lead % 4 == 0) &&
-                      (batch.count == 1 || (batch.a_stride % 4 == 0 && batch.b_stride % 4 == 0)) &&
-                      (right_lead % 4 == 0) && (lk ? a_cs == 1 : a_rs == 1) &&
-                      (rk ? b_rs == 1 : b_cs == 1);
+  // 16-byte loads need a unit stride along the axis the lanes step on (any
+  // 4-byte alignment serves).
+  const bool vector = (lk ? a_cs == 1 : a_rs == 1) && (rk ? b_rs == 1 : b_cs == 1);
   const TileShape shape = tile_shape(m, n);
   const int64_t gm = (m + shape.bm - 1) / shape.bm;
   const int64_t gn = (n + shape.bn - 1) / shape.bn;
