@@ -245,6 +245,65 @@ bool pointers_aligned(const Expr &e, const void *const *inputs) {
   return true;
 }
 
+// Emits in<i>_<lanes[j]> (j < 4): the expression inputs at the four points of
+// a quad (coordinates `c`, the innermost coordinate c[inner] the quad's first,
+// a multiple of four in an innermost extent that is one). Unit-stride inputs
+// take one 16-byte load when `vector_ok` holds at run time.
+void emit_quad_inputs(std::ostringstream &s, const Expr &e, const std::vector<std::string> &c,
+                      const std::string &tag, const std::vector<std::string> &lanes, const std::string &indent) {
+  const int inner = e.rank - 1;
+  for (size_t i = 0; i < e.inputs.size(); ++i) {
+    const ExprInput &in = e.inputs[i];
+    const std::string p = "p" + std::to_string(i);
+    auto v = [&](int j) { return ref(-(int)i - 1, lanes[j]); };
+    if (in.kind == ExprInput::kLiteral) {
+      for (int j = 0; j < 4; ++j) s << indent << "const float " << v(j) << " = " << float_literal(in.one) << ";\n";
+      continue;
+    }
+    if (in.kind == ExprInput::kSelection) {
+      const std::string sel = "sel" + std::to_string(i) + "_" + tag;
+      s << indent << "const int " << sel << " = " << p << "[" << c[0] << "];\n";
+      for (int j = 0; j < 4; ++j)
+        s << indent << "const float " << v(j) << " = (" << sel << " == (int)(" << c[1] << " + " << j << ")) ? "
+          << float_literal(in.one) << " : 0.0f;\n";
+      continue;
+    }
+    const bool padded = in.kind == ExprInput::kPadded;
+    const bool inner_window = padded && in.pad_axis == inner;
+    // A window test that holds for the whole quad: on an outer axis, or an
+    // inner window whose bounds are multiples of four.
+    const bool quad_window = padded && (!inner_window || (in.pad_start % 4 == 0 && in.pad_len % 4 == 0));
+    const std::string a = "a" + std::to_string(i) + "_" + tag;
+    s << indent << "const long long " << a << " = " << address(e, in, c) << ";\n";
+    if (!padded || quad_window) {
+      const std::string inside = padded ? window_test(in, c[in.pad_axis]) : "true";
+      s << indent << "float " << v(0) << " = 0.0f, " << v(1) << " = 0.0f, " << v(2) << " = 0.0f, " << v(3)
+        << " = 0.0f;\n";
+      s << indent << "if (" << inside << ") {\n";
+      if (in.strides[inner] == 0) {
+        s << indent << "  " << v(0) << " = " << p << "[" << a << "]; " << v(1) << " = " << v(0) << "; " << v(2)
+          << " = " << v(0) << "; " << v(3) << " = " << v(0) << ";\n";
+      } else if (vector_input(e, in)) {
+        s << indent << "  if (vector_ok) { const float4 w = *(const float4*)(" << p << " + " << a << "); " << v(0)
+          << " = w.x; " << v(1) << " = w.y; " << v(2) << " = w.z; " << v(3) << " = w.w; }\n";
+        s << indent << "  else { ";
+        for (int j = 0; j < 4; ++j) s << v(j) << " = " << p << "[" << a << " + " << j << "]; ";
+        s << "}\n";
+      } else {
+        for (int j = 0; j < 4; ++j)
+          s << indent << "  " << v(j) << " = " << p << "[" << a << " + " << ll(j * in.strides[inner]) << "];\n";
+      }
+      s << indent << "}\n";
+    } else {
+      for (int j = 0; j < 4; ++j) {
+        const std::string cj = "(" + c[inner] + " + " + std::to_string(j) + ")";
+        s << indent << "const float " << v(j) << " = " << window_test(in, cj) << " ? " << p << "[" << a << " + "
+          << ll(j * in.strides[inner]) << "] : 0.0f;\n";
+      }
+    }
+  }
+}
+
 void launch(const Generated &g, unsigned blocks, std::vector<void *> &arguments, hipStream_t stream) {
   if (!g || !g->loaded) throw RuntimeFailure{"generated kernel was not loaded"};
   check(hipModuleLaunchKernel(g->function, blocks, 1, 1, 256, 1, 1, 0, stream, arguments.data(), nullptr),
@@ -327,57 +386,10 @@ Generated generate_chain(const Expr &e) {
   const bool quads = e.rank > 0 && e.shape[e.rank - 1] % 4 == 0;
   const std::vector<std::string> lanes = {"0", "1", "2", "3"};
   if (quads) {
-    const int inner = e.rank - 1;
     s << "    {\n";
     std::vector<std::string> c;
     emit_coordinates(s, e.rank, e.shape, "base", "q", c);
-    for (size_t i = 0; i < e.inputs.size(); ++i) {
-      const ExprInput &in = e.inputs[i];
-      const std::string p = "p" + std::to_string(i), v = "in" + std::to_string(i) + "_";
-      if (in.kind == ExprInput::kLiteral) {
-        for (int j = 0; j < 4; ++j) s << "      const float " << v << j << " = " << float_literal(in.one) << ";\n";
-        continue;
-      }
-      if (in.kind == ExprInput::kSelection) {
-        s << "      const int sel" << i << " = " << p << "[" << c[0] << "];\n";
-        for (int j = 0; j < 4; ++j)
-          s << "      const float " << v << j << " = (sel" << i << " == (int)(" << c[1] << " + " << j << ")) ? "
-            << float_literal(in.one) << " : 0.0f;\n";
-        continue;
-      }
-      const bool padded = in.kind == ExprInput::kPadded;
-      const bool inner_window = padded && in.pad_axis == inner;
-      // A window test that holds for the whole quad: on an outer axis, or an
-      // inner window whose bounds are multiples of four.
-      const bool quad_window = padded && (!inner_window || (in.pad_start % 4 == 0 && in.pad_len % 4 == 0));
-      const std::string a = "a" + std::to_string(i);
-      s << "      const long long " << a << " = " << address(e, in, c) << ";\n";
-      if (!padded || quad_window) {
-        const std::string inside = padded ? window_test(in, c[in.pad_axis]) : "true";
-        s << "      float " << v << "0 = 0.0f, " << v << "1 = 0.0f, " << v << "2 = 0.0f, " << v << "3 = 0.0f;\n";
-        s << "      if (" << inside << ") {\n";
-        if (in.strides[inner] == 0) {
-          s << "        " << v << "0 = " << p << "[" << a << "]; " << v << "1 = " << v << "0; " << v << "2 = " << v
-            << "0; " << v << "3 = " << v << "0;\n";
-        } else if (vector_input(e, in)) {
-          s << "        if (vector_ok) { const float4 w = *(const float4*)(" << p << " + " << a << "); " << v
-            << "0 = w.x; " << v << "1 = w.y; " << v << "2 = w.z; " << v << "3 = w.w; }\n";
-          s << "        else { ";
-          for (int j = 0; j < 4; ++j) s << v << j << " = " << p << "[" << a << " + " << j << "]; ";
-          s << "}\n";
-        } else {
-          for (int j = 0; j < 4; ++j)
-            s << "        " << v << j << " = " << p << "[" << a << " + " << ll(j * in.strides[inner]) << "];\n";
-        }
-        s << "      }\n";
-      } else {
-        for (int j = 0; j < 4; ++j) {
-          const std::string cj = "(" + c[inner] + " + " + std::to_string(j) + ")";
-          s << "      const float " << v << j << " = " << window_test(in, cj) << " ? " << p << "[" << a << " + "
-            << ll(j * in.strides[inner]) << "] : 0.0f;\n";
-        }
-      }
-    }
+    emit_quad_inputs(s, e, c, "q", lanes, "      ");
     emit_steps(s, e, lanes);
     for (size_t o = 0; o < e.outputs.size(); ++o) {
       s << "      if (vector_ok) *(float4*)(q" << o << " + base) = make_float4(";
@@ -429,6 +441,108 @@ int64_t fold_width(int64_t outputs) { return outputs / 64 >= 256 ? 64 : 16; }
 
 }  // namespace
 
+namespace {
+
+// Column form with a quad-divisible innermost extent and 16 outputs per
+// workgroup: each lane evaluates the expression on quads (four consecutive
+// outputs at one step, one 16-byte load per unit-stride input) and parks
+// them transposed in LDS as tile[output][step], so lane j < 16 folds output
+// j from 16-byte LDS reads. A tile is kColumnSteps steps; the next tile's
+// quads are loaded before the fold of the current one, so their latency
+// hides behind it. Workgroups are renumbered so that neighbouring column
+// bands (which share cache lines) run on the same XCD.
+constexpr int kColumnQuads = 8;                                // quads per lane per tile
+constexpr int kColumnSteps = kColumnQuads * 256 * 4 / 16;      // 512 steps per tile
+
+Generated generate_column_fold(const Expr &e, int axis, FoldKind kind, const std::vector<int64_t> &rest,
+                               const std::vector<int> &rest_axes, int64_t outputs) {
+  const int64_t extent = e.shape[axis];
+  constexpr int W = 16, H = kColumnSteps;
+  std::ostringstream s;
+  s << preamble();
+  s << signature(e, "float* __restrict__ out, int vector_ok") << " {\n";
+  s << "  __shared__ __attribute__((aligned(16))) float tile[" << W << "][" << H + 4 << "];\n";
+  s << "  const int t = threadIdx.x;\n";
+  s << "  const unsigned blocks = gridDim.x;\n";
+  s << "  unsigned b = blockIdx.x;\n";
+  s << "  if (blocks % 8 == 0) b = (b % 8) * (blocks / 8) + b / 8;\n";
+  s << "  const long long first_output = (long long)b * " << W << ";\n";
+  // Quad i of this lane: local step (t + 256 i) / 4, local outputs
+  // ((t + 256 i) % 4) * 4 + 0..3.
+  auto quad = [&](int i, const std::string &k0, const std::string &prefix) {
+    const std::string tag = prefix + std::to_string(i);
+    const std::string lk = "((t + " + std::to_string(256 * i) + ") / 4)";
+    const std::string lo = "(((t + " + std::to_string(256 * i) + ") % 4) * 4)";
+    const std::vector<std::string> lanes = {tag + "_0", tag + "_1", tag + "_2", tag + "_3"};
+    for (const std::string &l : lanes) s << "    float " << prefix << "v_" << l << " = 0.0f;\n";
+    s << "    {\n";
+    s << "      const long long o_" << tag << " = first_output + " << lo << ";\n";
+    s << "      const long long k_" << tag << " = " << k0 << " + " << lk << ";\n";
+    s << "      if (o_" << tag << " < " << ll(outputs) << " && k_" << tag << " < " << ll(extent) << ") {\n";
+    std::vector<std::string> rc;
+    emit_coordinates(s, (int)rest.size(), rest.data(), "o_" + tag, tag, rc);
+    std::vector<std::string> c(e.rank);
+    for (size_t q = 0; q < rest_axes.size(); ++q) c[rest_axes[q]] = rc[q];
+    c[axis] = "k_" + tag;
+    emit_quad_inputs(s, e, c, tag, lanes, "        ");
+    emit_steps(s, e, lanes);
+    for (const std::string &l : lanes) s << "        " << prefix << "v_" << l << " = " << ref(e.outputs[0], l) << ";\n";
+    s << "      }\n    }\n";
+  };
+  auto load = [&](const std::string &k0, const std::string &prefix) {
+    for (int i = 0; i < kColumnQuads; ++i) quad(i, k0, prefix);
+  };
+  auto store = [&](const std::string &prefix) {
+    for (int i = 0; i < kColumnQuads; ++i) {
+      const std::string tag = prefix + std::to_string(i);
+      const std::string lk = "((t + " + std::to_string(256 * i) + ") / 4)";
+      const std::string lo = "(((t + " + std::to_string(256 * i) + ") % 4) * 4)";
+      for (int j = 0; j < 4; ++j)
+        s << "    tile[" << lo << " + " << j << "][" << lk << "] = " << prefix << "v_" << tag << "_" << j << ";\n";
+    }
+  };
+  const std::string combine = kind == kFoldSum ? "acc + x" : "topos_faithful::max_f32(acc, x)";
+  s << "  float acc = 0.0f;\n";
+  s << "  {\n";
+  load("0LL", "v");
+  store("v");
+  s << "  }\n";
+  s << "  for (long long k0 = 0; k0 < " << ll(extent) << "; k0 += " << H << ") {\n";
+  s << "    topos_lds_barrier();\n";
+  s << "    {\n";
+  load("k0 + " + std::to_string(H), "w");  // the next tile, in flight during this fold
+  s << "    if (t < " << W << ") {\n";
+  s << "      const int steps = " << ll(extent) << " - k0 < " << H << " ? (int)(" << ll(extent) << " - k0) : " << H
+    << ";\n";
+  s << "      if (steps == " << H << ") {\n";
+  for (int g = 0; g < H / 64; ++g) {
+    s << "        {\n          float r[64];\n";
+    s << "          #pragma unroll\n          for (int j = 0; j < 64; j += 4) { const float4 q = *(const float4*)&tile[t]["
+      << 64 * g << " + j]; r[j] = q.x; r[j + 1] = q.y; r[j + 2] = q.z; r[j + 3] = q.w; }\n";
+    if (g == 0)
+      s << "          if (k0 == 0) { acc = r[0]; } else { const float x = r[0]; acc = " << combine << "; }\n";
+    else
+      s << "          { const float x = r[0]; acc = " << combine << "; }\n";
+    s << "          #pragma unroll\n          for (int q = 1; q < 64; ++q) { const float x = r[q]; acc = " << combine
+      << "; }\n        }\n";
+  }
+  s << "      } else {\n";
+  s << "        int j = 0;\n";
+  s << "        if (k0 == 0) { acc = tile[t][0]; j = 1; }\n";
+  s << "        for (; j < steps; ++j) { const float x = tile[t][j]; acc = " << combine << "; }\n";
+  s << "      }\n";
+  s << "    }\n";
+  s << "    topos_lds_barrier();\n";
+  store("w");
+  s << "    }\n";
+  s << "  }\n";
+  s << "  if (t < " << W << " && first_output + t < " << ll(outputs) << ") out[first_output + t] = acc;\n";
+  s << "}\n";
+  return make(s.str());
+}
+
+}  // namespace
+
 Generated generate_fold(const Expr &e, int axis, FoldKind kind) {
   // A workgroup owns W consecutive outputs (W = 16 or 64). Per tile of
   // H = 4096 / W fold steps, all 256 lanes evaluate the expression at 16
@@ -459,6 +573,8 @@ Generated generate_fold(const Expr &e, int axis, FoldKind kind) {
   const int64_t extent = e.shape[axis];
   const bool row_form = axis == e.rank - 1;
   const int W = (int)fold_width(outputs), H = 4096 / W;
+  if (!row_form && W == 16 && e.shape[e.rank - 1] % 4 == 0)
+    return generate_column_fold(e, axis, kind, rest, rest_axes, outputs);
   s << "  __shared__ float tile[" << W << "][" << H + 1 << "];\n";
   s << "  const int t = threadIdx.x;\n";
   s << "  const long long first_output = (long long)blockIdx.x * " << W << ";\n";

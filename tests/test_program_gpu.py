@@ -260,3 +260,33 @@ def test_small_gpt2_adamw_steps_exact(hip):
         host = _adamw_reference(host, [want[g.id] for g in w.gradients], state)
         for i, (d, h) in enumerate(zip(device, host)):
             assert_bitwise(d, h, f"step {step} parameter {i}")
+
+
+def test_long_column_folds_exact(hip):
+    """Column folds over many steps (several LDS tiles, a partial last tile),
+    over an outer and a middle axis, with fused elementwise operands, a
+    broadcast operand and a max fold: bit-identical to the interpreter's
+    ascending first-term-seeded fold."""
+    banner("program long column folds")
+    rng = np.random.default_rng(21)
+    tape = t.Tape()
+    x = tape.input((1300, 52))
+    y = tape.input((1300, 52))
+    z = tape.input((3, 1100, 20))
+    bias = tape.parameter((52,))
+    roots = [
+        x.sum_along(0),
+        (x * y + bias.broadcast_along(0, x)).sum_along(0),
+        (x.exp() - y).maximum(x).sum_along(0),
+        z.sum_along(1),
+        (z * z).sum_along(0),
+        x.log_softmax(0).sum_along(0),
+    ]
+    params = [rng.standard_normal(52).astype(np.float32)]
+    dense = {x.node.slot: rng.standard_normal((1300, 52)).astype(np.float32),
+             y.node.slot: rng.standard_normal((1300, 52)).astype(np.float32),
+             z.node.slot: rng.standard_normal((3, 1100, 20)).astype(np.float32)}
+    want = run_oracle(tape, roots, params, dense)
+    got, _ = run_device(tape, roots, params, dense, numerics=hip.EXACT)
+    for r in roots:
+        assert_bitwise(got[r.id], want[r.id], f"node {r.id} {r.shape}")
