@@ -106,13 +106,12 @@ void validate(const Expr &e) {
 }
 
 // Input i may use 16-byte loads along the innermost axis: unit inner stride
-// and every quad start 16-byte aligned relative to the base pointer.
+// (gfx950 serves unaligned global_load_dwordx4, so any 4-byte alignment
+// does; a padded input's inner window must cover whole quads).
 bool vector_input(const Expr &e, const ExprInput &in) {
   if (e.rank == 0 || in.kind == ExprInput::kSelection || in.kind == ExprInput::kLiteral) return false;
   const int inner = e.rank - 1;
-  if (in.strides[inner] != 1 || in.offset % 4 != 0) return false;
-  for (int d = 0; d < inner; ++d)
-    if (in.strides[d] % 4 != 0) return false;
+  if (in.strides[inner] != 1) return false;
   if (in.kind == ExprInput::kPadded && in.pad_axis == inner && (in.pad_start % 4 != 0 || in.pad_len % 4 != 0))
     return false;
   return true;
@@ -184,6 +183,9 @@ void emit_coordinates(std::ostringstream &s, int rank, const int64_t *shape, con
 std::string preamble() {
   std::string s = "#pragma clang fp contract(off)\n";
   s += kFaithfulMathText;
+  // Four consecutive floats at any 4-byte-aligned address (one 16-byte
+  // access; gfx950 serves it unaligned).
+  s += "\ntypedef float topos_f4 __attribute__((ext_vector_type(4), aligned(4)));\n";
   // A barrier that orders LDS traffic only. __syncthreads() also waits for
   // every outstanding global load (a workgroup-scope fence), which would
   // stall the loads a fold keeps in flight across its barriers. Waiting for
@@ -239,16 +241,10 @@ Generated make(const std::string &source) {
   return g;
 }
 
-bool pointers_aligned(const Expr &e, const void *const *inputs) {
-  for (size_t i = 0; i < e.inputs.size(); ++i)
-    if (vector_input(e, e.inputs[i]) && reinterpret_cast<uintptr_t>(inputs[i]) % 16 != 0) return false;
-  return true;
-}
-
 // Emits in<i>_<lanes[j]> (j < 4): the expression inputs at the four points of
 // a quad (coordinates `c`, the innermost coordinate c[inner] the quad's first,
 // a multiple of four in an innermost extent that is one). Unit-stride inputs
-// take one 16-byte load when `vector_ok` holds at run time.
+// take one 16-byte load.
 void emit_quad_inputs(std::ostringstream &s, const Expr &e, const std::vector<std::string> &c,
                       const std::string &tag, const std::vector<std::string> &lanes, const std::string &indent) {
   const int inner = e.rank - 1;
@@ -284,11 +280,8 @@ void emit_quad_inputs(std::ostringstream &s, const Expr &e, const std::vector<st
         s << indent << "  " << v(0) << " = " << p << "[" << a << "]; " << v(1) << " = " << v(0) << "; " << v(2)
           << " = " << v(0) << "; " << v(3) << " = " << v(0) << ";\n";
       } else if (vector_input(e, in)) {
-        s << indent << "  if (vector_ok) { const float4 w = *(const float4*)(" << p << " + " << a << "); " << v(0)
-          << " = w.x; " << v(1) << " = w.y; " << v(2) << " = w.z; " << v(3) << " = w.w; }\n";
-        s << indent << "  else { ";
-        for (int j = 0; j < 4; ++j) s << v(j) << " = " << p << "[" << a << " + " << j << "]; ";
-        s << "}\n";
+        s << indent << "  const topos_f4 w = *(const topos_f4*)(" << p << " + " << a << "); " << v(0) << " = w.x; "
+          << v(1) << " = w.y; " << v(2) << " = w.z; " << v(3) << " = w.w;\n";
       } else {
         for (int j = 0; j < 4; ++j)
           s << indent << "  " << v(j) << " = " << p << "[" << a << " + " << ll(j * in.strides[inner]) << "];\n";
@@ -376,8 +369,7 @@ Generated generate_chain(const Expr &e) {
   std::ostringstream s;
   s << preamble();
   std::string tail;
-  for (size_t o = 0; o < e.outputs.size(); ++o) tail += "float* __restrict__ q" + std::to_string(o) + ", ";
-  tail += "int vector_ok";
+  for (size_t o = 0; o < e.outputs.size(); ++o) tail += (o ? ", " : "") + std::string("float* __restrict__ q") + std::to_string(o);
   s << signature(e, tail) << " {\n";
   const int64_t volume = e.volume();
   s << "  const long long volume = " << ll(volume) << ";\n";
@@ -392,11 +384,9 @@ Generated generate_chain(const Expr &e) {
     emit_quad_inputs(s, e, c, "q", lanes, "      ");
     emit_steps(s, e, lanes);
     for (size_t o = 0; o < e.outputs.size(); ++o) {
-      s << "      if (vector_ok) *(float4*)(q" << o << " + base) = make_float4(";
+      s << "      *(topos_f4*)(q" << o << " + base) = topos_f4{";
       for (int j = 0; j < 4; ++j) s << (j ? ", " : "") << ref(e.outputs[o], lanes[j]);
-      s << ");\n      else {";
-      for (int j = 0; j < 4; ++j) s << " q" << o << "[base + " << j << "] = " << ref(e.outputs[o], lanes[j]) << ";";
-      s << " }\n";
+      s << "};\n";
     }
     s << "    }\n";
   } else {
@@ -416,15 +406,11 @@ Generated generate_chain(const Expr &e) {
 
 void launch_generated_chain(const Generated &g, const Expr &e, const void *const *inputs, float *const *outputs,
                             hipStream_t stream) {
-  int vector_ok = pointers_aligned(e, inputs) ? 1 : 0;
-  for (size_t o = 0; o < e.outputs.size(); ++o)
-    if (reinterpret_cast<uintptr_t>(outputs[o]) % 16 != 0) vector_ok = 0;
   std::vector<const void *> pointers;
   for (size_t i = 0; i < e.inputs.size(); ++i) pointers.push_back(inputs[i]);
   for (size_t o = 0; o < e.outputs.size(); ++o) pointers.push_back(outputs[o]);
   std::vector<void *> arguments;
   for (auto &p : pointers) arguments.push_back(&p);
-  arguments.push_back(&vector_ok);
   int64_t blocks = (e.volume() + 1023) / 1024;
   if (blocks < 1) blocks = 1;
   if (blocks > 256 * 16) blocks = 256 * 16;
@@ -460,7 +446,7 @@ Generated generate_column_fold(const Expr &e, int axis, FoldKind kind, const std
   constexpr int W = 16, H = kColumnSteps;
   std::ostringstream s;
   s << preamble();
-  s << signature(e, "float* __restrict__ out, int vector_ok") << " {\n";
+  s << signature(e, "float* __restrict__ out") << " {\n";
   s << "  __shared__ __attribute__((aligned(16))) float tile[" << W << "][" << H + 4 << "];\n";
   s << "  const int t = threadIdx.x;\n";
   s << "  const unsigned blocks = gridDim.x;\n";
@@ -468,17 +454,17 @@ Generated generate_column_fold(const Expr &e, int axis, FoldKind kind, const std
   s << "  if (blocks % 8 == 0) b = (b % 8) * (blocks / 8) + b / 8;\n";
   s << "  const long long first_output = (long long)b * " << W << ";\n";
   // Quad i of this lane: local step (t + 256 i) / 4, local outputs
-  // ((t + 256 i) % 4) * 4 + 0..3.
-  auto quad = [&](int i, const std::string &k0, const std::string &prefix) {
+  // ((t + 256 i) % 4) * 4 + 0..3. Out-of-range quads read as zero (their
+  // values are never folded).
+  auto quad = [&](int i, const std::string &k0, const std::string &prefix, bool guarded) {
     const std::string tag = prefix + std::to_string(i);
     const std::string lk = "((t + " + std::to_string(256 * i) + ") / 4)";
     const std::string lo = "(((t + " + std::to_string(256 * i) + ") % 4) * 4)";
     const std::vector<std::string> lanes = {tag + "_0", tag + "_1", tag + "_2", tag + "_3"};
-    for (const std::string &l : lanes) s << "    float " << prefix << "v_" << l << " = 0.0f;\n";
-    s << "    {\n";
+    s << "      {\n";
     s << "      const long long o_" << tag << " = first_output + " << lo << ";\n";
     s << "      const long long k_" << tag << " = " << k0 << " + " << lk << ";\n";
-    s << "      if (o_" << tag << " < " << ll(outputs) << " && k_" << tag << " < " << ll(extent) << ") {\n";
+    if (guarded) s << "      if (o_" << tag << " < " << ll(outputs) << " && k_" << tag << " < " << ll(extent) << ") {\n";
     std::vector<std::string> rc;
     emit_coordinates(s, (int)rest.size(), rest.data(), "o_" + tag, tag, rc);
     std::vector<std::string> c(e.rank);
@@ -487,10 +473,20 @@ Generated generate_column_fold(const Expr &e, int axis, FoldKind kind, const std
     emit_quad_inputs(s, e, c, tag, lanes, "        ");
     emit_steps(s, e, lanes);
     for (const std::string &l : lanes) s << "        " << prefix << "v_" << l << " = " << ref(e.outputs[0], l) << ";\n";
-    s << "      }\n    }\n";
+    if (guarded) s << "      }\n";
+    s << "      }\n";
   };
+  // A tile wholly inside the operand (a uniform test) takes the unguarded
+  // path: one straight run of loads, all in flight together.
   auto load = [&](const std::string &k0, const std::string &prefix) {
-    for (int i = 0; i < kColumnQuads; ++i) quad(i, k0, prefix);
+    for (int i = 0; i < kColumnQuads; ++i)
+      for (int j = 0; j < 4; ++j) s << "    float " << prefix << "v_" << prefix << i << "_" << j << " = 0.0f;\n";
+    s << "    if (first_output + " << W << " <= " << ll(outputs) << " && " << k0 << " + " << H << " <= " << ll(extent)
+      << ") {\n";
+    for (int i = 0; i < kColumnQuads; ++i) quad(i, k0, prefix, false);
+    s << "    } else {\n";
+    for (int i = 0; i < kColumnQuads; ++i) quad(i, k0, prefix, true);
+    s << "    }\n";
   };
   auto store = [&](const std::string &prefix) {
     for (int i = 0; i < kColumnQuads; ++i) {
@@ -560,7 +556,7 @@ Generated generate_fold(const Expr &e, int axis, FoldKind kind) {
   if (axis < 0 || axis >= e.rank) throw InvalidArgument{"fold axis out of range"};
   std::ostringstream s;
   s << preamble();
-  s << signature(e, "float* __restrict__ out, int vector_ok") << " {\n";
+  s << signature(e, "float* __restrict__ out") << " {\n";
   std::vector<int64_t> rest;
   std::vector<int> rest_axes;
   for (int d = 0; d < e.rank; ++d)
@@ -671,10 +667,8 @@ void launch_generated_fold(const Generated &g, const Expr &e, int axis, const vo
   std::vector<const void *> pointers;
   for (size_t i = 0; i < e.inputs.size(); ++i) pointers.push_back(inputs[i]);
   pointers.push_back(out);
-  int vector_ok = pointers_aligned(e, inputs) ? 1 : 0;
   std::vector<void *> arguments;
   for (auto &p : pointers) arguments.push_back(&p);
-  arguments.push_back(&vector_ok);
   const int64_t width = fold_width(outputs);
   const int64_t blocks = (outputs + width - 1) / width;
   if (blocks > 0x7fffffff) throw Unsupported{"fold: too many outputs for one launch"};
