@@ -12,6 +12,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <functional>
 #include <map>
 #include <mutex>
 #include <sstream>
@@ -246,9 +247,11 @@ Generated make(const std::string &source) {
 // a multiple of four in an innermost extent that is one). Unit-stride inputs
 // take one 16-byte load.
 void emit_quad_inputs(std::ostringstream &s, const Expr &e, const std::vector<std::string> &c,
-                      const std::string &tag, const std::vector<std::string> &lanes, const std::string &indent) {
+                      const std::string &tag, const std::vector<std::string> &lanes, const std::string &indent,
+                      const std::vector<bool> *only = nullptr) {
   const int inner = e.rank - 1;
   for (size_t i = 0; i < e.inputs.size(); ++i) {
+    if (only && !(*only)[i]) continue;
     const ExprInput &in = e.inputs[i];
     const std::string p = "p" + std::to_string(i);
     auto v = [&](int j) { return ref(-(int)i - 1, lanes[j]); };
@@ -771,6 +774,365 @@ void launch_sum_compact(const Generated &g, const Expr &e, const void *const *in
   std::vector<void *> arguments;
   for (auto &p : pointers) arguments.push_back(&p);
   launch(g, (unsigned)chunks, arguments, stream);
+}
+
+
+// ---- row programs ----
+
+namespace {
+
+struct RowFold {
+  int pass;
+  bool max;
+  int node;          // the node whose operand a is folded
+  bool shifted_exp;  // fold exp(a - rowv[max_slot[node]]) instead of a
+  int target;        // row slot receiving the fold
+};
+
+struct RowLayout {
+  std::vector<int> avail, slot, max_slot, total_slot, lns_slot;
+  std::vector<RowFold> folds;
+  int passes = 0, slots = 0, levels = 0;
+};
+
+RowLayout lay_out(const RowProgram &p) {
+  const int n = (int)p.nodes.size();
+  RowLayout l;
+  l.avail.assign(n, 0);
+  l.slot.assign(n, -1);
+  l.max_slot.assign(n, -1);
+  l.total_slot.assign(n, -1);
+  l.lns_slot.assign(n, -1);
+  auto check_ref = [&](const RowRef &r, int at, bool want_full, bool want_row) {
+    if (r.kind == RowRef::kInput) {
+      if (r.index < 0 || r.index >= (int)p.inputs.size()) throw InvalidArgument{"row program input reference"};
+      return;
+    }
+    if (r.index < 0 || r.index >= at) throw InvalidArgument{"row program node reference"};
+    const bool full = p.nodes[r.index].full();
+    if ((full && !want_full) || (!full && !want_row)) throw InvalidArgument{"row program operand kind"};
+  };
+  auto level = [&](const RowRef &r) { return r.kind == RowRef::kInput ? 0 : l.avail[r.index]; };
+  for (int i = 0; i < n; ++i) {
+    const RowNode &x = p.nodes[i];
+    switch (x.kind) {
+      case RowNode::kFullOp:
+      case RowNode::kRowOp: {
+        const bool full = x.kind == RowNode::kFullOp;
+        if (!is_unary(x.op) && !is_binary(x.op)) throw InvalidArgument{"row program operation"};
+        check_ref(x.a, i, full, true);
+        int lv = level(x.a);
+        if (is_binary(x.op)) {
+          check_ref(x.b, i, full, true);
+          lv = std::max(lv, level(x.b));
+        }
+        l.avail[i] = lv;
+        if (!full) l.slot[i] = l.slots++;
+        break;
+      }
+      case RowNode::kSum:
+      case RowNode::kMax: {
+        check_ref(x.a, i, true, false);
+        l.slot[i] = l.slots++;
+        l.folds.push_back(RowFold{level(x.a), x.kind == RowNode::kMax, i, false, l.slot[i]});
+        l.avail[i] = level(x.a) + 1;
+        break;
+      }
+      case RowNode::kLogSumExp:
+      case RowNode::kLogSoftmax: {
+        check_ref(x.a, i, true, false);
+        const int lv = level(x.a);
+        l.max_slot[i] = l.slots++;
+        l.total_slot[i] = l.slots++;
+        l.folds.push_back(RowFold{lv, true, i, false, l.max_slot[i]});
+        l.folds.push_back(RowFold{lv + 1, false, i, true, l.total_slot[i]});
+        if (x.kind == RowNode::kLogSumExp)
+          l.slot[i] = l.slots++;
+        else
+          l.lns_slot[i] = l.slots++;
+        l.avail[i] = lv + 2;
+        break;
+      }
+      default:
+        throw InvalidArgument{"row program node kind"};
+    }
+    l.levels = std::max(l.levels, l.avail[i]);
+  }
+  for (const RowFold &f : l.folds) l.passes = std::max(l.passes, f.pass + 1);
+  for (int o : p.full_outputs)
+    if (o < 0 || o >= n || !p.nodes[o].full()) throw InvalidArgument{"row program full output"};
+  for (int o : p.row_outputs)
+    if (o < 0 || o >= n || p.nodes[o].full()) throw InvalidArgument{"row program row output"};
+  return l;
+}
+
+// Rows per workgroup and columns per staged slab.
+void row_blocking(const RowProgram &p, int &rows_per_block, int &slab) {
+  const int64_t c = p.columns();
+  const int64_t v = c % 4 == 0 ? 4 : 1;
+  slab = (int)std::min<int64_t>(512, (c + v - 1) / v * v);
+  rows_per_block = (int)std::min<int64_t>(64, std::max<int64_t>(8, 4096 / slab));
+}
+
+}  // namespace
+
+Generated generate_row_program(const RowProgram &p) {
+  if (p.rank < 1 || p.rank > kMaxRank) throw InvalidArgument{"row program rank"};
+  for (int d = 0; d < p.rank; ++d)
+    if (p.shape[d] <= 0) throw InvalidArgument{"row program shape"};
+  const RowLayout l = lay_out(p);
+  const int64_t C = p.columns(), R = p.rows();
+  const int V = C % 4 == 0 ? 4 : 1;
+  int G = 8, S = 512;
+  row_blocking(p, G, S);
+  const int n = (int)p.nodes.size();
+  const int inner = p.rank - 1;
+  // Inputs in row context must be constant along the row.
+  Expr e;  // the inputs over the full shape, for the shared emitters
+  e.rank = p.rank;
+  for (int d = 0; d < p.rank; ++d) e.shape[d] = p.shape[d];
+  e.inputs = p.inputs;
+  e.outputs.push_back(0);
+  int folds_per_pass = 1;
+  for (int q = 0; q < l.passes; ++q) {
+    int k = 0;
+    for (const RowFold &f : l.folds) k += f.pass == q;
+    folds_per_pass = std::max(folds_per_pass, k);
+  }
+
+  std::ostringstream s;
+  s << preamble();
+  std::string tail;
+  for (size_t o = 0; o < p.full_outputs.size(); ++o) tail += "float* __restrict__ fo" + std::to_string(o) + ", ";
+  for (size_t o = 0; o < p.row_outputs.size(); ++o) tail += "float* __restrict__ ro" + std::to_string(o) + ", ";
+  tail += "int unused";
+  s << signature(e, tail) << " {\n";
+  s << "  __shared__ float rowv[" << std::max(l.slots, 1) << "][" << G << "];\n";
+  if (l.passes > 0)
+    s << "  __shared__ __attribute__((aligned(16))) float slab[" << folds_per_pass << "][" << G << "][" << S + 4
+      << "];\n";
+  s << "  const int t = threadIdx.x;\n";
+  s << "  const long long row0 = (long long)blockIdx.x * " << G << ";\n";
+
+  // ---- emitters ----
+  // The name of a reference's value in full context (lane `lane`, row `r`).
+  auto full_name = [&](const RowRef &x, const std::string &lane, const std::string &r) -> std::string {
+    if (x.kind == RowRef::kInput) return ref(-x.index - 1, lane);
+    if (p.nodes[x.index].full()) return "f" + std::to_string(x.index) + "_" + lane;
+    return "rowv[" + std::to_string(l.slot[x.index]) + "][" + r + "]";
+  };
+  // Marks the full nodes and inputs that evaluating `x` needs.
+  std::function<void(const RowRef &, std::vector<bool> &, std::vector<bool> &)> need =
+      [&](const RowRef &x, std::vector<bool> &nodes_needed, std::vector<bool> &inputs_needed) {
+        if (x.kind == RowRef::kInput) {
+          inputs_needed[x.index] = true;
+          return;
+        }
+        const RowNode &y = p.nodes[x.index];
+        if (!y.full() || nodes_needed[x.index]) return;
+        nodes_needed[x.index] = true;
+        need(y.a, nodes_needed, inputs_needed);
+        if (y.kind == RowNode::kFullOp && is_binary(y.op)) need(y.b, nodes_needed, inputs_needed);
+      };
+  // Emits the values of the needed inputs and full nodes at the point(s)
+  // (row r of the block, column `col`), V lanes named tag_j.
+  auto emit_point = [&](const std::vector<bool> &nodes_needed, const std::vector<bool> &inputs_needed,
+                        const std::string &col, const std::string &tag, const std::string &indent) {
+    std::vector<std::string> lanes;
+    for (int j = 0; j < V; ++j) lanes.push_back(tag + "_" + std::to_string(j));
+    s << indent << "const long long g_" << tag << " = row0 + r;\n";
+    std::vector<std::string> c;
+    if (p.rank > 1) emit_coordinates(s, p.rank - 1, p.shape, "g_" + tag, tag, c);
+    c.push_back(col);
+    if (V == 4) {
+      emit_quad_inputs(s, e, c, tag, lanes, indent, &inputs_needed);
+    } else {
+      for (size_t i = 0; i < p.inputs.size(); ++i)
+        if (inputs_needed[i])
+          s << indent << "const float " << ref(-(int)i - 1, lanes[0]) << " = " << scalar_value(e, (int)i, c) << ";\n";
+    }
+    for (int k = 0; k < n; ++k) {
+      if (!nodes_needed[k]) continue;
+      const RowNode &y = p.nodes[k];
+      for (const std::string &lane : lanes) {
+        std::string value;
+        const std::string a = full_name(y.a, lane, "r");
+        if (y.kind == RowNode::kLogSoftmax) {
+          value = "((" + a + " - rowv[" + std::to_string(l.max_slot[k]) + "][r]) - rowv[" +
+                  std::to_string(l.lns_slot[k]) + "][r])";
+        } else if (is_unary(y.op)) {
+          value = substitute(unary_pattern(y.op), a, "");
+        } else {
+          value = substitute(binary_pattern(y.op), a, full_name(y.b, lane, "r"));
+        }
+        s << indent << "const float f" << k << "_" << lane << " = " << value << ";\n";
+      }
+    }
+  };
+  // Row-context value of a reference, for lane t of the fold wave.
+  auto row_name = [&](const RowRef &x) -> std::string {
+    if (x.kind == RowRef::kInput) return "rin" + std::to_string(x.index);
+    return "rowv[" + std::to_string(l.slot[x.index]) + "][t]";
+  };
+  // Row nodes that become available at `level`, computed by lane t < G.
+  auto emit_row_stage = [&](int level) {
+    std::ostringstream body;
+    std::vector<bool> inputs_needed(p.inputs.size(), false);
+    bool any = false;
+    for (int k = 0; k < n; ++k) {
+      const RowNode &y = p.nodes[k];
+      if ((y.full() && y.kind != RowNode::kLogSoftmax) || l.avail[k] != level) continue;
+      if (y.kind == RowNode::kRowOp) {
+        for (const RowRef *x : {&y.a, &y.b}) {
+          if (x == &y.b && !is_binary(y.op)) break;
+          if (x->kind == RowRef::kInput) inputs_needed[x->index] = true;
+        }
+        const std::string a = row_name(y.a);
+        const std::string v = is_unary(y.op) ? substitute(unary_pattern(y.op), a, "")
+                                             : substitute(binary_pattern(y.op), a, row_name(y.b));
+        body << "    rowv[" << l.slot[k] << "][t] = " << v << ";\n";
+        any = true;
+      } else if (y.kind == RowNode::kLogSumExp) {
+        body << "    rowv[" << l.slot[k] << "][t] = rowv[" << l.max_slot[k] << "][t] + topos_faithful::ln_f32(rowv["
+             << l.total_slot[k] << "][t]);\n";
+        any = true;
+      } else if (y.kind == RowNode::kLogSoftmax) {
+        body << "    rowv[" << l.lns_slot[k] << "][t] = topos_faithful::ln_f32(rowv[" << l.total_slot[k] << "][t]);\n";
+        any = true;
+      }
+    }
+    if (!any) return;
+    s << "  if (t < " << G << ") {\n";
+    bool inputs = false;
+    for (bool b : inputs_needed) inputs = inputs || b;
+    if (inputs) {
+      s << "    const long long g_row = row0 + t;\n";
+      std::vector<std::string> c;
+      if (p.rank > 1) emit_coordinates(s, p.rank - 1, p.shape, "g_row", "row", c);
+      c.push_back("0LL");
+      for (size_t i = 0; i < p.inputs.size(); ++i) {
+        if (!inputs_needed[i]) continue;
+        const ExprInput &in = p.inputs[i];
+        if (in.kind == ExprInput::kSelection || (in.kind == ExprInput::kPadded && in.pad_axis == inner) ||
+            (in.kind != ExprInput::kLiteral && in.strides[inner] != 0))
+          throw InvalidArgument{"row program: a row operand varies along the row"};
+        s << "    const float rin" << i << " = (g_row < " << ll(R) << ") ? " << scalar_value(e, (int)i, c)
+          << " : 0.0f;\n";
+      }
+    }
+    s << body.str();
+    s << "  }\n";
+  };
+
+  emit_row_stage(0);
+  s << "  topos_lds_barrier();\n";
+  for (int q = 0; q < l.passes; ++q) {
+    std::vector<const RowFold *> folds;
+    for (const RowFold &f : l.folds)
+      if (f.pass == q) folds.push_back(&f);
+    std::vector<bool> nodes_needed(n, false), inputs_needed(p.inputs.size(), false);
+    for (const RowFold *f : folds) need(p.nodes[f->node].a, nodes_needed, inputs_needed);
+    s << "  {\n";
+    for (size_t j = 0; j < folds.size(); ++j) s << "    float acc" << j << " = 0.0f;\n";
+    s << "    for (long long c0 = 0; c0 < " << ll(C) << "; c0 += " << S << ") {\n";
+    s << "      for (int u = t; u < " << G * (S / V) << "; u += 256) {\n";
+    s << "        const int r = u / " << S / V << ";\n";
+    s << "        const int cu = (u % " << S / V << ") * " << V << ";\n";
+    s << "        const long long col = c0 + cu;\n";
+    for (size_t j = 0; j < folds.size(); ++j)
+      for (int v = 0; v < V; ++v) s << "        float v" << j << "_" << v << " = 0.0f;\n";
+    s << "        if (row0 + r < " << ll(R) << " && col < " << ll(C) << ") {\n";
+    emit_point(nodes_needed, inputs_needed, "col", "p", "          ");
+    for (size_t j = 0; j < folds.size(); ++j) {
+      const RowFold &f = *folds[j];
+      for (int v = 0; v < V; ++v) {
+        const std::string a = full_name(p.nodes[f.node].a, "p_" + std::to_string(v), "r");
+        std::string value = a;
+        if (f.shifted_exp)
+          value = "topos_faithful::exp_f32(" + a + " - rowv[" + std::to_string(l.max_slot[f.node]) + "][r])";
+        s << "          v" << j << "_" << v << " = " << value << ";\n";
+      }
+    }
+    s << "        }\n";
+    for (size_t j = 0; j < folds.size(); ++j)
+      for (int v = 0; v < V; ++v) s << "        slab[" << j << "][r][cu + " << v << "] = v" << j << "_" << v << ";\n";
+    s << "      }\n";
+    s << "      topos_lds_barrier();\n";
+    s << "      if (t < " << G << ") {\n";
+    s << "        const int width = " << ll(C) << " - c0 < " << S << " ? (int)(" << ll(C) << " - c0) : " << S << ";\n";
+    s << "        int q0 = 0;\n";
+    s << "        if (c0 == 0) {\n";
+    for (size_t j = 0; j < folds.size(); ++j) s << "          acc" << j << " = slab[" << j << "][t][0];\n";
+    s << "          q0 = 1;\n        }\n";
+    s << "        #pragma unroll 8\n";
+    s << "        for (int q = q0; q < width; ++q) {\n";
+    for (size_t j = 0; j < folds.size(); ++j) {
+      const std::string x = "slab[" + std::to_string(j) + "][t][q]";
+      if (folds[j]->max)
+        s << "          acc" << j << " = topos_faithful::max_f32(acc" << j << ", " << x << ");\n";
+      else
+        s << "          acc" << j << " = acc" << j << " + " << x << ";\n";
+    }
+    s << "        }\n      }\n";
+    s << "      topos_lds_barrier();\n";
+    s << "    }\n";
+    s << "    if (t < " << G << ") {\n";
+    for (size_t j = 0; j < folds.size(); ++j) s << "      rowv[" << folds[j]->target << "][t] = acc" << j << ";\n";
+    s << "    }\n";
+    s << "  }\n";
+    emit_row_stage(q + 1);
+    s << "  topos_lds_barrier();\n";
+  }
+  for (int level = l.passes + 1; level <= l.levels; ++level) {
+    emit_row_stage(level);
+    s << "  topos_lds_barrier();\n";
+  }
+  // The output pass.
+  if (!p.full_outputs.empty()) {
+    std::vector<bool> nodes_needed(n, false), inputs_needed(p.inputs.size(), false);
+    for (int o : p.full_outputs) need(RowRef{RowRef::kFull, o}, nodes_needed, inputs_needed);
+    s << "  for (long long u = t; u < " << ll((int64_t)G * (C / V)) << "; u += 256) {\n";
+    s << "    const int r = (int)(u / " << ll(C / V) << ");\n";
+    s << "    const long long col = (u % " << ll(C / V) << ") * " << V << ";\n";
+    s << "    if (row0 + r < " << ll(R) << ") {\n";
+    emit_point(nodes_needed, inputs_needed, "col", "o", "      ");
+    s << "      const long long at = (row0 + r) * " << ll(C) << " + col;\n";
+    for (size_t o = 0; o < p.full_outputs.size(); ++o) {
+      const int k = p.full_outputs[o];
+      if (V == 4) {
+        s << "      *(topos_f4*)(fo" << o << " + at) = topos_f4{f" << k << "_o_0, f" << k << "_o_1, f" << k << "_o_2, f"
+          << k << "_o_3};\n";
+      } else {
+        s << "      fo" << o << "[at] = f" << k << "_o_0;\n";
+      }
+    }
+    s << "    }\n  }\n";
+  }
+  if (!p.row_outputs.empty()) {
+    s << "  if (t < " << G << " && row0 + t < " << ll(R) << ") {\n";
+    for (size_t o = 0; o < p.row_outputs.size(); ++o)
+      s << "    ro" << o << "[row0 + t] = rowv[" << l.slot[p.row_outputs[o]] << "][t];\n";
+    s << "  }\n";
+  }
+  s << "}\n";
+  return make(s.str());
+}
+
+void launch_row_program(const Generated &g, const RowProgram &p, const void *const *inputs,
+                        float *const *full_outputs, float *const *row_outputs, hipStream_t stream) {
+  int G = 8, S = 512;
+  row_blocking(p, G, S);
+  std::vector<const void *> pointers;
+  for (size_t i = 0; i < p.inputs.size(); ++i) pointers.push_back(inputs[i]);
+  for (size_t o = 0; o < p.full_outputs.size(); ++o) pointers.push_back(full_outputs[o]);
+  for (size_t o = 0; o < p.row_outputs.size(); ++o) pointers.push_back(row_outputs[o]);
+  int unused = 0;
+  std::vector<void *> arguments;
+  for (auto &q : pointers) arguments.push_back(&q);
+  arguments.push_back(&unused);
+  const int64_t blocks = (p.rows() + G - 1) / G;
+  if (blocks > 0x7fffffff) throw Unsupported{"row program: too many rows for one launch"};
+  launch(g, (unsigned)blocks, arguments, stream);
 }
 
 }  // namespace topos_hip

@@ -94,6 +94,51 @@ Generated generate_fold(const Expr &e, int axis, FoldKind kind);
 void launch_generated_fold(const Generated &g, const Expr &e, int axis, const void *const *inputs,
                            float *out, hipStream_t stream);
 
+// A row program: one launch evaluating a group of row-local nodes of a plan
+// over the [rows, columns] view of `shape` (columns = the last axis, rows =
+// the leading axes flattened). Full values live per element, row values per
+// row; a row value enters full expressions broadcast along the row. Folds
+// (sum, max, and the max-then-shifted-exponential-sum pairs of LogSumExp and
+// LogSoftmax) are the interpreter's: one lane per row, ascending, seeded with
+// the row's first term. The kernel makes one pass over the columns per fold
+// level and a last pass writing the requested full values (contiguous
+// [rows, columns]) and row values (contiguous [rows]).
+struct RowRef {
+  enum Kind { kInput = 0, kFull = 1, kRow = 2 };
+  int kind = kInput;
+  int index = 0;  // an input, or an earlier node
+};
+
+struct RowNode {
+  // kFullOp / kRowOp: TOPOS_HIP_CHAIN_* `op` on a (and b); kSum / kMax: the
+  // ordered fold of full operand a; kLogSumExp: max + ln(sum exp(a - max));
+  // kLogSoftmax (a full value): (a - max) - ln(sum exp(a - max)).
+  enum Kind { kFullOp = 0, kRowOp = 1, kSum = 2, kMax = 3, kLogSumExp = 4, kLogSoftmax = 5 };
+  int kind = kFullOp;
+  int op = 0;
+  RowRef a, b;
+  bool full() const { return kind == kFullOp || kind == kLogSoftmax; }
+};
+
+struct RowProgram {
+  int rank = 0;
+  int64_t shape[kMaxRank] = {1, 1, 1, 1};
+  std::vector<ExprInput> inputs;   // layouts over the full shape (row inputs: stride 0 on the last axis)
+  std::vector<RowNode> nodes;      // in evaluation order
+  std::vector<int> full_outputs;   // full nodes written [rows, columns]
+  std::vector<int> row_outputs;    // row nodes written [rows]
+  int64_t columns() const { return shape[rank - 1]; }
+  int64_t rows() const {
+    int64_t r = 1;
+    for (int d = 0; d + 1 < rank; ++d) r *= shape[d];
+    return r;
+  }
+};
+
+Generated generate_row_program(const RowProgram &p);
+void launch_row_program(const Generated &g, const RowProgram &p, const void *const *inputs,
+                        float *const *full_outputs, float *const *row_outputs, hipStream_t stream);
+
 // Whole-tensor exact sum over a large operand, in chunks of kSumChunk flat
 // elements (one workgroup each, lanes on consecutive elements): pass one
 // counts each chunk's nonzero terms (and whether the chunk holds a +0), pass

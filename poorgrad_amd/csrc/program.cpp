@@ -487,17 +487,330 @@ struct topos_hip_program {
     readable.assign(n, false);
     for (int64_t i = 0; i < n; ++i)
       if (nodes[i].flags & TOPOS_HIP_NODE_READABLE) wanted[i] = readable[i] = true;
+    // A readable duplicate reads its original's value, which must then be
+    // materialised like a readable node.
+    for (int64_t i = 0; i < n; ++i)
+      if (readable[i] && alias_of[i] >= 0) wanted[alias_of[i]] = readable[alias_of[i]] = true;
     for (int64_t i = n - 1; i >= 0; --i) {
-      if (!wanted[i]) continue;
+      if (!wanted[i] || alias_of[i] >= 0) continue;
       for (int j = 0; j < value_links(nodes[i].op); ++j) wanted[nodes[i].operands[j]] = true;
     }
     consumers.assign(n, {});
     for (int64_t i = 0; i < n; ++i) {
-      if (!wanted[i]) continue;
+      if (!wanted[i] || alias_of[i] >= 0) continue;
       for (int j = 0; j < value_links(nodes[i].op); ++j) {
         auto &c = consumers[nodes[i].operands[j]];
         if (c.empty() || c.back() != i) c.push_back((int)i);
       }
+    }
+  }
+
+  // ---- common subexpressions ----
+
+  // alias_of[i] >= 0: node i repeats an earlier node (same operation, same
+  // operands after this rewrite, same parameters and shape), so it has the
+  // same value bit for bit; later nodes read the earlier one instead.
+  std::vector<int64_t> alias_of;
+
+  void deduplicate() {
+    const int64_t n = (int64_t)nodes.size();
+    alias_of.assign(n, -1);
+    std::vector<int64_t> rep(n);
+    std::map<std::vector<int64_t>, int64_t> seen;
+    for (int64_t i = 0; i < n; ++i) {
+      rep[i] = i;
+      topos_hip_node &x = nodes[i];
+      for (int j = 0; j < arity(x.op); ++j) x.operands[j] = rep[x.operands[j]];
+      if (x.op == TOPOS_HIP_OP_LEAF || x.op == TOPOS_HIP_OP_PARAMETER || x.op == TOPOS_HIP_OP_INPUT) continue;
+      std::vector<int64_t> key = {x.op, x.rank, x.operands[0], x.operands[1]};
+      for (int d = 0; d < kMaxRank; ++d) key.push_back(x.params[d]);
+      for (int d = 0; d < x.rank; ++d) key.push_back(x.shape[d]);
+      auto it = seen.find(key);
+      if (it != seen.end()) {
+        rep[i] = it->second;
+        alias_of[i] = it->second;
+      } else {
+        seen.emplace(std::move(key), i);
+      }
+    }
+  }
+
+  // ---- row groups ----
+
+  // A row group: nodes over one [rows, columns] iteration space (full nodes
+  // share `shape`; row nodes drop its last axis) whose reductions all run
+  // along the last axis, evaluated by one generated row program. Members are
+  // elementwise nodes of either shape, broadcasts of row nodes along the last
+  // axis, and last-axis SumAlong / LogSumExp / LogSoftmax. The group is
+  // launched at its last member; no node outside it consumes a member before
+  // that point, and every outside operand is planned before it.
+  struct RowGroup {
+    std::vector<int64_t> members;  // ascending
+    int rank = 0;
+    int64_t shape[kMaxRank] = {1, 1, 1, 1};
+  };
+  std::vector<RowGroup> row_groups;
+  std::vector<int> group_of;
+
+  static bool group_full(const topos_hip_node &x, const RowGroup &g) {
+    if (x.rank != g.rank) return false;
+    for (int d = 0; d < g.rank; ++d)
+      if (x.shape[d] != g.shape[d]) return false;
+    return true;
+  }
+  static bool group_row(const topos_hip_node &x, const RowGroup &g) {
+    if (x.rank != g.rank - 1) return false;
+    for (int d = 0; d < x.rank; ++d)
+      if (x.shape[d] != g.shape[d]) return false;
+    return true;
+  }
+
+  bool row_eligible(int64_t i, const RowGroup &g) const {
+    const topos_hip_node &x = nodes[i];
+    if (!wanted[i] || group_of[i] >= 0 || alias_of[i] >= 0) return false;
+    const int last = g.rank - 1;
+    if (is_elementwise(x.op)) return x.op != TOPOS_HIP_OP_POWF && (group_full(x, g) || group_row(x, g));
+    switch (x.op) {
+      case TOPOS_HIP_OP_BROADCAST_ALONG: return x.params[0] == last && group_full(x, g);
+      case TOPOS_HIP_OP_SUM_ALONG:
+      case TOPOS_HIP_OP_LOG_SUM_EXP: return x.params[0] == last && group_row(x, g);
+      case TOPOS_HIP_OP_LOG_SOFTMAX: return x.params[0] == last && group_full(x, g);
+    }
+    return false;
+  }
+
+  void form_row_groups() {
+    const int64_t n = (int64_t)nodes.size();
+    group_of.assign(n, -1);
+    for (int64_t seed = 0; seed < n; ++seed) {
+      if (!wanted[seed] || group_of[seed] >= 0 || alias_of[seed] >= 0) continue;
+      const topos_hip_node &x = nodes[seed];
+      RowGroup g;
+      if (x.op == TOPOS_HIP_OP_SUM_ALONG || x.op == TOPOS_HIP_OP_LOG_SUM_EXP) {
+        const topos_hip_node &a = nodes[x.operands[0]];
+        if (x.params[0] != a.rank - 1) continue;
+        g.rank = a.rank;
+        for (int d = 0; d < a.rank; ++d) g.shape[d] = a.shape[d];
+      } else if (x.op == TOPOS_HIP_OP_LOG_SOFTMAX) {
+        if (x.params[0] != x.rank - 1) continue;
+        g.rank = x.rank;
+        for (int d = 0; d < x.rank; ++d) g.shape[d] = x.shape[d];
+      } else {
+        continue;
+      }
+      const int id = (int)row_groups.size();
+      std::vector<int64_t> members;
+      auto add = [&](int64_t j) {
+        group_of[j] = id;
+        members.push_back(j);
+      };
+      // Eligible operands whose every consumer is a member join the group.
+      auto close_over_operands = [&]() {
+        for (bool changed = true; changed;) {
+          changed = false;
+          for (size_t m = 0; m < members.size(); ++m) {
+            const topos_hip_node &y = nodes[members[m]];
+            for (int j = 0; j < value_links(y.op); ++j) {
+              const int64_t o = y.operands[j];
+              if (!row_eligible(o, g) || readable[o]) continue;
+              bool inside = true;
+              for (int c : consumers[o]) inside = inside && group_of[c] == id;
+              if (inside) {
+                add(o);
+                changed = true;
+              }
+            }
+          }
+        }
+      };
+      add(seed);
+      close_over_operands();
+      // Consumers in plan order, up to the first outside consumer of a member.
+      for (int64_t j = seed + 1; j < n; ++j) {
+        if (!wanted[j] || alias_of[j] >= 0) continue;
+        bool consumes = false;
+        for (int k = 0; k < value_links(nodes[j].op); ++k) consumes = consumes || group_of[nodes[j].operands[k]] == id;
+        if (!consumes) continue;
+        if (!row_eligible(j, g)) break;
+        add(j);
+      }
+      close_over_operands();
+      std::sort(members.begin(), members.end());
+      g.members = members;
+      row_groups.push_back(g);
+    }
+  }
+
+  // The input of a row program that reads node o (planned, outside the
+  // group) over the group's iteration space: a full node through its layout,
+  // a row node through its layout with stride 0 along the last axis.
+  int row_input(RowProgram &p, std::vector<int> &storage_of, std::map<int64_t, int> &input_of, int64_t o) {
+    auto found = input_of.find(o);
+    if (found != input_of.end()) return found->second;
+    const topos_hip_node &x = nodes[o];
+    const Value &v = values[o];
+    const bool row = x.rank == p.rank - 1;
+    ExprInput in;
+    int storage = v.storage;
+    if (v.kind == Value::kDense && v.host_known) {
+      in.kind = ExprInput::kLiteral;
+      in.one = v.host_value;
+      storage = -1;
+    } else if (v.kind == Value::kDense) {
+      in.kind = ExprInput::kStrided;
+      in.offset = v.layout.offset;
+      for (int d = 0; d < x.rank; ++d) in.strides[d] = v.layout.strides[d];
+      if (row) in.strides[p.rank - 1] = 0;
+    } else if (v.kind == Value::kSelection && !row) {
+      in.kind = ExprInput::kSelection;
+      in.one = storages[v.storage].one;
+    } else if (v.kind == Value::kPadInline && !row) {
+      const Value &src = values[x.operands[0]];
+      if (src.kind != Value::kDense) throw RuntimeFailure{"padded input of a non-dense value"};
+      in.kind = ExprInput::kPadded;
+      in.offset = src.layout.offset;
+      for (int d = 0; d < x.rank; ++d) in.strides[d] = src.layout.strides[d];
+      in.pad_axis = (int)x.params[0];
+      in.pad_start = x.params[1];
+      in.pad_len = nodes[x.operands[0]].shape[x.params[0]];
+      storage = src.storage;
+    } else {
+      throw RuntimeFailure{"row program operand without a readable value"};
+    }
+    p.inputs.push_back(in);
+    storage_of.push_back(storage);
+    const int index = (int)p.inputs.size() - 1;
+    input_of[o] = index;
+    return index;
+  }
+
+  void plan_row_group(int id) {
+    const RowGroup &g = row_groups[id];
+    RowProgram p;
+    p.rank = g.rank;
+    for (int d = 0; d < g.rank; ++d) p.shape[d] = g.shape[d];
+    std::vector<int> storage_of;
+    std::map<int64_t, int> input_of;
+    std::map<int64_t, RowRef> ref_of;
+    auto ref = [&](int64_t o) -> RowRef {
+      if (group_of[o] == id) return ref_of.at(o);
+      return RowRef{RowRef::kInput, row_input(p, storage_of, input_of, o)};
+    };
+    int zero_input = -1;
+    for (int64_t m : g.members) {
+      const topos_hip_node &x = nodes[m];
+      if (x.op == TOPOS_HIP_OP_BROADCAST_ALONG) {
+        ref_of[m] = ref(x.operands[0]);
+        continue;
+      }
+      RowNode rn;
+      const bool full = group_full(x, g);
+      if (is_elementwise(x.op)) {
+        rn.kind = full ? RowNode::kFullOp : RowNode::kRowOp;
+        rn.a = ref(x.operands[0]);
+        if (x.op == TOPOS_HIP_OP_RELU) {
+          if (zero_input < 0) {
+            ExprInput zero;
+            zero.kind = ExprInput::kLiteral;
+            zero.one = 0.0f;  // zero_like of an f32 element: +0
+            p.inputs.push_back(zero);
+            storage_of.push_back(-1);
+            zero_input = (int)p.inputs.size() - 1;
+          }
+          rn.op = TOPOS_HIP_CHAIN_MAX;
+          rn.b = RowRef{RowRef::kInput, zero_input};
+        } else {
+          rn.op = chain_op(x.op);
+          if (is_binary(rn.op)) rn.b = ref(x.operands[1]);
+        }
+      } else {
+        rn.kind = x.op == TOPOS_HIP_OP_SUM_ALONG    ? RowNode::kSum
+                  : x.op == TOPOS_HIP_OP_LOG_SUM_EXP ? RowNode::kLogSumExp
+                                                     : RowNode::kLogSoftmax;
+        rn.a = ref(x.operands[0]);
+      }
+      p.nodes.push_back(rn);
+      ref_of[m] = RowRef{rn.full() ? RowRef::kFull : RowRef::kRow, (int)p.nodes.size() - 1};
+    }
+    // Members read outside the group (or readable) are written out; a
+    // broadcast member read outside is its row operand, viewed.
+    auto outside = [&](int64_t m) {
+      if (readable[m]) return true;
+      for (int c : consumers[m])
+        if (group_of[c] != id) return true;
+      return false;
+    };
+    std::map<int64_t, int> full_out, row_out;  // member -> output position
+    std::vector<int64_t> broadcast_views;
+    for (int64_t m : g.members) {
+      if (!outside(m)) continue;
+      int64_t w = m;
+      if (nodes[m].op == TOPOS_HIP_OP_BROADCAST_ALONG) {
+        broadcast_views.push_back(m);
+        w = nodes[m].operands[0];
+        if (group_of[w] != id) continue;  // an outside operand: already has a value
+      }
+      const RowRef r = ref_of.at(w);
+      if (r.kind == RowRef::kFull && !full_out.count(w)) {
+        full_out[w] = (int)p.full_outputs.size();
+        p.full_outputs.push_back(r.index);
+      } else if (r.kind == RowRef::kRow && !row_out.count(w)) {
+        row_out[w] = (int)p.row_outputs.size();
+        p.row_outputs.push_back(r.index);
+      }
+    }
+    const int64_t rows = p.rows(), columns = p.columns();
+    std::vector<int> full_storage, row_storage, writes;
+    for (size_t o = 0; o < p.full_outputs.size(); ++o) {
+      full_storage.push_back(arena_storage(rows * columns * 4));
+      writes.push_back(full_storage.back());
+    }
+    for (size_t o = 0; o < p.row_outputs.size(); ++o) {
+      row_storage.push_back(arena_storage(rows * 4));
+      writes.push_back(row_storage.back());
+    }
+    Generated gen = generate_row_program(p);
+    pending.push_back(gen);
+    ++fused_groups;
+    int folds = 0;
+    for (const RowNode &rn : p.nodes)
+      folds += rn.kind == RowNode::kSum ? 1 : (rn.kind == RowNode::kLogSumExp || rn.kind == RowNode::kLogSoftmax) ? 2 : 0;
+    std::ostringstream what;
+    what << "rows [";
+    for (int d = 0; d < p.rank; ++d) what << (d ? "," : "") << p.shape[d];
+    what << "] " << p.inputs.size() << " inputs, " << p.nodes.size() << " nodes, " << folds << " folds, "
+         << p.full_outputs.size() << "+" << p.row_outputs.size() << " outputs";
+    add_launch(what.str(), real(storage_of), writes,
+               [this, p, gen, storage_of, full_storage, row_storage](const Exec &ex) {
+                 auto in = pointers_for(storage_of);
+                 std::vector<float *> fo, ro;
+                 for (int s : full_storage) fo.push_back((float *)base(s));
+                 for (int s : row_storage) ro.push_back((float *)base(s));
+                 launch_row_program(gen, p, in.data(), fo.data(), ro.data(), ex.stream);
+               });
+    {
+      Expr e;
+      e.rank = p.rank;
+      for (int d = 0; d < p.rank; ++d) e.shape[d] = p.shape[d];
+      e.inputs = p.inputs;
+      account(e, (double)rows * columns * p.full_outputs.size() + (double)rows * p.row_outputs.size());
+    }
+    int64_t row_shape[kMaxRank];
+    for (int d = 0; d + 1 < p.rank; ++d) row_shape[d] = p.shape[d];
+    for (auto &kv : full_out) values[kv.first] = dense_value(full_storage[kv.second], contiguous(p.rank, p.shape));
+    for (auto &kv : row_out) values[kv.first] = dense_value(row_storage[kv.second], contiguous(p.rank - 1, row_shape));
+    for (int64_t b : broadcast_views) {
+      const Value &a = values[nodes[b].operands[0]];
+      Layout l;
+      l.rank = p.rank;
+      l.offset = a.layout.offset;
+      for (int d = 0; d + 1 < p.rank; ++d) {
+        l.shape[d] = p.shape[d];
+        l.strides[d] = a.layout.strides[d];
+      }
+      l.shape[p.rank - 1] = columns;
+      l.strides[p.rank - 1] = 0;
+      values[b] = view_of(a, l);
     }
   }
 
@@ -1234,7 +1547,9 @@ struct topos_hip_program {
     const bool full = x.op == TOPOS_HIP_OP_LOG_SOFTMAX;
     const int out = arena_storage((full ? volume_of(a) : rows) * 4);
     const int kind = full ? TOPOS_HIP_ROWS_LOG_SOFTMAX : TOPOS_HIP_ROWS_LOG_SUM_EXP;
-    const int numerics_ = numerics;
+    // Row reductions are exact in both postures (only products take the
+    // matrix-core envelope).
+    const int numerics_ = TOPOS_HIP_EXACT;
     add_launch(std::string(full ? "log_softmax " : "log_sum_exp ") + std::to_string(rows) + "x" +
                    std::to_string(extent),
                {source}, {out}, [this, source, source_offset, out, rows, extent, kind, numerics_](const Exec &ex) {
@@ -1470,10 +1785,22 @@ struct topos_hip_program {
 
   void plan() {
     validate();
+    deduplicate();
     mark_wanted();
+    form_row_groups();
     values.assign(nodes.size(), Value());
+    for (int64_t i = 0; i < (int64_t)nodes.size(); ++i) {
+      if (!wanted[i] || alias_of[i] >= 0) continue;
+      const int group = group_of[i];
+      if (group >= 0) {
+        if (i == row_groups[group].members.back()) plan_row_group(group);
+        continue;
+      }
+      plan_node(i);
+    }
+    // A duplicate (wanted only when readable) reads its original's value.
     for (int64_t i = 0; i < (int64_t)nodes.size(); ++i)
-      if (wanted[i]) plan_node(i);
+      if (wanted[i] && alias_of[i] >= 0) values[i] = values[alias_of[i]];
     finish_readables();
     assign_streams();
     assign_arena();

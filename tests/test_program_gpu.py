@@ -290,3 +290,51 @@ def test_long_column_folds_exact(hip):
     got, _ = run_device(tape, roots, params, dense, numerics=hip.EXACT)
     for r in roots:
         assert_bitwise(got[r.id], want[r.id], f"node {r.id} {r.shape}")
+
+
+@pytest.mark.parametrize("rows, columns", [(37, 1100), (24, 1028), (130, 40), (9, 3)])
+def test_row_groups_exact(hip, rows, columns):
+    """Row programs (groups of row-local nodes with last-axis reductions):
+    several column slabs, a partial last row block, quads and single
+    columns, row operands broadcast back along the row, LogSumExp and
+    LogSoftmax with fused operands and consumers, a ReLU member, and a row
+    input: bit-identical to the interpreter."""
+    banner(f"program row groups {rows}x{columns}")
+    rng = np.random.default_rng(rows * 7 + columns)
+    tape = t.Tape()
+    x = tape.input((rows, columns))
+    y = tape.input((rows, columns))
+    v = tape.input((rows,))
+    eps = tape.leaf(t.Constant((), 1e-5))
+    mean = x.sum_along(1) / t.counted((rows,), columns)
+    c = x - mean.broadcast_along(1, x)
+    var = (c * c).sum_along(1) / t.counted((rows,), columns) + v.abs()
+    n = c / (var + eps.broadcast_like(var)).sqrt().broadcast_along(1, x)
+    soft = (n * y).relu().log_softmax(1)
+    roots = [n, var, soft, soft.exp() * y, (x * y).logsumexp(1), (y - x).logsumexp(1).exp()]
+    dense = {x.node.slot: (3 * rng.standard_normal((rows, columns))).astype(np.float32),
+             y.node.slot: rng.standard_normal((rows, columns)).astype(np.float32),
+             v.node.slot: rng.standard_normal(rows).astype(np.float32)}
+    want = run_oracle(tape, roots, [], dense)
+    got, program = run_device(tape, roots, [], dense, numerics=hip.EXACT)
+    assert ": rows [" in program.describe
+    for r in roots:
+        assert_bitwise(got[r.id], want[r.id], f"node {r.id} {r.shape}")
+
+
+def test_row_groups_rank3_and_selection(hip):
+    banner("program row groups rank 3 and selection")
+    rng = np.random.default_rng(31)
+    tape = t.Tape()
+    z = tape.input((5, 6, 16))
+    logits = tape.input((12, 7))
+    targets = tape.selection_input(12, 7)
+    roots = [z.log_softmax(2).exp(), (z * z).sum_along(2), t.cross_entropy(logits, targets),
+             tape.value(targets.id).sum_along(1)]
+    dense = {z.node.slot: rng.standard_normal((5, 6, 16)).astype(np.float32),
+             logits.node.slot: rng.standard_normal((12, 7)).astype(np.float32)}
+    selections = {targets.node.slot: (rng.integers(0, 7, 12).astype(np.int32), 1.0)}
+    want = run_oracle(tape, roots, [], dense, selections)
+    got, _ = run_device(tape, roots, [], dense, selections, hip.EXACT)
+    for r in roots:
+        assert_bitwise(got[r.id], want[r.id], f"node {r.id} {r.shape}")
