@@ -248,7 +248,9 @@ Generated make(const std::string &source) {
 // take one 16-byte load.
 void emit_quad_inputs(std::ostringstream &s, const Expr &e, const std::vector<std::string> &c,
                       const std::string &tag, const std::vector<std::string> &lanes, const std::string &indent,
-                      const std::vector<bool> *only = nullptr) {
+                      const std::vector<bool> *only = nullptr, bool declare = true) {
+  // declare = false: assign to registers the caller declared (zeroed).
+  const std::string cf = declare ? "const float " : "";
   const int inner = e.rank - 1;
   for (size_t i = 0; i < e.inputs.size(); ++i) {
     if (only && !(*only)[i]) continue;
@@ -256,14 +258,14 @@ void emit_quad_inputs(std::ostringstream &s, const Expr &e, const std::vector<st
     const std::string p = "p" + std::to_string(i);
     auto v = [&](int j) { return ref(-(int)i - 1, lanes[j]); };
     if (in.kind == ExprInput::kLiteral) {
-      for (int j = 0; j < 4; ++j) s << indent << "const float " << v(j) << " = " << float_literal(in.one) << ";\n";
+      for (int j = 0; j < 4; ++j) s << indent << cf << v(j) << " = " << float_literal(in.one) << ";\n";
       continue;
     }
     if (in.kind == ExprInput::kSelection) {
       const std::string sel = "sel" + std::to_string(i) + "_" + tag;
       s << indent << "const int " << sel << " = " << p << "[" << c[0] << "];\n";
       for (int j = 0; j < 4; ++j)
-        s << indent << "const float " << v(j) << " = (" << sel << " == (int)(" << c[1] << " + " << j << ")) ? "
+        s << indent << cf << v(j) << " = (" << sel << " == (int)(" << c[1] << " + " << j << ")) ? "
           << float_literal(in.one) << " : 0.0f;\n";
       continue;
     }
@@ -276,8 +278,9 @@ void emit_quad_inputs(std::ostringstream &s, const Expr &e, const std::vector<st
     s << indent << "const long long " << a << " = " << address(e, in, c) << ";\n";
     if (!padded || quad_window) {
       const std::string inside = padded ? window_test(in, c[in.pad_axis]) : "true";
-      s << indent << "float " << v(0) << " = 0.0f, " << v(1) << " = 0.0f, " << v(2) << " = 0.0f, " << v(3)
-        << " = 0.0f;\n";
+      if (declare)
+        s << indent << "float " << v(0) << " = 0.0f, " << v(1) << " = 0.0f, " << v(2) << " = 0.0f, " << v(3)
+          << " = 0.0f;\n";
       s << indent << "if (" << inside << ") {\n";
       if (in.strides[inner] == 0) {
         s << indent << "  " << v(0) << " = " << p << "[" << a << "]; " << v(1) << " = " << v(0) << "; " << v(2)
@@ -293,7 +296,7 @@ void emit_quad_inputs(std::ostringstream &s, const Expr &e, const std::vector<st
     } else {
       for (int j = 0; j < 4; ++j) {
         const std::string cj = "(" + c[inner] + " + " + std::to_string(j) + ")";
-        s << indent << "const float " << v(j) << " = " << window_test(in, cj) << " ? " << p << "[" << a << " + "
+        s << indent << cf << v(j) << " = " << window_test(in, cj) << " ? " << p << "[" << a << " + "
           << ll(j * in.strides[inner]) << "] : 0.0f;\n";
       }
     }
@@ -866,12 +869,314 @@ RowLayout lay_out(const RowProgram &p) {
   return l;
 }
 
-// Rows per workgroup and columns per staged slab.
-void row_blocking(const RowProgram &p, int &rows_per_block, int &slab) {
+// How a row program is laid out on the GPU.
+//   resident: a workgroup owns G whole rows (G * columns <= 8192) and keeps
+//     every non-literal input of its points in registers, read once; each
+//     fold parks its operand row-major in LDS, max folds reduce contiguous
+//     segments and combine them in column order, sum folds run one lane per
+//     row in column order;
+//   streaming: G rows per workgroup, the columns in slabs of S, every fold
+//     level re-reading its inputs, one lane per row folding each slab.
+struct RowBlocking {
+  bool resident = false;
+  int rows = 8;      // G
+  int slab = 512;    // S (streaming)
+  int width = 4;     // V: columns per point
+  int points = 0;    // P: points per lane (resident)
+};
+
+RowBlocking row_blocking(const RowProgram &p) {
+  RowBlocking b;
   const int64_t c = p.columns();
-  const int64_t v = c % 4 == 0 ? 4 : 1;
-  slab = (int)std::min<int64_t>(512, (c + v - 1) / v * v);
-  rows_per_block = (int)std::min<int64_t>(64, std::max<int64_t>(8, 4096 / slab));
+  b.width = c % 4 == 0 ? 4 : 1;
+  int varying = 0;
+  for (const ExprInput &in : p.inputs) varying += in.kind != ExprInput::kLiteral;
+  if (c * 4 <= 8192) {
+    int g = 64;
+    while ((int64_t)g * c > 8192) g /= 2;
+    auto points = [&](int rows) { return (int)((rows * (c / b.width) + 255) / 256); };
+    while (g > 4 && (int64_t)points(g) * b.width * varying > 128) g /= 2;
+    if ((int64_t)points(g) * b.width * varying <= 128 && points(g) <= 32) {
+      b.resident = true;
+      b.rows = g;
+      b.points = points(g);
+      return b;
+    }
+  }
+  b.slab = (int)std::min<int64_t>(512, (c + b.width - 1) / b.width * b.width);
+  b.rows = (int)std::min<int64_t>(64, std::max<int64_t>(8, 4096 / b.slab));
+  return b;
+}
+
+// Shared pieces of the two row-program layouts.
+struct RowEmit {
+  const RowProgram &p;
+  const RowLayout &l;
+  Expr e;  // the inputs over the full shape, for the shared emitters
+  int n;
+  RowEmit(const RowProgram &program, const RowLayout &layout) : p(program), l(layout) {
+    e.rank = p.rank;
+    for (int d = 0; d < p.rank; ++d) e.shape[d] = p.shape[d];
+    e.inputs = p.inputs;
+    e.outputs.push_back(0);
+    n = (int)p.nodes.size();
+  }
+  // The name of a reference's value in full context (lane `lane`, block row `r`).
+  std::string full_name(const RowRef &x, const std::string &lane, const std::string &r) const {
+    if (x.kind == RowRef::kInput) return ref(-x.index - 1, lane);
+    if (p.nodes[x.index].full()) return "f" + std::to_string(x.index) + "_" + lane;
+    return "rowv[" + std::to_string(l.slot[x.index]) + "][" + r + "]";
+  }
+  // Marks the full nodes and inputs that evaluating `x` needs.
+  void need(const RowRef &x, std::vector<bool> &nodes_needed, std::vector<bool> &inputs_needed) const {
+    if (x.kind == RowRef::kInput) {
+      inputs_needed[x.index] = true;
+      return;
+    }
+    const RowNode &y = p.nodes[x.index];
+    if (!y.full() || nodes_needed[x.index]) return;
+    nodes_needed[x.index] = true;
+    need(y.a, nodes_needed, inputs_needed);
+    if (y.kind == RowNode::kFullOp && is_binary(y.op)) need(y.b, nodes_needed, inputs_needed);
+  }
+  // Emits the needed full nodes for each lane (inputs already named).
+  void emit_nodes(std::ostringstream &s, const std::vector<bool> &nodes_needed, const std::vector<std::string> &lanes,
+                  const std::string &r, const std::string &indent) const {
+    for (int k = 0; k < n; ++k) {
+      if (!nodes_needed[k]) continue;
+      const RowNode &y = p.nodes[k];
+      for (const std::string &lane : lanes) {
+        std::string value;
+        const std::string a = full_name(y.a, lane, r);
+        if (y.kind == RowNode::kLogSoftmax) {
+          value = "((" + a + " - rowv[" + std::to_string(l.max_slot[k]) + "][" + r + "]) - rowv[" +
+                  std::to_string(l.lns_slot[k]) + "][" + r + "])";
+        } else if (is_unary(y.op)) {
+          value = substitute(unary_pattern(y.op), a, "");
+        } else {
+          value = substitute(binary_pattern(y.op), a, full_name(y.b, lane, r));
+        }
+        s << indent << "const float f" << k << "_" << lane << " = " << value << ";\n";
+      }
+    }
+  }
+  // The operand of fold f at one lane.
+  std::string fold_operand(const RowFold &f, const std::string &lane, const std::string &r) const {
+    const std::string a = full_name(p.nodes[f.node].a, lane, r);
+    if (!f.shifted_exp) return a;
+    return "topos_faithful::exp_f32(" + a + " - rowv[" + std::to_string(l.max_slot[f.node]) + "][" + r + "])";
+  }
+  // Row nodes that become available at `level`, computed by lane t < G.
+  void emit_row_stage(std::ostringstream &s, int level, int G) const {
+    const int inner = p.rank - 1;
+    const int64_t R = p.rows();
+    auto row_name = [&](const RowRef &x) -> std::string {
+      if (x.kind == RowRef::kInput) return "rin" + std::to_string(x.index);
+      return "rowv[" + std::to_string(l.slot[x.index]) + "][t]";
+    };
+    std::ostringstream body;
+    std::vector<bool> inputs_needed(p.inputs.size(), false);
+    bool any = false;
+    for (int k = 0; k < n; ++k) {
+      const RowNode &y = p.nodes[k];
+      if ((y.full() && y.kind != RowNode::kLogSoftmax) || l.avail[k] != level) continue;
+      if (y.kind == RowNode::kRowOp) {
+        if (y.a.kind == RowRef::kInput) inputs_needed[y.a.index] = true;
+        if (is_binary(y.op) && y.b.kind == RowRef::kInput) inputs_needed[y.b.index] = true;
+        const std::string a = row_name(y.a);
+        const std::string v = is_unary(y.op) ? substitute(unary_pattern(y.op), a, "")
+                                             : substitute(binary_pattern(y.op), a, row_name(y.b));
+        body << "    rowv[" << l.slot[k] << "][t] = " << v << ";\n";
+        any = true;
+      } else if (y.kind == RowNode::kLogSumExp) {
+        body << "    rowv[" << l.slot[k] << "][t] = rowv[" << l.max_slot[k] << "][t] + topos_faithful::ln_f32(rowv["
+             << l.total_slot[k] << "][t]);\n";
+        any = true;
+      } else if (y.kind == RowNode::kLogSoftmax) {
+        body << "    rowv[" << l.lns_slot[k] << "][t] = topos_faithful::ln_f32(rowv[" << l.total_slot[k] << "][t]);\n";
+        any = true;
+      }
+    }
+    if (!any) return;
+    s << "  if (t < " << G << ") {\n";
+    bool inputs = false;
+    for (bool x : inputs_needed) inputs = inputs || x;
+    if (inputs) {
+      s << "    const long long g_row = row0 + t;\n";
+      std::vector<std::string> c;
+      if (p.rank > 1) emit_coordinates(s, p.rank - 1, p.shape, "g_row", "row", c);
+      c.push_back("0LL");
+      for (size_t i = 0; i < p.inputs.size(); ++i) {
+        if (!inputs_needed[i]) continue;
+        const ExprInput &in = p.inputs[i];
+        if (in.kind == ExprInput::kSelection || (in.kind == ExprInput::kPadded && in.pad_axis == inner) ||
+            (in.kind != ExprInput::kLiteral && in.strides[inner] != 0))
+          throw InvalidArgument{"row program: a row operand varies along the row"};
+        s << "    const float rin" << i << " = (g_row < " << ll(R) << ") ? " << scalar_value(e, (int)i, c)
+          << " : 0.0f;\n";
+      }
+    }
+    s << body.str();
+    s << "  }\n";
+  }
+  std::string tail() const {
+    std::string t;
+    for (size_t o = 0; o < p.full_outputs.size(); ++o) t += "float* __restrict__ fo" + std::to_string(o) + ", ";
+    for (size_t o = 0; o < p.row_outputs.size(); ++o) t += "float* __restrict__ ro" + std::to_string(o) + ", ";
+    return t + "int unused";
+  }
+};
+
+Generated generate_row_resident(const RowProgram &p, const RowLayout &l, const RowBlocking &b) {
+  const RowEmit m(p, l);
+  const int64_t C = p.columns(), R = p.rows();
+  const int V = b.width, G = b.rows, P = b.points;
+  const int64_t CV = C / V;
+  const int n = m.n;
+  std::ostringstream s;
+  s << preamble();
+  s << signature(m.e, m.tail()) << " {\n";
+  s << "  __shared__ float rowv[" << std::max(l.slots, 1) << "][" << G << "];\n";
+  if (!l.folds.empty())
+    s << "  __shared__ __attribute__((aligned(16))) float slab[" << G << "][" << C + 4 << "];\n";
+  s << "  const int t = threadIdx.x;\n";
+  s << "  const long long row0 = (long long)blockIdx.x * " << G << ";\n";
+  // Every input read anywhere, loaded once per point into registers.
+  std::vector<bool> nodes_all(n, false), inputs_all(p.inputs.size(), false);
+  for (const RowFold &f : l.folds) m.need(p.nodes[f.node].a, nodes_all, inputs_all);
+  for (int o : p.full_outputs) m.need(RowRef{RowRef::kFull, o}, nodes_all, inputs_all);
+  std::vector<bool> loaded(p.inputs.size(), false);
+  for (size_t k = 0; k < p.inputs.size(); ++k) loaded[k] = inputs_all[k] && p.inputs[k].kind != ExprInput::kLiteral;
+  auto lanes_of = [&](int i) {
+    std::vector<std::string> lanes;
+    for (int j = 0; j < V; ++j) lanes.push_back("r" + std::to_string(i) + "_" + std::to_string(j));
+    return lanes;
+  };
+  for (int i = 0; i < P; ++i) {
+    const std::string I = std::to_string(i);
+    s << "  const int q" << I << " = t + " << 256 * i << ";\n";
+    s << "  const int r" << I << " = q" << I << " / " << CV << ";\n";
+    s << "  const long long col" << I << " = (long long)(q" << I << " % " << CV << ") * " << V << ";\n";
+    s << "  const bool ok" << I << " = q" << I << " < " << (int64_t)G * CV << " && row0 + r" << I << " < " << ll(R) << ";\n";
+    const std::vector<std::string> lanes = lanes_of(i);
+    for (size_t k = 0; k < p.inputs.size(); ++k) {
+      if (!inputs_all[k]) continue;
+      for (const std::string &lane : lanes) {
+        if (p.inputs[k].kind == ExprInput::kLiteral)
+          s << "  const float " << ref(-(int)k - 1, lane) << " = " << float_literal(p.inputs[k].one) << ";\n";
+        else
+          s << "  float " << ref(-(int)k - 1, lane) << " = 0.0f;\n";
+      }
+    }
+    s << "  if (ok" << I << ") {\n";
+    s << "    const long long g_r" << I << " = row0 + r" << I << ";\n";
+    std::vector<std::string> c;
+    if (p.rank > 1) emit_coordinates(s, p.rank - 1, p.shape, "g_r" + I, "r" + I, c);
+    c.push_back("col" + I);
+    if (V == 4) {
+      emit_quad_inputs(s, m.e, c, "r" + I, lanes, "    ", &loaded, false);
+    } else {
+      for (size_t k = 0; k < p.inputs.size(); ++k)
+        if (loaded[k]) s << "    " << ref(-(int)k - 1, lanes[0]) << " = " << scalar_value(m.e, (int)k, c) << ";\n";
+    }
+    s << "  }\n";
+  }
+  m.emit_row_stage(s, 0, G);
+  s << "  topos_lds_barrier();\n";
+  const int per = 256 / G;  // lanes per row in a max fold
+  const int64_t seg = (C + per - 1) / per;
+  for (int q = 0; q < l.passes; ++q) {
+    for (const RowFold &f : l.folds) {
+      if (f.pass != q) continue;
+      std::vector<bool> nodes_needed(n, false), inputs_needed(p.inputs.size(), false);
+      m.need(p.nodes[f.node].a, nodes_needed, inputs_needed);
+      // The operand, row-major into the slab.
+      for (int i = 0; i < P; ++i) {
+        const std::string I = std::to_string(i);
+        const std::vector<std::string> lanes = lanes_of(i);
+        s << "  if (ok" << I << ") {\n";
+        m.emit_nodes(s, nodes_needed, lanes, "r" + I, "    ");
+        for (int j = 0; j < V; ++j)
+          s << "    slab[r" << I << "][col" << I << " + " << j << "] = " << m.fold_operand(f, lanes[j], "r" + I) << ";\n";
+        s << "  }\n";
+      }
+      s << "  topos_lds_barrier();\n";
+      if (f.max) {
+        // Contiguous segments folded in order, then combined in column order
+        // (the ordered fold of max_f32 splits at any point into the max_f32
+        // of its two halves' folds).
+        s << "  {\n";
+        s << "    const int rr = t / " << per << ", sg = t % " << per << ";\n";
+        s << "    const int cb = sg * " << seg << ";\n";
+        s << "    const int ce = cb + " << seg << " < " << C << " ? cb + " << seg << " : " << C << ";\n";
+        s << "    bool has = cb < ce;\n";
+        s << "    float mx = has ? slab[rr][cb] : 0.0f;\n";
+        s << "    for (int c = cb + 1; c < ce; ++c) mx = topos_faithful::max_f32(mx, slab[rr][c]);\n";
+        s << "    #pragma unroll\n";
+        s << "    for (int off = 1; off < " << per << "; off <<= 1) {\n";
+        s << "      const float om = __shfl_xor(mx, off, 64);\n";
+        s << "      const bool oh = __shfl_xor((int)has, off, 64) != 0;\n";
+        s << "      const bool right = (t & off) != 0;\n";
+        s << "      const float lm = right ? om : mx, rm = right ? mx : om;\n";
+        s << "      const bool lh = right ? oh : has, rh = right ? has : oh;\n";
+        s << "      mx = !lh ? rm : (!rh ? lm : topos_faithful::max_f32(lm, rm));\n";
+        s << "      has = lh || rh;\n";
+        s << "    }\n";
+        s << "    if (sg == 0) rowv[" << f.target << "][rr] = mx;\n";
+        s << "  }\n";
+      } else {
+        s << "  if (t < " << G << ") {\n";
+        if (V == 4) {
+          s << "    const float4 w0 = *(const float4*)&slab[t][0];\n";
+          s << "    float acc = w0.x;\n    acc = acc + w0.y;\n    acc = acc + w0.z;\n    acc = acc + w0.w;\n";
+          s << "    for (int c = 4; c < " << C << "; c += 4) {\n";
+          s << "      const float4 w = *(const float4*)&slab[t][c];\n";
+          s << "      acc = acc + w.x;\n      acc = acc + w.y;\n      acc = acc + w.z;\n      acc = acc + w.w;\n";
+          s << "    }\n";
+        } else {
+          s << "    float acc = slab[t][0];\n";
+          s << "    for (int c = 1; c < " << C << "; ++c) acc = acc + slab[t][c];\n";
+        }
+        s << "    rowv[" << f.target << "][t] = acc;\n";
+        s << "  }\n";
+      }
+      s << "  topos_lds_barrier();\n";
+    }
+    m.emit_row_stage(s, q + 1, G);
+    s << "  topos_lds_barrier();\n";
+  }
+  for (int level = l.passes + 1; level <= l.levels; ++level) {
+    m.emit_row_stage(s, level, G);
+    s << "  topos_lds_barrier();\n";
+  }
+  if (!p.full_outputs.empty()) {
+    std::vector<bool> nodes_needed(n, false), inputs_needed(p.inputs.size(), false);
+    for (int o : p.full_outputs) m.need(RowRef{RowRef::kFull, o}, nodes_needed, inputs_needed);
+    for (int i = 0; i < P; ++i) {
+      const std::string I = std::to_string(i);
+      const std::vector<std::string> lanes = lanes_of(i);
+      s << "  if (ok" << I << ") {\n";
+      m.emit_nodes(s, nodes_needed, lanes, "r" + I, "    ");
+      s << "    const long long at = (row0 + r" << I << ") * " << ll(C) << " + col" << I << ";\n";
+      for (size_t o = 0; o < p.full_outputs.size(); ++o) {
+        const int k = p.full_outputs[o];
+        if (V == 4)
+          s << "    *(topos_f4*)(fo" << o << " + at) = topos_f4{f" << k << "_" << lanes[0] << ", f" << k << "_" << lanes[1]
+            << ", f" << k << "_" << lanes[2] << ", f" << k << "_" << lanes[3] << "};\n";
+        else
+          s << "    fo" << o << "[at] = f" << k << "_" << lanes[0] << ";\n";
+      }
+      s << "  }\n";
+    }
+  }
+  if (!p.row_outputs.empty()) {
+    s << "  if (t < " << G << " && row0 + t < " << ll(R) << ") {\n";
+    for (size_t o = 0; o < p.row_outputs.size(); ++o)
+      s << "    ro" << o << "[row0 + t] = rowv[" << l.slot[p.row_outputs[o]] << "][t];\n";
+    s << "  }\n";
+  }
+  s << "}\n";
+  return make(s.str());
 }
 
 }  // namespace
@@ -882,9 +1187,10 @@ Generated generate_row_program(const RowProgram &p) {
     if (p.shape[d] <= 0) throw InvalidArgument{"row program shape"};
   const RowLayout l = lay_out(p);
   const int64_t C = p.columns(), R = p.rows();
-  const int V = C % 4 == 0 ? 4 : 1;
-  int G = 8, S = 512;
-  row_blocking(p, G, S);
+  const RowBlocking blocking = row_blocking(p);
+  if (blocking.resident) return generate_row_resident(p, l, blocking);
+  const int V = blocking.width;
+  const int G = blocking.rows, S = blocking.slab;
   const int n = (int)p.nodes.size();
   const int inner = p.rank - 1;
   // Inputs in row context must be constant along the row.
@@ -1120,8 +1426,7 @@ Generated generate_row_program(const RowProgram &p) {
 
 void launch_row_program(const Generated &g, const RowProgram &p, const void *const *inputs,
                         float *const *full_outputs, float *const *row_outputs, hipStream_t stream) {
-  int G = 8, S = 512;
-  row_blocking(p, G, S);
+  const int G = row_blocking(p).rows;
   std::vector<const void *> pointers;
   for (size_t i = 0; i < p.inputs.size(); ++i) pointers.push_back(inputs[i]);
   for (size_t o = 0; o < p.full_outputs.size(); ++o) pointers.push_back(full_outputs[o]);
