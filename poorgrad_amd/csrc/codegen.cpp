@@ -34,8 +34,8 @@ std::map<std::string, Kernel> &cache() {
 const char *unary_pattern(int op) {
   switch (op) {
     case TOPOS_HIP_CHAIN_NEG: return "(-%a)";
-    case TOPOS_HIP_CHAIN_EXP: return "topos_faithful::exp_f32(%a)";
-    case TOPOS_HIP_CHAIN_LN: return "topos_faithful::ln_f32(%a)";
+    case TOPOS_HIP_CHAIN_EXP: return "topos_exp(%a)";
+    case TOPOS_HIP_CHAIN_LN: return "topos_ln(%a)";
     case TOPOS_HIP_CHAIN_SQRT: return "__builtin_sqrtf(%a)";
     case TOPOS_HIP_CHAIN_TANH: return "topos_faithful::tanh_f32(%a)";
   }
@@ -201,6 +201,17 @@ std::string preamble() {
        "  __builtin_amdgcn_s_barrier();\n"
        "  __atomic_signal_fence(__ATOMIC_SEQ_CST);\n"
        "}\n";
+  // The exp and ln tables, copied into LDS by every generated kernel on
+  // entry: a per-lane table index then costs an LDS read, not a global load.
+  s += "__shared__ uint64_t topos_exp_lds[32];\n"
+       "__shared__ topos_faithful::LogRow topos_log_lds[16];\n"
+       "__device__ __forceinline__ void topos_tables_init() {\n"
+       "  if (threadIdx.x < 32) topos_exp_lds[threadIdx.x] = topos_faithful::kExpTableDevice[threadIdx.x];\n"
+       "  if (threadIdx.x < 16) topos_log_lds[threadIdx.x] = topos_faithful::kLogTableDevice[threadIdx.x];\n"
+       "  __syncthreads();\n"
+       "}\n"
+       "__device__ __forceinline__ float topos_exp(float x) { return topos_faithful::exp_f32_table(x, topos_exp_lds); }\n"
+       "__device__ __forceinline__ float topos_ln(float x) { return topos_faithful::ln_f32_table(x, topos_log_lds); }\n";
   return s;
 }
 
@@ -376,7 +387,7 @@ Generated generate_chain(const Expr &e) {
   s << preamble();
   std::string tail;
   for (size_t o = 0; o < e.outputs.size(); ++o) tail += (o ? ", " : "") + std::string("float* __restrict__ q") + std::to_string(o);
-  s << signature(e, tail) << " {\n";
+  s << signature(e, tail) << " {\n  topos_tables_init();\n";
   const int64_t volume = e.volume();
   s << "  const long long volume = " << ll(volume) << ";\n";
   s << "  const long long stride = (long long)gridDim.x * 1024;\n";
@@ -452,7 +463,7 @@ Generated generate_column_fold(const Expr &e, int axis, FoldKind kind, const std
   constexpr int W = 16, H = kColumnSteps;
   std::ostringstream s;
   s << preamble();
-  s << signature(e, "float* __restrict__ out") << " {\n";
+  s << signature(e, "float* __restrict__ out") << " {\n  topos_tables_init();\n";
   s << "  __shared__ __attribute__((aligned(16))) float tile[" << W << "][" << H + 4 << "];\n";
   s << "  const int t = threadIdx.x;\n";
   s << "  const unsigned blocks = gridDim.x;\n";
@@ -562,7 +573,7 @@ Generated generate_fold(const Expr &e, int axis, FoldKind kind) {
   if (axis < 0 || axis >= e.rank) throw InvalidArgument{"fold axis out of range"};
   std::ostringstream s;
   s << preamble();
-  s << signature(e, "float* __restrict__ out") << " {\n";
+  s << signature(e, "float* __restrict__ out") << " {\n  topos_tables_init();\n";
   std::vector<int64_t> rest;
   std::vector<int> rest_axes;
   for (int d = 0; d < e.rank; ++d)
@@ -710,7 +721,7 @@ Generated generate_sum_count(const Expr &e) {
   validate(e);
   std::ostringstream s;
   s << preamble();
-  s << signature(e, "int* __restrict__ counts, int* __restrict__ positive_zero") << " {\n";
+  s << signature(e, "int* __restrict__ counts, int* __restrict__ positive_zero") << " {\n  topos_tables_init();\n";
   s << "  __shared__ int wave_counts[4];\n  __shared__ int wave_plus[4];\n";
   s << "  const long long chunk = blockIdx.x;\n";
   s << "  int nonzero = 0, plus_zero = 0;\n";
@@ -735,7 +746,7 @@ Generated generate_sum_compact(const Expr &e) {
   validate(e);
   std::ostringstream s;
   s << preamble();
-  s << signature(e, "const long long* __restrict__ offsets, float* __restrict__ compacted") << " {\n";
+  s << signature(e, "const long long* __restrict__ offsets, float* __restrict__ compacted") << " {\n  topos_tables_init();\n";
   s << "  __shared__ int wave_counts[4];\n";
   s << "  const long long chunk = blockIdx.x;\n";
   s << "  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;\n";
@@ -908,6 +919,39 @@ RowBlocking row_blocking(const RowProgram &p) {
   return b;
 }
 
+// The ordered sum of row[0 .. count) into `acc` (declared here): seeded with
+// the first term, ascending. Reads go out in batches of eight 16-byte LDS
+// loads ahead of their additions, so the chain of additions, not LDS
+// latency, sets the pace.
+void emit_lane_sum(std::ostringstream &s, const std::string &row, int64_t count, bool quads, const std::string &indent) {
+  if (quads && count % 4 == 0) {
+    const int64_t body = count / 32 * 32;
+    s << indent << "float acc;\n";
+    s << indent << "#pragma unroll 1\n";
+    s << indent << "for (int c = 0; c < " << body << "; c += 32) {\n";
+    s << indent << "  float4 w[8];\n";
+    s << indent << "  #pragma unroll\n";
+    s << indent << "  for (int k = 0; k < 8; ++k) w[k] = *(const float4*)&" << row << "[c + 4 * k];\n";
+    s << indent << "  if (c == 0) acc = w[0].x; else acc = acc + w[0].x;\n";
+    s << indent << "  acc = acc + w[0].y;\n  " << indent << "acc = acc + w[0].z;\n  " << indent << "acc = acc + w[0].w;\n";
+    s << indent << "  #pragma unroll\n";
+    s << indent << "  for (int k = 1; k < 8; ++k) { acc = acc + w[k].x; acc = acc + w[k].y; acc = acc + w[k].z; acc = acc + w[k].w; }\n";
+    s << indent << "}\n";
+    for (int64_t c = body; c < count; c += 4) {
+      s << indent << "{ const float4 w = *(const float4*)&" << row << "[" << c << "]; ";
+      if (c == 0)
+        s << "acc = w.x; ";
+      else
+        s << "acc = acc + w.x; ";
+      s << "acc = acc + w.y; acc = acc + w.z; acc = acc + w.w; }\n";
+    }
+    return;
+  }
+  s << indent << "float acc = " << row << "[0];\n";
+  s << indent << "#pragma unroll 16\n";
+  s << indent << "for (int c = 1; c < " << count << "; ++c) acc = acc + " << row << "[c];\n";
+}
+
 // Shared pieces of the two row-program layouts.
 struct RowEmit {
   const RowProgram &p;
@@ -964,7 +1008,7 @@ struct RowEmit {
   std::string fold_operand(const RowFold &f, const std::string &lane, const std::string &r) const {
     const std::string a = full_name(p.nodes[f.node].a, lane, r);
     if (!f.shifted_exp) return a;
-    return "topos_faithful::exp_f32(" + a + " - rowv[" + std::to_string(l.max_slot[f.node]) + "][" + r + "])";
+    return "topos_exp(" + a + " - rowv[" + std::to_string(l.max_slot[f.node]) + "][" + r + "])";
   }
   // Row nodes that become available at `level`, computed by lane t < G.
   void emit_row_stage(std::ostringstream &s, int level, int G) const {
@@ -989,11 +1033,11 @@ struct RowEmit {
         body << "    rowv[" << l.slot[k] << "][t] = " << v << ";\n";
         any = true;
       } else if (y.kind == RowNode::kLogSumExp) {
-        body << "    rowv[" << l.slot[k] << "][t] = rowv[" << l.max_slot[k] << "][t] + topos_faithful::ln_f32(rowv["
+        body << "    rowv[" << l.slot[k] << "][t] = rowv[" << l.max_slot[k] << "][t] + topos_ln(rowv["
              << l.total_slot[k] << "][t]);\n";
         any = true;
       } else if (y.kind == RowNode::kLogSoftmax) {
-        body << "    rowv[" << l.lns_slot[k] << "][t] = topos_faithful::ln_f32(rowv[" << l.total_slot[k] << "][t]);\n";
+        body << "    rowv[" << l.lns_slot[k] << "][t] = topos_ln(rowv[" << l.total_slot[k] << "][t]);\n";
         any = true;
       }
     }
@@ -1035,7 +1079,7 @@ Generated generate_row_resident(const RowProgram &p, const RowLayout &l, const R
   const int n = m.n;
   std::ostringstream s;
   s << preamble();
-  s << signature(m.e, m.tail()) << " {\n";
+  s << signature(m.e, m.tail()) << " {\n  topos_tables_init();\n";
   s << "  __shared__ float rowv[" << std::max(l.slots, 1) << "][" << G << "];\n";
   if (!l.folds.empty())
     s << "  __shared__ __attribute__((aligned(16))) float slab[" << G << "][" << C + 4 << "];\n";
@@ -1096,47 +1140,41 @@ Generated generate_row_resident(const RowProgram &p, const RowLayout &l, const R
         const std::vector<std::string> lanes = lanes_of(i);
         s << "  if (ok" << I << ") {\n";
         m.emit_nodes(s, nodes_needed, lanes, "r" + I, "    ");
-        for (int j = 0; j < V; ++j)
-          s << "    slab[r" << I << "][col" << I << " + " << j << "] = " << m.fold_operand(f, lanes[j], "r" + I) << ";\n";
+        if (V == 4) {
+          s << "    *(float4*)&slab[r" << I << "][col" << I << "] = make_float4(";
+          for (int j = 0; j < 4; ++j) s << (j ? ", " : "") << m.fold_operand(f, lanes[j], "r" + I);
+          s << ");\n";
+        } else {
+          s << "    slab[r" << I << "][col" << I << "] = " << m.fold_operand(f, lanes[0], "r" + I) << ";\n";
+        }
         s << "  }\n";
       }
       s << "  topos_lds_barrier();\n";
       if (f.max) {
-        // Contiguous segments folded in order, then combined in column order
-        // (the ordered fold of max_f32 splits at any point into the max_f32
-        // of its two halves' folds).
+        // The ordered max_f32 fold is the first occurrence of the largest
+        // non-NaN term (the last term when every term is NaN). Lane sg of a
+        // row's group takes columns sg, sg + per, ... (conflict-free LDS
+        // reads), keeping its first largest term and that term's column; the
+        // group then keeps the largest, earliest.
         s << "  {\n";
         s << "    const int rr = t / " << per << ", sg = t % " << per << ";\n";
-        s << "    const int cb = sg * " << seg << ";\n";
-        s << "    const int ce = cb + " << seg << " < " << C << " ? cb + " << seg << " : " << C << ";\n";
-        s << "    bool has = cb < ce;\n";
-        s << "    float mx = has ? slab[rr][cb] : 0.0f;\n";
-        s << "    for (int c = cb + 1; c < ce; ++c) mx = topos_faithful::max_f32(mx, slab[rr][c]);\n";
+        s << "    float mv = 0.0f;\n    int mi = -1;\n";
+        s << "    #pragma unroll 8\n";
+        s << "    for (int c = sg; c < " << C << "; c += " << per << ") {\n";
+        s << "      const float x = slab[rr][c];\n";
+        s << "      if (x == x && (mi < 0 || x > mv)) { mv = x; mi = c; }\n";
+        s << "    }\n";
         s << "    #pragma unroll\n";
         s << "    for (int off = 1; off < " << per << "; off <<= 1) {\n";
-        s << "      const float om = __shfl_xor(mx, off, 64);\n";
-        s << "      const bool oh = __shfl_xor((int)has, off, 64) != 0;\n";
-        s << "      const bool right = (t & off) != 0;\n";
-        s << "      const float lm = right ? om : mx, rm = right ? mx : om;\n";
-        s << "      const bool lh = right ? oh : has, rh = right ? has : oh;\n";
-        s << "      mx = !lh ? rm : (!rh ? lm : topos_faithful::max_f32(lm, rm));\n";
-        s << "      has = lh || rh;\n";
+        s << "      const float ov = __shfl_xor(mv, off, 64);\n";
+        s << "      const int oi = __shfl_xor(mi, off, 64);\n";
+        s << "      if (oi >= 0 && (mi < 0 || ov > mv || (!(mv > ov) && oi < mi))) { mv = ov; mi = oi; }\n";
         s << "    }\n";
-        s << "    if (sg == 0) rowv[" << f.target << "][rr] = mx;\n";
+        s << "    if (sg == 0) rowv[" << f.target << "][rr] = mi < 0 ? slab[rr][" << C - 1 << "] : mv;\n";
         s << "  }\n";
       } else {
         s << "  if (t < " << G << ") {\n";
-        if (V == 4) {
-          s << "    const float4 w0 = *(const float4*)&slab[t][0];\n";
-          s << "    float acc = w0.x;\n    acc = acc + w0.y;\n    acc = acc + w0.z;\n    acc = acc + w0.w;\n";
-          s << "    for (int c = 4; c < " << C << "; c += 4) {\n";
-          s << "      const float4 w = *(const float4*)&slab[t][c];\n";
-          s << "      acc = acc + w.x;\n      acc = acc + w.y;\n      acc = acc + w.z;\n      acc = acc + w.w;\n";
-          s << "    }\n";
-        } else {
-          s << "    float acc = slab[t][0];\n";
-          s << "    for (int c = 1; c < " << C << "; ++c) acc = acc + slab[t][c];\n";
-        }
+        emit_lane_sum(s, "slab[t]", C, V == 4, "    ");
         s << "    rowv[" << f.target << "][t] = acc;\n";
         s << "  }\n";
       }
@@ -1212,7 +1250,7 @@ Generated generate_row_program(const RowProgram &p) {
   for (size_t o = 0; o < p.full_outputs.size(); ++o) tail += "float* __restrict__ fo" + std::to_string(o) + ", ";
   for (size_t o = 0; o < p.row_outputs.size(); ++o) tail += "float* __restrict__ ro" + std::to_string(o) + ", ";
   tail += "int unused";
-  s << signature(e, tail) << " {\n";
+  s << signature(e, tail) << " {\n  topos_tables_init();\n";
   s << "  __shared__ float rowv[" << std::max(l.slots, 1) << "][" << G << "];\n";
   if (l.passes > 0)
     s << "  __shared__ __attribute__((aligned(16))) float slab[" << folds_per_pass << "][" << G << "][" << S + 4
@@ -1299,11 +1337,11 @@ Generated generate_row_program(const RowProgram &p) {
         body << "    rowv[" << l.slot[k] << "][t] = " << v << ";\n";
         any = true;
       } else if (y.kind == RowNode::kLogSumExp) {
-        body << "    rowv[" << l.slot[k] << "][t] = rowv[" << l.max_slot[k] << "][t] + topos_faithful::ln_f32(rowv["
+        body << "    rowv[" << l.slot[k] << "][t] = rowv[" << l.max_slot[k] << "][t] + topos_ln(rowv["
              << l.total_slot[k] << "][t]);\n";
         any = true;
       } else if (y.kind == RowNode::kLogSoftmax) {
-        body << "    rowv[" << l.lns_slot[k] << "][t] = topos_faithful::ln_f32(rowv[" << l.total_slot[k] << "][t]);\n";
+        body << "    rowv[" << l.lns_slot[k] << "][t] = topos_ln(rowv[" << l.total_slot[k] << "][t]);\n";
         any = true;
       }
     }
@@ -1355,13 +1393,18 @@ Generated generate_row_program(const RowProgram &p) {
         const std::string a = full_name(p.nodes[f.node].a, "p_" + std::to_string(v), "r");
         std::string value = a;
         if (f.shifted_exp)
-          value = "topos_faithful::exp_f32(" + a + " - rowv[" + std::to_string(l.max_slot[f.node]) + "][r])";
+          value = "topos_exp(" + a + " - rowv[" + std::to_string(l.max_slot[f.node]) + "][r])";
         s << "          v" << j << "_" << v << " = " << value << ";\n";
       }
     }
     s << "        }\n";
-    for (size_t j = 0; j < folds.size(); ++j)
-      for (int v = 0; v < V; ++v) s << "        slab[" << j << "][r][cu + " << v << "] = v" << j << "_" << v << ";\n";
+    for (size_t j = 0; j < folds.size(); ++j) {
+      if (V == 4)
+        s << "        *(float4*)&slab[" << j << "][r][cu] = make_float4(v" << j << "_0, v" << j << "_1, v" << j << "_2, v" << j
+          << "_3);\n";
+      else
+        s << "        slab[" << j << "][r][cu] = v" << j << "_0;\n";
+    }
     s << "      }\n";
     s << "      topos_lds_barrier();\n";
     s << "      if (t < " << G << ") {\n";

@@ -99,7 +99,7 @@ static const LogRow kLogTableHost[16] = {
 // 1.5 * 2^52 shift; 2^(k/32) = table[k mod 32] with k/32 added to the exponent
 // field; 2^(r/32) by a cubic. The product x * 32/ln2 is fused into both the
 // shift addition and the remainder subtraction, as the FMA build of glibc does.
-TOPOS_HD float exp_f32(float x) {
+TOPOS_HD float exp_f32_table(float x, const uint64_t *table) {
   const double inv_ln2_scaled = 0x1.71547652b82fep+0 * 32;
   const double shift = 0x1.8p+52;
   const double c0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32;
@@ -117,7 +117,7 @@ TOPOS_HD float exp_f32(float x) {
   const uint64_t ki = bits_of(kd);
   kd -= shift;
   const double r = __builtin_fma(inv_ln2_scaled, xd, -kd);
-  uint64_t t = TOPOS_EXP_TABLE[ki % 32];
+  uint64_t t = table[ki % 32];
   t += ki << (52 - 5);
   const double s = double_of(t);
   const double z = __builtin_fma(c0, r, c1);
@@ -128,10 +128,13 @@ TOPOS_HD float exp_f32(float x) {
   return (float)y;
 }
 
+// e^x with the built-in table (a kernel may pass a copy it keeps in LDS).
+TOPOS_HD float exp_f32(float x) { return exp_f32_table(x, TOPOS_EXP_TABLE); }
+
 // ln x. x = 2^k z with z in [0x3f330000, 2 * 0x3f330000); the top four
 // mantissa bits of z pick c; ln x = log1p(z/c - 1) + ln c + k ln2 with a cubic
 // for log1p, evaluated with the fused multiply-adds of glibc's FMA build.
-TOPOS_HD float ln_f32(float x) {
+TOPOS_HD float ln_f32_table(float x, const LogRow *table) {
   const double ln2 = 0x1.62e42fefa39efp-1;
   const double a0 = -0x1.00ea348b88334p-2, a1 = 0x1.5575b0be00b6ap-2, a2 = -0x1.ffffef20a4123p-2;
   uint32_t ix = bits_of(x);
@@ -151,8 +154,8 @@ TOPOS_HD float ln_f32(float x) {
   const int i = (int)((tmp >> (23 - 4)) % 16);
   const int k = (int32_t)tmp >> 23;
   const uint32_t iz = ix - (tmp & 0xff800000u);
-  const double invc = TOPOS_LOG_TABLE[i].invc;
-  const double logc = TOPOS_LOG_TABLE[i].logc;
+  const double invc = table[i].invc;
+  const double logc = table[i].logc;
   const double z = (double)float_of(iz);
   const double r = __builtin_fma(z, invc, -1.0);
   const double y0 = __builtin_fma((double)k, ln2, logc);
@@ -162,6 +165,8 @@ TOPOS_HD float ln_f32(float x) {
   y = __builtin_fma(y, r2, y0 + r);
   return (float)y;
 }
+
+TOPOS_HD float ln_f32(float x) { return ln_f32_table(x, TOPOS_LOG_TABLE); }
 
 // e^x - 1 in single precision (fdlibm): reduce by k ln2 with a hi/lo split
 // of ln2, rational approximation on the primary range, then rescale.
