@@ -914,8 +914,14 @@ RowBlocking row_blocking(const RowProgram &p) {
       return b;
     }
   }
-  b.slab = (int)std::min<int64_t>(512, (c + b.width - 1) / b.width * b.width);
-  b.rows = (int)std::min<int64_t>(64, std::max<int64_t>(8, 4096 / b.slab));
+  // Streaming: up to 64 rows per workgroup while that leaves 1024
+  // workgroups (four per CU, so one workgroup's loads cover another's
+  // folds); a slab gives each lane 16 points (V = 1) or 8 quads.
+  const int64_t rows = p.rows();
+  b.rows = 64;
+  while (b.rows > 8 && (rows + b.rows - 1) / b.rows < 1024) b.rows /= 2;
+  const int per_lane = b.width == 4 ? 8 : 16;
+  b.slab = per_lane * 256 * b.width / b.rows;
   return b;
 }
 
@@ -1217,245 +1223,210 @@ Generated generate_row_resident(const RowProgram &p, const RowLayout &l, const R
   return make(s.str());
 }
 
-}  // namespace
-
-Generated generate_row_program(const RowProgram &p) {
-  if (p.rank < 1 || p.rank > kMaxRank) throw InvalidArgument{"row program rank"};
-  for (int d = 0; d < p.rank; ++d)
-    if (p.shape[d] <= 0) throw InvalidArgument{"row program shape"};
-  const RowLayout l = lay_out(p);
+Generated generate_row_streaming(const RowProgram &p, const RowLayout &l, const RowBlocking &b) {
+  const RowEmit m(p, l);
   const int64_t C = p.columns(), R = p.rows();
-  const RowBlocking blocking = row_blocking(p);
-  if (blocking.resident) return generate_row_resident(p, l, blocking);
-  const int V = blocking.width;
-  const int G = blocking.rows, S = blocking.slab;
-  const int n = (int)p.nodes.size();
-  const int inner = p.rank - 1;
-  // Inputs in row context must be constant along the row.
-  Expr e;  // the inputs over the full shape, for the shared emitters
-  e.rank = p.rank;
-  for (int d = 0; d < p.rank; ++d) e.shape[d] = p.shape[d];
-  e.inputs = p.inputs;
-  e.outputs.push_back(0);
+  const int V = b.width, G = b.rows, S = b.slab;
+  const int SV = S / V;               // points per row of a slab
+  const int PP = G * SV / 256;        // points per lane per slab
+  const int per = 256 / G;            // lanes per row in a max fold
+  const int n = m.n;
   int folds_per_pass = 1;
   for (int q = 0; q < l.passes; ++q) {
     int k = 0;
     for (const RowFold &f : l.folds) k += f.pass == q;
     folds_per_pass = std::max(folds_per_pass, k);
   }
-
   std::ostringstream s;
   s << preamble();
-  std::string tail;
-  for (size_t o = 0; o < p.full_outputs.size(); ++o) tail += "float* __restrict__ fo" + std::to_string(o) + ", ";
-  for (size_t o = 0; o < p.row_outputs.size(); ++o) tail += "float* __restrict__ ro" + std::to_string(o) + ", ";
-  tail += "int unused";
-  s << signature(e, tail) << " {\n  topos_tables_init();\n";
+  s << signature(m.e, m.tail()) << " {\n  topos_tables_init();\n";
   s << "  __shared__ float rowv[" << std::max(l.slots, 1) << "][" << G << "];\n";
   if (l.passes > 0)
     s << "  __shared__ __attribute__((aligned(16))) float slab[" << folds_per_pass << "][" << G << "][" << S + 4
       << "];\n";
   s << "  const int t = threadIdx.x;\n";
   s << "  const long long row0 = (long long)blockIdx.x * " << G << ";\n";
-
-  // ---- emitters ----
-  // The name of a reference's value in full context (lane `lane`, row `r`).
-  auto full_name = [&](const RowRef &x, const std::string &lane, const std::string &r) -> std::string {
-    if (x.kind == RowRef::kInput) return ref(-x.index - 1, lane);
-    if (p.nodes[x.index].full()) return "f" + std::to_string(x.index) + "_" + lane;
-    return "rowv[" + std::to_string(l.slot[x.index]) + "][" + r + "]";
-  };
-  // Marks the full nodes and inputs that evaluating `x` needs.
-  std::function<void(const RowRef &, std::vector<bool> &, std::vector<bool> &)> need =
-      [&](const RowRef &x, std::vector<bool> &nodes_needed, std::vector<bool> &inputs_needed) {
-        if (x.kind == RowRef::kInput) {
-          inputs_needed[x.index] = true;
-          return;
-        }
-        const RowNode &y = p.nodes[x.index];
-        if (!y.full() || nodes_needed[x.index]) return;
-        nodes_needed[x.index] = true;
-        need(y.a, nodes_needed, inputs_needed);
-        if (y.kind == RowNode::kFullOp && is_binary(y.op)) need(y.b, nodes_needed, inputs_needed);
-      };
-  // Emits the values of the needed inputs and full nodes at the point(s)
-  // (row r of the block, column `col`), V lanes named tag_j.
-  auto emit_point = [&](const std::vector<bool> &nodes_needed, const std::vector<bool> &inputs_needed,
-                        const std::string &col, const std::string &tag, const std::string &indent) {
+  s << "  const int rr = t / " << per << ", sg = t % " << per << ";\n";
+  auto lanes_of = [&](int i) {
     std::vector<std::string> lanes;
-    for (int j = 0; j < V; ++j) lanes.push_back(tag + "_" + std::to_string(j));
-    s << indent << "const long long g_" << tag << " = row0 + r;\n";
-    std::vector<std::string> c;
-    if (p.rank > 1) emit_coordinates(s, p.rank - 1, p.shape, "g_" + tag, tag, c);
-    c.push_back(col);
-    if (V == 4) {
-      emit_quad_inputs(s, e, c, tag, lanes, indent, &inputs_needed);
-    } else {
-      for (size_t i = 0; i < p.inputs.size(); ++i)
-        if (inputs_needed[i])
-          s << indent << "const float " << ref(-(int)i - 1, lanes[0]) << " = " << scalar_value(e, (int)i, c) << ";\n";
-    }
-    for (int k = 0; k < n; ++k) {
-      if (!nodes_needed[k]) continue;
-      const RowNode &y = p.nodes[k];
-      for (const std::string &lane : lanes) {
-        std::string value;
-        const std::string a = full_name(y.a, lane, "r");
-        if (y.kind == RowNode::kLogSoftmax) {
-          value = "((" + a + " - rowv[" + std::to_string(l.max_slot[k]) + "][r]) - rowv[" +
-                  std::to_string(l.lns_slot[k]) + "][r])";
-        } else if (is_unary(y.op)) {
-          value = substitute(unary_pattern(y.op), a, "");
-        } else {
-          value = substitute(binary_pattern(y.op), a, full_name(y.b, lane, "r"));
-        }
-        s << indent << "const float f" << k << "_" << lane << " = " << value << ";\n";
-      }
-    }
+    for (int j = 0; j < V; ++j) lanes.push_back("s" + std::to_string(i) + "_" + std::to_string(j));
+    return lanes;
   };
-  // Row-context value of a reference, for lane t of the fold wave.
-  auto row_name = [&](const RowRef &x) -> std::string {
-    if (x.kind == RowRef::kInput) return "rin" + std::to_string(x.index);
-    return "rowv[" + std::to_string(l.slot[x.index]) + "][t]";
-  };
-  // Row nodes that become available at `level`, computed by lane t < G.
-  auto emit_row_stage = [&](int level) {
-    std::ostringstream body;
-    std::vector<bool> inputs_needed(p.inputs.size(), false);
-    bool any = false;
-    for (int k = 0; k < n; ++k) {
-      const RowNode &y = p.nodes[k];
-      if ((y.full() && y.kind != RowNode::kLogSoftmax) || l.avail[k] != level) continue;
-      if (y.kind == RowNode::kRowOp) {
-        for (const RowRef *x : {&y.a, &y.b}) {
-          if (x == &y.b && !is_binary(y.op)) break;
-          if (x->kind == RowRef::kInput) inputs_needed[x->index] = true;
+  for (int i = 0; i < PP; ++i) {
+    s << "  const int r" << i << " = (t + " << 256 * i << ") / " << SV << ";\n";
+    s << "  const int cu" << i << " = ((t + " << 256 * i << ") % " << SV << ") * " << V << ";\n";
+  }
+  // Declares registers for the loaded inputs of each point (literals as
+  // constants), then emits the loads of the slab at column `c0`: one straight
+  // run of loads when the slab lies wholly inside the rows and columns.
+  auto declare = [&](const std::vector<bool> &loaded, const std::vector<bool> &inputs_needed) {
+    for (int i = 0; i < PP; ++i)
+      for (const std::string &lane : lanes_of(i))
+        for (size_t k = 0; k < p.inputs.size(); ++k) {
+          if (!inputs_needed[k]) continue;
+          if (p.inputs[k].kind == ExprInput::kLiteral)
+            s << "  const float " << ref(-(int)k - 1, lane) << " = " << float_literal(p.inputs[k].one) << ";\n";
+          else if (loaded[k])
+            s << "  float " << ref(-(int)k - 1, lane) << " = 0.0f;\n";
         }
-        const std::string a = row_name(y.a);
-        const std::string v = is_unary(y.op) ? substitute(unary_pattern(y.op), a, "")
-                                             : substitute(binary_pattern(y.op), a, row_name(y.b));
-        body << "    rowv[" << l.slot[k] << "][t] = " << v << ";\n";
-        any = true;
-      } else if (y.kind == RowNode::kLogSumExp) {
-        body << "    rowv[" << l.slot[k] << "][t] = rowv[" << l.max_slot[k] << "][t] + topos_ln(rowv["
-             << l.total_slot[k] << "][t]);\n";
-        any = true;
-      } else if (y.kind == RowNode::kLogSoftmax) {
-        body << "    rowv[" << l.lns_slot[k] << "][t] = topos_ln(rowv[" << l.total_slot[k] << "][t]);\n";
-        any = true;
-      }
-    }
-    if (!any) return;
-    s << "  if (t < " << G << ") {\n";
-    bool inputs = false;
-    for (bool b : inputs_needed) inputs = inputs || b;
-    if (inputs) {
-      s << "    const long long g_row = row0 + t;\n";
+  };
+  auto load = [&](const std::vector<bool> &loaded, const std::string &c0, const std::string &indent) {
+    auto one = [&](int i, bool guarded, const std::string &ind) {
+      const std::string I = std::to_string(i);
+      s << ind << "{\n";
+      s << ind << "  const long long g = row0 + r" << I << ";\n";
+      s << ind << "  const long long col = " << c0 << " + cu" << I << ";\n";
+      if (guarded) s << ind << "  if (g < " << ll(R) << " && col < " << ll(C) << ") {\n";
       std::vector<std::string> c;
-      if (p.rank > 1) emit_coordinates(s, p.rank - 1, p.shape, "g_row", "row", c);
-      c.push_back("0LL");
-      for (size_t i = 0; i < p.inputs.size(); ++i) {
-        if (!inputs_needed[i]) continue;
-        const ExprInput &in = p.inputs[i];
-        if (in.kind == ExprInput::kSelection || (in.kind == ExprInput::kPadded && in.pad_axis == inner) ||
-            (in.kind != ExprInput::kLiteral && in.strides[inner] != 0))
-          throw InvalidArgument{"row program: a row operand varies along the row"};
-        s << "    const float rin" << i << " = (g_row < " << ll(R) << ") ? " << scalar_value(e, (int)i, c)
-          << " : 0.0f;\n";
+      if (p.rank > 1) emit_coordinates(s, p.rank - 1, p.shape, "g", "s" + I, c);
+      c.push_back("col");
+      const std::vector<std::string> lanes = lanes_of(i);
+      if (V == 4) {
+        emit_quad_inputs(s, m.e, c, "s" + I, lanes, ind + "    ", &loaded, false);
+      } else {
+        for (size_t k = 0; k < p.inputs.size(); ++k)
+          if (loaded[k]) s << ind << "    " << ref(-(int)k - 1, lanes[0]) << " = " << scalar_value(m.e, (int)k, c) << ";\n";
       }
-    }
-    s << body.str();
-    s << "  }\n";
+      if (guarded) s << ind << "  }\n";
+      s << ind << "}\n";
+    };
+    s << indent << "if (row0 + " << G << " <= " << ll(R) << " && " << c0 << " + " << S << " <= " << ll(C) << ") {\n";
+    for (int i = 0; i < PP; ++i) one(i, false, indent + "  ");
+    s << indent << "} else {\n";
+    for (int i = 0; i < PP; ++i) one(i, true, indent + "  ");
+    s << indent << "}\n";
+  };
+  auto loaded_of = [&](const std::vector<bool> &inputs_needed) {
+    std::vector<bool> loaded(p.inputs.size(), false);
+    for (size_t k = 0; k < p.inputs.size(); ++k) loaded[k] = inputs_needed[k] && p.inputs[k].kind != ExprInput::kLiteral;
+    return loaded;
   };
 
-  emit_row_stage(0);
+  m.emit_row_stage(s, 0, G);
   s << "  topos_lds_barrier();\n";
   for (int q = 0; q < l.passes; ++q) {
     std::vector<const RowFold *> folds;
     for (const RowFold &f : l.folds)
       if (f.pass == q) folds.push_back(&f);
     std::vector<bool> nodes_needed(n, false), inputs_needed(p.inputs.size(), false);
-    for (const RowFold *f : folds) need(p.nodes[f->node].a, nodes_needed, inputs_needed);
+    for (const RowFold *f : folds) m.need(p.nodes[f->node].a, nodes_needed, inputs_needed);
+    const std::vector<bool> loaded = loaded_of(inputs_needed);
     s << "  {\n";
-    for (size_t j = 0; j < folds.size(); ++j) s << "    float acc" << j << " = 0.0f;\n";
-    s << "    for (long long c0 = 0; c0 < " << ll(C) << "; c0 += " << S << ") {\n";
-    s << "      for (int u = t; u < " << G * (S / V) << "; u += 256) {\n";
-    s << "        const int r = u / " << S / V << ";\n";
-    s << "        const int cu = (u % " << S / V << ") * " << V << ";\n";
-    s << "        const long long col = c0 + cu;\n";
-    for (size_t j = 0; j < folds.size(); ++j)
-      for (int v = 0; v < V; ++v) s << "        float v" << j << "_" << v << " = 0.0f;\n";
-    s << "        if (row0 + r < " << ll(R) << " && col < " << ll(C) << ") {\n";
-    emit_point(nodes_needed, inputs_needed, "col", "p", "          ");
     for (size_t j = 0; j < folds.size(); ++j) {
-      const RowFold &f = *folds[j];
-      for (int v = 0; v < V; ++v) {
-        const std::string a = full_name(p.nodes[f.node].a, "p_" + std::to_string(v), "r");
-        std::string value = a;
-        if (f.shifted_exp)
-          value = "topos_exp(" + a + " - rowv[" + std::to_string(l.max_slot[f.node]) + "][r])";
-        s << "          v" << j << "_" << v << " = " << value << ";\n";
+      if (folds[j]->max)
+        s << "  float mv" << j << " = 0.0f;\n  int mi" << j << " = -1;\n";
+      else
+        s << "  float acc" << j << " = 0.0f;\n";
+    }
+    declare(loaded, inputs_needed);
+    load(loaded, "0LL", "  ");
+    s << "  for (long long c0 = 0; c0 < " << ll(C) << "; c0 += " << S << ") {\n";
+    // This slab's operands into LDS.
+    for (int i = 0; i < PP; ++i) {
+      const std::string I = std::to_string(i);
+      const std::vector<std::string> lanes = lanes_of(i);
+      s << "    if (c0 + cu" << I << " < " << ll(C) << ") {\n";
+      m.emit_nodes(s, nodes_needed, lanes, "r" + I, "      ");
+      for (size_t j = 0; j < folds.size(); ++j) {
+        if (V == 4) {
+          s << "      *(float4*)&slab[" << j << "][r" << I << "][cu" << I << "] = make_float4(";
+          for (int v = 0; v < 4; ++v) s << (v ? ", " : "") << m.fold_operand(*folds[j], lanes[v], "r" + I);
+          s << ");\n";
+        } else {
+          s << "      slab[" << j << "][r" << I << "][cu" << I << "] = " << m.fold_operand(*folds[j], lanes[0], "r" + I)
+            << ";\n";
+        }
+      }
+      s << "    }\n";
+    }
+    // The next slab's loads, in flight during the folds.
+    s << "    if (c0 + " << S << " < " << ll(C) << ") {\n";
+    load(loaded, "(c0 + " + std::to_string(S) + ")", "      ");
+    s << "    }\n";
+    s << "    topos_lds_barrier();\n";
+    s << "    const int width = " << ll(C) << " - c0 < " << S << " ? (int)(" << ll(C) << " - c0) : " << S << ";\n";
+    for (size_t j = 0; j < folds.size(); ++j) {
+      const std::string J = std::to_string(j);
+      if (folds[j]->max) {
+        s << "    {\n";
+        s << "      float sv = 0.0f;\n      int si = -1;\n";
+        s << "      #pragma unroll 4\n";
+        s << "      for (int c = sg; c < width; c += " << per << ") {\n";
+        s << "        const float x = slab[" << J << "][rr][c];\n";
+        s << "        if (x == x && (si < 0 || x > sv)) { sv = x; si = c; }\n";
+        s << "      }\n";
+        s << "      #pragma unroll\n";
+        s << "      for (int off = 1; off < " << per << "; off <<= 1) {\n";
+        s << "        const float ov = __shfl_xor(sv, off, 64);\n";
+        s << "        const int oi = __shfl_xor(si, off, 64);\n";
+        s << "        if (oi >= 0 && (si < 0 || ov > sv || (!(sv > ov) && oi < si))) { sv = ov; si = oi; }\n";
+        s << "      }\n";
+        // Earlier slabs hold earlier columns: they win ties.
+        s << "      if (si >= 0 && (mi" << J << " < 0 || sv > mv" << J << ")) { mv" << J << " = sv; mi" << J
+          << " = (int)c0 + si; }\n";
+        s << "    }\n";
+      } else {
+        s << "    if (t < " << G << ") {\n";
+        s << "      int c = 0;\n";
+        s << "      if (c0 == 0) { acc" << J << " = slab[" << J << "][t][0]; c = 1; }\n";
+        if (V == 4) {
+          s << "      for (; c < width && (c & 3); ++c) acc" << J << " = acc" << J << " + slab[" << J << "][t][c];\n";
+          s << "      #pragma unroll 4\n";
+          s << "      for (; c + 4 <= width; c += 4) {\n";
+          s << "        const float4 w = *(const float4*)&slab[" << J << "][t][c];\n";
+          s << "        acc" << J << " = acc" << J << " + w.x; acc" << J << " = acc" << J << " + w.y; acc" << J << " = acc"
+            << J << " + w.z; acc" << J << " = acc" << J << " + w.w;\n";
+          s << "      }\n";
+        }
+        s << "      #pragma unroll 8\n";
+        s << "      for (; c < width; ++c) acc" << J << " = acc" << J << " + slab[" << J << "][t][c];\n";
+        s << "    }\n";
       }
     }
-    s << "        }\n";
-    for (size_t j = 0; j < folds.size(); ++j) {
-      if (V == 4)
-        s << "        *(float4*)&slab[" << j << "][r][cu] = make_float4(v" << j << "_0, v" << j << "_1, v" << j << "_2, v" << j
-          << "_3);\n";
-      else
-        s << "        slab[" << j << "][r][cu] = v" << j << "_0;\n";
-    }
-    s << "      }\n";
-    s << "      topos_lds_barrier();\n";
-    s << "      if (t < " << G << ") {\n";
-    s << "        const int width = " << ll(C) << " - c0 < " << S << " ? (int)(" << ll(C) << " - c0) : " << S << ";\n";
-    s << "        int q0 = 0;\n";
-    s << "        if (c0 == 0) {\n";
-    for (size_t j = 0; j < folds.size(); ++j) s << "          acc" << j << " = slab[" << j << "][t][0];\n";
-    s << "          q0 = 1;\n        }\n";
-    s << "        #pragma unroll 8\n";
-    s << "        for (int q = q0; q < width; ++q) {\n";
-    for (size_t j = 0; j < folds.size(); ++j) {
-      const std::string x = "slab[" + std::to_string(j) + "][t][q]";
-      if (folds[j]->max)
-        s << "          acc" << j << " = topos_faithful::max_f32(acc" << j << ", " << x << ");\n";
-      else
-        s << "          acc" << j << " = acc" << j << " + " << x << ";\n";
-    }
-    s << "        }\n      }\n";
-    s << "      topos_lds_barrier();\n";
-    s << "    }\n";
-    s << "    if (t < " << G << ") {\n";
-    for (size_t j = 0; j < folds.size(); ++j) s << "      rowv[" << folds[j]->target << "][t] = acc" << j << ";\n";
-    s << "    }\n";
+    s << "    topos_lds_barrier();\n";
     s << "  }\n";
-    emit_row_stage(q + 1);
+    // Results: the last slab is still in LDS for an all-NaN max (its last term).
+    const int64_t last_slab = (C - 1) / S * S;
+    for (size_t j = 0; j < folds.size(); ++j) {
+      const std::string J = std::to_string(j);
+      if (folds[j]->max)
+        s << "  if (sg == 0) rowv[" << folds[j]->target << "][rr] = mi" << J << " < 0 ? slab[" << J << "][rr]["
+          << C - 1 - last_slab << "] : mv" << J << ";\n";
+      else
+        s << "  if (t < " << G << ") rowv[" << folds[j]->target << "][t] = acc" << J << ";\n";
+    }
+    s << "  }\n";
+    m.emit_row_stage(s, q + 1, G);
     s << "  topos_lds_barrier();\n";
   }
   for (int level = l.passes + 1; level <= l.levels; ++level) {
-    emit_row_stage(level);
+    m.emit_row_stage(s, level, G);
     s << "  topos_lds_barrier();\n";
   }
-  // The output pass.
   if (!p.full_outputs.empty()) {
     std::vector<bool> nodes_needed(n, false), inputs_needed(p.inputs.size(), false);
-    for (int o : p.full_outputs) need(RowRef{RowRef::kFull, o}, nodes_needed, inputs_needed);
-    s << "  for (long long u = t; u < " << ll((int64_t)G * (C / V)) << "; u += 256) {\n";
-    s << "    const int r = (int)(u / " << ll(C / V) << ");\n";
-    s << "    const long long col = (u % " << ll(C / V) << ") * " << V << ";\n";
-    s << "    if (row0 + r < " << ll(R) << ") {\n";
-    emit_point(nodes_needed, inputs_needed, "col", "o", "      ");
-    s << "      const long long at = (row0 + r) * " << ll(C) << " + col;\n";
-    for (size_t o = 0; o < p.full_outputs.size(); ++o) {
-      const int k = p.full_outputs[o];
-      if (V == 4) {
-        s << "      *(topos_f4*)(fo" << o << " + at) = topos_f4{f" << k << "_o_0, f" << k << "_o_1, f" << k << "_o_2, f"
-          << k << "_o_3};\n";
-      } else {
-        s << "      fo" << o << "[at] = f" << k << "_o_0;\n";
+    for (int o : p.full_outputs) m.need(RowRef{RowRef::kFull, o}, nodes_needed, inputs_needed);
+    const std::vector<bool> loaded = loaded_of(inputs_needed);
+    s << "  for (long long c0 = 0; c0 < " << ll(C) << "; c0 += " << S << ") {\n";
+    declare(loaded, inputs_needed);
+    load(loaded, "c0", "    ");
+    for (int i = 0; i < PP; ++i) {
+      const std::string I = std::to_string(i);
+      const std::vector<std::string> lanes = lanes_of(i);
+      s << "    if (row0 + r" << I << " < " << ll(R) << " && c0 + cu" << I << " < " << ll(C) << ") {\n";
+      m.emit_nodes(s, nodes_needed, lanes, "r" + I, "      ");
+      s << "      const long long at = (row0 + r" << I << ") * " << ll(C) << " + c0 + cu" << I << ";\n";
+      for (size_t o = 0; o < p.full_outputs.size(); ++o) {
+        const int k = p.full_outputs[o];
+        if (V == 4)
+          s << "      *(topos_f4*)(fo" << o << " + at) = topos_f4{f" << k << "_" << lanes[0] << ", f" << k << "_"
+            << lanes[1] << ", f" << k << "_" << lanes[2] << ", f" << k << "_" << lanes[3] << "};\n";
+        else
+          s << "      fo" << o << "[at] = f" << k << "_" << lanes[0] << ";\n";
       }
+      s << "    }\n";
     }
-    s << "    }\n  }\n";
+    s << "  }\n";
   }
   if (!p.row_outputs.empty()) {
     s << "  if (t < " << G << " && row0 + t < " << ll(R) << ") {\n";
@@ -1465,6 +1436,18 @@ Generated generate_row_program(const RowProgram &p) {
   }
   s << "}\n";
   return make(s.str());
+}
+
+}  // namespace
+
+Generated generate_row_program(const RowProgram &p) {
+  if (p.rank < 1 || p.rank > kMaxRank) throw InvalidArgument{"row program rank"};
+  for (int d = 0; d < p.rank; ++d)
+    if (p.shape[d] <= 0) throw InvalidArgument{"row program shape"};
+  const RowLayout l = lay_out(p);
+  const RowBlocking blocking = row_blocking(p);
+  if (blocking.resident) return generate_row_resident(p, l, blocking);
+  return generate_row_streaming(p, l, blocking);
 }
 
 void launch_row_program(const Generated &g, const RowProgram &p, const void *const *inputs,

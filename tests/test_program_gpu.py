@@ -292,11 +292,11 @@ def test_long_column_folds_exact(hip):
         assert_bitwise(got[r.id], want[r.id], f"node {r.id} {r.shape}")
 
 
-@pytest.mark.parametrize("rows, columns", [(37, 1100), (24, 1028), (130, 40), (9, 3)])
+@pytest.mark.parametrize("rows, columns", [(37, 1100), (24, 1028), (130, 40), (9, 3), (5, 9001), (70, 3000)])
 def test_row_groups_exact(hip, rows, columns):
     """Row programs (groups of row-local nodes with last-axis reductions):
-    several column slabs, a partial last row block, quads and single
-    columns, row operands broadcast back along the row, LogSumExp and
+    register-resident rows and streamed wide rows (several column slabs),
+    a partial last row block, quads and single columns, row operands broadcast back along the row, LogSumExp and
     LogSoftmax with fused operands and consumers, a ReLU member, and a row
     input: bit-identical to the interpreter."""
     banner(f"program row groups {rows}x{columns}")
