@@ -8,13 +8,13 @@
 //
 // Shape: a BM x BN output tile per workgroup of 64 * (BM / 64) * (BN / 64)
 // lanes, each wave owning a 64x64 block (2x2 MFMA blocks of 32x32). Tiles are
-// 128x128, or 128x64 / 64x128 when one output extent is at most 64 (the
-// attention products with a 64-wide head), so no half-empty tiles are
-// launched. k is staged 16 deep through LDS, double-buffered: the next slab's
+// 256x128 (eight waves) for products with enough tiles, 128x128, or 128x64 /
+// 64x128 when one output extent is at most 64 (the attention products with a
+// 64-wide head), so no half-empty tiles are launched. k is staged 16 deep through LDS, double-buffered: the next slab's
 // global loads are in flight while the current slab feeds the matrix cores.
 // LDS holds both operands k-major ([k][outer]) so an MFMA fragment is one
-// 32-lane b32 read; rows are padded to 148 (128-wide) or 84 (64-wide) floats,
-// 20 mod 64 banks, which measured fastest for both the fragment reads and the
+// 32-lane b32 read; rows are padded by 20 floats (276, 148 or 84: 20 mod 64
+// banks), which measured fastest for both the fragment reads and the
 // transposing stores of k-contiguous operands. A tile wholly inside the
 // operands takes a branch-free load path (one uniform test per slab); only
 // edge tiles pay per-element bounds checks.
@@ -222,15 +222,20 @@ __global__ __launch_bounds__(BM * BN / 64) void gemm_mfma_kernel(
     }
 }
 
-// The tile shape for an m x n product: 128x128, or a 64-wide side when that
-// output extent is at most 64.
+// The tile shape for an m x n product (over `batches`): 128x64 or 64x128
+// when one output extent is at most 64; 256x128 (eight waves, less operand
+// traffic per flop than 128x128) when its tiles fill whole rounds of two
+// workgroups per CU, or at least two such rounds; else 128x128. `per_cu` is how many of its workgroups a CU
+// holds at once.
 struct TileShape {
-  int bm, bn;
+  int bm, bn, per_cu;
 };
-TileShape tile_shape(int64_t m, int64_t n) {
-  if (n <= 64 && m > 64) return {128, 64};
-  if (m <= 64 && n > 64) return {64, 128};
-  return {128, 128};
+TileShape tile_shape(int64_t m, int64_t n, int64_t batches) {
+  if (n <= 64 && m > 64) return {128, 64, 3};
+  if (m <= 64 && n > 64) return {64, 128, 3};
+  const int64_t wide = ((m + 255) / 256) * ((n + 127) / 128) * batches;
+  if (wide >= 1024 || (wide >= 512 && wide % 512 == 0)) return {256, 128, 2};
+  return {128, 128, 3};
 }
 
 template <int BM, int BN, bool kL, bool kR>
@@ -283,15 +288,16 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float *__restri
 }  // namespace
 
 int mfma_splits(int64_t m, int64_t n, int64_t k, int64_t batches) {
-  // Three workgroups per CU (the kernel's occupancy) is 768 over the 256 CUs;
-  // a product with fewer tiles is split along k until it reaches that, each
-  // split at least 256 deep, and deep products are split further (up to 2048
+  // A full chip holds per_cu workgroups on each of the 256 CUs; a product
+  // with fewer tiles is split along k until it reaches that, each split at
+  // least 256 deep, and deep products are split further (up to 2048
   // workgroups while each split stays 512 deep): measured on MI355X, the
   // partial products' extra traffic costs less than idle CUs.
-  const TileShape shape = tile_shape(m, n);
+  const TileShape shape = tile_shape(m, n, batches);
   const int64_t tiles = ((m + shape.bm - 1) / shape.bm) * ((n + shape.bn - 1) / shape.bn) * batches;
-  if (tiles >= 768 || k < 512) return 1;
-  int64_t splits = std::min<int64_t>((768 + tiles - 1) / tiles, k / 256);
+  const int64_t full = 256 * shape.per_cu;
+  if (tiles >= full || k < 512) return 1;
+  int64_t splits = std::min<int64_t>((full + tiles - 1) / tiles, k / 256);
   while (splits * 2 * tiles <= 2048 && k / (splits * 2) >= 512) splits *= 2;
   splits = std::min<int64_t>(splits, 16);
   return (int)std::max<int64_t>(splits, 1);
@@ -312,7 +318,7 @@ bool launch_gemm_mfma(const float *a, int64_t a_rs, int64_t a_cs, const float *b
   // 16-byte loads need a unit stride along the axis the lanes step on (any
   // 4-byte alignment serves).
   const bool vector = (lk ? a_cs == 1 : a_rs == 1) && (rk ? b_rs == 1 : b_cs == 1);
-  const TileShape shape = tile_shape(m, n);
+  const TileShape shape = tile_shape(m, n, batch.count);
   const int64_t gm = (m + shape.bm - 1) / shape.bm;
   const int64_t gn = (n + shape.bn - 1) / shape.bn;
   if (gm * gn > 0x7fffffff || batch.count > 65535 || batch.count < 1) throw Unsupported{"mfma gemm: grid too large"};
@@ -330,7 +336,9 @@ bool launch_gemm_mfma(const float *a, int64_t a_rs, int64_t a_cs, const float *b
   float *target = splits > 1 ? workspace : c;
   const int64_t target_ld = splits > 1 ? n : ldc;
   const int64_t target_bs = splits > 1 ? m * n : batch.c_stride;
-  if (shape.bn == 64)
+  if (shape.bm == 256)
+    dispatch_orientation<256, 128>(lk, rk, vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, target, target_ld, (int)gm, (int)gn, batch, target_bs, split_len, split_stride);
+  else if (shape.bn == 64)
     dispatch_orientation<128, 64>(lk, rk, vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, target, target_ld, (int)gm, (int)gn, batch, target_bs, split_len, split_stride);
   else if (shape.bm == 64)
     dispatch_orientation<64, 128>(lk, rk, vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, target, target_ld, (int)gm, (int)gn, batch, target_bs, split_len, split_stride);
