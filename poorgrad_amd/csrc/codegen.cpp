@@ -389,11 +389,46 @@ Generated generate_chain(const Expr &e) {
   for (size_t o = 0; o < e.outputs.size(); ++o) tail += (o ? ", " : "") + std::string("float* __restrict__ q") + std::to_string(o);
   s << signature(e, tail) << " {\n  topos_tables_init();\n";
   const int64_t volume = e.volume();
+  const std::vector<std::string> lanes = {"0", "1", "2", "3"};
+  const int64_t inner_extent = e.rank > 0 ? e.shape[e.rank - 1] : 1;
+  if (e.rank > 0 && inner_extent % 4 != 0 && inner_extent >= 8) {
+    // An odd innermost extent: quads run along each row from its start
+    // (16-byte accesses at any alignment), the row's last partial quad lane
+    // by lane.
+    const int64_t quads_per_row = (inner_extent + 3) / 4;
+    const int64_t total = volume / inner_extent * quads_per_row;
+    s << "  for (long long qi = (long long)blockIdx.x * 256 + threadIdx.x; qi < " << ll(total)
+      << "; qi += (long long)gridDim.x * 256) {\n";
+    s << "    const long long row = qi / " << ll(quads_per_row) << ";\n";
+    s << "    const long long cq = (qi % " << ll(quads_per_row) << ") * 4;\n";
+    s << "    const long long base = row * " << ll(inner_extent) << " + cq;\n";
+    s << "    if (cq + 4 <= " << ll(inner_extent) << ") {\n";
+    std::vector<std::string> c;
+    if (e.rank > 1) emit_coordinates(s, e.rank - 1, e.shape, "row", "q", c);
+    c.push_back("cq");
+    emit_quad_inputs(s, e, c, "q", lanes, "      ");
+    emit_steps(s, e, lanes);
+    for (size_t o = 0; o < e.outputs.size(); ++o) {
+      s << "      *(topos_f4*)(q" << o << " + base) = topos_f4{";
+      for (int j = 0; j < 4; ++j) s << (j ? ", " : "") << ref(e.outputs[o], lanes[j]);
+      s << "};\n";
+    }
+    s << "    } else {\n";
+    s << "      for (int j = 0; cq + j < " << ll(inner_extent) << "; ++j) {\n";
+    s << "        const long long f = base + j;\n";
+    std::vector<std::string> cg;
+    emit_coordinates(s, e.rank, e.shape, "f", "g", cg);
+    for (size_t i = 0; i < e.inputs.size(); ++i)
+      s << "        const float in" << i << "_g = " << scalar_value(e, (int)i, cg) << ";\n";
+    emit_steps(s, e, {"g"});
+    for (size_t o = 0; o < e.outputs.size(); ++o) s << "        q" << o << "[f] = " << ref(e.outputs[o], "g") << ";\n";
+    s << "      }\n    }\n  }\n}\n";
+    return make(s.str());
+  }
   s << "  const long long volume = " << ll(volume) << ";\n";
   s << "  const long long stride = (long long)gridDim.x * 1024;\n";
   s << "  for (long long base = ((long long)blockIdx.x * 256 + threadIdx.x) * 4; base < volume; base += stride) {\n";
   const bool quads = e.rank > 0 && e.shape[e.rank - 1] % 4 == 0;
-  const std::vector<std::string> lanes = {"0", "1", "2", "3"};
   if (quads) {
     s << "    {\n";
     std::vector<std::string> c;

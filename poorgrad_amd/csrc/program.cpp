@@ -565,9 +565,16 @@ struct topos_hip_program {
     return true;
   }
 
+  bool is_selection_node(int64_t i) const {
+    const topos_hip_node &x = nodes[i];
+    if (x.op == TOPOS_HIP_OP_INPUT) return (x.flags & TOPOS_HIP_NODE_SELECTION) != 0;
+    return x.op == TOPOS_HIP_OP_LEAF && leaves[x.slot].kind == TOPOS_HIP_LEAF_SELECTION;
+  }
+
   bool row_eligible(int64_t i, const RowGroup &g) const {
     const topos_hip_node &x = nodes[i];
     if (!wanted[i] || group_of[i] >= 0 || alias_of[i] >= 0) return false;
+    if (x.op == TOPOS_HIP_OP_SUM_ALONG && is_selection_node(x.operands[0])) return false;
     const int last = g.rank - 1;
     if (is_elementwise(x.op)) return x.op != TOPOS_HIP_OP_POWF && (group_full(x, g) || group_row(x, g));
     switch (x.op) {
@@ -589,6 +596,7 @@ struct topos_hip_program {
       if (x.op == TOPOS_HIP_OP_SUM_ALONG || x.op == TOPOS_HIP_OP_LOG_SUM_EXP) {
         const topos_hip_node &a = nodes[x.operands[0]];
         if (x.params[0] != a.rank - 1) continue;
+        if (x.op == TOPOS_HIP_OP_SUM_ALONG && is_selection_node(x.operands[0])) continue;
         g.rank = a.rank;
         for (int d = 0; d < a.rank; ++d) g.shape[d] = a.shape[d];
       } else if (x.op == TOPOS_HIP_OP_LOG_SOFTMAX) {
@@ -1429,6 +1437,17 @@ struct topos_hip_program {
     return e;
   }
 
+  // A selection's ordered sums are fixed by `one` and the shape: a row
+  // holds +0 everywhere but `one` at its index, so its fold is one + 0
+  // (one itself in a single-column row: +0 + one = one for every non-zero,
+  // and +0 for a zero `one`); the whole selection's row-major fold is the
+  // fold of one such value per row, since zero terms leave a non-zero
+  // accumulator unchanged.
+  float selection_row_sum(const Value &v, int64_t vocab) const {
+    const float one = storages[v.storage].one;
+    return vocab > 1 ? fold_scalar(TOPOS_HIP_OP_ADD, 0.0f, one) : one;
+  }
+
   void plan_sum_along(int64_t i) {
     const topos_hip_node &x = nodes[i];
     const int64_t operand = x.operands[0];
@@ -1436,6 +1455,10 @@ struct topos_hip_program {
     const Value &a = values[operand];
     if (a.kind == Value::kDense && a.host_known) {
       values[i] = host_constant(x, fold_repeated(a.host_value, nodes[operand].shape[axis]));
+      return;
+    }
+    if (a.kind == Value::kSelection && axis == 1) {
+      values[i] = host_constant(x, selection_row_sum(a, nodes[operand].shape[1]));
       return;
     }
     std::vector<int> storage_of;
@@ -1459,6 +1482,11 @@ struct topos_hip_program {
     const Value &a = values[operand];
     if (a.kind == Value::kDense && a.host_known) {
       values[i] = host_constant(x, fold_repeated(a.host_value, volume_of(nodes[operand])));
+      return;
+    }
+    if (a.kind == Value::kSelection) {
+      const topos_hip_node &o = nodes[operand];
+      values[i] = host_constant(x, fold_repeated(selection_row_sum(a, o.shape[1]), o.shape[0]));
       return;
     }
     std::vector<int> storage_of;

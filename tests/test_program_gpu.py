@@ -338,3 +338,24 @@ def test_row_groups_rank3_and_selection(hip):
     got, _ = run_device(tape, roots, [], dense, selections, hip.EXACT)
     for r in roots:
         assert_bitwise(got[r.id], want[r.id], f"node {r.id} {r.shape}")
+
+
+@pytest.mark.parametrize("one", [1.0, -0.0, 0.0, 2.5, -3.0e38, float("inf")])
+@pytest.mark.parametrize("vocab", [1, 7])
+def test_selection_sums_exact(hip, one, vocab):
+    """Sums of a selection (a one-hot [rows, vocab] with `one` at each row's
+    index and +0 elsewhere) along its rows and over everything: planned as
+    constants, bit-identical to the interpreter's ordered folds, signed zeros
+    and overflow included."""
+    banner(f"program selection sums one={one} vocab={vocab}")
+    rng = np.random.default_rng(vocab)
+    rows = 300
+    tape = t.Tape()
+    sel = tape.selection_input(rows, vocab, one)
+    v = tape.value(sel.id)
+    roots = [v.sum_along(1), v.sum(), (v.sum_along(1) * v.sum_along(1)).sum()]
+    selections = {sel.node.slot: (rng.integers(0, vocab, rows).astype(np.int32), one)}
+    want = run_oracle(tape, roots, [], {}, selections)
+    got, _ = run_device(tape, roots, [], {}, selections, hip.EXACT)
+    for r in roots:
+        assert_bitwise(got[r.id], want[r.id], f"node {r.id} {r.shape}")
