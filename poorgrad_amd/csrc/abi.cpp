@@ -243,7 +243,13 @@ int topos_hip_rows_f32_device(int reduction, const float *x, int64_t rows, int64
   if (numerics != TOPOS_HIP_EXACT && numerics != TOPOS_HIP_FAST) return TOPOS_HIP_INVALID_ARGUMENT;
   const int status = ready_for_device_face();
   if (status != TOPOS_HIP_OK) return status;
-  return guarded([&] { launch_rows(reduction, x, rows, columns, numerics, out, static_cast<hipStream_t>(stream)); });
+  if (reduction < TOPOS_HIP_ROWS_SUM || reduction > TOPOS_HIP_ROWS_LOG_SUM_EXP) return TOPOS_HIP_INVALID_ARGUMENT;
+  return guarded([&] {
+    if (numerics == TOPOS_HIP_EXACT)
+      launch_rows_program(reduction, x, rows, columns, out, static_cast<hipStream_t>(stream));
+    else
+      launch_rows(reduction, x, rows, columns, numerics, out, static_cast<hipStream_t>(stream));
+  });
 }
 
 int topos_hip_layer_norm_f32_device(const float *x, int64_t rows, int64_t columns,
@@ -254,7 +260,10 @@ int topos_hip_layer_norm_f32_device(const float *x, int64_t rows, int64_t column
   const int status = ready_for_device_face();
   if (status != TOPOS_HIP_OK) return status;
   return guarded([&] {
-    launch_layer_norm(x, rows, columns, scale, shift, epsilon, numerics, out, static_cast<hipStream_t>(stream));
+    if (numerics == TOPOS_HIP_EXACT)
+      launch_layer_norm_program(x, rows, columns, scale, shift, epsilon, out, static_cast<hipStream_t>(stream));
+    else
+      launch_layer_norm(x, rows, columns, scale, shift, epsilon, numerics, out, static_cast<hipStream_t>(stream));
   });
 }
 

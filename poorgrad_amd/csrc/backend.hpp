@@ -168,4 +168,11 @@ void launch_layer_norm(const float *x, int64_t rows, int64_t columns, const floa
                        const float *shift, float epsilon, int numerics, float *out,
                        hipStream_t stream);
 
+// rows_device.cpp: the exact posture of the two above as generated row
+// programs (cached per shape).
+void launch_rows_program(int reduction, const float *x, int64_t rows, int64_t columns, float *out,
+                         hipStream_t stream);
+void launch_layer_norm_program(const float *x, int64_t rows, int64_t columns, const float *scale,
+                               const float *shift, float epsilon, float *out, hipStream_t stream);
+
 }  // namespace topos_hip

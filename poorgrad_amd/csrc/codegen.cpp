@@ -1401,20 +1401,27 @@ Generated generate_row_streaming(const RowProgram &p, const RowLayout &l, const 
           << " = (int)c0 + si; }\n";
         s << "    }\n";
       } else {
+        // Blocks of 32 terms: eight 16-byte LDS reads go out ahead of the
+        // block's ordered additions.
+        const std::string A = "acc" + J;
         s << "    if (t < " << G << ") {\n";
-        s << "      int c = 0;\n";
-        s << "      if (c0 == 0) { acc" << J << " = slab[" << J << "][t][0]; c = 1; }\n";
-        if (V == 4) {
-          s << "      for (; c < width && (c & 3); ++c) acc" << J << " = acc" << J << " + slab[" << J << "][t][c];\n";
-          s << "      #pragma unroll 4\n";
-          s << "      for (; c + 4 <= width; c += 4) {\n";
-          s << "        const float4 w = *(const float4*)&slab[" << J << "][t][c];\n";
-          s << "        acc" << J << " = acc" << J << " + w.x; acc" << J << " = acc" << J << " + w.y; acc" << J << " = acc"
-            << J << " + w.z; acc" << J << " = acc" << J << " + w.w;\n";
-          s << "      }\n";
-        }
-        s << "      #pragma unroll 8\n";
-        s << "      for (; c < width; ++c) acc" << J << " = acc" << J << " + slab[" << J << "][t][c];\n";
+        s << "      const float *row = &slab[" << J << "][t][0];\n";
+        s << "      const int blocks = width / 32 * 32;\n";
+        s << "      #pragma unroll 1\n";
+        s << "      for (int c = 0; c < blocks; c += 32) {\n";
+        s << "        float4 w[8];\n";
+        s << "        #pragma unroll\n";
+        s << "        for (int k = 0; k < 8; ++k) w[k] = *(const float4*)&row[c + 4 * k];\n";
+        s << "        if (c0 == 0 && c == 0) " << A << " = w[0].x; else " << A << " = " << A << " + w[0].x;\n";
+        s << "        " << A << " = " << A << " + w[0].y; " << A << " = " << A << " + w[0].z; " << A << " = " << A
+          << " + w[0].w;\n";
+        s << "        #pragma unroll\n";
+        s << "        for (int k = 1; k < 8; ++k) { " << A << " = " << A << " + w[k].x; " << A << " = " << A
+          << " + w[k].y; " << A << " = " << A << " + w[k].z; " << A << " = " << A << " + w[k].w; }\n";
+        s << "      }\n";
+        s << "      for (int c = blocks; c < width; ++c) {\n";
+        s << "        if (c0 == 0 && c == 0) " << A << " = row[0]; else " << A << " = " << A << " + row[c];\n";
+        s << "      }\n";
         s << "    }\n";
       }
     }
