@@ -381,6 +381,18 @@ bool is_binary(int op) { return binary_pattern(op) != nullptr; }
 
 // ---- chain ----
 
+namespace {
+
+// Quads per lane per loop iteration of an aligned chain: enough loads in
+// flight to cover HBM latency, within a register budget.
+int chain_unroll(const Expr &e) {
+  int loaded = 0;
+  for (const ExprInput &in : e.inputs) loaded += in.kind != ExprInput::kLiteral;
+  return loaded <= 3 ? 4 : 2;
+}
+
+}  // namespace
+
 Generated generate_chain(const Expr &e) {
   validate(e);
   std::ostringstream s;
@@ -425,33 +437,63 @@ Generated generate_chain(const Expr &e) {
     s << "      }\n    }\n  }\n}\n";
     return make(s.str());
   }
-  s << "  const long long volume = " << ll(volume) << ";\n";
-  s << "  const long long stride = (long long)gridDim.x * 1024;\n";
-  s << "  for (long long base = ((long long)blockIdx.x * 256 + threadIdx.x) * 4; base < volume; base += stride) {\n";
   const bool quads = e.rank > 0 && e.shape[e.rank - 1] % 4 == 0;
   if (quads) {
-    s << "    {\n";
+    // U quads per lane per iteration, all loads issued before any use; a
+    // block whose U * 256 quads lie wholly inside takes the unguarded path.
+    const int U = chain_unroll(e);
+    const int64_t span = 1024LL * U;
+    s << "  for (long long block = (long long)blockIdx.x * " << span << "; block < " << ll(volume)
+      << "; block += (long long)gridDim.x * " << span << ") {\n";
+    s << "    if (block + " << span << " <= " << ll(volume) << ") {\n";
+    std::vector<std::string> all_lanes;
+    for (int u = 0; u < U; ++u) {
+      const std::string tag = "q" + std::to_string(u);
+      std::vector<std::string> lanes_u;
+      for (int j = 0; j < 4; ++j) lanes_u.push_back(tag + "_" + std::to_string(j));
+      all_lanes.insert(all_lanes.end(), lanes_u.begin(), lanes_u.end());
+      s << "      const long long base_" << tag << " = block + (" << 256 * u << " + threadIdx.x) * 4;\n";
+      std::vector<std::string> c;
+      emit_coordinates(s, e.rank, e.shape, "base_" + tag, tag, c);
+      emit_quad_inputs(s, e, c, tag, lanes_u, "      ");
+    }
+    emit_steps(s, e, all_lanes);
+    for (int u = 0; u < U; ++u) {
+      const std::string tag = "q" + std::to_string(u);
+      for (size_t o = 0; o < e.outputs.size(); ++o) {
+        s << "      *(topos_f4*)(q" << o << " + base_" << tag << ") = topos_f4{";
+        for (int j = 0; j < 4; ++j) s << (j ? ", " : "") << ref(e.outputs[o], tag + "_" + std::to_string(j));
+        s << "};\n";
+      }
+    }
+    s << "    } else {\n";
+    s << "      for (int u = 0; u < " << U << "; ++u) {\n";
+    s << "        const long long base = block + (u * 256 + threadIdx.x) * 4;\n";
+    s << "        if (base >= " << ll(volume) << ") break;\n";
     std::vector<std::string> c;
     emit_coordinates(s, e.rank, e.shape, "base", "q", c);
-    emit_quad_inputs(s, e, c, "q", lanes, "      ");
+    emit_quad_inputs(s, e, c, "q", lanes, "        ");
     emit_steps(s, e, lanes);
     for (size_t o = 0; o < e.outputs.size(); ++o) {
-      s << "      *(topos_f4*)(q" << o << " + base) = topos_f4{";
+      s << "        *(topos_f4*)(q" << o << " + base) = topos_f4{";
       for (int j = 0; j < 4; ++j) s << (j ? ", " : "") << ref(e.outputs[o], lanes[j]);
       s << "};\n";
     }
-    s << "    }\n";
-  } else {
-    s << "    for (int j = 0; j < 4 && base + j < volume; ++j) {\n";
-    s << "      const long long f = base + j;\n";
-    std::vector<std::string> c;
-    if (e.rank > 0) emit_coordinates(s, e.rank, e.shape, "f", "g", c);
-    for (size_t i = 0; i < e.inputs.size(); ++i)
-      s << "      const float in" << i << "_g = " << scalar_value(e, (int)i, c) << ";\n";
-    emit_steps(s, e, {"g"});
-    for (size_t o = 0; o < e.outputs.size(); ++o) s << "      q" << o << "[f] = " << ref(e.outputs[o], "g") << ";\n";
-    s << "    }\n";
+    s << "      }\n    }\n  }\n}\n";
+    return make(s.str());
   }
+  s << "  const long long volume = " << ll(volume) << ";\n";
+  s << "  const long long stride = (long long)gridDim.x * 1024;\n";
+  s << "  for (long long base = ((long long)blockIdx.x * 256 + threadIdx.x) * 4; base < volume; base += stride) {\n";
+  s << "    for (int j = 0; j < 4 && base + j < volume; ++j) {\n";
+  s << "      const long long f = base + j;\n";
+  std::vector<std::string> c;
+  if (e.rank > 0) emit_coordinates(s, e.rank, e.shape, "f", "g", c);
+  for (size_t i = 0; i < e.inputs.size(); ++i)
+    s << "      const float in" << i << "_g = " << scalar_value(e, (int)i, c) << ";\n";
+  emit_steps(s, e, {"g"});
+  for (size_t o = 0; o < e.outputs.size(); ++o) s << "      q" << o << "[f] = " << ref(e.outputs[o], "g") << ";\n";
+  s << "    }\n";
   s << "  }\n}\n";
   return make(s.str());
 }
@@ -463,7 +505,9 @@ void launch_generated_chain(const Generated &g, const Expr &e, const void *const
   for (size_t o = 0; o < e.outputs.size(); ++o) pointers.push_back(outputs[o]);
   std::vector<void *> arguments;
   for (auto &p : pointers) arguments.push_back(&p);
-  int64_t blocks = (e.volume() + 1023) / 1024;
+  const bool quads = e.rank > 0 && e.shape[e.rank - 1] % 4 == 0;
+  const int64_t per_block = quads ? 1024LL * chain_unroll(e) : 1024;
+  int64_t blocks = (e.volume() + per_block - 1) / per_block;
   if (blocks < 1) blocks = 1;
   if (blocks > 256 * 16) blocks = 256 * 16;
   launch(g, (unsigned)blocks, arguments, stream);
