@@ -271,17 +271,35 @@ void dispatch_orientation(bool lk, bool rk, bool vector, dim3 grid, hipStream_t 
 
 // The fixed-order sum of `splits` partial products (each [count][m][n],
 // contiguous) into c: partial 0 seeds, then 1, 2, ... are added in order, so
-// the result is the same on every run.
-__global__ __launch_bounds__(256) void split_reduce_kernel(const float *__restrict__ partials, int splits,
-                                                           int64_t split_stride, int64_t m, int64_t n,
-                                                           int64_t count, float *__restrict__ c, int64_t ldc,
-                                                           int64_t c_bs) {
-  const int64_t total = count * m * n;
-  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (int64_t)gridDim.x * blockDim.x) {
-    float acc = partials[e];
-    for (int s = 1; s < splits; ++s) acc += partials[s * split_stride + e];
-    const int64_t q = e / (m * n), r = (e / n) % m, col = e % n;
-    c[q * c_bs + r * ldc + col] = acc;
+// the result is the same on every run. Four consecutive elements per lane:
+// every split's 16-byte load is issued before the additions. (The caller
+// guarantees n % 4 == 0, so a quad never leaves its row.)
+__global__ __launch_bounds__(256) void split_reduce_kernel(const float4 *__restrict__ partials, int splits,
+                                                           int64_t split_quads, int64_t m, int64_t n,
+                                                           float *__restrict__ c, int64_t ldc, int64_t c_bs) {
+  constexpr int kMax = 16;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < split_quads;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    float4 v[kMax];
+#pragma unroll
+    for (int s = 0; s < kMax; ++s)
+      if (s < splits) v[s] = partials[s * split_quads + e];
+    float4 acc = v[0];
+#pragma unroll
+    for (int s = 1; s < kMax; ++s)
+      if (s < splits) {
+        acc.x = acc.x + v[s].x;
+        acc.y = acc.y + v[s].y;
+        acc.z = acc.z + v[s].z;
+        acc.w = acc.w + v[s].w;
+      }
+    const int64_t f = e * 4;
+    const int64_t q = f / (m * n), r = (f / n) % m, col = f % n;
+    float *out = c + q * c_bs + r * ldc + col;
+    out[0] = acc.x;
+    out[1] = acc.y;
+    out[2] = acc.z;
+    out[3] = acc.w;
   }
 }
 
@@ -324,7 +342,9 @@ bool launch_gemm_mfma(const float *a, int64_t a_rs, int64_t a_cs, const float *b
   if (gm * gn > 0x7fffffff || batch.count > 65535 || batch.count < 1) throw Unsupported{"mfma gemm: grid too large"};
   int splits = mfma_splits(m, n, k, batch.count);
   const int64_t split_stride = batch.count * m * n;
-  if (splits > 1 && (!workspace || workspace_floats < splits * split_stride)) splits = 1;
+  if (splits > 1 && (!workspace || workspace_floats < splits * split_stride || n % 4 != 0 ||
+                     reinterpret_cast<uintptr_t>(workspace) % 16 != 0 || splits > 16))
+    splits = 1;
   int64_t split_len = k;
   if (splits > 1) {
     split_len = ((k + splits - 1) / splits + kTileK - 1) / kTileK * kTileK;
@@ -346,11 +366,11 @@ bool launch_gemm_mfma(const float *a, int64_t a_rs, int64_t a_cs, const float *b
     dispatch_orientation<128, 128>(lk, rk, vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, target, target_ld, (int)gm, (int)gn, batch, target_bs, split_len, split_stride);
   check_launch("gemm_mfma_kernel launch");
   if (splits > 1) {
-    const int64_t total = split_stride;
-    int64_t blocks = (total + 255) / 256;
+    const int64_t quads = split_stride / 4;
+    int64_t blocks = (quads + 255) / 256;
     if (blocks > 256 * 32) blocks = 256 * 32;
-    split_reduce_kernel<<<(unsigned)blocks, 256, 0, stream>>>(workspace, splits, split_stride, m, n, batch.count, c,
-                                                              ldc, batch.c_stride);
+    split_reduce_kernel<<<(unsigned)blocks, 256, 0, stream>>>(reinterpret_cast<const float4 *>(workspace), splits,
+                                                              quads, m, n, c, ldc, batch.c_stride);
     check_launch("split_reduce_kernel launch");
   }
   return true;
