@@ -138,6 +138,10 @@ void launch_gemm_exact(const float *a, int64_t a_rs, int64_t a_cs, const float *
 // along k into that many partial products, reduced in a fixed order
 // (deterministic; envelope fidelity like the unsplit kernel).
 int mfma_splits(int64_t m, int64_t n, int64_t k, int64_t batches);
+// Whether launch_gemm_mfma takes operands with these strides (else the
+// caller's exact fallback runs). Its products are never -0: every
+// accumulator starts at +0, and a sum of +0 with any zero is +0.
+bool mfma_serves(int64_t a_rs, int64_t a_cs, int64_t b_rs, int64_t b_cs, int64_t m, int64_t k, int64_t n);
 bool launch_gemm_mfma(const float *a, int64_t a_rs, int64_t a_cs, const float *b, int64_t b_rs,
                       int64_t b_cs, int64_t m, int64_t k, int64_t n, float *c, int64_t ldc,
                       hipStream_t stream, const Batch &batch = Batch(), float *workspace = nullptr,

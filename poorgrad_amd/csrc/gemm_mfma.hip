@@ -321,16 +321,20 @@ int mfma_splits(int64_t m, int64_t n, int64_t k, int64_t batches) {
   return (int)std::max<int64_t>(splits, 1);
 }
 
+bool mfma_serves(int64_t a_rs, int64_t a_cs, int64_t b_rs, int64_t b_cs, int64_t m, int64_t k, int64_t n) {
+  // Orientation: each operand needs a unit stride along k or along its outer
+  // axis; an extent-1 axis leaves its stride unused (any value serves).
+  const bool left = a_cs == 1 || m == 1 || a_rs == 1 || k == 1;
+  const bool right = b_rs == 1 || n == 1 || b_cs == 1 || k == 1;
+  return left && right;
+}
+
 bool launch_gemm_mfma(const float *a, int64_t a_rs, int64_t a_cs, const float *b, int64_t b_rs,
                       int64_t b_cs, int64_t m, int64_t k, int64_t n, float *c, int64_t ldc,
                       hipStream_t stream, const Batch &batch, float *workspace, int64_t workspace_floats) {
-  // Orientation: each operand needs a unit stride along k or along its outer
-  // axis; an extent-1 axis leaves its stride unused (any value serves).
+  if (!mfma_serves(a_rs, a_cs, b_rs, b_cs, m, k, n)) return false;
   const bool left_inner_k = a_cs == 1 || m == 1;
-  const bool left_outer = a_rs == 1 || k == 1;
   const bool right_inner_k = b_rs == 1 || n == 1;
-  const bool right_outer = b_cs == 1 || k == 1;
-  if (!(left_inner_k || left_outer) || !(right_inner_k || right_outer)) return false;
   const bool lk = left_inner_k && !(a_rs == 1 && a_cs != 1);
   const bool rk = right_inner_k && !(b_cs == 1 && b_rs != 1);
   // 16-byte loads need a unit stride along the axis the lanes step on (any

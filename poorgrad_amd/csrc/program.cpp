@@ -257,6 +257,7 @@ struct topos_hip_program {
 
   // ---- the plan ----
   std::vector<bool> wanted, readable;
+  std::vector<bool> mfma_product;  // a product the matrix-core kernel computes (never -0)
   std::vector<std::vector<int>> consumers;
   std::vector<Value> values;
   std::vector<Storage> storages;
@@ -1259,6 +1260,20 @@ struct topos_hip_program {
     }
     if (x.op == TOPOS_HIP_OP_POWF)
       throw Unsupported{"node " + std::to_string(i) + ": Powf is served for host-known constant operands only"};
+    // +0 + p (or p + +0) of a matrix-core product p is p itself: the
+    // addition only maps -0 to +0, and such products are never -0 (the
+    // zero-seeded gradient accumulation behind every backward product).
+    if (x.op == TOPOS_HIP_OP_ADD) {
+      for (int side = 0; side < 2; ++side) {
+        const Value &zero = values[x.operands[side]];
+        const int64_t product = x.operands[1 - side];
+        if (zero.kind == Value::kDense && zero.host_known && __builtin_bit_cast(uint32_t, zero.host_value) == 0 &&
+            mfma_product[product] && values[product].kind == Value::kDense) {
+          values[i] = values[product];
+          return;
+        }
+      }
+    }
     if (all_constant) {
       // A Constant payload computed at run time: one element, rank 0.
       Expr e;
@@ -1388,6 +1403,7 @@ struct topos_hip_program {
     const int64_t ars = a.layout.strides[s], acs = a.layout.strides[s + 1];
     const int64_t brs = b.layout.strides[s], bcs = b.layout.strides[s + 1];
     const int numerics_ = numerics;
+    mfma_product[i] = numerics == TOPOS_HIP_FAST && mfma_serves(ars, acs, brs, bcs, m, k, n);
     // Scratch for the partial products of a split along k (fast posture).
     int64_t workspace_floats = 0;
     int workspace = -1;
@@ -1817,6 +1833,7 @@ struct topos_hip_program {
     mark_wanted();
     form_row_groups();
     values.assign(nodes.size(), Value());
+    mfma_product.assign(nodes.size(), false);
     for (int64_t i = 0; i < (int64_t)nodes.size(); ++i) {
       if (!wanted[i] || alias_of[i] >= 0) continue;
       const int group = group_of[i];

@@ -359,3 +359,27 @@ def test_selection_sums_exact(hip, one, vocab):
     got, _ = run_device(tape, roots, [], {}, selections, hip.EXACT)
     for r in roots:
         assert_bitwise(got[r.id], want[r.id], f"node {r.id} {r.shape}")
+
+
+def test_fast_zero_seeded_product_is_the_product(hip):
+    """Under Fast, +0 + p of a matrix-core product is planned as p itself:
+    the addition only maps -0 to +0, and the matrix-core accumulators start
+    at +0, so a product whose terms are all -0 (or cancel) is +0 already."""
+    banner("program fast zero-seeded product")
+    tape = t.Tape()
+    a = tape.input((64, 32))
+    b = tape.input((32, 48))
+    zero = tape.leaf(t.Constant((64, 48), 0.0))
+    p = a.matmul(b)
+    roots = [zero + p]
+    av = np.full((64, 32), -0.0, np.float32)
+    av[1] = 1.0
+    av[2, :2] = [1.0, -1.0]
+    bv = np.abs(np.random.default_rng(3).standard_normal((32, 48))).astype(np.float32)
+    bv[:2] = 1.0
+    got, program = run_device(tape, roots, [], {a.node.slot: av, b.node.slot: bv}, numerics=hip.FAST)
+    assert "chain" not in program.describe, program.describe
+    out = got[roots[0].id]
+    assert (out[0].view(np.uint32) == 0).all() and (out[2].view(np.uint32) == 0).all()  # +0, never -0
+    want = run_oracle(tape, roots, [], {a.node.slot: av, b.node.slot: bv})[roots[0].id]
+    assert np.allclose(out, want, rtol=1e-5, atol=0)
