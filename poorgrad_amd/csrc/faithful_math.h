@@ -261,13 +261,12 @@ TOPOS_HD float tanh_f32(float x) {
     if (ix == 0) return x;
     if (ix < 0x24000000) return x * (one + x);  // |x| < 2^-55
     const float ax = __builtin_fabsf(x);
-    if (ix >= 0x3f800000) {
-      t = expm1_f32(two * ax);
-      z = one - two / (t + two);
-    } else {
-      t = expm1_f32(-two * ax);
-      z = -t / (t + two);
-    }
+    // One expm1 for both ranges (its argument and the quotient selected per
+    // lane), so lanes of a wave on either side of 1 share one evaluation.
+    const bool large = ix >= 0x3f800000;
+    t = expm1_f32(large ? two * ax : -two * ax);
+    const float q = (large ? two : -t) / (t + two);
+    z = large ? one - q : q;
   } else {
     z = one - tiny;
   }
