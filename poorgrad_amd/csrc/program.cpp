@@ -92,31 +92,60 @@ bool is_contiguous(const Layout &l) {
   return true;
 }
 
-// Layout::reshape (layout.rs): a contiguous layout takes any shape; else the
-// unit-axis view when only extent-1 axes move; else None.
+// Layout::reshape (layout.rs:...) answers a contiguous layout for any shape
+// and a unit-axis view when only extent-1 axes move; otherwise the
+// interpreter copies the elements out in logical order. Any layout whose
+// groups of merged source axes are themselves contiguous is a view of the
+// same elements in the same logical order, so it is taken as a view here
+// too (no value changes: a copy and a view read identical elements).
 bool reshape_view(const Layout &from, int rank, const int64_t *shape, Layout &out) {
   if (is_contiguous(from)) {
     out = contiguous(rank, shape, from.offset);
     return true;
   }
-  std::vector<std::pair<int64_t, int64_t>> source;
+  // Source and target axes without the extent-1 ones.
+  std::vector<int64_t> os, ost, ns;
+  std::vector<int> nidx;
   for (int d = 0; d < from.rank; ++d)
-    if (from.shape[d] != 1) source.push_back({from.shape[d], from.strides[d]});
-  size_t next = 0;
+    if (from.shape[d] != 1) {
+      os.push_back(from.shape[d]);
+      ost.push_back(from.strides[d]);
+    }
+  for (int d = 0; d < rank; ++d)
+    if (shape[d] != 1) {
+      ns.push_back(shape[d]);
+      nidx.push_back(d);
+    }
+  std::vector<int64_t> nst(ns.size(), 0);
+  size_t oi = 0, ni = 0;
+  while (oi < os.size() && ni < ns.size()) {
+    int64_t op = os[oi], np = ns[ni];
+    size_t oj = oi + 1, nj = ni + 1;
+    while (op != np) {
+      if (np < op) {
+        if (nj >= ns.size()) return false;
+        np *= ns[nj++];
+      } else {
+        if (oj >= os.size()) return false;
+        op *= os[oj++];
+      }
+    }
+    for (size_t k = oi; k + 1 < oj; ++k)
+      if (ost[k] != ost[k + 1] * os[k + 1]) return false;  // merged axes must be contiguous
+    nst[nj - 1] = ost[oj - 1];
+    for (size_t k = nj - 1; k-- > ni;) nst[k] = nst[k + 1] * ns[k + 1];
+    oi = oj;
+    ni = nj;
+  }
+  if (oi != os.size() || ni != ns.size()) return false;
   Layout l;
   l.rank = rank;
   l.offset = from.offset;
   for (int d = 0; d < rank; ++d) {
     l.shape[d] = shape[d];
-    if (shape[d] == 1) {
-      l.strides[d] = 0;
-      continue;
-    }
-    if (next >= source.size() || source[next].first != shape[d]) return false;
-    l.strides[d] = source[next].second;
-    ++next;
+    l.strides[d] = 0;
   }
-  if (next != source.size()) return false;
+  for (size_t k = 0; k < ns.size(); ++k) l.strides[nidx[k]] = nst[k];
   out = l;
   return true;
 }
@@ -144,6 +173,8 @@ struct Value {
   bool constant = false;
   bool host_known = false;
   float host_value = 0.0f;
+  // No element is -0 (a matrix-core product, and views of one).
+  bool never_minus_zero = false;
 };
 
 // Device buffers of a bound selection: its indices and their row-sorted
@@ -1260,16 +1291,17 @@ struct topos_hip_program {
     }
     if (x.op == TOPOS_HIP_OP_POWF)
       throw Unsupported{"node " + std::to_string(i) + ": Powf is served for host-known constant operands only"};
-    // +0 + p (or p + +0) of a matrix-core product p is p itself: the
-    // addition only maps -0 to +0, and such products are never -0 (the
-    // zero-seeded gradient accumulation behind every backward product).
+    // +0 + v (or v + +0) of a value with no -0 element is v itself: the
+    // addition only maps -0 to +0. Matrix-core products are never -0, nor are
+    // views of them (the zero-seeded gradient accumulation behind every
+    // backward product, and behind the views its gradient flows through).
     if (x.op == TOPOS_HIP_OP_ADD) {
       for (int side = 0; side < 2; ++side) {
         const Value &zero = values[x.operands[side]];
-        const int64_t product = x.operands[1 - side];
+        const Value &v = values[x.operands[1 - side]];
         if (zero.kind == Value::kDense && zero.host_known && __builtin_bit_cast(uint32_t, zero.host_value) == 0 &&
-            mfma_product[product] && values[product].kind == Value::kDense) {
-          values[i] = values[product];
+            v.kind == Value::kDense && v.never_minus_zero) {
+          values[i] = v;
           return;
         }
       }
@@ -1439,6 +1471,7 @@ struct topos_hip_program {
     launches.back().flops = 2.0 * (double)batches * m * n * k;
     launches.back().bytes = 4.0 * (double)batches * ((double)m * k + (double)k * n + (double)m * n);
     values[i] = dense_value(out, contiguous(x.rank, x.shape));
+    values[i].never_minus_zero = mfma_product[i];
   }
 
   // The expression a reduction folds: the operand's inlined tree, or the

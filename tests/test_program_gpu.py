@@ -383,3 +383,23 @@ def test_fast_zero_seeded_product_is_the_product(hip):
     assert (out[0].view(np.uint32) == 0).all() and (out[2].view(np.uint32) == 0).all()  # +0, never -0
     want = run_oracle(tape, roots, [], {a.node.slot: av, b.node.slot: bv})[roots[0].id]
     assert np.allclose(out, want, rtol=1e-5, atol=0)
+
+
+def test_strided_reshape_views_exact(hip):
+    """Reshapes that split strided axes are views; reshapes that merge
+    strided axes copy: both read the interpreter's elements in logical
+    order."""
+    banner("program strided reshape views")
+    rng = np.random.default_rng(17)
+    tape = t.Tape()
+    fused = tape.input((48, 36))
+    q = fused.narrow(1, 12, 12).reshape((2, 24, 3, 4))          # split a strided row axis: a view
+    heads = q.permute((0, 2, 1, 3)).reshape((6, 24, 4))         # merge strided axes: copied
+    back = heads.reshape((2, 3, 24, 4)).permute((0, 2, 1, 3)).reshape((48, 12))
+    roots = [q * q, heads.matmul(heads.permute((0, 2, 1))), back + fused.narrow(1, 0, 12),
+             fused.transpose().narrow(0, 3, 8).reshape((2, 4, 48)).sum_along(1)]
+    dense = {fused.node.slot: rng.standard_normal((48, 36)).astype(np.float32)}
+    want = run_oracle(tape, roots, [], dense)
+    got, _ = run_device(tape, roots, [], dense, numerics=hip.EXACT)
+    for r in roots:
+        assert_bitwise(got[r.id], want[r.id], f"node {r.id} {r.shape}")

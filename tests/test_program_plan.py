@@ -83,11 +83,14 @@ v = a.transpose().narrow(0, 1, 4).reshape((4, 1, 8)).permute((2, 0, 1))   # a un
 s = v.sum_along(0)
 p = DeviceProgram(tape, [s])
 print(p.info["launches"])
-w = a.transpose().narrow(0, 1, 4).reshape((2, 2, 8)).sum_along(0)         # not a view: copied first
+w = a.transpose().narrow(0, 1, 4).reshape((2, 2, 8)).sum_along(0)         # splitting a strided axis: a view
 q = DeviceProgram(tape, [w])
 print(q.info["launches"])
+u = a.transpose().reshape((48,)).reshape((6, 8)).sum_along(0)              # merging strided axes: copied first
+r = DeviceProgram(tape, [u])
+print(r.info["launches"])
 ''')
-    assert out.splitlines()[:2] == ["1", "2"], out
+    assert out.splitlines()[:3] == ["1", "1", "2"], out
 
 
 def test_mlp_step_plans_with_side_branches_and_an_arena():
