@@ -127,6 +127,15 @@ struct Batch {
   int64_t a_stride = 0, b_stride = 0, c_stride = 0;
 };
 
+// A per-column vector added to a product as it is written: c = p + bias[j]
+// (or bias[j] + p when `bias_first`), the interpreter's separate addition
+// (one f32 rounding) fused into the store (linear layers' bias).
+struct Epilogue {
+  const float *bias = nullptr;
+  int64_t bias_stride = 0;
+  bool bias_first = false;
+};
+
 // gemm_exact.hip: bit-identical to src/payload/gemm.rs:140-211.
 void launch_gemm_exact(const float *a, int64_t a_rs, int64_t a_cs, const float *b, int64_t b_rs,
                        int64_t b_cs, int64_t m, int64_t k, int64_t n, float *c, int64_t ldc,
@@ -145,7 +154,7 @@ bool mfma_serves(int64_t a_rs, int64_t a_cs, int64_t b_rs, int64_t b_cs, int64_t
 bool launch_gemm_mfma(const float *a, int64_t a_rs, int64_t a_cs, const float *b, int64_t b_rs,
                       int64_t b_cs, int64_t m, int64_t k, int64_t n, float *c, int64_t ldc,
                       hipStream_t stream, const Batch &batch = Batch(), float *workspace = nullptr,
-                      int64_t workspace_floats = 0);
+                      int64_t workspace_floats = 0, const Epilogue &epilogue = Epilogue());
 
 // index.hip
 void launch_gather(const float *table, int64_t row_stride, int64_t column_stride, const int32_t *indices,

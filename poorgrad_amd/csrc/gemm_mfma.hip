@@ -118,7 +118,8 @@ template <int BM, int BN, bool kLeftInnerK, bool kRightInnerK, bool kVector>
 __global__ __launch_bounds__(BM * BN / 64) void gemm_mfma_kernel(
     const float *__restrict__ a, int64_t a_rs, int64_t a_cs, const float *__restrict__ b,
     int64_t b_rs, int64_t b_cs, int64_t m, int64_t k, int64_t n, float *__restrict__ c, int64_t ldc,
-    int grid_m, int grid_n, int64_t a_bs, int64_t b_bs, int64_t c_bs, int64_t split_len, int64_t split_stride) {
+    int grid_m, int grid_n, int64_t a_bs, int64_t b_bs, int64_t c_bs, int64_t split_len, int64_t split_stride,
+    const float *__restrict__ bias, int64_t bias_cs, int bias_mode) {
   constexpr int T = BM * BN / 64;  // one 64x64 block per wave
   constexpr int WN = BN / 64;
   __shared__ float left[2][kTileK][BM + kPad];
@@ -214,10 +215,15 @@ __global__ __launch_bounds__(BM * BN / 64) void gemm_mfma_kernel(
     for (int j = 0; j < 2; ++j) {
       const int64_t col = n0 + wn + 32 * j + (lane % 32);
       if (col >= n) continue;
+      // bias_mode: 0 the product, 1 product + bias[col], 2 bias[col] + product.
+      const float add = bias_mode != 0 ? bias[col * bias_cs] : 0.0f;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int64_t row = m0 + wm + 32 * i + 8 * (r / 4) + 4 * (lane / 32) + (r % 4);
-        if (row < m) c[row * ldc + col] = acc[i][j][r];
+        float v = acc[i][j][r];
+        if (bias_mode == 1) v = v + add;
+        if (bias_mode == 2) v = add + v;
+        if (row < m) c[row * ldc + col] = v;
       }
     }
 }
@@ -242,31 +248,31 @@ template <int BM, int BN, bool kL, bool kR>
 void dispatch_vector(bool vector, dim3 grid, hipStream_t stream, const float *a, int64_t a_rs,
                      int64_t a_cs, const float *b, int64_t b_rs, int64_t b_cs, int64_t m, int64_t k,
                      int64_t n, float *c, int64_t ldc, int gm, int gn, const Batch &batch, int64_t c_bs,
-                     int64_t split_len, int64_t split_stride) {
+                     int64_t split_len, int64_t split_stride, const Epilogue &e, int mode) {
   constexpr int T = BM * BN / 64;
   if (vector)
     gemm_mfma_kernel<BM, BN, kL, kR, true><<<grid, T, 0, stream>>>(a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, gm,
                                                                    gn, batch.a_stride, batch.b_stride, c_bs,
-                                                                   split_len, split_stride);
+                                                                   split_len, split_stride, e.bias, e.bias_stride, mode);
   else
     gemm_mfma_kernel<BM, BN, kL, kR, false><<<grid, T, 0, stream>>>(a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, gm,
                                                                     gn, batch.a_stride, batch.b_stride, c_bs,
-                                                                    split_len, split_stride);
+                                                                    split_len, split_stride, e.bias, e.bias_stride, mode);
 }
 
 template <int BM, int BN>
 void dispatch_orientation(bool lk, bool rk, bool vector, dim3 grid, hipStream_t stream, const float *a,
                           int64_t a_rs, int64_t a_cs, const float *b, int64_t b_rs, int64_t b_cs, int64_t m,
                           int64_t k, int64_t n, float *c, int64_t ldc, int gm, int gn, const Batch &batch,
-                          int64_t c_bs, int64_t split_len, int64_t split_stride) {
+                          int64_t c_bs, int64_t split_len, int64_t split_stride, const Epilogue &e, int mode) {
   if (lk && rk)
-    dispatch_vector<BM, BN, true, true>(vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, gm, gn, batch, c_bs, split_len, split_stride);
+    dispatch_vector<BM, BN, true, true>(vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, gm, gn, batch, c_bs, split_len, split_stride, e, mode);
   else if (lk)
-    dispatch_vector<BM, BN, true, false>(vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, gm, gn, batch, c_bs, split_len, split_stride);
+    dispatch_vector<BM, BN, true, false>(vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, gm, gn, batch, c_bs, split_len, split_stride, e, mode);
   else if (rk)
-    dispatch_vector<BM, BN, false, true>(vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, gm, gn, batch, c_bs, split_len, split_stride);
+    dispatch_vector<BM, BN, false, true>(vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, gm, gn, batch, c_bs, split_len, split_stride, e, mode);
   else
-    dispatch_vector<BM, BN, false, false>(vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, gm, gn, batch, c_bs, split_len, split_stride);
+    dispatch_vector<BM, BN, false, false>(vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, gm, gn, batch, c_bs, split_len, split_stride, e, mode);
 }
 
 // The fixed-order sum of `splits` partial products (each [count][m][n],
@@ -276,7 +282,9 @@ void dispatch_orientation(bool lk, bool rk, bool vector, dim3 grid, hipStream_t 
 // guarantees n % 4 == 0, so a quad never leaves its row.)
 __global__ __launch_bounds__(256) void split_reduce_kernel(const float4 *__restrict__ partials, int splits,
                                                            int64_t split_quads, int64_t m, int64_t n,
-                                                           float *__restrict__ c, int64_t ldc, int64_t c_bs) {
+                                                           float *__restrict__ c, int64_t ldc, int64_t c_bs,
+                                                           const float *__restrict__ bias, int64_t bias_cs,
+                                                           int bias_mode) {
   constexpr int kMax = 16;
   for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < split_quads;
        e += (int64_t)gridDim.x * blockDim.x) {
@@ -295,6 +303,21 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float4 *__restr
       }
     const int64_t f = e * 4;
     const int64_t q = f / (m * n), r = (f / n) % m, col = f % n;
+    if (bias_mode != 0) {
+      const float b0 = bias[col * bias_cs], b1 = bias[(col + 1) * bias_cs], b2 = bias[(col + 2) * bias_cs],
+                  b3 = bias[(col + 3) * bias_cs];
+      if (bias_mode == 1) {
+        acc.x = acc.x + b0;
+        acc.y = acc.y + b1;
+        acc.z = acc.z + b2;
+        acc.w = acc.w + b3;
+      } else {
+        acc.x = b0 + acc.x;
+        acc.y = b1 + acc.y;
+        acc.z = b2 + acc.z;
+        acc.w = b3 + acc.w;
+      }
+    }
     float *out = c + q * c_bs + r * ldc + col;
     out[0] = acc.x;
     out[1] = acc.y;
@@ -331,7 +354,8 @@ bool mfma_serves(int64_t a_rs, int64_t a_cs, int64_t b_rs, int64_t b_cs, int64_t
 
 bool launch_gemm_mfma(const float *a, int64_t a_rs, int64_t a_cs, const float *b, int64_t b_rs,
                       int64_t b_cs, int64_t m, int64_t k, int64_t n, float *c, int64_t ldc,
-                      hipStream_t stream, const Batch &batch, float *workspace, int64_t workspace_floats) {
+                      hipStream_t stream, const Batch &batch, float *workspace, int64_t workspace_floats,
+                      const Epilogue &epilogue) {
   if (!mfma_serves(a_rs, a_cs, b_rs, b_cs, m, k, n)) return false;
   const bool left_inner_k = a_cs == 1 || m == 1;
   const bool right_inner_k = b_rs == 1 || n == 1;
@@ -355,26 +379,29 @@ bool launch_gemm_mfma(const float *a, int64_t a_rs, int64_t a_cs, const float *b
     splits = (int)((k + split_len - 1) / split_len);
   }
   const dim3 grid((unsigned)(gm * gn), (unsigned)batch.count, (unsigned)splits);
+  const int bias_mode = epilogue.bias ? (epilogue.bias_first ? 2 : 1) : 0;
+  const int gemm_mode = splits > 1 ? 0 : bias_mode;  // with splits, the reduction adds the bias
   // With splits, each partial is written contiguous ([count][m][n]) into the
   // workspace, then reduced into c.
   float *target = splits > 1 ? workspace : c;
   const int64_t target_ld = splits > 1 ? n : ldc;
   const int64_t target_bs = splits > 1 ? m * n : batch.c_stride;
   if (shape.bm == 256)
-    dispatch_orientation<256, 128>(lk, rk, vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, target, target_ld, (int)gm, (int)gn, batch, target_bs, split_len, split_stride);
+    dispatch_orientation<256, 128>(lk, rk, vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, target, target_ld, (int)gm, (int)gn, batch, target_bs, split_len, split_stride, epilogue, gemm_mode);
   else if (shape.bn == 64)
-    dispatch_orientation<128, 64>(lk, rk, vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, target, target_ld, (int)gm, (int)gn, batch, target_bs, split_len, split_stride);
+    dispatch_orientation<128, 64>(lk, rk, vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, target, target_ld, (int)gm, (int)gn, batch, target_bs, split_len, split_stride, epilogue, gemm_mode);
   else if (shape.bm == 64)
-    dispatch_orientation<64, 128>(lk, rk, vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, target, target_ld, (int)gm, (int)gn, batch, target_bs, split_len, split_stride);
+    dispatch_orientation<64, 128>(lk, rk, vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, target, target_ld, (int)gm, (int)gn, batch, target_bs, split_len, split_stride, epilogue, gemm_mode);
   else
-    dispatch_orientation<128, 128>(lk, rk, vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, target, target_ld, (int)gm, (int)gn, batch, target_bs, split_len, split_stride);
+    dispatch_orientation<128, 128>(lk, rk, vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, target, target_ld, (int)gm, (int)gn, batch, target_bs, split_len, split_stride, epilogue, gemm_mode);
   check_launch("gemm_mfma_kernel launch");
   if (splits > 1) {
     const int64_t quads = split_stride / 4;
     int64_t blocks = (quads + 255) / 256;
     if (blocks > 256 * 32) blocks = 256 * 32;
     split_reduce_kernel<<<(unsigned)blocks, 256, 0, stream>>>(reinterpret_cast<const float4 *>(workspace), splits,
-                                                              quads, m, n, c, ldc, batch.c_stride);
+                                                              quads, m, n, c, ldc, batch.c_stride, epilogue.bias,
+                                                              epilogue.bias_stride, bias_mode);
     check_launch("split_reduce_kernel launch");
   }
   return true;

@@ -289,6 +289,18 @@ struct topos_hip_program {
   // ---- the plan ----
   std::vector<bool> wanted, readable;
   std::vector<bool> mfma_product;  // a product the matrix-core kernel computes (never -0)
+  // A per-column addend a matrix-core product adds as it is written (a
+  // linear layer's bias), filled in when the addition is planned.
+  struct BiasEpilogue {
+    int storage = -1;
+    int64_t offset = 0, stride = 0;
+    bool first = false;  // bias + product rather than product + bias
+  };
+  struct ProductLaunch {
+    int launch;
+    std::shared_ptr<BiasEpilogue> bias;
+  };
+  std::map<int64_t, ProductLaunch> product_launch;
   std::vector<std::vector<int>> consumers;
   std::vector<Value> values;
   std::vector<Storage> storages;
@@ -1306,6 +1318,7 @@ struct topos_hip_program {
         }
       }
     }
+    if (x.op == TOPOS_HIP_OP_ADD && fuse_bias(i)) return;
     if (all_constant) {
       // A Constant payload computed at run time: one element, rank 0.
       Expr e;
@@ -1358,6 +1371,44 @@ struct topos_hip_program {
     }
     values[i].kind = Value::kNone;  // the root of its own expression
     values[i] = emit_chain(i);
+  }
+
+  // product + bias (or bias + product), the bias repeated along every axis
+  // but the last (Linear::express, src/neural/linear.rs:94-105): the
+  // matrix-core kernel that writes the product adds the bias in its store,
+  // the same one f32 addition. Served when the product is read by this
+  // addition only and the bias is complete before the product's launch.
+  bool fuse_bias(int64_t i) {
+    const topos_hip_node &x = nodes[i];
+    for (int side = 0; side < 2; ++side) {
+      const int64_t p = x.operands[side], q = x.operands[1 - side];
+      auto it = product_launch.find(p);
+      if (it == product_launch.end() || !mfma_product[p] || readable[p] || consumers[p].size() != 1 ||
+          it->second.bias->storage >= 0)
+        continue;
+      const Value &b = values[q];
+      if (b.kind != Value::kDense || b.storage < 0 || b.layout.rank != x.rank) continue;
+      bool repeated = true;
+      for (int d = 0; d + 1 < x.rank; ++d) repeated = repeated && b.layout.strides[d] == 0;
+      if (!repeated) continue;
+      const int l = it->second.launch;
+      bool ready = true;
+      for (size_t later = l; later < launches.size(); ++later)
+        for (int w : launches[later].writes) ready = ready && w != b.storage;
+      if (!ready) continue;
+      BiasEpilogue &e = *it->second.bias;
+      e.storage = b.storage;
+      e.offset = b.layout.offset;
+      e.stride = b.layout.strides[x.rank - 1];
+      e.first = side == 1;
+      launches[l].reads.push_back(b.storage);
+      launches[l].what += e.first ? " bias+" : " +bias";
+      launches[l].bytes += 4.0 * (double)x.shape[x.rank - 1];
+      values[i] = values[p];
+      values[i].never_minus_zero = false;
+      return true;
+    }
+    return false;
   }
 
   void plan_pad(int64_t i) {
@@ -1451,23 +1502,33 @@ struct topos_hip_program {
          << "," << k << ") a[" << ars << "," << acs << "] b[" << brs << "," << bcs << "]";
     std::vector<int> writes = {out};
     if (workspace >= 0) writes.push_back(workspace);
-    add_launch(what.str(), {a.storage, b.storage}, writes,
-               [this, a, b, out, parts, batch, m, n, k, ars, acs, brs, bcs, numerics_, workspace,
-                workspace_floats](const Exec &ex) {
-                 const float *pa = (const float *)base(a.storage);
-                 const float *pb = (const float *)base(b.storage);
-                 float *pc = (float *)base(out);
-                 float *pw = workspace >= 0 ? (float *)base(workspace) : nullptr;
-                 for (const auto &part : parts) {
-                   const float *qa = pa + part[0], *qb = pb + part[1];
-                   float *qc = pc + part[2];
-                   if (numerics_ == TOPOS_HIP_FAST &&
-                       launch_gemm_mfma(qa, ars, acs, qb, brs, bcs, m, k, n, qc, n, ex.stream, batch, pw,
-                                        workspace_floats))
-                     continue;
-                   launch_gemm_exact(qa, ars, acs, qb, brs, bcs, m, k, n, qc, n, ex.stream, batch);
-                 }
-               });
+    auto bias = std::make_shared<BiasEpilogue>();
+    const int launch =
+        add_launch(what.str(), {a.storage, b.storage}, writes,
+                   [this, a, b, out, parts, batch, m, n, k, ars, acs, brs, bcs, numerics_, workspace, workspace_floats,
+                    bias](const Exec &ex) {
+                     const float *pa = (const float *)base(a.storage);
+                     const float *pb = (const float *)base(b.storage);
+                     float *pc = (float *)base(out);
+                     float *pw = workspace >= 0 ? (float *)base(workspace) : nullptr;
+                     Epilogue epilogue;
+                     if (bias->storage >= 0) {
+                       epilogue.bias = (const float *)base(bias->storage) + bias->offset;
+                       epilogue.bias_stride = bias->stride;
+                       epilogue.bias_first = bias->first;
+                     }
+                     for (const auto &part : parts) {
+                       const float *qa = pa + part[0], *qb = pb + part[1];
+                       float *qc = pc + part[2];
+                       if (numerics_ == TOPOS_HIP_FAST &&
+                           launch_gemm_mfma(qa, ars, acs, qb, brs, bcs, m, k, n, qc, n, ex.stream, batch, pw,
+                                            workspace_floats, epilogue))
+                         continue;
+                       // A fused bias is planned only where the matrix-core kernel serves.
+                       launch_gemm_exact(qa, ars, acs, qb, brs, bcs, m, k, n, qc, n, ex.stream, batch);
+                     }
+                   });
+    if (mfma_product[i]) product_launch[i] = ProductLaunch{launch, bias};
     launches.back().flops = 2.0 * (double)batches * m * n * k;
     launches.back().bytes = 4.0 * (double)batches * ((double)m * k + (double)k * n + (double)m * n);
     values[i] = dense_value(out, contiguous(x.rank, x.shape));

@@ -403,3 +403,52 @@ def test_strided_reshape_views_exact(hip):
     got, _ = run_device(tape, roots, [], dense, numerics=hip.EXACT)
     for r in roots:
         assert_bitwise(got[r.id], want[r.id], f"node {r.id} {r.shape}")
+
+
+@pytest.mark.parametrize("m, n, k, bias_first", [(64, 48, 32, False), (256, 256, 8192, False),
+                                                 (256, 256, 8192, True), (100, 70, 50, True)])
+def test_fast_linear_bias_is_added_by_the_product(hip, m, n, k, bias_first):
+    """Under Fast, product + bias (Linear::express, src/neural/linear.rs:94-105)
+    is written by the matrix-core kernel, with the split-k reduction adding
+    the bias when the product is split: bit-identical to the same product
+    read back and added in f32 on the host, in the recorded operand order."""
+    banner(f"program fast fused bias {m}x{n}x{k} first={bias_first}")
+    rng = np.random.default_rng(m + n + k)
+    tape = t.Tape()
+    a = tape.input((m, k))
+    b = tape.input((k, n))
+    c = tape.input((n,))
+    p = a.matmul(b)
+    bias = c.broadcast_along(0, p)
+    y = bias + p if bias_first else p + bias
+    dense = {a.node.slot: rng.standard_normal((m, k)).astype(np.float32),
+             b.node.slot: rng.standard_normal((k, n)).astype(np.float32),
+             c.node.slot: rng.standard_normal(n).astype(np.float32)}
+    dense[c.node.slot][:3] = [np.inf, -0.0, np.nan]
+    got, program = run_device(tape, [y], [], dense, numerics=hip.FAST)
+    assert "bias" in program.describe and "chain" not in program.describe, program.describe
+    product, _ = run_device(tape, [p], [], dense, numerics=hip.FAST)
+    p_host, c_host = product[p.id], dense[c.node.slot][None, :]
+    want = (c_host + p_host) if bias_first else (p_host + c_host)
+    assert_bitwise(got[y.id], want, "fused bias")
+
+
+def test_fast_bias_computed_after_the_product_is_not_fused(hip):
+    """A bias whose own launch comes after the product's stays a separate
+    addition; the result is the interpreter's within the Fast envelope."""
+    banner("program fast late bias")
+    rng = np.random.default_rng(5)
+    tape = t.Tape()
+    a = tape.input((96, 40))
+    b = tape.input((40, 56))
+    c = tape.input((56,))
+    p = a.matmul(b)
+    late = c * c + c
+    y = p + late.broadcast_along(0, p)
+    dense = {a.node.slot: rng.standard_normal((96, 40)).astype(np.float32),
+             b.node.slot: rng.standard_normal((40, 56)).astype(np.float32),
+             c.node.slot: rng.standard_normal(56).astype(np.float32)}
+    got, program = run_device(tape, [y], [], dense, numerics=hip.FAST)
+    assert "bias" not in program.describe, program.describe
+    want = run_oracle(tape, [y], [], dense)[y.id]
+    assert (np.abs(got[y.id] - want) <= 1e-4 * np.maximum(np.abs(want), 1.0)).all()
