@@ -114,14 +114,15 @@ struct Slab {
   }
 };
 
-template <int BM, int BN, bool kLeftInnerK, bool kRightInnerK, bool kVector>
-__global__ __launch_bounds__(BM * BN / 64) void gemm_mfma_kernel(
+template <int BM, int BN, int WM, bool kLeftInnerK, bool kRightInnerK, bool kVector>
+__global__ __launch_bounds__(BM / WM * BN) void gemm_mfma_kernel(
     const float *__restrict__ a, int64_t a_rs, int64_t a_cs, const float *__restrict__ b,
     int64_t b_rs, int64_t b_cs, int64_t m, int64_t k, int64_t n, float *__restrict__ c, int64_t ldc,
     int grid_m, int grid_n, int64_t a_bs, int64_t b_bs, int64_t c_bs, int64_t split_len, int64_t split_stride,
     const float *__restrict__ bias, int64_t bias_cs, int bias_mode) {
-  constexpr int T = BM * BN / 64;  // one 64x64 block per wave
+  constexpr int T = BM / WM * BN;  // one WM x 64 block per wave
   constexpr int WN = BN / 64;
+  constexpr int WI = WM / 32;      // 32-row MFMA blocks per wave
   __shared__ float left[2][kTileK][BM + kPad];
   __shared__ float right[2][kTileK][BN + kPad];
   a += (int64_t)blockIdx.y * a_bs;
@@ -151,12 +152,12 @@ __global__ __launch_bounds__(BM * BN / 64) void gemm_mfma_kernel(
 
   const int lane = threadIdx.x % 64;
   const int wave = threadIdx.x / 64;
-  const int wm = (wave / WN) * 64;  // wave's row offset inside the tile
+  const int wm = (wave / WN) * WM;  // wave's row offset inside the tile
   const int wn = (wave % WN) * 64;  // wave's column offset
 
-  floatx16 acc[2][2];
+  floatx16 acc[WI][2];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < WI; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -191,14 +192,16 @@ __global__ __launch_bounds__(BM * BN / 64) void gemm_mfma_kernel(
 #pragma unroll
     for (int kk = 0; kk < kTileK; kk += 2) {
       const int kr = kk + lane / 32;
-      const float a0 = left[cur][kr][wm + (lane % 32)];
-      const float a1 = left[cur][kr][wm + 32 + (lane % 32)];
+      float av[WI];
+#pragma unroll
+      for (int i = 0; i < WI; ++i) av[i] = left[cur][kr][wm + 32 * i + (lane % 32)];
       const float b0 = right[cur][kr][wn + (lane % 32)];
       const float b1 = right[cur][kr][wn + 32 + (lane % 32)];
-      acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b0, acc[0][0], 0, 0, 0);
-      acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b1, acc[0][1], 0, 0, 0);
-      acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b0, acc[1][0], 0, 0, 0);
-      acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b1, acc[1][1], 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < WI; ++i) {
+        acc[i][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i], b0, acc[i][0], 0, 0, 0);
+        acc[i][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i], b1, acc[i][1], 0, 0, 0);
+      }
     }
     if (more) {
       sa.store(left[cur ^ 1]);
@@ -210,7 +213,7 @@ __global__ __launch_bounds__(BM * BN / 64) void gemm_mfma_kernel(
   // 32x32 accumulator layout: register r of lane l holds
   // row 8 * (r / 4) + 4 * (l / 32) + r % 4, column l % 32.
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < WI; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int64_t col = n0 + wn + 32 * j + (lane % 32);
@@ -244,18 +247,25 @@ TileShape tile_shape(int64_t m, int64_t n, int64_t batches) {
   return {128, 128, 3};
 }
 
+// Rows of one wave's block: 64, or 32 for the thin tiles (128x64, 64x128),
+// which then run four waves instead of two. A thin product (an attention
+// head's 64-wide operand) has few tiles, so two waves per tile leave most
+// SIMDs with a single wave and nothing to hide its waits behind.
+constexpr int wave_rows(int bm, int bn) { return bm == 64 || bn == 64 ? 32 : 64; }
+
 template <int BM, int BN, bool kL, bool kR>
 void dispatch_vector(bool vector, dim3 grid, hipStream_t stream, const float *a, int64_t a_rs,
                      int64_t a_cs, const float *b, int64_t b_rs, int64_t b_cs, int64_t m, int64_t k,
                      int64_t n, float *c, int64_t ldc, int gm, int gn, const Batch &batch, int64_t c_bs,
                      int64_t split_len, int64_t split_stride, const Epilogue &e, int mode) {
-  constexpr int T = BM * BN / 64;
+  constexpr int WM = wave_rows(BM, BN);
+  constexpr int T = BM / WM * BN;
   if (vector)
-    gemm_mfma_kernel<BM, BN, kL, kR, true><<<grid, T, 0, stream>>>(a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, gm,
+    gemm_mfma_kernel<BM, BN, WM, kL, kR, true><<<grid, T, 0, stream>>>(a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, gm,
                                                                    gn, batch.a_stride, batch.b_stride, c_bs,
                                                                    split_len, split_stride, e.bias, e.bias_stride, mode);
   else
-    gemm_mfma_kernel<BM, BN, kL, kR, false><<<grid, T, 0, stream>>>(a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, gm,
+    gemm_mfma_kernel<BM, BN, WM, kL, kR, false><<<grid, T, 0, stream>>>(a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, gm,
                                                                     gn, batch.a_stride, batch.b_stride, c_bs,
                                                                     split_len, split_stride, e.bias, e.bias_stride, mode);
 }
@@ -279,19 +289,19 @@ void dispatch_orientation(bool lk, bool rk, bool vector, dim3 grid, hipStream_t 
 // contiguous) into c: partial 0 seeds, then 1, 2, ... are added in order, so
 // the result is the same on every run. Four consecutive elements per lane:
 // every split's 16-byte load is issued before the additions. (The caller
-// guarantees n % 4 == 0, so a quad never leaves its row.)
+// guarantees n % 4 == 0, so a quad never leaves its row, and fewer than 2^32
+// quads per partial.) `aligned`: c, ldc and c_bs allow one 16-byte store.
 __global__ __launch_bounds__(256) void split_reduce_kernel(const float4 *__restrict__ partials, int splits,
-                                                           int64_t split_quads, int64_t m, int64_t n,
+                                                           uint32_t split_quads, uint32_t m, uint32_t row_quads,
                                                            float *__restrict__ c, int64_t ldc, int64_t c_bs,
                                                            const float *__restrict__ bias, int64_t bias_cs,
-                                                           int bias_mode) {
+                                                           int bias_mode, bool aligned) {
   constexpr int kMax = 16;
-  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < split_quads;
-       e += (int64_t)gridDim.x * blockDim.x) {
+  for (uint32_t e = blockIdx.x * blockDim.x + threadIdx.x; e < split_quads; e += gridDim.x * blockDim.x) {
     float4 v[kMax];
 #pragma unroll
     for (int s = 0; s < kMax; ++s)
-      if (s < splits) v[s] = partials[s * split_quads + e];
+      if (s < splits) v[s] = partials[(size_t)s * split_quads + e];
     float4 acc = v[0];
 #pragma unroll
     for (int s = 1; s < kMax; ++s)
@@ -301,8 +311,8 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float4 *__restr
         acc.z = acc.z + v[s].z;
         acc.w = acc.w + v[s].w;
       }
-    const int64_t f = e * 4;
-    const int64_t q = f / (m * n), r = (f / n) % m, col = f % n;
+    const uint32_t row = e / row_quads, col = (e - row * row_quads) * 4;
+    const uint32_t q = row / m, r = row - q * m;
     if (bias_mode != 0) {
       const float b0 = bias[col * bias_cs], b1 = bias[(col + 1) * bias_cs], b2 = bias[(col + 2) * bias_cs],
                   b3 = bias[(col + 3) * bias_cs];
@@ -319,10 +329,14 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float4 *__restr
       }
     }
     float *out = c + q * c_bs + r * ldc + col;
-    out[0] = acc.x;
-    out[1] = acc.y;
-    out[2] = acc.z;
-    out[3] = acc.w;
+    if (aligned) {
+      *reinterpret_cast<float4 *>(out) = acc;
+    } else {
+      out[0] = acc.x;
+      out[1] = acc.y;
+      out[2] = acc.z;
+      out[3] = acc.w;
+    }
   }
 }
 
@@ -371,7 +385,8 @@ bool launch_gemm_mfma(const float *a, int64_t a_rs, int64_t a_cs, const float *b
   int splits = mfma_splits(m, n, k, batch.count);
   const int64_t split_stride = batch.count * m * n;
   if (splits > 1 && (!workspace || workspace_floats < splits * split_stride || n % 4 != 0 ||
-                     reinterpret_cast<uintptr_t>(workspace) % 16 != 0 || splits > 16))
+                     reinterpret_cast<uintptr_t>(workspace) % 16 != 0 || splits > 16 ||
+                     split_stride / 4 >= (int64_t(1) << 31)))
     splits = 1;
   int64_t split_len = k;
   if (splits > 1) {
@@ -399,9 +414,10 @@ bool launch_gemm_mfma(const float *a, int64_t a_rs, int64_t a_cs, const float *b
     const int64_t quads = split_stride / 4;
     int64_t blocks = (quads + 255) / 256;
     if (blocks > 256 * 32) blocks = 256 * 32;
-    split_reduce_kernel<<<(unsigned)blocks, 256, 0, stream>>>(reinterpret_cast<const float4 *>(workspace), splits,
-                                                              quads, m, n, c, ldc, batch.c_stride, epilogue.bias,
-                                                              epilogue.bias_stride, bias_mode);
+    const bool aligned = reinterpret_cast<uintptr_t>(c) % 16 == 0 && ldc % 4 == 0 && batch.c_stride % 4 == 0;
+    split_reduce_kernel<<<(unsigned)blocks, 256, 0, stream>>>(
+        reinterpret_cast<const float4 *>(workspace), splits, (uint32_t)quads, (uint32_t)m, (uint32_t)(n / 4), c, ldc,
+        batch.c_stride, epilogue.bias, epilogue.bias_stride, bias_mode, aligned);
     check_launch("split_reduce_kernel launch");
   }
   return true;
