@@ -114,8 +114,11 @@ struct Slab {
   }
 };
 
+// The 256x128 tile (eight waves) with 16-byte loads is held to 128
+// registers per lane so that two of its workgroups share a CU (four waves
+// per SIMD); at the compiler's own choice (129) a CU held one.
 template <int BM, int BN, int WM, bool kLeftInnerK, bool kRightInnerK, bool kVector>
-__global__ __launch_bounds__(BM / WM * BN) void gemm_mfma_kernel(
+__global__ __launch_bounds__(BM / WM * BN, BM == 256 && kVector ? 4 : 1) void gemm_mfma_kernel(
     const float *__restrict__ a, int64_t a_rs, int64_t a_cs, const float *__restrict__ b,
     int64_t b_rs, int64_t b_cs, int64_t m, int64_t k, int64_t n, float *__restrict__ c, int64_t ldc,
     int grid_m, int grid_n, int64_t a_bs, int64_t b_bs, int64_t c_bs, int64_t split_len, int64_t split_stride,
