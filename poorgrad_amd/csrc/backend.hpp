@@ -162,9 +162,10 @@ void launch_gather(const float *table, int64_t row_stride, int64_t column_stride
 void launch_scatter(const float *gradient, int64_t row_stride, int64_t column_stride, const int32_t *row_start,
                     const int32_t *sources, int64_t rows, int64_t row_size, float *out, hipStream_t stream);
 void launch_one_hot(const int32_t *indices, int64_t rows, int64_t vocab, float one, float *out, hipStream_t stream);
-void launch_scan(const int32_t *counts, int64_t chunks, int64_t *offsets, hipStream_t stream);
-void launch_ordered_fold(const float *compacted, const int64_t *offsets, int64_t chunks, const int32_t *positive_zero,
-                         float *out, hipStream_t stream);
+// Folds a whole-tensor sum's gathered nonzero terms in element order (chunk
+// c's counts[c] terms at slots + c * chunk_size) into out[0].
+void launch_slot_fold(const float *slots, const int32_t *counts, const int32_t *positive_zero, int64_t chunks,
+                      int64_t chunk_size, float *out, hipStream_t stream);
 void launch_sgd(float *parameter, const float *gradient, int64_t count, float rate, hipStream_t stream);
 void launch_adamw(float *parameter, const float *gradient, float *first, float *second, int64_t count, float beta1,
                   float beta2, float first_share, float second_share, float first_correction,

@@ -163,15 +163,30 @@ void emit_steps(std::ostringstream &s, const Expr &e, const std::vector<std::str
 }
 
 // Coordinates of flat index `flat` over `shape[0..rank)`, named c<d>_<tag>.
+// Below 2^31 elements the divisions run on 32-bit unsigned values (a
+// multiply-high and a shift per constant divisor instead of a 64-bit
+// sequence); `flat` is then in range for any flat index of the shape.
 void emit_coordinates(std::ostringstream &s, int rank, const int64_t *shape, const std::string &flat,
                       const std::string &tag, std::vector<std::string> &names) {
   names.assign(rank, "");
+  int64_t volume = 1;
+  for (int d = 0; d < rank; ++d) volume *= shape[d];
+  const bool narrow = volume < (int64_t(1) << 31);
   std::string rem = flat;
+  if (narrow && rank > 1) {
+    rem = "u_" + tag;
+    s << "      const unsigned " << rem << " = (unsigned)(" << flat << ");\n";
+  }
   for (int d = rank - 1; d >= 0; --d) {
     const std::string name = "c" + std::to_string(d) + "_" + tag;
     names[d] = name;
     if (d == 0) {
       s << "      const long long " << name << " = " << rem << ";\n";
+    } else if (narrow) {
+      s << "      const long long " << name << " = (long long)(" << rem << " % " << shape[d] << "u);\n";
+      const std::string next = "r" + std::to_string(d) + "_" + tag;
+      s << "      const unsigned " << next << " = " << rem << " / " << shape[d] << "u;\n";
+      rem = next;
     } else {
       s << "      const long long " << name << " = (" << rem << ") % " << ll(shape[d]) << ";\n";
       const std::string next = "r" + std::to_string(d) + "_" + tag;
@@ -796,74 +811,74 @@ constexpr int kRounds = (int)(kSumChunk / 256);
 
 }  // namespace
 
-Generated generate_sum_count(const Expr &e) {
+Generated generate_sum_gather(const Expr &e) {
+  // Every round's value is evaluated first (all loads in flight together);
+  // one barrier publishes each wave's per-round term count, then every lane
+  // writes its term at (rounds before) + (waves before in its round) + (lanes
+  // before in its wave): element order within the chunk.
   validate(e);
   std::ostringstream s;
   s << preamble();
-  s << signature(e, "int* __restrict__ counts, int* __restrict__ positive_zero") << " {\n  topos_tables_init();\n";
-  s << "  __shared__ int wave_counts[4];\n  __shared__ int wave_plus[4];\n";
+  s << signature(e, "float* __restrict__ slots, int* __restrict__ counts, int* __restrict__ positive_zero")
+    << " {\n  topos_tables_init();\n";
+  s << "  __shared__ int wave_counts[" << kRounds << "][4];\n  __shared__ int wave_plus[4];\n";
   s << "  const long long chunk = blockIdx.x;\n";
-  s << "  int nonzero = 0, plus_zero = 0;\n";
-  s << "  for (int round = 0; round < " << kRounds << "; ++round) {\n";
-  s << "    const long long f = chunk * " << ll(kSumChunk) << " + round * 256 + threadIdx.x;\n    {\n";
-  emit_flat_value(s, e, "f", "x");
-  // A term is zero only when it compares equal to zero; NaN counts as a term.
-  s << "      if (live) { if (v == 0.0f) { if (!__builtin_signbit(v)) plus_zero = 1; } else { ++nonzero; } }\n";
+  s << "  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;\n";
+  s << "  const unsigned long long below = (1ull << lane) - 1ull;\n";
+  s << "  float vals[" << kRounds << "];\n  int before[" << kRounds << "];\n  unsigned keep = 0;\n  int plus_zero = 0;\n";
+  // Evaluation without branches (a lane past the end reads element 0 and
+  // discards it), so every round's loads are in flight together.
+  s << "  unsigned lives = 0;\n";
+  s << "  #pragma unroll\n  for (int round = 0; round < " << kRounds << "; ++round) {\n";
+  s << "    const long long f = chunk * " << ll(kSumChunk) << " + round * 256 + threadIdx.x;\n";
+  s << "    const bool live = f < " << ll(e.volume()) << ";\n";
+  s << "    const long long fc = live ? f : 0;\n    {\n";
+  {
+    std::vector<std::string> c;
+    if (e.rank > 0) emit_coordinates(s, e.rank, e.shape, "fc", "x", c);
+    for (size_t i = 0; i < e.inputs.size(); ++i)
+      s << "      const float in" << i << "_x = " << scalar_value(e, (int)i, c) << ";\n";
+    emit_steps(s, e, {"x"});
+    s << "      vals[round] = " << ref(e.outputs[0], "x") << ";\n";
+  }
+  s << "      if (live) lives |= 1u << round;\n";
   s << "    }\n  }\n";
-  // Lane totals -> the chunk's count (integers: any order is exact).
-  s << "  for (int off = 32; off >= 1; off >>= 1) { nonzero += __shfl_xor(nonzero, off, 64); "
-       "plus_zero |= __shfl_xor(plus_zero, off, 64); }\n";
-  s << "  if ((threadIdx.x & 63) == 0) { wave_counts[threadIdx.x >> 6] = nonzero; wave_plus[threadIdx.x >> 6] = plus_zero; }\n";
+  // A term is zero only when it compares equal to zero; NaN counts as a term.
+  s << "  #pragma unroll\n  for (int round = 0; round < " << kRounds << "; ++round) {\n";
+  s << "    const float v = vals[round];\n";
+  s << "    const bool live = (lives >> round) & 1u;\n";
+  s << "    const bool term = live && !(v == 0.0f);\n";
+  s << "    if (live && v == 0.0f && !__builtin_signbit(v)) plus_zero = 1;\n";
+  s << "    if (term) keep |= 1u << round;\n";
+  s << "    const unsigned long long mask = __ballot(term);\n";
+  s << "    before[round] = __popcll(mask & below);\n";
+  s << "    if (lane == 0) wave_counts[round][wave] = __popcll(mask);\n";
+  s << "  }\n";
+  s << "  for (int off = 32; off >= 1; off >>= 1) plus_zero |= __shfl_xor(plus_zero, off, 64);\n";
+  s << "  if (lane == 0) wave_plus[wave] = plus_zero;\n";
   s << "  __syncthreads();\n";
+  s << "  float* __restrict__ out = slots + chunk * " << ll(kSumChunk) << ";\n";
+  s << "  int at = 0;\n";
+  s << "  #pragma unroll\n  for (int round = 0; round < " << kRounds << "; ++round) {\n";
+  s << "    int offset = at;\n";
+  s << "    for (int w = 0; w < wave; ++w) offset += wave_counts[round][w];\n";
+  s << "    if (keep & (1u << round)) out[offset + before[round]] = vals[round];\n";
+  s << "    at += wave_counts[round][0] + wave_counts[round][1] + wave_counts[round][2] + wave_counts[round][3];\n";
+  s << "  }\n";
   s << "  if (threadIdx.x == 0) {\n";
-  s << "    counts[chunk] = wave_counts[0] + wave_counts[1] + wave_counts[2] + wave_counts[3];\n";
+  s << "    counts[chunk] = at;\n";
   s << "    positive_zero[chunk] = wave_plus[0] | wave_plus[1] | wave_plus[2] | wave_plus[3];\n  }\n}\n";
   return make(s.str());
 }
 
-Generated generate_sum_compact(const Expr &e) {
-  validate(e);
-  std::ostringstream s;
-  s << preamble();
-  s << signature(e, "const long long* __restrict__ offsets, float* __restrict__ compacted") << " {\n  topos_tables_init();\n";
-  s << "  __shared__ int wave_counts[4];\n";
-  s << "  const long long chunk = blockIdx.x;\n";
-  s << "  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;\n";
-  s << "  long long at = offsets[chunk];\n";
-  s << "  for (int round = 0; round < " << kRounds << "; ++round) {\n";
-  s << "    const long long f = chunk * " << ll(kSumChunk) << " + round * 256 + threadIdx.x;\n    {\n";
-  emit_flat_value(s, e, "f", "x");
-  s << "      const bool keep = live && !(v == 0.0f);\n";
-  s << "      const unsigned long long mask = __ballot(keep);\n";
-  s << "      const int before = __popcll(mask & ((1ull << lane) - 1ull));\n";
-  s << "      if (lane == 0) wave_counts[wave] = __popcll(mask);\n";
-  s << "      __syncthreads();\n";
-  s << "      int offset = 0;\n";
-  s << "      for (int w = 0; w < wave; ++w) offset += wave_counts[w];\n";
-  s << "      if (keep) compacted[at + offset + before] = v;\n";
-  s << "      at += wave_counts[0] + wave_counts[1] + wave_counts[2] + wave_counts[3];\n";
-  s << "      __syncthreads();\n";
-  s << "    }\n  }\n}\n";
-  return make(s.str());
-}
-
-void launch_sum_count(const Generated &g, const Expr &e, const void *const *inputs, int32_t *counts,
-                      int32_t *positive_zero, hipStream_t stream) {
+void launch_sum_gather(const Generated &g, const Expr &e, const void *const *inputs, float *slots, int32_t *counts,
+                       int32_t *positive_zero, hipStream_t stream) {
   const int64_t chunks = (e.volume() + kSumChunk - 1) / kSumChunk;
+  if (chunks > 0x7fffffff) throw Unsupported{"sum: too many chunks for one launch"};
   std::vector<const void *> pointers(inputs, inputs + e.inputs.size());
+  pointers.push_back(slots);
   pointers.push_back(counts);
   pointers.push_back(positive_zero);
-  std::vector<void *> arguments;
-  for (auto &p : pointers) arguments.push_back(&p);
-  launch(g, (unsigned)chunks, arguments, stream);
-}
-
-void launch_sum_compact(const Generated &g, const Expr &e, const void *const *inputs, const int64_t *offsets,
-                        float *compacted, hipStream_t stream) {
-  const int64_t chunks = (e.volume() + kSumChunk - 1) / kSumChunk;
-  std::vector<const void *> pointers(inputs, inputs + e.inputs.size());
-  pointers.push_back(offsets);
-  pointers.push_back(compacted);
   std::vector<void *> arguments;
   for (auto &p : pointers) arguments.push_back(&p);
   launch(g, (unsigned)chunks, arguments, stream);

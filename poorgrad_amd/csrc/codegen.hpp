@@ -140,15 +140,13 @@ void launch_row_program(const Generated &g, const RowProgram &p, const void *con
                         float *const *full_outputs, float *const *row_outputs, hipStream_t stream);
 
 // Whole-tensor exact sum over a large operand, in chunks of kSumChunk flat
-// elements (one workgroup each, lanes on consecutive elements): pass one
-// counts each chunk's nonzero terms (and whether the chunk holds a +0), pass
-// two writes them compacted in element order.
+// elements (one workgroup each, lanes on consecutive elements): one pass
+// writes each chunk's nonzero terms, in element order, to the front of the
+// chunk's own slot range [chunk * kSumChunk, ...), with the chunk's count and
+// whether it holds a +0 (launch_slot_fold then folds the slots in order).
 constexpr int64_t kSumChunk = 4096;
-Generated generate_sum_count(const Expr &e);
-Generated generate_sum_compact(const Expr &e);
-void launch_sum_count(const Generated &g, const Expr &e, const void *const *inputs, int32_t *counts,
-                      int32_t *positive_zero, hipStream_t stream);
-void launch_sum_compact(const Generated &g, const Expr &e, const void *const *inputs,
-                        const int64_t *offsets, float *compacted, hipStream_t stream);
+Generated generate_sum_gather(const Expr &e);
+void launch_sum_gather(const Generated &g, const Expr &e, const void *const *inputs, float *slots, int32_t *counts,
+                       int32_t *positive_zero, hipStream_t stream);
 
 }  // namespace topos_hip

@@ -237,8 +237,9 @@ __global__ __launch_bounds__(BM / WM * BN, BM == 256 && kVector ? 4 : 1) void ge
 // The tile shape for an m x n product (over `batches`): 128x64 or 64x128
 // when one output extent is at most 64; 256x128 (eight waves, less operand
 // traffic per flop than 128x128) when its tiles fill whole rounds of two
-// workgroups per CU, or at least two such rounds; else 128x128. `per_cu` is how many of its workgroups a CU
-// holds at once.
+// workgroups per CU, or at least one and a half such rounds (measured on
+// MI355X: the [8192, 3072] products gain, [8192, 2304] loses); else 128x128.
+// `per_cu` is how many of its workgroups a CU holds at once.
 struct TileShape {
   int bm, bn, per_cu;
 };
@@ -246,7 +247,7 @@ TileShape tile_shape(int64_t m, int64_t n, int64_t batches) {
   if (n <= 64 && m > 64) return {128, 64, 3};
   if (m <= 64 && n > 64) return {64, 128, 3};
   const int64_t wide = ((m + 255) / 256) * ((n + 127) / 128) * batches;
-  if (wide >= 1024 || (wide >= 512 && wide % 512 == 0)) return {256, 128, 2};
+  if (wide >= 768 || (wide >= 512 && wide % 512 == 0)) return {256, 128, 2};
   return {128, 128, 3};
 }
 

@@ -9,7 +9,7 @@
 //           in ascending order: deterministic, no atomics.
 //   one-hot (Storage::Selection read through Tensor::get, tensor.rs:220-240).
 //   sum     (tensor.rs:1055-1063): the ordered fold of the nonzero terms the
-//           generated passes compacted. Dropping the +-0 terms of a sequential
+//           generated pass gathered per chunk. Dropping the +-0 terms of a sequential
 //           sum changes nothing once a nonzero term has been added (x + +-0 = x,
 //           and an exact cancellation gives +0, which +-0 terms keep), and
 //           +-0 + x = x; so the fold over the nonzero terms, seeded with the
@@ -56,60 +56,162 @@ __global__ __launch_bounds__(256) void one_hot_kernel(const int32_t *__restrict_
   }
 }
 
-// Exclusive scan of the per-chunk nonzero counts, one workgroup: each lane
-// owns a contiguous run of chunks.
-__global__ __launch_bounds__(1024) void scan_kernel(const int32_t *__restrict__ counts, int64_t chunks,
-                                                    int64_t *__restrict__ offsets) {
-  __shared__ int64_t totals[1024];
-  const int t = threadIdx.x;
-  const int64_t per = (chunks + 1023) / 1024;
-  const int64_t begin = t * per, end = begin + per < chunks ? begin + per : chunks;
-  int64_t mine = 0;
-#pragma unroll 8
-  for (int64_t c = begin; c < end; ++c) mine += counts[c];
-  totals[t] = mine;
-  __syncthreads();
-  if (t == 0) {
-    int64_t running = 0;
-    for (int i = 0; i < 1024; ++i) {
-      const int64_t v = totals[i];
-      totals[i] = running;
-      running += v;
-    }
-    offsets[chunks] = running;  // the total number of nonzero terms
-  }
-  __syncthreads();
-  int64_t running = totals[t];
-#pragma unroll 8
-  for (int64_t c = begin; c < end; ++c) {
-    offsets[c] = running;
-    running += counts[c];
-  }
-}
+// The ordered fold of a whole-tensor sum's nonzero terms, gathered per chunk:
+// chunk c's count[c] terms sit, in element order, at slots[c * chunk_size].
+// One workgroup walks the chunks in passes of 256 x 16 (each lane reads the
+// counts of 16 consecutive chunks; the next pass's counts are loaded while
+// this one is copied). A block prefix lists the pass's nonempty chunks in
+// order with each one's place among the pass's terms; their terms are copied
+// into an LDS stage in element order (a lane per chunk when every chunk
+// holds few terms, else chunk by chunk with all lanes), and lane 0 folds the
+// stage whenever it fills. With no nonzero term the sum is -0 exactly when
+// every term is -0.
+constexpr int kFoldThreads = 256;
+constexpr int kFoldPer = 16;
+constexpr int kFoldPass = kFoldThreads * kFoldPer;
+constexpr int kFoldStage = 8192;
 
-// The ordered fold of the compacted terms (one lane).
-__global__ void ordered_sum_kernel(const float *__restrict__ compacted, const int64_t *__restrict__ offsets,
-                                   int64_t chunks, const int32_t *__restrict__ positive_zero,
-                                   float *__restrict__ out) {
-  if (threadIdx.x != 0 || blockIdx.x != 0) return;
-  const int64_t n = offsets[chunks];
-  if (n == 0) {
-    int any_positive = 0;
-    for (int64_t c = 0; c < chunks; ++c) any_positive |= positive_zero[c];
-    out[0] = any_positive ? 0.0f : -0.0f;
-    return;
+__global__ __launch_bounds__(kFoldThreads) void slot_fold_kernel(const float *__restrict__ slots,
+                                                                 const int32_t *__restrict__ counts,
+                                                                 const int32_t *__restrict__ positive_zero,
+                                                                 int64_t chunks, int64_t chunk_size,
+                                                                 float *__restrict__ out) {
+  __shared__ __attribute__((aligned(16))) float stage[kFoldStage];
+  __shared__ int wave_terms[kFoldThreads / 64], wave_entries[kFoldThreads / 64], wave_most[kFoldThreads / 64];
+  __shared__ int entry_chunk[kFoldPass], entry_count[kFoldPass], entry_place[kFoldPass];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  float acc = 0.0f;   // lane 0's running fold
+  bool have = false;  // lane 0: a term is folded
+  int any_plus = 0;
+  int fill = 0;       // staged terms (the same in every lane)
+  auto flush = [&]() {
+    __syncthreads();
+    if (t == 0) {
+      int i = 0;
+      if (!have && fill > 0) {
+        acc = stage[0];
+        have = true;
+        i = 1;
+      }
+      for (; i < fill && (i & 3) != 0; ++i) acc = acc + stage[i];
+      // Eight 16-byte LDS reads in flight ahead of each 32 additions.
+      for (; i + 32 <= fill; i += 32) {
+        float4 q[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) q[u] = *reinterpret_cast<const float4 *>(&stage[i + 4 * u]);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          acc = acc + q[u].x;
+          acc = acc + q[u].y;
+          acc = acc + q[u].z;
+          acc = acc + q[u].w;
+        }
+      }
+      for (; i < fill; ++i) acc = acc + stage[i];
+    }
+    __syncthreads();
+    fill = 0;
+  };
+  int next[kFoldPer];
+  auto load = [&](int64_t first) {
+    const int64_t mine = first + (int64_t)t * kFoldPer;
+    if (mine + kFoldPer <= chunks) {
+#pragma unroll
+      for (int q = 0; q < kFoldPer; q += 4) {
+        const int4 c4 = *reinterpret_cast<const int4 *>(counts + mine + q);
+        const int4 p4 = *reinterpret_cast<const int4 *>(positive_zero + mine + q);
+        next[q] = c4.x;
+        next[q + 1] = c4.y;
+        next[q + 2] = c4.z;
+        next[q + 3] = c4.w;
+        any_plus |= p4.x | p4.y | p4.z | p4.w;
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < kFoldPer; ++q) {
+        next[q] = mine + q < chunks ? counts[mine + q] : 0;
+        any_plus |= mine + q < chunks ? positive_zero[mine + q] : 0;
+      }
+    }
+  };
+  load(0);
+  for (int64_t first = 0; first < chunks; first += kFoldPass) {
+    int cnt[kFoldPer];
+    int terms = 0, entries = 0, most = 0;
+#pragma unroll
+    for (int q = 0; q < kFoldPer; ++q) {
+      cnt[q] = next[q];
+      terms += cnt[q];
+      entries += cnt[q] > 0 ? 1 : 0;
+      most = max(most, cnt[q]);
+    }
+    if (first + kFoldPass < chunks) load(first + kFoldPass);
+    // Block prefixes of this lane's terms and nonempty chunks.
+    int terms_in = terms, entries_in = entries;
+    for (int off = 1; off < 64; off <<= 1) {
+      const int y = __shfl_up(terms_in, off, 64), z = __shfl_up(entries_in, off, 64);
+      if (lane >= off) {
+        terms_in += y;
+        entries_in += z;
+      }
+      most = max(most, __shfl_xor(most, off, 64));
+    }
+    if (lane == 63) {
+      wave_terms[wave] = terms_in;
+      wave_entries[wave] = entries_in;
+    }
+    if (lane == 0) wave_most[wave] = most;
+    __syncthreads();
+    int place = terms_in - terms, slot = entries_in - entries, total = 0, listed = 0;
+    for (int w = 0; w < kFoldThreads / 64; ++w) {
+      if (w < wave) {
+        place += wave_terms[w];
+        slot += wave_entries[w];
+      }
+      total += wave_terms[w];
+      listed += wave_entries[w];
+      most = max(most, wave_most[w]);
+    }
+#pragma unroll
+    for (int q = 0; q < kFoldPer; ++q)
+      if (cnt[q] > 0) {
+        entry_chunk[slot] = t * kFoldPer + q;
+        entry_count[slot] = cnt[q];
+        entry_place[slot] = place;
+        ++slot;
+        place += cnt[q];
+      }
+    __syncthreads();
+    if (total > 0) {
+      if (fill + total > kFoldStage) flush();
+      if (total <= kFoldStage && most <= 64) {
+        // A lane per nonempty chunk (few terms each).
+        for (int e = t; e < listed; e += kFoldThreads) {
+          const float *src = slots + (first + entry_chunk[e]) * chunk_size;
+          const int n = entry_count[e], at = fill + entry_place[e];
+          for (int j = 0; j < n; ++j) stage[at + j] = src[j];
+        }
+        fill += total;  // the next flush's barrier orders these stores before lane 0 reads them
+      } else {
+        // Chunk by chunk, all lanes on consecutive terms.
+        for (int e = 0; e < listed; ++e) {
+          const float *src = slots + (first + entry_chunk[e]) * chunk_size;
+          const int n = entry_count[e];
+          for (int j0 = 0; j0 < n;) {
+            if (fill == kFoldStage) flush();
+            const int piece = min(n - j0, kFoldStage - fill);
+            for (int j = t; j < piece; j += kFoldThreads) stage[fill + j] = src[j0 + j];
+            fill += piece;
+            j0 += piece;
+          }
+        }
+      }
+    }
+    __syncthreads();  // the entry lists and wave totals are rewritten next pass
   }
-  float acc = compacted[0];
-  int64_t i = 1;
-  for (; i + 4 <= n; i += 4) {
-    const float a = compacted[i], b = compacted[i + 1], c = compacted[i + 2], d = compacted[i + 3];
-    acc = acc + a;
-    acc = acc + b;
-    acc = acc + c;
-    acc = acc + d;
-  }
-  for (; i < n; ++i) acc = acc + compacted[i];
-  out[0] = acc;
+  flush();
+  any_plus = __syncthreads_or(any_plus);
+  if (t == 0) out[0] = have ? acc : (any_plus ? 0.0f : -0.0f);
 }
 
 __global__ __launch_bounds__(256) void sgd_kernel(float *__restrict__ parameter, const float *__restrict__ gradient,
@@ -168,15 +270,10 @@ void launch_one_hot(const int32_t *indices, int64_t rows, int64_t vocab, float o
   check_launch("one_hot_kernel launch");
 }
 
-void launch_scan(const int32_t *counts, int64_t chunks, int64_t *offsets, hipStream_t stream) {
-  scan_kernel<<<1, 1024, 0, stream>>>(counts, chunks, offsets);
-  check_launch("scan_kernel launch");
-}
-
-void launch_ordered_fold(const float *compacted, const int64_t *offsets, int64_t chunks, const int32_t *positive_zero,
-                         float *out, hipStream_t stream) {
-  ordered_sum_kernel<<<1, 64, 0, stream>>>(compacted, offsets, chunks, positive_zero, out);
-  check_launch("ordered_sum_kernel launch");
+void launch_slot_fold(const float *slots, const int32_t *counts, const int32_t *positive_zero, int64_t chunks,
+                      int64_t chunk_size, float *out, hipStream_t stream) {
+  slot_fold_kernel<<<1, kFoldThreads, 0, stream>>>(slots, counts, positive_zero, chunks, chunk_size, out);
+  check_launch("slot_fold_kernel launch");
 }
 
 void launch_sgd(float *parameter, const float *gradient, int64_t count, float rate, hipStream_t stream) {

@@ -20,7 +20,7 @@
 //                 windowed input of that node's kernel;
 //   launches      one per materialised elementwise tree (a generated chain),
 //                 per reduction (a generated fold, the row kernels, or the
-//                 exact compacted whole-tensor sum), per product (the GEMM
+//                 exact gathered whole-tensor sum), per product (the GEMM
 //                 kernels, batched over leading axes), per gather/scatter;
 //   liveness      a storage lives from the launch that writes it to the last
 //                 launch that reads it (readable values to the end of the
@@ -1606,23 +1606,18 @@ struct topos_hip_program {
     const int out = arena_storage(4);
     const int counts = arena_storage(chunks * 4);
     const int flags = arena_storage(chunks * 4);
-    const int offsets = arena_storage((chunks + 1) * 8);
-    const int compacted = arena_storage(volume * 4);
-    Generated count = generate_sum_count(e);
-    Generated compact = generate_sum_compact(e);
-    pending.push_back(count);
-    pending.push_back(compact);
+    const int slots = arena_storage(chunks * kSumChunk * 4);
+    Generated gather = generate_sum_gather(e);
+    pending.push_back(gather);
     ++fused_groups;
     std::vector<int> reads = real(storage_of);
-    add_launch("sum (ordered, compacted) " + describe_expr(e), reads, {out, counts, flags, offsets, compacted},
-               [this, e, count, compact, storage_of, out, counts, flags, offsets, compacted, chunks](const Exec &ex) {
+    add_launch("sum (ordered, gathered) " + describe_expr(e), reads, {out, counts, flags, slots},
+               [this, e, gather, storage_of, out, counts, flags, slots, chunks](const Exec &ex) {
                  auto p = pointers_for(storage_of);
-                 launch_sum_count(count, e, p.data(), (int32_t *)base(counts), (int32_t *)base(flags), ex.stream);
-                 launch_scan((const int32_t *)base(counts), chunks, (int64_t *)base(offsets), ex.stream);
-                 launch_sum_compact(compact, e, p.data(), (const int64_t *)base(offsets), (float *)base(compacted),
-                                    ex.stream);
-                 launch_ordered_fold((const float *)base(compacted), (const int64_t *)base(offsets), chunks,
-                                     (const int32_t *)base(flags), (float *)base(out), ex.stream);
+                 launch_sum_gather(gather, e, p.data(), (float *)base(slots), (int32_t *)base(counts),
+                                   (int32_t *)base(flags), ex.stream);
+                 launch_slot_fold((const float *)base(slots), (const int32_t *)base(counts),
+                                  (const int32_t *)base(flags), chunks, kSumChunk, (float *)base(out), ex.stream);
                });
     account(e, 1.0);
     Value v = dense_value(out, constant_layout(0, x.shape, 0));

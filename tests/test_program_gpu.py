@@ -141,7 +141,7 @@ def test_signed_zero_seeding_survives(hip):
 
 def test_large_sparse_sum_is_exact(hip):
     """The cross-entropy alignment term (targets * logits).sum() over a wide
-    vocabulary: the ordered sum over the compacted nonzero terms equals the
+    vocabulary: the ordered sum over the gathered nonzero terms equals the
     interpreter's 1.6M-term left fold."""
     banner("program sparse sum")
     rng = np.random.default_rng(9)
@@ -452,3 +452,49 @@ def test_fast_bias_computed_after_the_product_is_not_fused(hip):
     assert "bias" not in program.describe, program.describe
     want = run_oracle(tape, [y], [], dense)[y.id]
     assert (np.abs(got[y.id] - want) <= 1e-4 * np.maximum(np.abs(want), 1.0)).all()
+
+
+@pytest.mark.parametrize("case", ["dense", "zeros", "nonfinite", "passes"])
+def test_whole_sums_exact(hip, case):
+    """Whole-tensor sums (tensor.rs:1055-1063) through the gathered ordered
+    fold: dense operands whose terms overflow the fold's LDS stage, all-zero
+    operands (-0 only when every term is -0), infinities and NaN among the
+    terms, and a sparse operand spanning several passes of chunks."""
+    banner(f"program whole sum {case}")
+    rng = np.random.default_rng(31)
+    tape = t.Tape()
+    dense, selections = {}, {}
+    if case == "dense":
+        x = tape.input((1500, 2000))
+        dense[x.node.slot] = rng.standard_normal((1500, 2000)).astype(np.float32)
+        roots = [x.sum(), (x * x).sum()]
+    elif case == "zeros":
+        x = tape.input((64, 1000))
+        neg = np.full((64, 1000), -0.0, np.float32)
+        mixed = neg.copy()
+        mixed[40, 999] = 0.0
+        y = tape.input((64, 1000))
+        dense[x.node.slot], dense[y.node.slot] = neg, mixed
+        roots = [x.sum(), y.sum(), (x + x).sum()]
+    elif case == "nonfinite":
+        x = tape.input((300, 700))
+        v = np.zeros((300, 700), np.float32)
+        v[3, 5], v[100, 2], v[250, 600] = 2.5, np.inf, -1.0
+        w = v.copy()
+        w[299, 699] = -np.inf
+        u = np.where(rng.random((300, 700)) < 0.001, np.float32(np.nan), np.float32(0.0)).astype(np.float32)
+        u[0, 0] = 1.0
+        y, z = tape.input((300, 700)), tape.input((300, 700))
+        dense[x.node.slot], dense[y.node.slot], dense[z.node.slot] = v, w, u
+        roots = [x.sum(), y.sum(), z.sum()]
+    else:
+        logits = tape.input((2048, 9000))
+        targets = tape.selection_input(2048, 9000)
+        dense[logits.node.slot] = rng.standard_normal((2048, 9000)).astype(np.float32)
+        selections[targets.node.slot] = (rng.integers(0, 9000, 2048).astype(np.int32), 1.0)
+        roots = [(targets * logits).sum()]
+    want = run_oracle(tape, roots, [], dense, selections)
+    got, program = run_device(tape, roots, [], dense, selections)
+    assert "sum (ordered, gathered)" in program.describe, program.describe
+    for r in roots:
+        assert_bitwise(got[r.id], want[r.id], f"{case} sum node {r.id}")
