@@ -322,6 +322,20 @@ struct topos_hip_program {
   };
   std::vector<Launch> launches;
   std::vector<Generated> pending;  // generated kernels, compiled together after planning
+  // A generated chain launch: its expression grows while it is the last
+  // launch planned (a following chain over the same shape whose inputs are
+  // complete by then joins it as one more output); its source is generated
+  // once planning ends.
+  struct ChainRecord {
+    int launch = -1;
+    Expr e;
+    std::vector<int> storage_of;  // per expression input
+    std::vector<int> outs;        // per expression output
+    std::string ops;
+    Generated g;
+  };
+  std::vector<std::shared_ptr<ChainRecord>> chains;
+  std::shared_ptr<ChainRecord> open_chain;
   std::map<int64_t, int> output_storage;  // readable node -> storage holding it contiguous
   std::map<int64_t, int64_t> output_offset;
   uint64_t arena_bytes = 0;
@@ -1082,18 +1096,127 @@ struct topos_hip_program {
     std::vector<int> storage_of;
     Expr e = expression_for(root, storage_of);
     const int out = arena_storage(e.volume() * 4);
-    Generated g = generate_chain(e);
-    pending.push_back(g);
+    const topos_hip_node &n = nodes[root];
+    if (join_open_chain(e, storage_of, out, op_name(n.op))) return dense_value(out, contiguous(n.rank, n.shape));
+    auto record = std::make_shared<ChainRecord>();
+    record->e = e;
+    record->storage_of = storage_of;
+    record->outs = {out};
+    record->ops = op_name(n.op);
     ++fused_groups;
-    add_launch(std::string("chain ") + op_name(nodes[root].op) + " " + describe_expr(e), real(storage_of), {out},
-               [this, e, g, storage_of, out](const Exec &x) {
-                 auto p = pointers_for(storage_of);
-                 float *q = (float *)base(out);
-                 launch_generated_chain(g, e, p.data(), &q, x.stream);
+    add_launch(std::string("chain ") + record->ops + " " + describe_expr(e), real(storage_of), {out},
+               [this, record](const Exec &x) {
+                 auto p = pointers_for(record->storage_of);
+                 std::vector<float *> q;
+                 for (int o : record->outs) q.push_back((float *)base(o));
+                 launch_generated_chain(record->g, record->e, p.data(), q.data(), x.stream);
                });
     account(e, (double)e.volume());
-    const topos_hip_node &n = nodes[root];
+    record->launch = (int)launches.size() - 1;
+    chains.push_back(record);
+    open_chain = record;
     return dense_value(out, contiguous(n.rank, n.shape));
+  }
+
+  // Generates every chain's source. A joined chain's output that no other
+  // launch reads and no readable value keeps stays in registers (it was
+  // written only for the members that joined after it).
+  void finish_chains() {
+    std::vector<int> readers(storages.size(), 0);
+    for (const Launch &l : launches)
+      for (int r : l.reads) ++readers[r];
+    for (auto &record : chains) {
+      Launch &l = launches[record->launch];
+      Expr &e = record->e;
+      std::vector<int> kept_outputs, kept_storages;
+      for (size_t k = 0; k < record->outs.size(); ++k) {
+        const int o = record->outs[k];
+        if (readers[o] > 0 || storages[o].pinned || k + 1 == record->outs.size()) {
+          kept_outputs.push_back(e.outputs[k]);
+          kept_storages.push_back(o);
+        }
+      }
+      if (kept_storages.size() != record->outs.size()) {
+        e.outputs = kept_outputs;
+        record->outs = kept_storages;
+        l.writes = kept_storages;
+        double reads = 0;
+        for (const ExprInput &in : e.inputs) reads += distinct_elements(e, in);
+        l.bytes = 4.0 * (reads + (double)e.volume() * (double)e.outputs.size());
+        l.what = "chain " + record->ops + " " + describe_expr(e) + ", " + std::to_string(e.outputs.size()) +
+                 " outputs";
+      }
+      record->g = generate_chain(e);
+      pending.push_back(record->g);
+    }
+  }
+
+  static bool same_input(const ExprInput &a, const ExprInput &b, int rank) {
+    if (a.kind != b.kind || a.offset != b.offset) return false;
+    if (a.kind == ExprInput::kLiteral || a.kind == ExprInput::kSelection)
+      return __builtin_bit_cast(uint32_t, a.one) == __builtin_bit_cast(uint32_t, b.one);
+    for (int d = 0; d < rank; ++d)
+      if (a.strides[d] != b.strides[d]) return false;
+    return a.kind != ExprInput::kPadded ||
+           (a.pad_axis == b.pad_axis && a.pad_start == b.pad_start && a.pad_len == b.pad_len);
+  }
+
+  // Joins chain `e` (writing `out`) to the open chain when that chain is the
+  // last launch, iterates the same shape, and every input of `e` is either
+  // complete before it or one of its outputs read in its own layout (then
+  // the joined expression takes the value from registers). The operations
+  // and their order per element are unchanged, so are the bits.
+  bool join_open_chain(const Expr &e, const std::vector<int> &storage_of, int out, const std::string &op) {
+    auto record = open_chain;
+    if (!record || record->launch != (int)launches.size() - 1) return false;
+    Expr m = record->e;
+    if (m.rank != e.rank || m.outputs.size() >= 8) return false;
+    for (int d = 0; d < e.rank; ++d)
+      if (m.shape[d] != e.shape[d]) return false;
+    const Layout whole = contiguous(e.rank, e.shape);
+    std::vector<int> so = record->storage_of;
+    std::vector<int> mapped(e.inputs.size());
+    for (size_t j = 0; j < e.inputs.size(); ++j) {
+      const ExprInput &in = e.inputs[j];
+      const int storage = storage_of[j];
+      int produced = -1;
+      for (size_t k = 0; k < record->outs.size(); ++k)
+        if (storage >= 0 && record->outs[k] == storage) produced = (int)k;
+      if (produced >= 0) {
+        if (in.kind != ExprInput::kStrided || in.offset != 0) return false;
+        for (int d = 0; d < e.rank; ++d)
+          if (e.shape[d] != 1 && in.strides[d] != whole.strides[d]) return false;
+        mapped[j] = m.outputs[produced];
+        continue;
+      }
+      int found = -1;
+      for (size_t i = 0; i < m.inputs.size() && found < 0; ++i)
+        if (so[i] == storage && same_input(m.inputs[i], in, e.rank)) found = (int)i;
+      if (found < 0) {
+        m.inputs.push_back(in);
+        so.push_back(storage);
+        found = (int)m.inputs.size() - 1;
+      }
+      mapped[j] = -(found + 1);
+    }
+    if (m.inputs.size() > 24) return false;
+    const int shift = (int)m.steps.size();
+    auto remap = [&](int r) { return r >= 0 ? r + shift : mapped[-r - 1]; };
+    for (const ExprStep &x : e.steps)
+      m.steps.push_back(ExprStep{x.op, remap(x.left), is_binary(x.op) ? remap(x.right) : x.right});
+    m.outputs.push_back(remap(e.outputs[0]));
+    record->e = m;
+    record->storage_of = so;
+    record->outs.push_back(out);
+    record->ops += "+" + op;
+    Launch &l = launches[record->launch];
+    l.reads = real(so);
+    l.writes = record->outs;
+    l.what = "chain " + record->ops + " " + describe_expr(m) + ", " + std::to_string(m.outputs.size()) + " outputs";
+    double reads = 0;
+    for (const ExprInput &in : m.inputs) reads += distinct_elements(m, in);
+    l.bytes = 4.0 * (reads + (double)m.volume() * (double)m.outputs.size());
+    return true;
   }
 
   // Copies any dense/constant value into a fresh contiguous buffer.
@@ -1935,7 +2058,9 @@ struct topos_hip_program {
     // A duplicate (wanted only when readable) reads its original's value.
     for (int64_t i = 0; i < (int64_t)nodes.size(); ++i)
       if (wanted[i] && alias_of[i] >= 0) values[i] = values[alias_of[i]];
+    open_chain.reset();
     finish_readables();
+    finish_chains();
     assign_streams();
     assign_arena();
     compile_kernels(pending, device);

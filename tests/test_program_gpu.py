@@ -498,3 +498,28 @@ def test_whole_sums_exact(hip, case):
     assert "sum (ordered, gathered)" in program.describe, program.describe
     for r in roots:
         assert_bitwise(got[r.id], want[r.id], f"{case} sum node {r.id}")
+
+
+def test_joined_chains_exact(hip):
+    """Consecutive chains over one shape run as one multi-output kernel (a
+    member reading an earlier member's output takes it from registers); a
+    chain reading that output transposed runs after it. Bit-identical to the
+    interpreter either way, including outputs only the joined members read."""
+    banner("program joined chains")
+    rng = np.random.default_rng(23)
+    tape = t.Tape()
+    x = tape.input((48, 48))
+    y = tape.input((48, 48))
+    a = x * x + y
+    b = a * x
+    c = (b + a).exp()
+    d = a.transpose() * y
+    g = (c * b).tanh() + b
+    roots = [c, d, g]
+    dense = {x.node.slot: rng.standard_normal((48, 48)).astype(np.float32),
+             y.node.slot: rng.standard_normal((48, 48)).astype(np.float32)}
+    want = run_oracle(tape, roots, [], dense)
+    got, program = run_device(tape, roots, [], dense)
+    assert "outputs" in program.describe, program.describe
+    for r in roots:
+        assert_bitwise(got[r.id], want[r.id], f"node {r.id}")

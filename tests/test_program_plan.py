@@ -153,3 +153,25 @@ print(p.info["launches"], d.count("gemm mfma"), d.count("[side]"), d.count(": ro
 ''')
     launches, gemms, side, rows = map(int, out.split())
     assert launches > 100 and gemms > 20 and side > 10 and rows >= 10, out
+
+
+def test_consecutive_chains_join():
+    # a = x*x + y has two consumers, so it is materialised; the chains that
+    # follow over the same shape join its launch (one kernel, several
+    # outputs), except one that reads it transposed, which must wait for the
+    # whole of it.
+    out = run(r'''
+tape = t.Tape()
+x = tape.input((48, 48))
+y = tape.input((48, 48))
+a = x * x + y
+b = a * x
+c = (b + a).exp()
+d = a.transpose() * y
+p = DeviceProgram(tape, [c, b, d])
+print(p.info["launches"])
+print(p.describe)
+''')
+    lines = out.splitlines()
+    assert lines[0] == "2", out
+    assert "chain Add+Mul+Exp [48,48]" in out and ", 3 outputs" in out, out
