@@ -234,6 +234,215 @@ __global__ __launch_bounds__(BM / WM * BN, BM == 256 && kVector ? 4 : 1) void ge
     }
 }
 
+// ---- the LDS-DMA variant ----
+//
+// Interior-friendly operands (16-byte aligned rows, k a multiple of 16) are
+// staged by global_load_lds_dwordx4: each lane's 16 bytes land in LDS
+// without passing through registers, so no LDS store instructions and no
+// register staging. Three LDS stages: slab s + 2 is in flight while slab s
+// feeds the matrix cores, and each wave waits only for slab s + 1's loads
+// (vmcnt) before the one barrier per slab. A wave-wide DMA writes 1 KB at
+// consecutive 16-byte positions, so the layouts are chosen through which
+// address each lane loads:
+//  * k-contiguous operand: 16 rows x 16 k per KB; the k-quad q of local row
+//    r sits at position 4r + (q ^ swz(r)) (conflict-free 16-byte fragment
+//    reads for 32 or 64 banks). A fragment read gives a lane four k values;
+//    MFMA t of a k-group of 8 then takes k = t from lanes 0-31 and k = 4 + t
+//    from lanes 32-63 (the other operand is read in the same k order).
+//  * outer-contiguous operand: k-rows of O floats; quad j of row kk sits at
+//    quad position j ^ (kk & 4 ? 8 : 0) (rows kk and kk + 4, read by the two
+//    half-waves together, land on different banks).
+// Rows or columns past the operand's edge load a clamped in-range address;
+// they only feed outputs that are not stored.
+__device__ __forceinline__ int dma_swizzle(int r) { return ((r >> 1) ^ (r >> 2)) & 3; }
+
+template <int O>
+__device__ __forceinline__ int dma_outer_index(int kk, int o) {
+  return kk * O + (((o >> 2) ^ ((kk & 4) ? 8 : 0)) << 2) + (o & 3);
+}
+
+#define TOPOS_COMPILER_FENCE() __atomic_signal_fence(__ATOMIC_SEQ_CST)
+
+// One slab (16 deep) of an operand with outer extent O into `lds`.
+template <int O, int W, bool kInnerK>
+__device__ __forceinline__ void dma_slab(const float *__restrict__ p, int64_t outer_stride, int64_t k_stride,
+                                         int64_t outer_extent, int64_t o0, int64_t k0, float *lds, int wave,
+                                         int lane) {
+  constexpr int kChunks = O * kTileK / 256;  // 1 KB per wave-wide load
+  static_assert(kChunks % W == 0, "whole chunks per wave");
+#pragma unroll
+  for (int i = 0; i < kChunks / W; ++i) {
+    const int c = wave + W * i;
+    const float *src;
+    if (kInnerK) {
+      const int r = lane >> 2;
+      const int q = (lane & 3) ^ dma_swizzle(r);
+      const int64_t row = min(o0 + 16 * c + r, outer_extent - 1);
+      src = p + row * outer_stride + (k0 + 4 * q);
+    } else {
+      constexpr int kRows = 256 / O;  // k-rows per chunk
+      const int kk = c * kRows + lane / (O / 4);
+      const int quad = (lane % (O / 4)) ^ ((kk & 4) ? 8 : 0);
+      const int64_t col = min(o0 + 4 * quad, outer_extent - 4);
+      src = p + (k0 + kk) * k_stride + col;
+    }
+    TOPOS_COMPILER_FENCE();
+    __builtin_amdgcn_global_load_lds(src, lds + c * 256, 16, 0, 0);
+    TOPOS_COMPILER_FENCE();
+  }
+}
+
+// Waits until at most N of this lane's vector-memory operations are
+// outstanding (s_waitcnt vmcnt(N); expcnt and lgkmcnt left at their maxima).
+template <int N>
+__device__ __forceinline__ void dma_wait() {
+  static_assert(N < 16, "vmcnt field");
+  TOPOS_COMPILER_FENCE();
+  __builtin_amdgcn_s_waitcnt(0xF70 | N);
+  TOPOS_COMPILER_FENCE();
+}
+
+// A barrier without the workgroup fence of __syncthreads(), which would also
+// wait for the DMA loads kept in flight across it.
+__device__ __forceinline__ void dma_barrier() {
+  TOPOS_COMPILER_FENCE();
+  __builtin_amdgcn_s_barrier();
+  TOPOS_COMPILER_FENCE();
+}
+
+template <int BM, int BN, bool kLeftInnerK, bool kRightInnerK>
+__global__ __launch_bounds__(BM * BN / 64) void gemm_dma_kernel(
+    const float *__restrict__ a, int64_t a_rs, int64_t a_cs, const float *__restrict__ b, int64_t b_rs,
+    int64_t b_cs, int64_t m, int64_t k, int64_t n, float *__restrict__ c, int64_t ldc, int grid_m, int grid_n,
+    int64_t a_bs, int64_t b_bs, int64_t c_bs, int64_t split_len, int64_t split_stride,
+    const float *__restrict__ bias, int64_t bias_cs, int bias_mode) {
+  constexpr int W = BM * BN / 4096;  // waves, one 64x64 block each
+  constexpr int WN = BN / 64;
+  constexpr int SA = BM * kTileK, SB = BN * kTileK;  // floats per stage
+  constexpr int kIssue = BM * kTileK / 256 / W + BN * kTileK / 256 / W;  // DMA loads per wave per slab
+  __shared__ __attribute__((aligned(1024))) float lds[3 * (SA + SB)];
+  a += (int64_t)blockIdx.y * a_bs;
+  b += (int64_t)blockIdx.y * b_bs;
+  c += (int64_t)blockIdx.y * c_bs;
+  const int64_t k_begin = (int64_t)blockIdx.z * split_len;
+  const int64_t k_end = min(k, k_begin + split_len);
+  c += (int64_t)blockIdx.z * split_stride;
+
+  const int blocks = grid_m * grid_n;
+  int pid = blockIdx.x;
+  if (blocks % 8 == 0) pid = (pid % 8) * (blocks / 8) + pid / 8;
+  const int in_group = kGroupM * grid_n;
+  const int group = pid / in_group;
+  const int first_m = group * kGroupM;
+  const int group_rows = min(grid_m - first_m, kGroupM);
+  const int tile_m = first_m + (pid % in_group) % group_rows;
+  const int tile_n = (pid % in_group) / group_rows;
+  const int64_t m0 = (int64_t)tile_m * BM;
+  const int64_t n0 = (int64_t)tile_n * BN;
+
+  const int lane = threadIdx.x % 64;
+  const int wave = threadIdx.x / 64;
+  const int wm = (wave / WN) * 64;
+  const int wn = (wave % WN) * 64;
+  const int half = lane / 32, l32 = lane % 32;
+
+  floatx16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  auto issue = [&](int s) {
+    float *stage = lds + (s % 3) * (SA + SB);
+    const int64_t k0 = k_begin + (int64_t)s * kTileK;
+    dma_slab<BM, W, kLeftInnerK>(a, a_rs, a_cs, m, m0, k0, stage, wave, lane);
+    dma_slab<BN, W, kRightInnerK>(b, b_cs, b_rs, n, n0, k0, stage + SA, wave, lane);
+  };
+  const int slabs = (int)((k_end - k_begin) / kTileK);
+  issue(0);
+  if (slabs > 1) {
+    issue(1);
+    dma_wait<kIssue>();
+  } else {
+    dma_wait<0>();
+  }
+  dma_barrier();
+  for (int s = 0; s < slabs; ++s) {
+    if (s + 2 < slabs) issue(s + 2);
+    const float *sa = lds + (s % 3) * (SA + SB);
+    const float *sb = sa + SA;
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {  // k groups of 8
+      float av[2][4], bv[2][4];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int row = wm + 32 * i + l32;
+        if (kLeftInnerK) {
+          const int q = 2 * g + half;
+          const float4 v = *reinterpret_cast<const float4 *>(
+              sa + 256 * (row >> 4) + 4 * (4 * (row & 15) + (q ^ dma_swizzle(row & 15))));
+          av[i][0] = v.x;
+          av[i][1] = v.y;
+          av[i][2] = v.z;
+          av[i][3] = v.w;
+        } else {
+#pragma unroll
+          for (int t = 0; t < 4; ++t) av[i][t] = sa[dma_outer_index<BM>(8 * g + 4 * half + t, row)];
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int col = wn + 32 * j + l32;
+        if (kRightInnerK) {
+          const int q = 2 * g + half;
+          const float4 v = *reinterpret_cast<const float4 *>(
+              sb + 256 * (col >> 4) + 4 * (4 * (col & 15) + (q ^ dma_swizzle(col & 15))));
+          bv[j][0] = v.x;
+          bv[j][1] = v.y;
+          bv[j][2] = v.z;
+          bv[j][3] = v.w;
+        } else {
+#pragma unroll
+          for (int t = 0; t < 4; ++t) bv[j][t] = sb[dma_outer_index<BN>(8 * g + 4 * half + t, col)];
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][t], bv[j][t], acc[i][j], 0, 0, 0);
+    }
+    if (s + 1 < slabs) {
+      if (s + 2 < slabs)
+        dma_wait<kIssue>();
+      else
+        dma_wait<0>();
+      dma_barrier();
+    }
+  }
+
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int64_t col = n0 + wn + 32 * j + (lane % 32);
+      if (col >= n) continue;
+      const float add = bias_mode != 0 ? bias[col * bias_cs] : 0.0f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t row = m0 + wm + 32 * i + 8 * (r / 4) + 4 * (lane / 32) + (r % 4);
+        float v = acc[i][j][r];
+        if (bias_mode == 1) v = v + add;
+        if (bias_mode == 2) v = add + v;
+        if (row < m) c[row * ldc + col] = v;
+      }
+    }
+}
+
 // The tile shape for an m x n product (over `batches`): 128x64 or 64x128
 // when one output extent is at most 64; 256x128 (eight waves, less operand
 // traffic per flop than 128x128) when its tiles fill whole rounds of two
@@ -287,6 +496,26 @@ void dispatch_orientation(bool lk, bool rk, bool vector, dim3 grid, hipStream_t 
     dispatch_vector<BM, BN, false, true>(vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, gm, gn, batch, c_bs, split_len, split_stride, e, mode);
   else
     dispatch_vector<BM, BN, false, false>(vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, gm, gn, batch, c_bs, split_len, split_stride, e, mode);
+}
+
+template <int BM, int BN>
+void dispatch_dma(bool lk, bool rk, dim3 grid, hipStream_t stream, const float *a, int64_t a_rs, int64_t a_cs,
+                  const float *b, int64_t b_rs, int64_t b_cs, int64_t m, int64_t k, int64_t n, float *c, int64_t ldc,
+                  int gm, int gn, const Batch &batch, int64_t c_bs, int64_t split_len, int64_t split_stride,
+                  const Epilogue &e, int mode) {
+  constexpr int T = BM * BN / 64;
+#define TOPOS_DMA_ARGS                                                                                           \
+  a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, gm, gn, batch.a_stride, batch.b_stride, c_bs, split_len, \
+      split_stride, e.bias, e.bias_stride, mode
+  if (lk && rk)
+    gemm_dma_kernel<BM, BN, true, true><<<grid, T, 0, stream>>>(TOPOS_DMA_ARGS);
+  else if (lk)
+    gemm_dma_kernel<BM, BN, true, false><<<grid, T, 0, stream>>>(TOPOS_DMA_ARGS);
+  else if (rk)
+    gemm_dma_kernel<BM, BN, false, true><<<grid, T, 0, stream>>>(TOPOS_DMA_ARGS);
+  else
+    gemm_dma_kernel<BM, BN, false, false><<<grid, T, 0, stream>>>(TOPOS_DMA_ARGS);
+#undef TOPOS_DMA_ARGS
 }
 
 // The fixed-order sum of `splits` partial products (each [count][m][n],
@@ -405,7 +634,19 @@ bool launch_gemm_mfma(const float *a, int64_t a_rs, int64_t a_cs, const float *b
   float *target = splits > 1 ? workspace : c;
   const int64_t target_ld = splits > 1 ? n : ldc;
   const int64_t target_bs = splits > 1 ? m * n : batch.c_stride;
-  if (shape.bm == 256)
+  // The LDS-DMA kernel: the 256x128 and 128x128 tiles, k in whole slabs, and
+  // every row an operand's loads start on 16-byte aligned (clamped edge
+  // loads included).
+  const bool aligned_a = reinterpret_cast<uintptr_t>(a) % 16 == 0 && batch.a_stride % 4 == 0 &&
+                         (lk ? a_rs % 4 == 0 : a_cs % 4 == 0 && m % 4 == 0);
+  const bool aligned_b = reinterpret_cast<uintptr_t>(b) % 16 == 0 && batch.b_stride % 4 == 0 &&
+                         (rk ? b_cs % 4 == 0 : b_rs % 4 == 0 && n % 4 == 0);
+  const bool dma = vector && shape.bn == 128 && shape.bm >= 128 && k % kTileK == 0 && aligned_a && aligned_b;
+  if (dma && shape.bm == 256)
+    dispatch_dma<256, 128>(lk, rk, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, target, target_ld, (int)gm, (int)gn, batch, target_bs, split_len, split_stride, epilogue, gemm_mode);
+  else if (dma)
+    dispatch_dma<128, 128>(lk, rk, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, target, target_ld, (int)gm, (int)gn, batch, target_bs, split_len, split_stride, epilogue, gemm_mode);
+  else if (shape.bm == 256)
     dispatch_orientation<256, 128>(lk, rk, vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, target, target_ld, (int)gm, (int)gn, batch, target_bs, split_len, split_stride, epilogue, gemm_mode);
   else if (shape.bn == 64)
     dispatch_orientation<128, 64>(lk, rk, vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, target, target_ld, (int)gm, (int)gn, batch, target_bs, split_len, split_stride, epilogue, gemm_mode);

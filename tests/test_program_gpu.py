@@ -523,3 +523,31 @@ def test_joined_chains_exact(hip):
     assert "outputs" in program.describe, program.describe
     for r in roots:
         assert_bitwise(got[r.id], want[r.id], f"node {r.id}")
+
+
+@pytest.mark.parametrize("form", ["plain", "left_transposed", "right_transposed"])
+def test_fast_batched_products_with_edges(hip, form):
+    """Batched fast products whose tiles overhang m and n (the LDS-DMA
+    kernel clamps those loads), in each operand orientation: within the
+    envelope of the interpreter's exact product."""
+    banner(f"program fast batched edges {form}")
+    rng = np.random.default_rng(41)
+    B, M, K, N = 3, 300, 96, 260
+    tape = t.Tape()
+    if form == "left_transposed":
+        a = tape.input((B, K, M)); av = a.permute((0, 2, 1))
+    else:
+        a = tape.input((B, M, K)); av = a
+    if form == "right_transposed":
+        b = tape.input((B, N, K)); bv = b.permute((0, 2, 1))
+    else:
+        b = tape.input((B, K, N)); bv = b
+    y = av.matmul(bv)
+    dense = {a.node.slot: rng.standard_normal(tape.input_shapes[0]).astype(np.float32),
+             b.node.slot: rng.standard_normal(tape.input_shapes[1]).astype(np.float32)}
+    want = run_oracle(tape, [y], [], dense)[y.id].astype(np.float64)
+    got, _ = run_device(tape, [y], [], dense, numerics=hip.FAST)
+    la = dense[a.node.slot] if form != "left_transposed" else dense[a.node.slot].transpose(0, 2, 1)
+    lb = dense[b.node.slot] if form != "right_transposed" else dense[b.node.slot].transpose(0, 2, 1)
+    bound = 1e-5 * np.einsum("bmk,bkn->bmn", np.abs(la.astype(np.float64)), np.abs(lb.astype(np.float64)))
+    assert (np.abs(got[y.id].astype(np.float64) - want) <= bound).all()
