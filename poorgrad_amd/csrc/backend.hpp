@@ -122,9 +122,15 @@ void check_launch(const char *what);
 // A batch of equally shaped products: product `i` reads a + i * a_bs and
 // b + i * b_bs and writes c + i * c_bs (the batch odometer of
 // src/payload/tensor.rs:950-1006 flattened to one axis).
+// Leading (batch) axes of a product. Batch y sits at
+// (y / inner) * x_stride + (y % inner) * x_inner for x in a, b, c: one
+// strided batch axis (inner = 1), or two merged ones (attention heads viewed
+// as one axis of batch x heads).
 struct Batch {
   int64_t count = 1;
   int64_t a_stride = 0, b_stride = 0, c_stride = 0;
+  int64_t inner = 1;
+  int64_t a_inner = 0, b_inner = 0, c_inner = 0;
 };
 
 // A per-column vector added to a product as it is written: c = p + bias[j]

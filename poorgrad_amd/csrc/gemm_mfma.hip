@@ -122,15 +122,19 @@ __global__ __launch_bounds__(BM / WM * BN, BM == 256 && kVector ? 4 : 1) void ge
     const float *__restrict__ a, int64_t a_rs, int64_t a_cs, const float *__restrict__ b,
     int64_t b_rs, int64_t b_cs, int64_t m, int64_t k, int64_t n, float *__restrict__ c, int64_t ldc,
     int grid_m, int grid_n, int64_t a_bs, int64_t b_bs, int64_t c_bs, int64_t split_len, int64_t split_stride,
-    const float *__restrict__ bias, int64_t bias_cs, int bias_mode) {
+    const float *__restrict__ bias, int64_t bias_cs, int bias_mode, int64_t inner, int64_t a_bs2, int64_t b_bs2,
+    int64_t c_bs2) {
   constexpr int T = BM / WM * BN;  // one WM x 64 block per wave
   constexpr int WN = BN / 64;
   constexpr int WI = WM / 32;      // 32-row MFMA blocks per wave
   __shared__ float left[2][kTileK][BM + kPad];
   __shared__ float right[2][kTileK][BN + kPad];
-  a += (int64_t)blockIdx.y * a_bs;
-  b += (int64_t)blockIdx.y * b_bs;
-  c += (int64_t)blockIdx.y * c_bs;
+  {
+    const int64_t outer = (int64_t)blockIdx.y / inner, within = (int64_t)blockIdx.y - outer * inner;
+    a += outer * a_bs + within * a_bs2;
+    b += outer * b_bs + within * b_bs2;
+    c += outer * c_bs + within * c_bs2;
+  }
   // Split k: this workgroup sums k in [k_begin, k_end) into its own partial
   // product (the fixed-order reduction adds the partials afterwards).
   const int64_t k_begin = (int64_t)blockIdx.z * split_len;
@@ -315,15 +319,19 @@ __global__ __launch_bounds__(BM * BN / 64) void gemm_dma_kernel(
     const float *__restrict__ a, int64_t a_rs, int64_t a_cs, const float *__restrict__ b, int64_t b_rs,
     int64_t b_cs, int64_t m, int64_t k, int64_t n, float *__restrict__ c, int64_t ldc, int grid_m, int grid_n,
     int64_t a_bs, int64_t b_bs, int64_t c_bs, int64_t split_len, int64_t split_stride,
-    const float *__restrict__ bias, int64_t bias_cs, int bias_mode) {
+    const float *__restrict__ bias, int64_t bias_cs, int bias_mode, int64_t inner, int64_t a_bs2, int64_t b_bs2,
+    int64_t c_bs2) {
   constexpr int W = BM * BN / 4096;  // waves, one 64x64 block each
   constexpr int WN = BN / 64;
   constexpr int SA = BM * kTileK, SB = BN * kTileK;  // floats per stage
   constexpr int kIssue = BM * kTileK / 256 / W + BN * kTileK / 256 / W;  // DMA loads per wave per slab
   __shared__ __attribute__((aligned(1024))) float lds[3 * (SA + SB)];
-  a += (int64_t)blockIdx.y * a_bs;
-  b += (int64_t)blockIdx.y * b_bs;
-  c += (int64_t)blockIdx.y * c_bs;
+  {
+    const int64_t outer = (int64_t)blockIdx.y / inner, within = (int64_t)blockIdx.y - outer * inner;
+    a += outer * a_bs + within * a_bs2;
+    b += outer * b_bs + within * b_bs2;
+    c += outer * c_bs + within * c_bs2;
+  }
   const int64_t k_begin = (int64_t)blockIdx.z * split_len;
   const int64_t k_end = min(k, k_begin + split_len);
   c += (int64_t)blockIdx.z * split_stride;
@@ -470,43 +478,46 @@ template <int BM, int BN, bool kL, bool kR>
 void dispatch_vector(bool vector, dim3 grid, hipStream_t stream, const float *a, int64_t a_rs,
                      int64_t a_cs, const float *b, int64_t b_rs, int64_t b_cs, int64_t m, int64_t k,
                      int64_t n, float *c, int64_t ldc, int gm, int gn, const Batch &batch, int64_t c_bs,
-                     int64_t split_len, int64_t split_stride, const Epilogue &e, int mode) {
+                     int64_t c_bs2, int64_t split_len, int64_t split_stride, const Epilogue &e, int mode) {
   constexpr int WM = wave_rows(BM, BN);
   constexpr int T = BM / WM * BN;
   if (vector)
     gemm_mfma_kernel<BM, BN, WM, kL, kR, true><<<grid, T, 0, stream>>>(a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, gm,
                                                                    gn, batch.a_stride, batch.b_stride, c_bs,
-                                                                   split_len, split_stride, e.bias, e.bias_stride, mode);
+                                                                   split_len, split_stride, e.bias, e.bias_stride, mode,
+                                                                   batch.inner, batch.a_inner, batch.b_inner, c_bs2);
   else
     gemm_mfma_kernel<BM, BN, WM, kL, kR, false><<<grid, T, 0, stream>>>(a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, gm,
                                                                     gn, batch.a_stride, batch.b_stride, c_bs,
-                                                                    split_len, split_stride, e.bias, e.bias_stride, mode);
+                                                                    split_len, split_stride, e.bias, e.bias_stride, mode,
+                                                                   batch.inner, batch.a_inner, batch.b_inner, c_bs2);
 }
 
 template <int BM, int BN>
 void dispatch_orientation(bool lk, bool rk, bool vector, dim3 grid, hipStream_t stream, const float *a,
                           int64_t a_rs, int64_t a_cs, const float *b, int64_t b_rs, int64_t b_cs, int64_t m,
                           int64_t k, int64_t n, float *c, int64_t ldc, int gm, int gn, const Batch &batch,
-                          int64_t c_bs, int64_t split_len, int64_t split_stride, const Epilogue &e, int mode) {
+                          int64_t c_bs, int64_t c_bs2, int64_t split_len, int64_t split_stride, const Epilogue &e,
+                          int mode) {
   if (lk && rk)
-    dispatch_vector<BM, BN, true, true>(vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, gm, gn, batch, c_bs, split_len, split_stride, e, mode);
+    dispatch_vector<BM, BN, true, true>(vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, gm, gn, batch, c_bs, c_bs2, split_len, split_stride, e, mode);
   else if (lk)
-    dispatch_vector<BM, BN, true, false>(vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, gm, gn, batch, c_bs, split_len, split_stride, e, mode);
+    dispatch_vector<BM, BN, true, false>(vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, gm, gn, batch, c_bs, c_bs2, split_len, split_stride, e, mode);
   else if (rk)
-    dispatch_vector<BM, BN, false, true>(vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, gm, gn, batch, c_bs, split_len, split_stride, e, mode);
+    dispatch_vector<BM, BN, false, true>(vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, gm, gn, batch, c_bs, c_bs2, split_len, split_stride, e, mode);
   else
-    dispatch_vector<BM, BN, false, false>(vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, gm, gn, batch, c_bs, split_len, split_stride, e, mode);
+    dispatch_vector<BM, BN, false, false>(vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, gm, gn, batch, c_bs, c_bs2, split_len, split_stride, e, mode);
 }
 
 template <int BM, int BN>
 void dispatch_dma(bool lk, bool rk, dim3 grid, hipStream_t stream, const float *a, int64_t a_rs, int64_t a_cs,
                   const float *b, int64_t b_rs, int64_t b_cs, int64_t m, int64_t k, int64_t n, float *c, int64_t ldc,
-                  int gm, int gn, const Batch &batch, int64_t c_bs, int64_t split_len, int64_t split_stride,
-                  const Epilogue &e, int mode) {
+                  int gm, int gn, const Batch &batch, int64_t c_bs, int64_t c_bs2, int64_t split_len,
+                  int64_t split_stride, const Epilogue &e, int mode) {
   constexpr int T = BM * BN / 64;
 #define TOPOS_DMA_ARGS                                                                                           \
   a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, gm, gn, batch.a_stride, batch.b_stride, c_bs, split_len, \
-      split_stride, e.bias, e.bias_stride, mode
+      split_stride, e.bias, e.bias_stride, mode, batch.inner, batch.a_inner, batch.b_inner, c_bs2
   if (lk && rk)
     gemm_dma_kernel<BM, BN, true, true><<<grid, T, 0, stream>>>(TOPOS_DMA_ARGS);
   else if (lk)
@@ -616,6 +627,8 @@ bool launch_gemm_mfma(const float *a, int64_t a_rs, int64_t a_cs, const float *b
   const int64_t gn = (n + shape.bn - 1) / shape.bn;
   if (gm * gn > 0x7fffffff || batch.count > 65535 || batch.count < 1) throw Unsupported{"mfma gemm: grid too large"};
   int splits = mfma_splits(m, n, k, batch.count);
+  if (batch.inner < 1) throw Unsupported{"mfma gemm: batch inner extent below one"};
+  if (batch.inner > 1) splits = 1;  // the reduction walks one flat batch axis
   const int64_t split_stride = batch.count * m * n;
   if (splits > 1 && (!workspace || workspace_floats < splits * split_stride || n % 4 != 0 ||
                      reinterpret_cast<uintptr_t>(workspace) % 16 != 0 || splits > 16 ||
@@ -633,27 +646,29 @@ bool launch_gemm_mfma(const float *a, int64_t a_rs, int64_t a_cs, const float *b
   // workspace, then reduced into c.
   float *target = splits > 1 ? workspace : c;
   const int64_t target_ld = splits > 1 ? n : ldc;
-  const int64_t target_bs = splits > 1 ? m * n : batch.c_stride;
+  // (partials: batch y at y * m * n, as (y / inner) * inner * m * n + (y % inner) * m * n)
+  const int64_t target_bs = splits > 1 ? batch.inner * m * n : batch.c_stride;
+  const int64_t target_bs2 = splits > 1 ? m * n : batch.c_inner;
   // The LDS-DMA kernel: the 256x128 and 128x128 tiles, k in whole slabs, and
   // every row an operand's loads start on 16-byte aligned (clamped edge
   // loads included).
-  const bool aligned_a = reinterpret_cast<uintptr_t>(a) % 16 == 0 && batch.a_stride % 4 == 0 &&
+  const bool aligned_a = reinterpret_cast<uintptr_t>(a) % 16 == 0 && batch.a_stride % 4 == 0 && batch.a_inner % 4 == 0 &&
                          (lk ? a_rs % 4 == 0 : a_cs % 4 == 0 && m % 4 == 0);
-  const bool aligned_b = reinterpret_cast<uintptr_t>(b) % 16 == 0 && batch.b_stride % 4 == 0 &&
+  const bool aligned_b = reinterpret_cast<uintptr_t>(b) % 16 == 0 && batch.b_stride % 4 == 0 && batch.b_inner % 4 == 0 &&
                          (rk ? b_cs % 4 == 0 : b_rs % 4 == 0 && n % 4 == 0);
   const bool dma = vector && shape.bn == 128 && shape.bm >= 128 && k % kTileK == 0 && aligned_a && aligned_b;
   if (dma && shape.bm == 256)
-    dispatch_dma<256, 128>(lk, rk, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, target, target_ld, (int)gm, (int)gn, batch, target_bs, split_len, split_stride, epilogue, gemm_mode);
+    dispatch_dma<256, 128>(lk, rk, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, target, target_ld, (int)gm, (int)gn, batch, target_bs, target_bs2, split_len, split_stride, epilogue, gemm_mode);
   else if (dma)
-    dispatch_dma<128, 128>(lk, rk, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, target, target_ld, (int)gm, (int)gn, batch, target_bs, split_len, split_stride, epilogue, gemm_mode);
+    dispatch_dma<128, 128>(lk, rk, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, target, target_ld, (int)gm, (int)gn, batch, target_bs, target_bs2, split_len, split_stride, epilogue, gemm_mode);
   else if (shape.bm == 256)
-    dispatch_orientation<256, 128>(lk, rk, vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, target, target_ld, (int)gm, (int)gn, batch, target_bs, split_len, split_stride, epilogue, gemm_mode);
+    dispatch_orientation<256, 128>(lk, rk, vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, target, target_ld, (int)gm, (int)gn, batch, target_bs, target_bs2, split_len, split_stride, epilogue, gemm_mode);
   else if (shape.bn == 64)
-    dispatch_orientation<128, 64>(lk, rk, vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, target, target_ld, (int)gm, (int)gn, batch, target_bs, split_len, split_stride, epilogue, gemm_mode);
+    dispatch_orientation<128, 64>(lk, rk, vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, target, target_ld, (int)gm, (int)gn, batch, target_bs, target_bs2, split_len, split_stride, epilogue, gemm_mode);
   else if (shape.bm == 64)
-    dispatch_orientation<64, 128>(lk, rk, vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, target, target_ld, (int)gm, (int)gn, batch, target_bs, split_len, split_stride, epilogue, gemm_mode);
+    dispatch_orientation<64, 128>(lk, rk, vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, target, target_ld, (int)gm, (int)gn, batch, target_bs, target_bs2, split_len, split_stride, epilogue, gemm_mode);
   else
-    dispatch_orientation<128, 128>(lk, rk, vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, target, target_ld, (int)gm, (int)gn, batch, target_bs, split_len, split_stride, epilogue, gemm_mode);
+    dispatch_orientation<128, 128>(lk, rk, vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, target, target_ld, (int)gm, (int)gn, batch, target_bs, target_bs2, split_len, split_stride, epilogue, gemm_mode);
   check_launch("gemm_mfma_kernel launch");
   if (splits > 1) {
     const int64_t quads = split_stride / 4;

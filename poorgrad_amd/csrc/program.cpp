@@ -175,6 +175,13 @@ struct Value {
   float host_value = 0.0f;
   // No element is -0 (a matrix-core product, and views of one).
   bool never_minus_zero = false;
+  // A rank-3 view whose axis 0 merges two strided axes (batch x heads):
+  // index y sits at (y / split_inner) * split_outer_stride + (y % split_inner)
+  // * split_inner_stride, and layout.strides[0] is unused. Only products
+  // read such a value (their two-level batch strides); anything else copies
+  // it first.
+  int64_t split_inner = 0;
+  int64_t split_outer_stride = 0, split_inner_stride = 0;
 };
 
 // Device buffers of a bound selection: its indices and their row-sorted
@@ -296,11 +303,22 @@ struct topos_hip_program {
     int64_t offset = 0, stride = 0;
     bool first = false;  // bias + product rather than product + bias
   };
+  // Where a product writes: its storage, row stride and batch strides (a
+  // product read only through a copying reshape of its permuted view writes
+  // straight into the reshape's layout instead).
+  struct ProductOutput {
+    int storage = -1;
+    int64_t ldc = 0;
+    Batch batch;
+  };
   struct ProductLaunch {
     int launch;
     std::shared_ptr<BiasEpilogue> bias;
+    std::shared_ptr<ProductOutput> output;
+    bool flat = true;
   };
   std::map<int64_t, ProductLaunch> product_launch;
+  std::map<int, int64_t> product_of_storage;  // a matrix-core product's output storage -> its node
   std::vector<std::vector<int>> consumers;
   std::vector<Value> values;
   std::vector<Storage> storages;
@@ -1022,6 +1040,7 @@ struct topos_hip_program {
       e.steps.push_back(ExprStep{op, a, b});
       result = (int)e.steps.size() - 1;
     } else {
+      if (v.split_inner > 0) throw RuntimeFailure{"a merged-batch view read by a generated expression"};
       ExprInput in;
       int storage = v.storage;
       if (v.kind == Value::kDense && v.host_known) {
@@ -1240,7 +1259,18 @@ struct topos_hip_program {
     for (int d = 0; d < n.rank; ++d) e.shape[d] = n.shape[d];
     ExprInput in;
     std::vector<int> storage_of;
-    if (v.host_known) {
+    if (v.split_inner > 0) {
+      // The merged axis copied as its two axes (the same element order).
+      e.rank = n.rank + 1;
+      e.shape[0] = n.shape[0] / v.split_inner;
+      e.shape[1] = v.split_inner;
+      for (int d = 1; d < n.rank; ++d) e.shape[d + 1] = n.shape[d];
+      in.offset = v.layout.offset;
+      in.strides[0] = v.split_outer_stride;
+      in.strides[1] = v.split_inner_stride;
+      for (int d = 1; d < n.rank; ++d) in.strides[d + 1] = v.layout.strides[d];
+      storage_of.push_back(v.storage);
+    } else if (v.host_known) {
       in.kind = ExprInput::kLiteral;
       in.one = v.host_value;
       storage_of.push_back(-1);
@@ -1263,10 +1293,127 @@ struct topos_hip_program {
     return dense_value(out, contiguous(n.rank, n.shape));
   }
 
+  // Reshape i copies a permuted view of a matrix-core product's output that
+  // nothing else reads (attention heads merged back into rows): the product
+  // writes straight into the reshape's contiguous layout instead, through
+  // its row and two-level batch strides, and the reshape is a view of that.
+  bool retarget_product(int64_t source, int64_t i, Value &out) {
+    const Value &v = values[source];
+    if (numerics != TOPOS_HIP_FAST || v.kind != Value::kDense || v.split_inner > 0 || v.layout.offset != 0)
+      return false;
+    auto found = product_of_storage.find(v.storage);
+    if (found == product_of_storage.end()) return false;
+    const int64_t product = found->second;
+    ProductLaunch &record = product_launch.at(product);
+    if (!record.flat || record.bias->storage >= 0) return false;
+    // Views, and +0 + v planned as v itself (the zero-seeded gradient
+    // accumulation), between the product and the reshape.
+    for (int64_t node = product; node != i;) {
+      if (readable[node] || consumers[node].size() != 1) return false;
+      const int64_t from = node;
+      node = consumers[node][0];
+      const topos_hip_node &y = nodes[node];
+      if (node == i || y.op == TOPOS_HIP_OP_RESHAPE || y.op == TOPOS_HIP_OP_PERMUTE) continue;
+      const bool identity = y.op == TOPOS_HIP_OP_ADD &&
+                            static_plus_zero(y.operands[0] == from ? y.operands[1] : y.operands[0]) &&
+                            values[node].kind == Value::kDense && values[node].storage == v.storage;
+      if (!identity) return false;
+    }
+    const topos_hip_node &p = nodes[product];
+    if (p.rank != 3) return false;
+    const int64_t count = p.shape[0], m = p.shape[1], n = p.shape[2];
+    const Layout &l = v.layout;
+    const Layout target = contiguous(l.rank, l.shape);
+    int col = -1, row = -1, outer = -1, inner_axis = -1;
+    for (int d = 0; d < l.rank; ++d) {
+      if (l.shape[d] == 1) continue;
+      if (l.strides[d] == 1 && l.shape[d] == n && col < 0) col = d;
+      else if (l.strides[d] == n && l.shape[d] == m && row < 0) row = d;
+      else if (l.strides[d] == m * n && inner_axis < 0) inner_axis = d;
+      else if (outer < 0) outer = d;
+      else return false;
+    }
+    if (col != l.rank - 1 || row < 0 || (n > 1 && col < 0)) return false;
+    int64_t inner = 1, c_stride = 0, c_inner = 0;
+    if (outer >= 0) {
+      // Two batch axes: (y / inner) along `outer`, (y % inner) along `inner_axis`.
+      if (inner_axis < 0) return false;
+      inner = l.shape[inner_axis];
+      if (l.strides[outer] != inner * m * n || l.shape[outer] * inner != count) return false;
+      c_stride = target.strides[outer];
+      c_inner = target.strides[inner_axis];
+    } else if (inner_axis >= 0) {
+      if (l.shape[inner_axis] != count) return false;
+      c_stride = target.strides[inner_axis];
+    } else if (count != 1) {
+      return false;
+    }
+    Batch batch = record.output->batch;
+    if (inner > 1) {
+      if (batch.inner == 1) {
+        batch.a_inner = batch.a_stride;
+        batch.a_stride *= inner;
+        batch.b_inner = batch.b_stride;
+        batch.b_stride *= inner;
+        batch.inner = inner;
+      } else if (batch.inner != inner) {
+        return false;
+      }
+      batch.c_stride = c_stride;
+      batch.c_inner = c_inner;
+    } else {
+      if (batch.inner != 1) return false;
+      batch.c_stride = c_stride;
+    }
+    const int storage = arena_storage(count * m * n * 4);
+    record.output->storage = storage;
+    record.output->ldc = target.strides[row];
+    record.output->batch = batch;
+    for (int &w : launches[record.launch].writes)
+      if (w == v.storage) w = storage;
+    product_of_storage.erase(found);
+    const topos_hip_node &x = nodes[i];
+    out = dense_value(storage, contiguous(x.rank, x.shape));
+    out.never_minus_zero = true;
+    return true;
+  }
+
   // Makes node i's value usable as a strided dense operand.
   const Value &dense_operand(int64_t i) {
-    if (values[i].kind == Value::kSelection) values[i] = materialize(i);
+    if (values[i].kind == Value::kSelection || values[i].split_inner > 0) values[i] = materialize(i);
     return values[i];
+  }
+
+  // A constant +0 known from the graph alone (a +0 Constant leaf, or a view
+  // of one): the zero_like seed of recorded gradient accumulations.
+  bool static_plus_zero(int64_t j) const {
+    const topos_hip_node &x = nodes[j];
+    if (x.op == TOPOS_HIP_OP_LEAF) {
+      const topos_hip_leaf &leaf = leaves[x.slot];
+      return leaf.kind == TOPOS_HIP_LEAF_CONSTANT && __builtin_bit_cast(uint32_t, leaf.value) == 0;
+    }
+    if (x.op == TOPOS_HIP_OP_BROADCAST || x.op == TOPOS_HIP_OP_BROADCAST_ALONG || x.op == TOPOS_HIP_OP_RESHAPE ||
+        x.op == TOPOS_HIP_OP_PERMUTE || x.op == TOPOS_HIP_OP_TRANSPOSE)
+      return static_plus_zero(x.operands[0]);
+    return false;
+  }
+
+  // Node i is read only by products, directly or through permutations that
+  // keep axis 0 first, or through +0 + i when i has no -0 element (planned
+  // as i itself); and nothing reads it from the host.
+  bool feeds_products_only(int64_t i, bool never_minus_zero) const {
+    if (readable[i]) return false;
+    for (int c : consumers[i]) {
+      const topos_hip_node &x = nodes[c];
+      if (x.op == TOPOS_HIP_OP_MATMUL && x.rank == 3) continue;
+      if (x.op == TOPOS_HIP_OP_PERMUTE && x.params[0] == 0 && feeds_products_only(c, never_minus_zero)) continue;
+      if (x.op == TOPOS_HIP_OP_ADD && never_minus_zero && group_of[c] < 0) {
+        const int64_t other = x.operands[0] == i ? x.operands[1] : x.operands[0];
+        if (other != i && static_plus_zero(other) && feeds_products_only(c, never_minus_zero)) continue;
+      }
+      return false;
+    }
+    return !consumers[i].empty();
   }
 
   // ---- the node loop ----
@@ -1331,6 +1478,17 @@ struct topos_hip_program {
         return;
       }
       case TOPOS_HIP_OP_PERMUTE: {
+        if (values[x.operands[0]].split_inner > 0 && x.params[0] == 0) {
+          Value v = values[x.operands[0]];
+          Layout l = v.layout;
+          for (int d = 1; d < x.rank; ++d) {
+            l.shape[d] = v.layout.shape[x.params[d]];
+            l.strides[d] = v.layout.strides[x.params[d]];
+          }
+          v.layout = l;
+          out = v;
+          return;
+        }
         const Value &a = dense_operand(x.operands[0]);
         Layout l = a.layout;
         for (int d = 0; d < x.rank; ++d) {
@@ -1379,6 +1537,30 @@ struct topos_hip_program {
           out = view_of(a, l);
           return;
         }
+        // Merging the two leading axes of a rank-4 view that only products
+        // read (attention heads as one batch axis): the products take the two
+        // strides themselves, with no copy.
+        const Layout &al = a.layout;
+        if (numerics == TOPOS_HIP_FAST && al.rank == 4 && x.rank == 3 && x.shape[0] == al.shape[0] * al.shape[1] &&
+            x.shape[1] == al.shape[2] && x.shape[2] == al.shape[3] && al.shape[1] > 1 &&
+            feeds_products_only(i, a.never_minus_zero)) {
+          Value v = a;
+          v.layout.rank = 3;
+          v.layout.shape[0] = x.shape[0];
+          v.layout.strides[0] = 0;
+          for (int d = 1; d < 3; ++d) {
+            v.layout.shape[d] = al.shape[d + 1];
+            v.layout.strides[d] = al.strides[d + 1];
+          }
+          v.layout.shape[3] = 1;
+          v.layout.strides[3] = 0;
+          v.split_inner = al.shape[1];
+          v.split_outer_stride = al.strides[0];
+          v.split_inner_stride = al.strides[1];
+          out = v;
+          return;
+        }
+        if (retarget_product(x.operands[0], i, out)) return;
         // Not a view (layout.rs reshape answers None): the interpreter copies
         // the elements out in logical order.
         Value copied = materialize(x.operands[0]);
@@ -1576,17 +1758,49 @@ struct topos_hip_program {
 
   void plan_matmul(int64_t i) {
     const topos_hip_node &x = nodes[i];
-    const Value a = dense_operand(x.operands[0]);
-    const Value b = dense_operand(x.operands[1]);
     const int r = x.rank, s = r - 2;
     const int64_t m = x.shape[s], n = x.shape[s + 1], k = nodes[x.operands[0]].shape[s + 1];
+    // Merged-batch operands: served by the matrix-core kernel's two-level
+    // batch strides when both merges agree, else copied.
+    const Value &va = values[x.operands[0]], &vb = values[x.operands[1]];
+    int64_t inner = va.split_inner > 0 ? va.split_inner : vb.split_inner;
+    if (inner > 0) {
+      const Layout &la = va.layout, &lb = vb.layout;
+      const bool agree = (va.split_inner == 0 || va.split_inner == inner) &&
+                         (vb.split_inner == 0 || vb.split_inner == inner);
+      if (!(numerics == TOPOS_HIP_FAST && r == 3 && agree &&
+            mfma_serves(la.strides[1], la.strides[2], lb.strides[1], lb.strides[2], m, k, n)))
+        inner = 0;
+    }
+    const Value a = inner > 0 ? values[x.operands[0]] : dense_operand(x.operands[0]);
+    const Value b = inner > 0 ? values[x.operands[1]] : dense_operand(x.operands[1]);
     int64_t batches = 1;
     for (int d = 0; d < s; ++d) batches *= x.shape[d];
     const int out = arena_storage(batches * m * n * 4);
     Batch batch;
     batch.count = batches;
     batch.c_stride = m * n;
-    bool flat = batch_stride(a.layout, s, batch.a_stride) && batch_stride(b.layout, s, batch.b_stride);
+    bool flat;
+    if (inner > 0) {
+      // Batch y at (y / inner) * stride + (y % inner) * inner stride.
+      auto two_level = [inner](const Value &v, int64_t &outer, int64_t &within) {
+        if (v.split_inner > 0) {
+          outer = v.split_outer_stride;
+          within = v.split_inner_stride;
+        } else {
+          within = v.layout.strides[0];
+          outer = within * inner;
+        }
+      };
+      batch.inner = inner;
+      two_level(a, batch.a_stride, batch.a_inner);
+      two_level(b, batch.b_stride, batch.b_inner);
+      batch.c_inner = m * n;
+      batch.c_stride = inner * m * n;
+      flat = true;
+    } else {
+      flat = batch_stride(a.layout, s, batch.a_stride) && batch_stride(b.layout, s, batch.b_stride);
+    }
     // Per-launch offsets when the batch axes do not flatten: one product per
     // batch index, each at its own operand offsets.
     std::vector<std::array<int64_t, 3>> parts;
@@ -1626,13 +1840,19 @@ struct topos_hip_program {
     std::vector<int> writes = {out};
     if (workspace >= 0) writes.push_back(workspace);
     auto bias = std::make_shared<BiasEpilogue>();
+    auto output = std::make_shared<ProductOutput>();
+    output->storage = out;
+    output->ldc = n;
+    output->batch = batch;
     const int launch =
         add_launch(what.str(), {a.storage, b.storage}, writes,
-                   [this, a, b, out, parts, batch, m, n, k, ars, acs, brs, bcs, numerics_, workspace, workspace_floats,
+                   [this, a, b, output, parts, m, n, k, ars, acs, brs, bcs, numerics_, workspace, workspace_floats,
                     bias](const Exec &ex) {
                      const float *pa = (const float *)base(a.storage);
                      const float *pb = (const float *)base(b.storage);
-                     float *pc = (float *)base(out);
+                     float *pc = (float *)base(output->storage);
+                     const Batch &batch = output->batch;
+                     const int64_t ldc = output->ldc;
                      float *pw = workspace >= 0 ? (float *)base(workspace) : nullptr;
                      Epilogue epilogue;
                      if (bias->storage >= 0) {
@@ -1644,14 +1864,18 @@ struct topos_hip_program {
                        const float *qa = pa + part[0], *qb = pb + part[1];
                        float *qc = pc + part[2];
                        if (numerics_ == TOPOS_HIP_FAST &&
-                           launch_gemm_mfma(qa, ars, acs, qb, brs, bcs, m, k, n, qc, n, ex.stream, batch, pw,
+                           launch_gemm_mfma(qa, ars, acs, qb, brs, bcs, m, k, n, qc, ldc, ex.stream, batch, pw,
                                             workspace_floats, epilogue))
                          continue;
-                       // A fused bias is planned only where the matrix-core kernel serves.
-                       launch_gemm_exact(qa, ars, acs, qb, brs, bcs, m, k, n, qc, n, ex.stream, batch);
+                       // A fused bias, two-level batches and a retargeted output
+                       // are planned only where the matrix-core kernel serves.
+                       launch_gemm_exact(qa, ars, acs, qb, brs, bcs, m, k, n, qc, ldc, ex.stream, batch);
                      }
                    });
-    if (mfma_product[i]) product_launch[i] = ProductLaunch{launch, bias};
+    if (mfma_product[i]) {
+      product_launch[i] = ProductLaunch{launch, bias, output, flat};
+      product_of_storage[out] = i;
+    }
     launches.back().flops = 2.0 * (double)batches * m * n * k;
     launches.back().bytes = 4.0 * (double)batches * ((double)m * k + (double)k * n + (double)m * n);
     values[i] = dense_value(out, contiguous(x.rank, x.shape));

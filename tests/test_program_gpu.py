@@ -551,3 +551,34 @@ def test_fast_batched_products_with_edges(hip, form):
     lb = dense[b.node.slot] if form != "right_transposed" else dense[b.node.slot].transpose(0, 2, 1)
     bound = 1e-5 * np.einsum("bmk,bkn->bmn", np.abs(la.astype(np.float64)), np.abs(lb.astype(np.float64)))
     assert (np.abs(got[y.id].astype(np.float64) - want) <= bound).all()
+
+
+def test_fast_head_merging_views_within_envelope(hip):
+    """Attention heads split from a fused projection and merged back
+    (examples/gpt2/model.rs split_heads): the products read the heads through
+    two-level batch strides and the head-merging reshape after the last
+    product is written by the product itself; gradients flow through both.
+    Within the envelope of the interpreter."""
+    banner("program fast head views")
+    rng = np.random.default_rng(43)
+    batch, context, heads, head = 2, 24, 3, 8
+    width = heads * head
+    tape = t.Tape()
+    fused = tape.parameter((batch * context, 3 * width))
+
+    def split(part):
+        x = fused.narrow(1, part * width, width).reshape((batch, context, heads, head))
+        return x.permute((0, 2, 1, 3)).reshape((batch * heads, context, head))
+
+    q, k, v = split(0), split(1), split(2)
+    weights = q.matmul(k.permute((0, 2, 1))).softmax(2)
+    attended = weights.matmul(v).reshape((batch, heads, context, head)).permute((0, 2, 1, 3))
+    merged = attended.reshape((batch * context, width))
+    loss = (merged * merged).sum()
+    (grad,) = tape.differentiate(loss, [fused])
+    params = [rng.standard_normal((batch * context, 3 * width)).astype(np.float32)]
+    want = run_oracle(tape, [loss, merged, grad], params)
+    got, program = run_device(tape, [loss, merged, grad], params, numerics=hip.FAST)
+    for r in (loss, merged, grad):
+        g, e = got[r.id].astype(np.float64), want[r.id].astype(np.float64)
+        assert (np.abs(g - e) <= 1e-4 * np.maximum(np.abs(e), 1.0)).all(), f"node {r.id}"
