@@ -296,13 +296,50 @@ __device__ __forceinline__ void dma_slab(const float *__restrict__ p, int64_t ou
   }
 }
 
+// The same slab through registers, element by element, with zeros past k_end
+// and past the outer extent: the slabs a 16-byte load could not serve (a k
+// tail, or a partial quad of an outer-contiguous operand whose extent is not
+// a multiple of four). Same LDS layout as dma_slab.
+template <int O, int W, bool kInnerK>
+__device__ __forceinline__ void guarded_slab(const float *__restrict__ p, int64_t outer_stride, int64_t k_stride,
+                                             int64_t outer_extent, int64_t k_end, int64_t o0, int64_t k0, float *lds,
+                                             int wave, int lane) {
+  constexpr int kChunks = O * kTileK / 256;
+#pragma unroll
+  for (int i = 0; i < kChunks / W; ++i) {
+    const int c = wave + W * i;
+    float v[4];
+    if (kInnerK) {
+      const int r = lane >> 2;
+      const int q = (lane & 3) ^ dma_swizzle(r);
+      const int64_t row = o0 + 16 * c + r;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int64_t kk = k0 + 4 * q + e;
+        v[e] = row < outer_extent && kk < k_end ? p[row * outer_stride + kk * k_stride] : 0.0f;
+      }
+    } else {
+      constexpr int kRows = 256 / O;
+      const int kk = c * kRows + lane / (O / 4);
+      const int quad = (lane % (O / 4)) ^ ((kk & 4) ? 8 : 0);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int64_t col = o0 + 4 * quad + e;
+        v[e] = col < outer_extent && k0 + kk < k_end ? p[(k0 + kk) * k_stride + col * outer_stride] : 0.0f;
+      }
+    }
+    *reinterpret_cast<float4 *>(lds + c * 256 + 4 * lane) = make_float4(v[0], v[1], v[2], v[3]);
+  }
+}
+
 // Waits until at most N of this lane's vector-memory operations are
-// outstanding (s_waitcnt vmcnt(N); expcnt and lgkmcnt left at their maxima).
+// outstanding and its LDS operations are done (s_waitcnt vmcnt(N)
+// lgkmcnt(0); expcnt left at its maximum).
 template <int N>
 __device__ __forceinline__ void dma_wait() {
   static_assert(N < 16, "vmcnt field");
   TOPOS_COMPILER_FENCE();
-  __builtin_amdgcn_s_waitcnt(0xF70 | N);
+  __builtin_amdgcn_s_waitcnt(0x070 | N);
   TOPOS_COMPILER_FENCE();
 }
 
@@ -362,13 +399,23 @@ __global__ __launch_bounds__(BM * BN / 64) void gemm_dma_kernel(
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
+  // Slabs a 16-byte load cannot serve go through registers (uniform tests).
+  const bool ragged_a = !kLeftInnerK && m % 4 != 0 && m0 + BM > m;
+  const bool ragged_b = !kRightInnerK && n % 4 != 0 && n0 + BN > n;
   auto issue = [&](int s) {
     float *stage = lds + (s % 3) * (SA + SB);
     const int64_t k0 = k_begin + (int64_t)s * kTileK;
-    dma_slab<BM, W, kLeftInnerK>(a, a_rs, a_cs, m, m0, k0, stage, wave, lane);
-    dma_slab<BN, W, kRightInnerK>(b, b_cs, b_rs, n, n0, k0, stage + SA, wave, lane);
+    const bool tail = k0 + kTileK > k_end;
+    if (tail || ragged_a)
+      guarded_slab<BM, W, kLeftInnerK>(a, a_rs, a_cs, m, k_end, m0, k0, stage, wave, lane);
+    else
+      dma_slab<BM, W, kLeftInnerK>(a, a_rs, a_cs, m, m0, k0, stage, wave, lane);
+    if (tail || ragged_b)
+      guarded_slab<BN, W, kRightInnerK>(b, b_cs, b_rs, n, k_end, n0, k0, stage + SA, wave, lane);
+    else
+      dma_slab<BN, W, kRightInnerK>(b, b_cs, b_rs, n, n0, k0, stage + SA, wave, lane);
   };
-  const int slabs = (int)((k_end - k_begin) / kTileK);
+  const int slabs = (int)((k_end - k_begin + kTileK - 1) / kTileK);
   issue(0);
   if (slabs > 1) {
     issue(1);
@@ -649,14 +696,11 @@ bool launch_gemm_mfma(const float *a, int64_t a_rs, int64_t a_cs, const float *b
   // (partials: batch y at y * m * n, as (y / inner) * inner * m * n + (y % inner) * m * n)
   const int64_t target_bs = splits > 1 ? batch.inner * m * n : batch.c_stride;
   const int64_t target_bs2 = splits > 1 ? m * n : batch.c_inner;
-  // The LDS-DMA kernel: the 256x128 and 128x128 tiles, k in whole slabs, and
-  // every row an operand's loads start on 16-byte aligned (clamped edge
-  // loads included).
-  const bool aligned_a = reinterpret_cast<uintptr_t>(a) % 16 == 0 && batch.a_stride % 4 == 0 && batch.a_inner % 4 == 0 &&
-                         (lk ? a_rs % 4 == 0 : a_cs % 4 == 0 && m % 4 == 0);
-  const bool aligned_b = reinterpret_cast<uintptr_t>(b) % 16 == 0 && batch.b_stride % 4 == 0 && batch.b_inner % 4 == 0 &&
-                         (rk ? b_cs % 4 == 0 : b_rs % 4 == 0 && n % 4 == 0);
-  const bool dma = vector && shape.bn == 128 && shape.bm >= 128 && k % kTileK == 0 && aligned_a && aligned_b;
+  // The LDS-DMA kernel serves the 256x128 and 128x128 tiles with 16-byte
+  // operand access (the DMA loads need 4-byte alignment only); an
+  // outer-contiguous operand needs an outer extent of at least 4 (its clamped
+  // edge quads).
+  const bool dma = vector && shape.bn == 128 && shape.bm >= 128 && (lk || m >= 4) && (rk || n >= 4);
   if (dma && shape.bm == 256)
     dispatch_dma<256, 128>(lk, rk, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, target, target_ld, (int)gm, (int)gn, batch, target_bs, target_bs2, split_len, split_stride, epilogue, gemm_mode);
   else if (dma)
