@@ -43,6 +43,7 @@ FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense fp32 matrix, published
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, published
 SWEEP = [(512, 512, 512), (1024, 4096, 1024), (4096, 4096, 4096), (8192, 768, 3072)]
 CHAIN_ROWS, CHAIN_COLUMNS = 16384, 4096
+CHAIN_REPEAT = 5  # back-to-back launches per event pair in the chains section
 CHAIN_BYTES = {  # each distinct input read once, each output written once, fp32
     "silu_bias": 4 * (2 * CHAIN_ROWS * CHAIN_COLUMNS + CHAIN_COLUMNS),
     "layer_norm": 4 * (2 * CHAIN_ROWS * CHAIN_COLUMNS + 2 * CHAIN_COLUMNS),
@@ -247,7 +248,10 @@ def mlp_section(torch, n, steps: int, warmup: int) -> dict:
             "gflop_per_step": round(3 * matmul_flops(w.tape, [w.loss]) / 1e9, 4)}
 
 
-def event_times(torch, launches, steps: int, warmup: int) -> dict:
+def event_times(torch, launches, steps: int, warmup: int, repeat: int = 1) -> dict:
+    """Seconds per launch of each labelled launch: per step, `repeat`
+    back-to-back launches of it between two events (the labels interleave,
+    so each is timed after the others have run)."""
     for _ in range(warmup):
         for _, fn in launches:
             fn()
@@ -258,13 +262,14 @@ def event_times(torch, launches, steps: int, warmup: int) -> dict:
         for label, fn in launches:
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             e0.record(stream)
-            fn()
+            for _ in range(repeat):
+                fn()
             e1.record(stream)
             marks.append((label, e0, e1))
     torch.cuda.synchronize()
     per = {}
     for label, e0, e1 in marks:
-        per.setdefault(label, []).append(e0.elapsed_time(e1) / 1e3)
+        per.setdefault(label, []).append(e0.elapsed_time(e1) / 1e3 / repeat)
     return {label: sum(v) / len(v) for label, v in per.items()}
 
 
@@ -345,7 +350,7 @@ def chains_section(torch, n, steps: int, warmup: int) -> dict:
                          ("row_softmax", rows(n.ROWS_SOFTMAX, y, numerics))):
             launches.append((f"{name}/{posture}", fn))
             bytes_of[f"{name}/{posture}"] = CHAIN_BYTES[name]
-    per = event_times(torch, launches, steps, warmup)
+    per = event_times(torch, launches, steps, warmup, repeat=CHAIN_REPEAT)
     return {label: {"us": round(t * 1e6, 1), "GB/s": round(bytes_of[label] / t / 1e9, 1),
                     "frac": round(bytes_of[label] / t / 1e9 / HBM_PEAK_GBS, 4)} for label, t in per.items()}
 

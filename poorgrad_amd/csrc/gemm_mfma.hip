@@ -351,14 +351,91 @@ __device__ __forceinline__ void dma_barrier() {
   TOPOS_COMPILER_FENCE();
 }
 
-template <int BM, int BN, bool kLeftInnerK, bool kRightInnerK>
-__global__ __launch_bounds__(BM * BN / 64) void gemm_dma_kernel(
+// One slab's fragment reads and matrix-core products for a wave's WM x 64
+// block (the k order described above).
+template <int BM, int BN, int WM, bool kLeftInnerK, bool kRightInnerK>
+__device__ __forceinline__ void dma_mfma_slab(const float *sa, const float *sb, int wm, int wn, int half, int l32,
+                                              floatx16 (&acc)[WM / 32][2]) {
+  constexpr int WI = WM / 32;
+#pragma unroll
+  for (int g = 0; g < 2; ++g) {  // k groups of 8
+    float av[WI][4], bv[2][4];
+#pragma unroll
+    for (int i = 0; i < WI; ++i) {
+      const int row = wm + 32 * i + l32;
+      if (kLeftInnerK) {
+        const int q = 2 * g + half;
+        const float4 v = *reinterpret_cast<const float4 *>(
+            sa + 256 * (row >> 4) + 4 * (4 * (row & 15) + (q ^ dma_swizzle(row & 15))));
+        av[i][0] = v.x;
+        av[i][1] = v.y;
+        av[i][2] = v.z;
+        av[i][3] = v.w;
+      } else {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) av[i][t] = sa[dma_outer_index<BM>(8 * g + 4 * half + t, row)];
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int col = wn + 32 * j + l32;
+      if (kRightInnerK) {
+        const int q = 2 * g + half;
+        const float4 v = *reinterpret_cast<const float4 *>(
+            sb + 256 * (col >> 4) + 4 * (4 * (col & 15) + (q ^ dma_swizzle(col & 15))));
+        bv[j][0] = v.x;
+        bv[j][1] = v.y;
+        bv[j][2] = v.z;
+        bv[j][3] = v.w;
+      } else {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) bv[j][t] = sb[dma_outer_index<BN>(8 * g + 4 * half + t, col)];
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int i = 0; i < WI; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][t], bv[j][t], acc[i][j], 0, 0, 0);
+  }
+}
+
+// A wave's block of the output tile at (m0, n0) into c, with the bias
+// epilogue (bias_mode 0 none, 1 product + bias[col], 2 bias[col] + product).
+template <int WM>
+__device__ __forceinline__ void dma_store_block(const floatx16 (&acc)[WM / 32][2], float *__restrict__ c, int64_t ldc,
+                                                int64_t m, int64_t n, int64_t m0, int64_t n0, int wm, int wn, int lane,
+                                                const float *__restrict__ bias, int64_t bias_cs, int bias_mode) {
+  constexpr int WI = WM / 32;
+#pragma unroll
+  for (int i = 0; i < WI; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int64_t col = n0 + wn + 32 * j + (lane % 32);
+      if (col >= n) continue;
+      const float add = bias_mode != 0 ? bias[col * bias_cs] : 0.0f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t row = m0 + wm + 32 * i + 8 * (r / 4) + 4 * (lane / 32) + (r % 4);
+        float v = acc[i][j][r];
+        if (bias_mode == 1) v = v + add;
+        if (bias_mode == 2) v = add + v;
+        if (row < m) c[row * ldc + col] = v;
+      }
+    }
+}
+
+template <int BM, int BN, int WM, bool kLeftInnerK, bool kRightInnerK>
+__global__ __launch_bounds__(BM / WM * BN) void gemm_dma_kernel(
     const float *__restrict__ a, int64_t a_rs, int64_t a_cs, const float *__restrict__ b, int64_t b_rs,
     int64_t b_cs, int64_t m, int64_t k, int64_t n, float *__restrict__ c, int64_t ldc, int grid_m, int grid_n,
     int64_t a_bs, int64_t b_bs, int64_t c_bs, int64_t split_len, int64_t split_stride,
     const float *__restrict__ bias, int64_t bias_cs, int bias_mode, int64_t inner, int64_t a_bs2, int64_t b_bs2,
     int64_t c_bs2) {
-  constexpr int W = BM * BN / 4096;  // waves, one 64x64 block each
+  constexpr int W = BM / WM * BN / 64;  // waves, one WM x 64 block each
+  constexpr int WI = WM / 32;           // 32-row MFMA blocks per wave
   constexpr int WN = BN / 64;
   constexpr int SA = BM * kTileK, SB = BN * kTileK;  // floats per stage
   constexpr int kIssue = BM * kTileK / 256 / W + BN * kTileK / 256 / W;  // DMA loads per wave per slab
@@ -387,13 +464,13 @@ __global__ __launch_bounds__(BM * BN / 64) void gemm_dma_kernel(
 
   const int lane = threadIdx.x % 64;
   const int wave = threadIdx.x / 64;
-  const int wm = (wave / WN) * 64;
+  const int wm = (wave / WN) * WM;
   const int wn = (wave % WN) * 64;
   const int half = lane / 32, l32 = lane % 32;
 
-  floatx16 acc[2][2];
+  floatx16 acc[WI][2];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < WI; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -428,49 +505,7 @@ __global__ __launch_bounds__(BM * BN / 64) void gemm_dma_kernel(
     if (s + 2 < slabs) issue(s + 2);
     const float *sa = lds + (s % 3) * (SA + SB);
     const float *sb = sa + SA;
-#pragma unroll
-    for (int g = 0; g < 2; ++g) {  // k groups of 8
-      float av[2][4], bv[2][4];
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int row = wm + 32 * i + l32;
-        if (kLeftInnerK) {
-          const int q = 2 * g + half;
-          const float4 v = *reinterpret_cast<const float4 *>(
-              sa + 256 * (row >> 4) + 4 * (4 * (row & 15) + (q ^ dma_swizzle(row & 15))));
-          av[i][0] = v.x;
-          av[i][1] = v.y;
-          av[i][2] = v.z;
-          av[i][3] = v.w;
-        } else {
-#pragma unroll
-          for (int t = 0; t < 4; ++t) av[i][t] = sa[dma_outer_index<BM>(8 * g + 4 * half + t, row)];
-        }
-      }
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int col = wn + 32 * j + l32;
-        if (kRightInnerK) {
-          const int q = 2 * g + half;
-          const float4 v = *reinterpret_cast<const float4 *>(
-              sb + 256 * (col >> 4) + 4 * (4 * (col & 15) + (q ^ dma_swizzle(col & 15))));
-          bv[j][0] = v.x;
-          bv[j][1] = v.y;
-          bv[j][2] = v.z;
-          bv[j][3] = v.w;
-        } else {
-#pragma unroll
-          for (int t = 0; t < 4; ++t) bv[j][t] = sb[dma_outer_index<BN>(8 * g + 4 * half + t, col)];
-        }
-      }
-#pragma unroll
-      for (int t = 0; t < 4; ++t)
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-          for (int j = 0; j < 2; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][t], bv[j][t], acc[i][j], 0, 0, 0);
-    }
+    dma_mfma_slab<BM, BN, WM, kLeftInnerK, kRightInnerK>(sa, sb, wm, wn, half, l32, acc);
     if (s + 1 < slabs) {
       if (s + 2 < slabs)
         dma_wait<kIssue>();
@@ -480,22 +515,7 @@ __global__ __launch_bounds__(BM * BN / 64) void gemm_dma_kernel(
     }
   }
 
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int64_t col = n0 + wn + 32 * j + (lane % 32);
-      if (col >= n) continue;
-      const float add = bias_mode != 0 ? bias[col * bias_cs] : 0.0f;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int64_t row = m0 + wm + 32 * i + 8 * (r / 4) + 4 * (lane / 32) + (r % 4);
-        float v = acc[i][j][r];
-        if (bias_mode == 1) v = v + add;
-        if (bias_mode == 2) v = add + v;
-        if (row < m) c[row * ldc + col] = v;
-      }
-    }
+  dma_store_block<WM>(acc, c, ldc, m, n, m0, n0, wm, wn, lane, bias, bias_cs, bias_mode);
 }
 
 // The tile shape for an m x n product (over `batches`): 128x64 or 64x128
@@ -561,18 +581,19 @@ void dispatch_dma(bool lk, bool rk, dim3 grid, hipStream_t stream, const float *
                   const float *b, int64_t b_rs, int64_t b_cs, int64_t m, int64_t k, int64_t n, float *c, int64_t ldc,
                   int gm, int gn, const Batch &batch, int64_t c_bs, int64_t c_bs2, int64_t split_len,
                   int64_t split_stride, const Epilogue &e, int mode) {
-  constexpr int T = BM * BN / 64;
+  constexpr int WM = wave_rows(BM, BN);
+  constexpr int T = BM / WM * BN;
 #define TOPOS_DMA_ARGS                                                                                           \
   a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, gm, gn, batch.a_stride, batch.b_stride, c_bs, split_len, \
       split_stride, e.bias, e.bias_stride, mode, batch.inner, batch.a_inner, batch.b_inner, c_bs2
   if (lk && rk)
-    gemm_dma_kernel<BM, BN, true, true><<<grid, T, 0, stream>>>(TOPOS_DMA_ARGS);
+    gemm_dma_kernel<BM, BN, WM, true, true><<<grid, T, 0, stream>>>(TOPOS_DMA_ARGS);
   else if (lk)
-    gemm_dma_kernel<BM, BN, true, false><<<grid, T, 0, stream>>>(TOPOS_DMA_ARGS);
+    gemm_dma_kernel<BM, BN, WM, true, false><<<grid, T, 0, stream>>>(TOPOS_DMA_ARGS);
   else if (rk)
-    gemm_dma_kernel<BM, BN, false, true><<<grid, T, 0, stream>>>(TOPOS_DMA_ARGS);
+    gemm_dma_kernel<BM, BN, WM, false, true><<<grid, T, 0, stream>>>(TOPOS_DMA_ARGS);
   else
-    gemm_dma_kernel<BM, BN, false, false><<<grid, T, 0, stream>>>(TOPOS_DMA_ARGS);
+    gemm_dma_kernel<BM, BN, WM, false, false><<<grid, T, 0, stream>>>(TOPOS_DMA_ARGS);
 #undef TOPOS_DMA_ARGS
 }
 
@@ -696,14 +717,17 @@ bool launch_gemm_mfma(const float *a, int64_t a_rs, int64_t a_cs, const float *b
   // (partials: batch y at y * m * n, as (y / inner) * inner * m * n + (y % inner) * m * n)
   const int64_t target_bs = splits > 1 ? batch.inner * m * n : batch.c_stride;
   const int64_t target_bs2 = splits > 1 ? m * n : batch.c_inner;
-  // The LDS-DMA kernel serves the 256x128 and 128x128 tiles with 16-byte
-  // operand access (the DMA loads need 4-byte alignment only); an
+  // The LDS-DMA kernel serves the 256x128, 128x128 and 64x128 tiles with
+  // 16-byte operand access (the DMA loads need 4-byte alignment only); an
   // outer-contiguous operand needs an outer extent of at least 4 (its clamped
-  // edge quads).
-  const bool dma = vector && shape.bn == 128 && shape.bm >= 128 && (lk || m >= 4) && (rk || n >= 4);
+  // edge quads). The 128x64 tile (the attention products with a 64-wide right
+  // operand) measured faster on the register-staged kernel.
+  const bool dma = vector && (lk || m >= 4) && (rk || n >= 4);
   if (dma && shape.bm == 256)
     dispatch_dma<256, 128>(lk, rk, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, target, target_ld, (int)gm, (int)gn, batch, target_bs, target_bs2, split_len, split_stride, epilogue, gemm_mode);
-  else if (dma)
+  else if (dma && shape.bm == 64)
+    dispatch_dma<64, 128>(lk, rk, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, target, target_ld, (int)gm, (int)gn, batch, target_bs, target_bs2, split_len, split_stride, epilogue, gemm_mode);
+  else if (dma && shape.bn == 128)
     dispatch_dma<128, 128>(lk, rk, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, target, target_ld, (int)gm, (int)gn, batch, target_bs, target_bs2, split_len, split_stride, epilogue, gemm_mode);
   else if (shape.bm == 256)
     dispatch_orientation<256, 128>(lk, rk, vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, target, target_ld, (int)gm, (int)gn, batch, target_bs, target_bs2, split_len, split_stride, epilogue, gemm_mode);

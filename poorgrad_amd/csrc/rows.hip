@@ -231,10 +231,141 @@ __global__ __launch_bounds__(kThreads) void rows_fast_kernel(const float *__rest
   }
 }
 
+// Fast posture, rows that fit in registers (at most 256 * kQ columns, a
+// multiple of four): one wave per row holds the row's quads (lane l: quads
+// l, l + 64, ...), so every pass after the first load runs from registers
+// and the row is read once and written once.
+template <int kReduction, int kQ>
+__global__ __launch_bounds__(kThreads) void rows_fast_resident_kernel(const float *__restrict__ x, int64_t rows,
+                                                                      int64_t columns, const float *scale,
+                                                                      const float *shift, float epsilon,
+                                                                      float *__restrict__ out) {
+  // e^x reads its 32-entry table from LDS (a gather from global memory per
+  // call would cost a vector-memory instruction each).
+  __shared__ uint64_t exp_table[32];
+  constexpr bool kExp = kReduction == TOPOS_HIP_ROWS_SOFTMAX || kReduction == TOPOS_HIP_ROWS_LOG_SOFTMAX ||
+                        kReduction == TOPOS_HIP_ROWS_LOG_SUM_EXP;
+  if (kExp) {
+    if (threadIdx.x < 32) exp_table[threadIdx.x] = topos_faithful::kExpTableDevice[threadIdx.x];
+    __syncthreads();
+  }
+  const int lane = threadIdx.x % 64;
+  const int64_t row = (int64_t)blockIdx.x * (kThreads / 64) + threadIdx.x / 64;
+  if (row >= rows) return;
+  const int quads = (int)(columns / 4);
+  const float4 *src = reinterpret_cast<const float4 *>(x + row * columns);
+  float v[kQ][4];
+#pragma unroll
+  for (int i = 0; i < kQ; ++i) {
+    const int q = lane + 64 * i;
+    const float4 w = q < quads ? src[q] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    v[i][0] = w.x;
+    v[i][1] = w.y;
+    v[i][2] = w.z;
+    v[i][3] = w.w;
+  }
+  auto valid = [&](int i) { return lane + 64 * i < quads; };
+  if (kReduction == TOPOS_HIP_ROWS_SUM || kReduction == kLayerNorm) {
+    float total = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kQ; ++i)
+      if (valid(i))
+#pragma unroll
+        for (int j = 0; j < 4; ++j) total += v[i][j];
+    total = wave_sum(total);
+    if (kReduction == TOPOS_HIP_ROWS_SUM) {
+      if (lane == 0) out[row] = total;
+      return;
+    }
+    const float mean = total / (float)columns;
+    float power = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kQ; ++i)
+      if (valid(i))
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float centred = v[i][j] - mean;
+          power += centred * centred;
+        }
+    const float deviation = __builtin_sqrtf(wave_sum(power) / (float)columns + epsilon);
+    float4 *dst = reinterpret_cast<float4 *>(out + row * columns);
+    const float4 *sc = reinterpret_cast<const float4 *>(scale);
+    const float4 *sh = reinterpret_cast<const float4 *>(shift);
+#pragma unroll
+    for (int i = 0; i < kQ; ++i)
+      if (valid(i)) {
+        const int q = lane + 64 * i;
+        const float4 a = sc[q], b = sh[q];
+        dst[q] = make_float4(((v[i][0] - mean) / deviation) * a.x + b.x, ((v[i][1] - mean) / deviation) * a.y + b.y,
+                             ((v[i][2] - mean) / deviation) * a.z + b.z, ((v[i][3] - mean) / deviation) * a.w + b.w);
+      }
+    return;
+  }
+  // The max fold, seeded with the row's first value (NaN loses under max_f32).
+  float peak = x[row * columns];
+#pragma unroll
+  for (int i = 0; i < kQ; ++i)
+    if (valid(i))
+#pragma unroll
+      for (int j = 0; j < 4; ++j) peak = max_f32(peak, v[i][j]);
+  peak = wave_max(peak);
+  if (kReduction == TOPOS_HIP_ROWS_MAX) {
+    if (lane == 0) out[row] = peak;
+    return;
+  }
+  float total = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kQ; ++i)
+    if (valid(i))
+#pragma unroll
+      for (int j = 0; j < 4; ++j) total += topos_faithful::exp_f32_table(v[i][j] - peak, exp_table);
+  total = wave_sum(total);
+  if (kReduction == TOPOS_HIP_ROWS_LOG_SUM_EXP) {
+    if (lane == 0) out[row] = peak + ln_f32(total);
+    return;
+  }
+  const float normalizer = ln_f32(total);
+  float4 *dst = reinterpret_cast<float4 *>(out + row * columns);
+#pragma unroll
+  for (int i = 0; i < kQ; ++i)
+    if (valid(i)) {
+      float r[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        r[j] = (v[i][j] - peak) - normalizer;
+        if (kReduction == TOPOS_HIP_ROWS_SOFTMAX) r[j] = topos_faithful::exp_f32_table(r[j], exp_table);
+      }
+      dst[lane + 64 * i] = make_float4(r[0], r[1], r[2], r[3]);
+    }
+}
+
+template <int kReduction, int kQ>
+bool try_resident(const float *x, int64_t rows, int64_t columns, const float *scale, const float *shift,
+                  float epsilon, float *out, hipStream_t stream) {
+  if (columns > 256 * kQ) return false;
+  const int64_t blocks = (rows + 3) / 4;
+  rows_fast_resident_kernel<kReduction, kQ><<<(unsigned)blocks, kThreads, 0, stream>>>(x, rows, columns, scale, shift,
+                                                                                       epsilon, out);
+  return true;
+}
+
 template <int kReduction>
 void launch_one(const float *x, int64_t rows, int64_t columns, int numerics, const float *scale,
                 const float *shift, float epsilon, float *out, hipStream_t stream) {
   if (numerics == TOPOS_HIP_FAST) {
+    auto aligned = [](const void *p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+    const bool full = kReduction == TOPOS_HIP_ROWS_SOFTMAX || kReduction == TOPOS_HIP_ROWS_LOG_SOFTMAX ||
+                      kReduction == kLayerNorm;
+    if (columns % 4 == 0 && aligned(x) && (!full || aligned(out)) &&
+        (kReduction != kLayerNorm || (aligned(scale) && aligned(shift)))) {
+      if (try_resident<kReduction, 2>(x, rows, columns, scale, shift, epsilon, out, stream) ||
+          try_resident<kReduction, 4>(x, rows, columns, scale, shift, epsilon, out, stream) ||
+          try_resident<kReduction, 8>(x, rows, columns, scale, shift, epsilon, out, stream) ||
+          try_resident<kReduction, 16>(x, rows, columns, scale, shift, epsilon, out, stream)) {
+        check_launch("row reduction launch");
+        return;
+      }
+    }
     const int64_t blocks = (rows + 3) / 4;
     rows_fast_kernel<kReduction><<<(unsigned)blocks, kThreads, 0, stream>>>(x, rows, columns, scale, shift, epsilon, out);
   } else {

@@ -553,6 +553,37 @@ def test_fast_batched_products_with_edges(hip, form):
     assert (np.abs(got[y.id].astype(np.float64) - want) <= bound).all()
 
 
+@pytest.mark.parametrize("form", ["plain", "left_transposed", "right_transposed"])
+@pytest.mark.parametrize("shape", [(256, 257, 72, 130), (200, 61, 40, 998)])
+def test_fast_many_short_products(hip, form, shape):
+    """Many short batched products (k at most 128, over a thousand output
+    tiles, like the attention scores): 256x128 tiles with a k tail and
+    row/column overhang, and 64x128 tiles with a ragged outer-contiguous
+    edge, in each operand orientation. Within the envelope of the
+    interpreter's exact product."""
+    B, M, K, N = shape
+    banner(f"program fast many short products {form} {shape}")
+    rng = np.random.default_rng(47)
+    tape = t.Tape()
+    if form == "left_transposed":
+        a = tape.input((B, K, M)); av = a.permute((0, 2, 1))
+    else:
+        a = tape.input((B, M, K)); av = a
+    if form == "right_transposed":
+        b = tape.input((B, N, K)); bv = b.permute((0, 2, 1))
+    else:
+        b = tape.input((B, K, N)); bv = b
+    y = av.matmul(bv)
+    dense = {a.node.slot: rng.standard_normal(tape.input_shapes[0]).astype(np.float32),
+             b.node.slot: rng.standard_normal(tape.input_shapes[1]).astype(np.float32)}
+    want = run_oracle(tape, [y], [], dense)[y.id].astype(np.float64)
+    got, _ = run_device(tape, [y], [], dense, numerics=hip.FAST)
+    la = dense[a.node.slot] if form != "left_transposed" else dense[a.node.slot].transpose(0, 2, 1)
+    lb = dense[b.node.slot] if form != "right_transposed" else dense[b.node.slot].transpose(0, 2, 1)
+    bound = 1e-5 * np.matmul(np.abs(la.astype(np.float64)), np.abs(lb.astype(np.float64)))
+    assert (np.abs(got[y.id].astype(np.float64) - want) <= bound).all()
+
+
 def test_fast_head_merging_views_within_envelope(hip):
     """Attention heads split from a fused projection and merged back
     (examples/gpt2/model.rs split_heads): the products read the heads through
