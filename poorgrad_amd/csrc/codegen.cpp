@@ -975,7 +975,10 @@ RowLayout lay_out(const RowProgram &p) {
 }
 
 // How a row program is laid out on the GPU.
-//   resident: a workgroup owns G whole rows (G * columns <= 8192) and keeps
+//   resident: a workgroup owns G whole rows (columns <= 2048; G * columns
+//     <= 4096 where G >= 4 allows it: a 16 KB slab leaves room for six or
+//     more workgroups a CU, whose phases overlap, measured faster than 32 KB
+//     slabs on the attention rows [98304, 1024]) and keeps
 //     every non-literal input of its points in registers, read once; each
 //     fold parks its operand row-major in LDS, max folds reduce contiguous
 //     segments and combine them in column order, sum folds run one lane per
@@ -998,7 +1001,7 @@ RowBlocking row_blocking(const RowProgram &p) {
   for (const ExprInput &in : p.inputs) varying += in.kind != ExprInput::kLiteral;
   if (c * 4 <= 8192) {
     int g = 64;
-    while ((int64_t)g * c > 8192) g /= 2;
+    while (g > 4 && (int64_t)g * c > 4096) g /= 2;  // G >= 4: a max fold's lanes per row stay in one wave
     auto points = [&](int rows) { return (int)((rows * (c / b.width) + 255) / 256); };
     while (g > 4 && (int64_t)points(g) * b.width * varying > 128) g /= 2;
     if ((int64_t)points(g) * b.width * varying <= 128 && points(g) <= 32) {
