@@ -16,7 +16,11 @@ Measured beside it, each in its own section of the JSON line:
 * ``gemm_sweep``: forward A.B plus A^T.G and G.B^T for the four
   (M,N,K), TFLOP/s per product and per sweep, fast and exact;
 * ``chains``: SiLU + bias, LayerNorm, row sum/max/softmax on
-  [16384, 4096], GB/s of algorithmic traffic.
+  [16384, 4096], GB/s of algorithmic traffic (five back-to-back launches per
+  event pair);
+* ``llama``: the Llama-style decoder's forward + backward (8
+  layers, d_model 2048, 16 heads of 128, SwiGLU 5632, seq 2048, batch 2,
+  vocab 32000), ms per step and product TFLOP/s.
 
 The roofline object describes the step's dominant kernel class (most time in
 a profiled step, HIP events around every launch on the library's stream);
@@ -248,6 +252,39 @@ def mlp_section(torch, n, steps: int, warmup: int) -> dict:
             "gflop_per_step": round(3 * matmul_flops(w.tape, [w.loss]) / 1e9, 4)}
 
 
+def llama_section(torch, n, steps: int, warmup: int) -> dict:
+    """the Llama-style decoder's forward + backward (loss and every
+    gradient; no optimizer) through the fast-posture program. Weights are drawn
+    on the device (N(0, 0.02), torch generator seed 7; RMSNorm scales 1)."""
+    from poorgrad_amd import workloads
+    from poorgrad_amd.program import DeviceProgram
+
+    w = workloads.llama(host_weights=False)
+    t0 = time.perf_counter()
+    program = DeviceProgram(w.tape, w.roots, numerics=n.FAST)
+    plan_s = time.perf_counter() - t0
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(7)
+    params = [torch.ones(shape, device="cuda") if len(shape) == 1 else
+              torch.empty(shape, device="cuda").normal_(0.0, 0.02, generator=gen) for shape in w.initial]
+    for slot, p in enumerate(params):
+        program.bind_parameter(slot, p)
+    for slot, (indices, one) in w.selection_inputs.items():
+        program.bind_selection(slot, indices, one)
+    program.run()
+    torch.cuda.synchronize()
+    loss = float(program.read(w.loss))
+    wall = time_steps(torch, program.run, steps, warmup)
+    profile = program.profile()
+    flops = matmul_flops(w.tape, w.roots)
+    ms = wall / steps * 1e3
+    gemm = breakdown(profile).get("gemm", {})
+    return {"config": w.config, "ms_per_step": round(ms, 2), "tflop_per_step_products": round(flops / 1e12, 3),
+            "products_TFLOP/s": round(flops / (ms / 1e3) / 1e12, 2), "gemm": gemm,
+            "launches_per_step": program.info["launches"], "arena_gib": round(program.info["arena_bytes"] / 2**30, 2),
+            "plan_s": round(plan_s, 1), "loss": loss}
+
+
 def event_times(torch, launches, steps: int, warmup: int, repeat: int = 1) -> dict:
     """Seconds per launch of each labelled launch: per step, `repeat`
     back-to-back launches of it between two events (the labels interleave,
@@ -416,6 +453,8 @@ def main() -> int:
         line["gemm_sweep"] = gemm_section(torch, n, args.steps, args.warmup)
         log("chains (configs[2])")
         line["chains"] = chains_section(torch, n, args.steps, args.warmup)
+        log("llama forward + backward (configs[4])")
+        line["llama"] = llama_section(torch, n, args.steps, args.warmup)
     if not args.no_cpu_baseline:
         log("cpu baseline: the oracle interpreter on one core")
         line["cpu_baseline"] = cpu_leg(full_flops)

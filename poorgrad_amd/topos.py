@@ -445,6 +445,14 @@ def layer_norm(x: Value, scale: Value, shift: Value, epsilon: Value) -> Value:
     return normalized * scale.broadcast_along(0, x) + shift.broadcast_along(0, x)
 
 
+def rms_norm(x: Value, scale: Value, epsilon: Value) -> Value:
+    """RmsNorm::express (src/neural/rms_norm.rs:89-114): x / sqrt(mean_j(x^2)
+    + epsilon) * scale; `epsilon` is a single-value leaf."""
+    power = (x * x).mean_along(1)
+    root = (power + epsilon.broadcast_like(power)).sqrt()
+    return x / root.broadcast_along(1, x) * scale.broadcast_along(0, x)
+
+
 def cross_entropy(logits: Value, targets: Value) -> Value:
     """cross_entropy (src/neural/loss.rs:44-63)."""
     assert len(logits.shape) == 2 and targets.shape == logits.shape

@@ -7,8 +7,12 @@
   softmax attention batched as rank-3 products over (batch x heads), GELU MLP
   of 4x width, tied embeddings, cross-entropy over the vocabulary — with any
   dimensions (the parity tests record the same graph at a small size).
+* ``llama``: the Llama-style decoder of configs[4] — RMSNorm, rotary position
+  embeddings rotated by narrow/neg/concat, causal attention batched over
+  (batch x heads), SwiGLU MLP, bias-free projections, an untied head
+  (examples/llama/model.rs:80-330) — forward and backward, no optimizer.
 
-Both use the recorded-gradients route (src/graph/tape.rs:335-411;
+All use the recorded-gradients route (src/graph/tape.rs:335-411;
 examples/makemore/mlp_compiled.rs:142-204): one forward program reads the
 loss and every parameter's gradient. The recipes follow the reference's
 facades and examples (src/neural/{linear,layer_norm,loss}.rs,
@@ -22,7 +26,7 @@ from dataclasses import dataclass, field
 
 import numpy as np
 
-from .topos import Constant, Dense, Selection, Tape, Value, cross_entropy, layer_norm, linear
+from .topos import Constant, Dense, Selection, Tape, Value, concat, cross_entropy, layer_norm, linear, rms_norm
 
 # ---- synthetic data: src/neural/init.rs:45-102, vectorized ----
 
@@ -198,3 +202,117 @@ def gpt2(batch: int = 8, context: int = 1024, vocab: int = 50257, width: int = 7
                     selection_inputs={tokens.node.slot: (token_ids, 1.0), targets.node.slot: (next_ids, 1.0)},
                     config={"model": "gpt2", "batch": batch, "context": context, "vocab": vocab, "width": width,
                             "heads": heads, "layers": layers})
+
+
+def rope_tables(context: int, head: int, base: float = 10000.0):
+    """examples/llama/model.rs:88-117: column j and j + head/2 share the
+    frequency base^(-2 (j mod head/2) / head); angles in f64, tables rounded to
+    f32."""
+    half = head // 2
+    position = np.arange(context, dtype=np.float64)[:, None]
+    column = np.arange(head)[None, :] % half
+    angle = position * np.power(base, -2.0 * column / head)
+    return np.cos(angle).astype(np.float32), np.sin(angle).astype(np.float32)
+
+
+def llama(batch: int = 2, context: int = 2048, vocab: int = 32000, width: int = 2048, heads: int = 16,
+          hidden: int = 5632, layers: int = 8, epsilon: float = 1e-6, weight_seed: int = 7,
+          token_seed: int = 13, host_weights: bool = True) -> Workload:
+    """BASELINE configs[4] (or the same graph at other dimensions): a Llama-style
+    decoder, forward and backward (the loss and every parameter's gradient).
+    Blocks follow examples/llama/model.rs: pre-norm RMSNorm (:280-300), q/k/v/o
+    projections without bias, rotary embeddings on q and k (:119-131), causal
+    softmax attention with scale 1/sqrt(head) (:177-198), SwiGLU
+    x / (exp(-x) + 1) * up (:252-258); final RMSNorm and an untied head.
+    host_weights=False leaves `initial` as the parameter shapes (a caller that
+    draws the weights on the device; 542M host draws take minutes)."""
+    assert width % heads == 0 and (width // heads) % 2 == 0
+    head = width // heads
+    half = head // 2
+    rows = batch * context
+    tape = Tape()
+    params, initial = [], []
+    seed = [weight_seed]
+
+    def weight(shape):
+        p = tape.parameter(shape)
+        params.append(p)
+        initial.append(normal(seed[0], 0.02, shape) if host_weights else shape)
+        seed[0] += 1
+        return p
+
+    def ones(shape):
+        p = tape.parameter(shape)
+        params.append(p)
+        initial.append(np.ones(shape, np.float32) if host_weights else shape)
+        return p
+
+    embed = weight((vocab, width))
+    blocks = []
+    for _ in range(layers):
+        blocks.append({
+            "norm1": ones((width,)),
+            "q": weight((width, width)), "k": weight((width, width)), "v": weight((width, width)),
+            "o": weight((width, width)),
+            "norm2": ones((width,)),
+            "gate": weight((width, hidden)), "up": weight((width, hidden)), "down": weight((hidden, width)),
+        })
+    final_norm = ones((width,))
+    lm_head = weight((width, vocab))
+
+    # Leaves shared by every block.
+    cos, sin = rope_tables(context, head)
+    cos_leaf, sin_leaf = tape.leaf(Dense(cos)), tape.leaf(Dense(sin))
+    causal = np.where(np.arange(context)[None, :] <= np.arange(context)[:, None], 0.0, -np.inf).astype(np.float32)
+    mask = tape.leaf(Dense(causal))
+    scale = tape.leaf(Constant((), float(np.float32(1.0 / math.sqrt(head)))))
+    eps = tape.leaf(Constant((), float(np.float32(epsilon))))
+    one = tape.leaf(Constant((), 1.0))
+
+    tokens = tape.selection_input(rows, vocab)
+    targets = tape.selection_input(rows, vocab)
+
+    def split_heads(x: Value) -> Value:
+        return x.reshape((batch, context, heads, head)).permute((0, 2, 1, 3)).reshape((batch * heads, context, head))
+
+    def rotate(x: Value) -> Value:
+        # value * cos + rotate_half(value) * sin over [batch x heads, context, head]
+        flipped = concat([-x.narrow(2, half, half), x.narrow(2, 0, half)], 2)
+        return x * cos_leaf.broadcast_along(0, x) + flipped * sin_leaf.broadcast_along(0, x)
+
+    x = embed.gather(tokens)
+    for b in blocks:
+        h = rms_norm(x, b["norm1"], eps)
+        q = rotate(split_heads(h.matmul(b["q"])))
+        k = rotate(split_heads(h.matmul(b["k"])))
+        v = split_heads(h.matmul(b["v"]))
+        scores = q.matmul(k.permute((0, 2, 1)))
+        weights = (scores * scale.broadcast_like(scores) + mask.broadcast_along(0, scores)).softmax(2)
+        attended = weights.matmul(v).reshape((batch, heads, context, head)).permute((0, 2, 1, 3))
+        x = x + attended.reshape((rows, width)).matmul(b["o"])
+        h = rms_norm(x, b["norm2"], eps)
+        gated = h.matmul(b["gate"])
+        activated = gated / ((-gated).exp() + one.broadcast_like(gated))
+        x = x + (activated * h.matmul(b["up"])).matmul(b["down"])
+    logits = rms_norm(x, final_norm, eps).matmul(lm_head)
+    loss = cross_entropy(logits, targets)
+    gradients = tape.differentiate(loss, params)
+
+    stream = labels(token_seed, rows + batch, vocab).reshape(batch, context + 1)
+    token_ids = stream[:, :-1].reshape(-1)
+    next_ids = stream[:, 1:].reshape(-1)
+    return Workload(tape, params, initial, loss, gradients,
+                    selection_inputs={tokens.node.slot: (token_ids, 1.0), targets.node.slot: (next_ids, 1.0)},
+                    config={"model": "llama", "batch": batch, "context": context, "vocab": vocab, "width": width,
+                            "heads": heads, "hidden": hidden, "layers": layers})
+
+
+def llama_product_flops(w: Workload) -> float:
+    """2·m·n·k over the forward products, times three (forward, and the two
+    backward products of each)."""
+    c = w.config
+    rows, width, hidden, vocab = c["batch"] * c["context"], c["width"], c["hidden"], c["vocab"]
+    head = width // c["heads"]
+    per_layer = 2 * rows * width * width * 4 + 2 * rows * width * hidden * 3
+    attention = 2 * 2 * c["batch"] * c["heads"] * c["context"] ** 2 * head
+    return 3.0 * (c["layers"] * (per_layer + attention) + 2 * rows * width * vocab)

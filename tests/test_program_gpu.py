@@ -66,6 +66,30 @@ def test_small_gpt2_fast_within_envelope(hip):
         assert np.abs(g - e).max() <= 1e-3 * scale, f"gradient {r.id} {r.shape}"
 
 
+@pytest.mark.parametrize("layers, heads", [(1, 2), (2, 4)])
+def test_small_llama_exact_is_bit_identical(hip, layers, heads):
+    """The Llama-style decoder (RMSNorm, rotary embeddings rotated by
+    narrow/neg/concat, causal attention, SwiGLU, untied head) at a small size:
+    the loss and every gradient bit-identical."""
+    banner(f"program llama small layers={layers}")
+    w = workloads.llama(batch=2, context=16, vocab=37, width=32, heads=heads, hidden=48, layers=layers)
+    want, got, _ = check_workload(w, hip.EXACT, hip)
+    for r in w.roots:
+        assert_bitwise(got[r.id], want[r.id], f"llama node {r.id} {r.shape}")
+
+
+def test_small_llama_fast_within_envelope(hip):
+    banner("program llama small fast")
+    w = workloads.llama(batch=2, context=32, vocab=61, width=64, heads=4, hidden=96, layers=2)
+    want, got, _ = check_workload(w, hip.FAST, hip)
+    loss_exact, loss_fast = float(want[w.loss.id]), float(got[w.loss.id])
+    assert abs(loss_fast - loss_exact) <= 1e-4 * max(abs(loss_exact), 1.0)
+    for r in w.gradients:
+        g, e = got[r.id].astype(np.float64), want[r.id].astype(np.float64)
+        scale = max(np.abs(e).max(), 1e-3)
+        assert np.abs(g - e).max() <= 1e-3 * scale, f"gradient {r.id} {r.shape}"
+
+
 def coverage_graph():
     """One graph touching every served variant and storage kind."""
     rng = np.random.default_rng(5)

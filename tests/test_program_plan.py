@@ -155,6 +155,17 @@ print(p.info["launches"], d.count("gemm mfma"), d.count("[side]"), d.count(": ro
     assert launches > 100 and gemms > 20 and side > 10 and rows >= 10, out
 
 
+def test_the_llama_graph_plans():
+    out = run(r'''
+w = workloads.llama(batch=2, context=16, vocab=37, width=32, heads=4, hidden=48, layers=2)
+p = DeviceProgram(w.tape, w.roots, numerics=n.FAST)
+d = p.describe
+print(p.info["launches"], d.count("gemm mfma"), d.count(": rows ["))
+''')
+    launches, gemms, rows = map(int, out.split())
+    assert launches > 60 and gemms >= 2 * 3 * 8 and rows >= 5, out
+
+
 def test_consecutive_chains_join():
     # a = x*x + y has two consumers, so it is materialised; the chains that
     # follow over the same shape join its launch (one kernel, several
