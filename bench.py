@@ -17,7 +17,8 @@ Measured beside it, each in its own section of the JSON line:
   (M,N,K), TFLOP/s per product and per sweep, fast and exact;
 * ``chains``: SiLU + bias, LayerNorm, row sum/max/softmax on
   [16384, 4096], GB/s of algorithmic traffic (five back-to-back launches per
-  event pair);
+  event pair, queued behind reads of an unrelated 1 GiB buffer so no host
+  gaps open between them and the operands start outside the last-level cache);
 * ``llama``: the Llama-style decoder's forward + backward (8
   layers, d_model 2048, 16 heads of 128, SwiGLU 5632, seq 2048, batch 2,
   vocab 32000), ms per step and product TFLOP/s.
@@ -28,6 +29,7 @@ a profiled step, HIP events around every launch on the library's stream);
 topos interpreter — on a bounded sample of the same step.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--quick]
+       python bench.py --only {mlp,gemm,chains,llama} [--steps K] [--warmup W]   (one section alone)
 """
 from __future__ import annotations
 
@@ -61,7 +63,7 @@ ADAMW = {"rate": 3e-4, "beta1": 0.9, "beta2": 0.999, "epsilon": 1e-8, "decay": 0
 # scaled by what it reads for a 256 MiB copy (x2.0 and x1.0): the summary
 # profiles/gpt2_train_step_traffic.md holds the commands and the figures. A
 # counter run cannot happen inside this process, so the figure is carried.
-MEASURED_PRODUCT_TRAFFIC_BYTES = 527.1 * 2**20
+MEASURED_PRODUCT_TRAFFIC_BYTES = 527.0 * 2**20
 
 
 def log(message: str) -> None:
@@ -75,6 +77,8 @@ def parse() -> argparse.Namespace:
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU oracle leg")
     p.add_argument("--quick", action="store_true", help="the GPT-2 step only (no side sections)")
+    p.add_argument("--only", choices=["mlp", "gemm", "chains", "llama"],
+                   help="run one side section alone and print its JSON (a diagnostic, not the bench line)")
     p.add_argument("--profile-out", help="write the profiled step's launches (one line each) to this file")
     p.add_argument("--calibration-copy-mib", type=int, default=0,
                    help="copy this many MiB device-to-device once before the step (a known-size kernel for "
@@ -285,10 +289,13 @@ def llama_section(torch, n, steps: int, warmup: int) -> dict:
             "plan_s": round(plan_s, 1), "loss": loss}
 
 
-def event_times(torch, launches, steps: int, warmup: int, repeat: int = 1) -> dict:
+def event_times(torch, launches, steps: int, warmup: int, repeat: int = 1, lead=None) -> dict:
     """Seconds per launch of each labelled launch: per step, `repeat`
     back-to-back launches of it between two events (the labels interleave,
-    so each is timed after the others have run)."""
+    so each is timed after the others have run). `lead`, when given, is
+    enqueued before each group's first event: device work long enough that
+    the group's launches are all queued before the device reaches them, so
+    host launch time does not open gaps between them."""
     for _ in range(warmup):
         for _, fn in launches:
             fn()
@@ -298,6 +305,8 @@ def event_times(torch, launches, steps: int, warmup: int, repeat: int = 1) -> di
     for _ in range(steps):
         for label, fn in launches:
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            if lead is not None:
+                lead()
             e0.record(stream)
             for _ in range(repeat):
                 fn()
@@ -387,7 +396,11 @@ def chains_section(torch, n, steps: int, warmup: int) -> dict:
                          ("row_softmax", rows(n.ROWS_SOFTMAX, y, numerics))):
             launches.append((f"{name}/{posture}", fn))
             bytes_of[f"{name}/{posture}"] = CHAIN_BYTES[name]
-    per = event_times(torch, launches, steps, warmup, repeat=CHAIN_REPEAT)
+    # Each group of launches queues behind two reads of a 1 GiB buffer (about
+    # 0.3 ms of device work that writes nothing back and leaves the 256 MB
+    # last-level cache holding that buffer, not the chain's operands).
+    busy = torch.ones(1 << 28, device="cuda")
+    per = event_times(torch, launches, steps, warmup, repeat=CHAIN_REPEAT, lead=lambda: (busy.sum(), busy.sum()))
     return {label: {"us": round(t * 1e6, 1), "GB/s": round(bytes_of[label] / t / 1e9, 1),
                     "frac": round(bytes_of[label] / t / 1e9 / HBM_PEAK_GBS, 4)} for label, t in per.items()}
 
@@ -411,6 +424,10 @@ def main() -> int:
         torch.empty_like(source).copy_(source)
         torch.cuda.synchronize()
         del source
+    if args.only:
+        sections = {"mlp": mlp_section, "gemm": gemm_section, "chains": chains_section, "llama": llama_section}
+        print(json.dumps({args.only: sections[args.only](torch, n, args.steps, args.warmup)}), flush=True)
+        return 0
     g = gpt2_section(torch, n, args)
     ms_per_step = g["wall"] / args.steps * 1e3
     line = {
