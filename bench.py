@@ -244,14 +244,18 @@ def mlp_section(torch, n, steps: int, warmup: int) -> dict:
     program.run()
     gradients = [program.pointer(g) for g in w.gradients]
 
-    def step():
-        program.run()
+    def step(run):
+        run()
         for p, g in zip(params, gradients):
             sgd_step(p, g, 0.01)
 
     reps = max(20, steps * 10)
-    wall = time_steps(torch, step, reps, warmup)
+    eager = time_steps(torch, lambda: step(program.run), reps, warmup)
+    # The program as one captured HIP graph per step (the launches are a few
+    # microseconds each, so host launch time dominates an eager step).
+    wall = time_steps(torch, lambda: step(program.replay), reps, warmup)
     return {"steps/s": round(reps / wall, 2), "us_per_step": round(wall / reps * 1e6, 1),
+            "eager_us_per_step": round(eager / reps * 1e6, 1), "program": "graph replay",
             "launches_per_step": program.info["launches"] + len(params), "posture": "exact (bit-identical)",
             "gflop_per_step": round(3 * matmul_flops(w.tape, [w.loss]) / 1e9, 4)}
 

@@ -322,6 +322,12 @@ int topos_hip_program_bind_selection(topos_hip_program *program, int32_t slot, c
                                      int64_t rows, float one);
 /* Enqueues one forward run on `stream` (the arena is reserved on first use). */
 int topos_hip_program_run(topos_hip_program *program, void *stream);
+/* Enqueues one forward run on `stream` as a single HIP graph launch: the
+ * first call (and the first after any bind) captures a run on a stream the
+ * program owns and instantiates it; later calls replay that graph. Same
+ * results as topos_hip_program_run, with one host call instead of one per
+ * kernel. (No counterpart in the reference, which has no device runs.) */
+int topos_hip_program_replay(topos_hip_program *program, void *stream);
 /* One run with a HIP event pair around every launch, waited for;
  * `milliseconds[l]` receives launch l's duration (an array of `launches`
  * floats, topos_hip_program_info). For measurement, not for the hot loop. */

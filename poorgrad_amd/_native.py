@@ -100,6 +100,7 @@ PROTOTYPES = {
     "topos_hip_program_bind": (c_int, [c_void_p, c_int, c_int32, c_void_p]),
     "topos_hip_program_bind_selection": (c_int, [c_void_p, c_int32, INT32_P, c_int64, c_float]),
     "topos_hip_program_run": (c_int, [c_void_p, c_void_p]),
+    "topos_hip_program_replay": (c_int, [c_void_p, c_void_p]),
     "topos_hip_program_run_profiled": (c_int, [c_void_p, c_void_p, FLOAT_P]),
     "topos_hip_program_launch": (c_int, [c_void_p, c_int64, POINTER(c_char_p), POINTER(ctypes.c_double),
                                          POINTER(ctypes.c_double)]),

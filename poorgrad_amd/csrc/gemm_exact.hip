@@ -124,6 +124,81 @@ __global__ __launch_bounds__(kThreads) void gemm_exact_kernel(
   }
 }
 
+// Products with too few 128x128 tiles to occupy the chip (the MLP's
+// [64, 784] x [784, 128], a 512-cube): one output per lane, 16x16 outputs per
+// workgroup, k staged through LDS 64 at a time (the next slab's loads in
+// flight during the current one's chain). Each lane runs its element's
+// chain, seed then ascending k, exactly as gemm_exact_kernel does.
+constexpr int kSmall = 16;
+constexpr int kSmallK = 64;
+
+template <bool kLeftUnitInner, bool kRightUnitInner>
+__global__ __launch_bounds__(kThreads) void gemm_exact_small_kernel(
+    const float *__restrict__ a, int64_t a_rs, int64_t a_cs, const float *__restrict__ b,
+    int64_t b_rs, int64_t b_cs, int64_t m, int64_t k, int64_t n, float *__restrict__ c, int64_t ldc,
+    int64_t a_bs, int64_t b_bs, int64_t c_bs) {
+  __shared__ float left[kSmallK][kSmall + 1];
+  __shared__ float right[kSmallK][kSmall + 1];
+  a += (int64_t)blockIdx.z * a_bs;
+  b += (int64_t)blockIdx.z * b_bs;
+  c += (int64_t)blockIdx.z * c_bs;
+  const int64_t m0 = (int64_t)blockIdx.y * kSmall;
+  const int64_t n0 = (int64_t)blockIdx.x * kSmall;
+  const int t = threadIdx.x;
+  const int ti = t / kSmall, tj = t % kSmall;
+  constexpr int kPer = kSmall * kSmallK / kThreads;  // staged values per lane per operand
+  float va[kPer], vb[kPer];
+  // Lane t's staged elements of slab k0: (row or column, k) pairs, with
+  // consecutive lanes on the operand's contiguous axis.
+  auto coords = [&](int e, bool unit_inner, int &outer, int &kk) {
+    const int flat = e * kThreads + t;
+    if (unit_inner) {
+      kk = flat % kSmallK;
+      outer = flat / kSmallK;
+    } else {
+      outer = flat % kSmall;
+      kk = flat / kSmall;
+    }
+  };
+  auto fetch = [&](int64_t k0) {
+#pragma unroll
+    for (int e = 0; e < kPer; ++e) {
+      int o, kk;
+      coords(e, kLeftUnitInner, o, kk);
+      const int64_t gm = m0 + o, gk = k0 + kk;
+      va[e] = (gm < m && gk < k) ? a[gm * a_rs + gk * a_cs] : 0.0f;
+      coords(e, kRightUnitInner, o, kk);
+      const int64_t gn = n0 + o, gkb = k0 + kk;
+      vb[e] = (gkb < k && gn < n) ? b[gkb * b_rs + gn * b_cs] : 0.0f;
+    }
+  };
+  float acc = 0.0f;
+  fetch(0);
+  for (int64_t k0 = 0; k0 < k; k0 += kSmallK) {
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < kPer; ++e) {
+      int o, kk;
+      coords(e, kLeftUnitInner, o, kk);
+      left[kk][o] = va[e];
+      coords(e, kRightUnitInner, o, kk);
+      right[kk][o] = vb[e];
+    }
+    __syncthreads();
+    if (k0 + kSmallK < k) fetch(k0 + kSmallK);
+    const int steps = (k - k0) < kSmallK ? (int)(k - k0) : kSmallK;
+    int s = 0;
+    if (k0 == 0) {
+      acc = __fmul_rn(left[0][ti], right[0][tj]);  // the seed: the first term itself (gemm.rs:151-160)
+      s = 1;
+    }
+#pragma unroll 8
+    for (; s < steps; ++s) acc = __fadd_rn(acc, __fmul_rn(left[s][ti], right[s][tj]));
+  }
+  const int64_t row = m0 + ti, col = n0 + tj;
+  if (row < m && col < n) c[row * ldc + col] = acc;
+}
+
 }  // namespace
 
 void launch_gemm_exact(const float *a, int64_t a_rs, int64_t a_cs, const float *b, int64_t b_rs,
@@ -137,6 +212,23 @@ void launch_gemm_exact(const float *a, int64_t a_rs, int64_t a_cs, const float *
   const int64_t a_bs = batch.a_stride, b_bs = batch.b_stride, c_bs = batch.c_stride;
   const bool left_unit = a_cs == 1;
   const bool right_unit = b_rs == 1 && b_cs != 1;
+  // Fewer 128x128 tiles than CUs: one output per lane instead.
+  const int64_t small_m = (m + kSmall - 1) / kSmall, small_n = (n + kSmall - 1) / kSmall;
+  if (grid_m * grid_n * batch.count < 256 && small_m <= 65535 && small_n <= 0x7fffffff) {
+    const dim3 small_grid((unsigned)small_n, (unsigned)small_m, (unsigned)batch.count);
+#define TOPOS_SMALL_ARGS a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, a_bs, b_bs, c_bs
+    if (left_unit && right_unit)
+      gemm_exact_small_kernel<true, true><<<small_grid, kThreads, 0, stream>>>(TOPOS_SMALL_ARGS);
+    else if (left_unit)
+      gemm_exact_small_kernel<true, false><<<small_grid, kThreads, 0, stream>>>(TOPOS_SMALL_ARGS);
+    else if (right_unit)
+      gemm_exact_small_kernel<false, true><<<small_grid, kThreads, 0, stream>>>(TOPOS_SMALL_ARGS);
+    else
+      gemm_exact_small_kernel<false, false><<<small_grid, kThreads, 0, stream>>>(TOPOS_SMALL_ARGS);
+#undef TOPOS_SMALL_ARGS
+    check_launch("gemm_exact_small_kernel launch");
+    return;
+  }
   if (left_unit && right_unit)
     gemm_exact_kernel<true, true><<<grid, kThreads, 0, stream>>>(a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, a_bs, b_bs, c_bs);
   else if (left_unit)

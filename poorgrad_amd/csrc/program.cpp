@@ -375,8 +375,18 @@ struct topos_hip_program {
   hipEvent_t side_start = nullptr, side_done = nullptr;
   int64_t side_launches = 0;
 
+  // A run captured as a HIP graph (replay): captured on a stream of the
+  // program's own (the caller's may be the legacy default stream, which
+  // cannot capture), launched on the caller's. Kernel arguments are captured
+  // by value, so any bind drops it.
+  hipStream_t capture_stream = nullptr;
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t graph_exec = nullptr;
+
   ~topos_hip_program() {
     if (!device) return;
+    drop_graph();
+    if (capture_stream) hipStreamDestroy(capture_stream);
     for (auto &kv : signal_events) hipEventDestroy(kv.second);
     if (side_done) hipEventDestroy(side_done);
     if (side_start) hipEventDestroy(side_start);
@@ -2339,7 +2349,16 @@ struct topos_hip_program {
     return b;
   }
 
-  void run(hipStream_t stream, float *milliseconds = nullptr) {
+  void drop_graph() {
+    if (graph_exec) hipGraphExecDestroy(graph_exec);
+    if (graph) hipGraphDestroy(graph);
+    graph_exec = nullptr;
+    graph = nullptr;
+  }
+
+  // The arena and the side stream's objects: created before the first run
+  // (and before any capture, which must not allocate).
+  void prepare() {
     if (!device) throw InvalidArgument{"the fake runtime plans programs but does not run them"};
     if (!arena) {
       void *p = nullptr;
@@ -2347,6 +2366,43 @@ struct topos_hip_program {
       allocations.push_back(p);
       arena = (char *)p;
     }
+    if (side_launches > 0 && !side_stream) {
+      check(hipStreamCreateWithFlags(&side_stream, hipStreamNonBlocking), "hipStreamCreate(side)");
+      check(hipEventCreateWithFlags(&side_done, hipEventDisableTiming), "hipEventCreate(side)");
+      check(hipEventCreateWithFlags(&side_start, hipEventDisableTiming), "hipEventCreate(side)");
+      for (size_t l = 0; l < launches.size(); ++l)
+        if (launches[l].signals) {
+          hipEvent_t e;
+          check(hipEventCreateWithFlags(&e, hipEventDisableTiming), "hipEventCreate(signal)");
+          signal_events[(int)l] = e;
+        }
+    }
+  }
+
+  // One run as the launch of a captured graph: the first replay (or the
+  // first after a bind) captures run() on the program's capture stream.
+  void replay(hipStream_t stream) {
+    prepare();
+    if (!graph_exec) {
+      if (!capture_stream)
+        check(hipStreamCreateWithFlags(&capture_stream, hipStreamNonBlocking), "hipStreamCreate(capture)");
+      check(hipStreamBeginCapture(capture_stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+      try {
+        run(capture_stream);
+      } catch (...) {
+        hipGraph_t partial = nullptr;
+        hipStreamEndCapture(capture_stream, &partial);
+        if (partial) hipGraphDestroy(partial);
+        throw;
+      }
+      check(hipStreamEndCapture(capture_stream, &graph), "hipStreamEndCapture");
+      check(hipGraphInstantiate(&graph_exec, graph, nullptr, nullptr, 0), "hipGraphInstantiate");
+    }
+    check(hipGraphLaunch(graph_exec, stream), "hipGraphLaunch");
+  }
+
+  void run(hipStream_t stream, float *milliseconds = nullptr) {
+    prepare();
     // Every binding must be present before anything is enqueued.
     for (const Storage &s : storages) {
       if (s.first == INT_MAX && s.last < 0) continue;
@@ -2362,17 +2418,6 @@ struct topos_hip_program {
       if (side_launches == 0) {
         for (const Launch &l : launches) l.run(ex);
         return;
-      }
-      if (!side_stream) {
-        check(hipStreamCreateWithFlags(&side_stream, hipStreamNonBlocking), "hipStreamCreate(side)");
-        check(hipEventCreateWithFlags(&side_done, hipEventDisableTiming), "hipEventCreate(side)");
-        check(hipEventCreateWithFlags(&side_start, hipEventDisableTiming), "hipEventCreate(side)");
-        for (size_t l = 0; l < launches.size(); ++l)
-          if (launches[l].signals) {
-            hipEvent_t e;
-            check(hipEventCreateWithFlags(&e, hipEventDisableTiming), "hipEventCreate(signal)");
-            signal_events[(int)l] = e;
-          }
       }
       // The side stream first waits for everything enqueued on the main
       // stream before this run (the caller's writes to parameters and inputs).
@@ -2456,7 +2501,10 @@ int topos_hip_program_info(const topos_hip_program *program, uint64_t *arena_byt
 
 int topos_hip_program_bind(topos_hip_program *program, int is_input, int32_t slot, const float *device) {
   if (!program || !device || slot < 0) return TOPOS_HIP_INVALID_ARGUMENT;
-  (is_input ? program->inputs : program->parameters)[slot] = device;
+  auto &bound = (is_input ? program->inputs : program->parameters);
+  auto old = bound.find(slot);
+  if (old == bound.end() || old->second != device) program->drop_graph();
+  bound[slot] = device;
   return TOPOS_HIP_OK;
 }
 
@@ -2473,6 +2521,7 @@ int topos_hip_program_bind_selection(topos_hip_program *program, int32_t slot, c
     if (indices[r] < 0 || indices[r] >= declared->vocab) return TOPOS_HIP_INVALID_ARGUMENT;
   if (!program->device) return TOPOS_HIP_OK;
   const int64_t vocab = declared->vocab;
+  program->drop_graph();
   return guarded([&] {
     auto old = program->selection_inputs.find(slot);
     if (old != program->selection_inputs.end()) {
@@ -2491,6 +2540,13 @@ int topos_hip_program_run(topos_hip_program *program, void *stream) {
   const int status = Context::get().status();
   if (status != TOPOS_HIP_OK) return status;
   return guarded([&] { program->run(static_cast<hipStream_t>(stream)); });
+}
+
+int topos_hip_program_replay(topos_hip_program *program, void *stream) {
+  if (!program) return TOPOS_HIP_INVALID_ARGUMENT;
+  const int status = Context::get().status();
+  if (status != TOPOS_HIP_OK) return status;
+  return guarded([&] { program->replay(static_cast<hipStream_t>(stream)); });
 }
 
 int topos_hip_program_run_profiled(topos_hip_program *program, void *stream, float *milliseconds) {

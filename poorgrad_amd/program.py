@@ -64,6 +64,14 @@ class DeviceProgram:
 
         n.checked(n.lib.topos_hip_program_run(self.handle, torch.cuda.current_stream().cuda_stream), "program run")
 
+    def replay(self) -> None:
+        """One run as a single HIP graph launch (captured on first use and
+        after any bind)."""
+        import torch
+
+        n.checked(n.lib.topos_hip_program_replay(self.handle, torch.cuda.current_stream().cuda_stream),
+                  "program replay")
+
     def profile(self) -> list:
         """One run with HIP events around every launch: per launch
         (kind, milliseconds, flops, bytes, description)."""
