@@ -353,7 +353,7 @@ __device__ __forceinline__ void dma_barrier() {
 
 // One slab's fragment reads and matrix-core products for a wave's WM x 64
 // block (the k order described above).
-template <int BM, int BN, int WM, bool kLeftInnerK, bool kRightInnerK>
+template <int BM, int BN, int WM, bool kLeftInnerK, bool kRightInnerK, bool kT>
 __device__ __forceinline__ void dma_mfma_slab(const float *sa, const float *sb, int wm, int wn, int half, int l32,
                                               floatx16 (&acc)[WM / 32][2]) {
   constexpr int WI = WM / 32;
@@ -392,42 +392,83 @@ __device__ __forceinline__ void dma_mfma_slab(const float *sa, const float *sb, 
         for (int t = 0; t < 4; ++t) bv[j][t] = sb[dma_outer_index<BN>(8 * g + 4 * half + t, col)];
       }
     }
+    // kT: the products go in as B^T A^T, so each 32x32 block accumulates
+    // transposed: a lane holds one output row and runs of four consecutive
+    // columns (16-byte stores in the epilogue). Otherwise a lane holds one
+    // column, and a store instruction writes two whole 128-byte row
+    // segments (the layout for outputs whose rows are not 16-byte aligned).
 #pragma unroll
     for (int t = 0; t < 4; ++t)
 #pragma unroll
       for (int i = 0; i < WI; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][t], bv[j][t], acc[i][j], 0, 0, 0);
+          acc[i][j] = kT ? __builtin_amdgcn_mfma_f32_32x32x2f32(bv[j][t], av[i][t], acc[i][j], 0, 0, 0)
+                         : __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][t], bv[j][t], acc[i][j], 0, 0, 0);
   }
 }
 
 // A wave's block of the output tile at (m0, n0) into c, with the bias
 // epilogue (bias_mode 0 none, 1 product + bias[col], 2 bias[col] + product).
-template <int WM>
+// kT: block (i, j) holds, for lane l, row 32i + l % 32 and columns
+// 32j + 8g + 4(l / 32) + {0..3} in elements 4g..4g+3, stored 16 bytes at a
+// time (the caller guarantees c and ldc allow it). Otherwise column
+// 32j + l % 32 and rows 32i + 8(r / 4) + 4(l / 32) + r % 4 in element r.
+template <int WM, bool kT>
 __device__ __forceinline__ void dma_store_block(const floatx16 (&acc)[WM / 32][2], float *__restrict__ c, int64_t ldc,
                                                 int64_t m, int64_t n, int64_t m0, int64_t n0, int wm, int wn, int lane,
                                                 const float *__restrict__ bias, int64_t bias_cs, int bias_mode) {
   constexpr int WI = WM / 32;
+  if (!kT) {
 #pragma unroll
-  for (int i = 0; i < WI; ++i)
+    for (int i = 0; i < WI; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int64_t col = n0 + wn + 32 * j + (lane % 32);
-      if (col >= n) continue;
-      const float add = bias_mode != 0 ? bias[col * bias_cs] : 0.0f;
+      for (int j = 0; j < 2; ++j) {
+        const int64_t col = n0 + wn + 32 * j + (lane % 32);
+        if (col >= n) continue;
+        const float add = bias_mode != 0 ? bias[col * bias_cs] : 0.0f;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int64_t row = m0 + wm + 32 * i + 8 * (r / 4) + 4 * (lane / 32) + (r % 4);
-        float v = acc[i][j][r];
-        if (bias_mode == 1) v = v + add;
-        if (bias_mode == 2) v = add + v;
-        if (row < m) c[row * ldc + col] = v;
+        for (int r = 0; r < 16; ++r) {
+          const int64_t row = m0 + wm + 32 * i + 8 * (r / 4) + 4 * (lane / 32) + (r % 4);
+          float v = acc[i][j][r];
+          if (bias_mode == 1) v = v + add;
+          if (bias_mode == 2) v = add + v;
+          if (row < m) c[row * ldc + col] = v;
+        }
       }
-    }
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < WI; ++i) {
+    const int64_t row = m0 + wm + 32 * i + (lane % 32);
+    if (row >= m) continue;
+    float *out = c + row * ldc;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int64_t col = n0 + wn + 32 * j + 8 * g + 4 * (lane / 32);
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          v[e] = acc[i][j][4 * g + e];
+          if (bias_mode != 0 && col + e < n) {
+            const float add = bias[(col + e) * bias_cs];
+            v[e] = bias_mode == 1 ? v[e] + add : add + v[e];
+          }
+        }
+        if (col + 3 < n) {
+          *reinterpret_cast<float4 *>(out + col) = make_float4(v[0], v[1], v[2], v[3]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (col + e < n) out[col + e] = v[e];
+        }
+      }
+  }
 }
 
-template <int BM, int BN, int WM, bool kLeftInnerK, bool kRightInnerK>
+template <int BM, int BN, int WM, bool kLeftInnerK, bool kRightInnerK, bool kT>
 __global__ __launch_bounds__(BM / WM * BN) void gemm_dma_kernel(
     const float *__restrict__ a, int64_t a_rs, int64_t a_cs, const float *__restrict__ b, int64_t b_rs,
     int64_t b_cs, int64_t m, int64_t k, int64_t n, float *__restrict__ c, int64_t ldc, int grid_m, int grid_n,
@@ -505,7 +546,7 @@ __global__ __launch_bounds__(BM / WM * BN) void gemm_dma_kernel(
     if (s + 2 < slabs) issue(s + 2);
     const float *sa = lds + (s % 3) * (SA + SB);
     const float *sb = sa + SA;
-    dma_mfma_slab<BM, BN, WM, kLeftInnerK, kRightInnerK>(sa, sb, wm, wn, half, l32, acc);
+    dma_mfma_slab<BM, BN, WM, kLeftInnerK, kRightInnerK, kT>(sa, sb, wm, wn, half, l32, acc);
     if (s + 1 < slabs) {
       if (s + 2 < slabs)
         dma_wait<kIssue>();
@@ -515,7 +556,7 @@ __global__ __launch_bounds__(BM / WM * BN) void gemm_dma_kernel(
     }
   }
 
-  dma_store_block<WM>(acc, c, ldc, m, n, m0, n0, wm, wn, lane, bias, bias_cs, bias_mode);
+  dma_store_block<WM, kT>(acc, c, ldc, m, n, m0, n0, wm, wn, lane, bias, bias_cs, bias_mode);
 }
 
 // The tile shape for an m x n product (over `batches`): 128x64 or 64x128
@@ -577,7 +618,8 @@ void dispatch_orientation(bool lk, bool rk, bool vector, dim3 grid, hipStream_t 
 }
 
 template <int BM, int BN>
-void dispatch_dma(bool lk, bool rk, dim3 grid, hipStream_t stream, const float *a, int64_t a_rs, int64_t a_cs,
+void dispatch_dma(bool lk, bool rk, bool vector_out, dim3 grid, hipStream_t stream, const float *a, int64_t a_rs,
+                  int64_t a_cs,
                   const float *b, int64_t b_rs, int64_t b_cs, int64_t m, int64_t k, int64_t n, float *c, int64_t ldc,
                   int gm, int gn, const Batch &batch, int64_t c_bs, int64_t c_bs2, int64_t split_len,
                   int64_t split_stride, const Epilogue &e, int mode) {
@@ -586,14 +628,21 @@ void dispatch_dma(bool lk, bool rk, dim3 grid, hipStream_t stream, const float *
 #define TOPOS_DMA_ARGS                                                                                           \
   a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, gm, gn, batch.a_stride, batch.b_stride, c_bs, split_len, \
       split_stride, e.bias, e.bias_stride, mode, batch.inner, batch.a_inner, batch.b_inner, c_bs2
-  if (lk && rk)
-    gemm_dma_kernel<BM, BN, WM, true, true><<<grid, T, 0, stream>>>(TOPOS_DMA_ARGS);
-  else if (lk)
-    gemm_dma_kernel<BM, BN, WM, true, false><<<grid, T, 0, stream>>>(TOPOS_DMA_ARGS);
-  else if (rk)
-    gemm_dma_kernel<BM, BN, WM, false, true><<<grid, T, 0, stream>>>(TOPOS_DMA_ARGS);
-  else
-    gemm_dma_kernel<BM, BN, WM, false, false><<<grid, T, 0, stream>>>(TOPOS_DMA_ARGS);
+#define TOPOS_DMA_ORIENT(kT)                                                  \
+  if (lk && rk)                                                               \
+    gemm_dma_kernel<BM, BN, WM, true, true, kT><<<grid, T, 0, stream>>>(TOPOS_DMA_ARGS);   \
+  else if (lk)                                                                \
+    gemm_dma_kernel<BM, BN, WM, true, false, kT><<<grid, T, 0, stream>>>(TOPOS_DMA_ARGS);  \
+  else if (rk)                                                                \
+    gemm_dma_kernel<BM, BN, WM, false, true, kT><<<grid, T, 0, stream>>>(TOPOS_DMA_ARGS);  \
+  else                                                                        \
+    gemm_dma_kernel<BM, BN, WM, false, false, kT><<<grid, T, 0, stream>>>(TOPOS_DMA_ARGS);
+  if (vector_out) {
+    TOPOS_DMA_ORIENT(true)
+  } else {
+    TOPOS_DMA_ORIENT(false)
+  }
+#undef TOPOS_DMA_ORIENT
 #undef TOPOS_DMA_ARGS
 }
 
@@ -723,12 +772,17 @@ bool launch_gemm_mfma(const float *a, int64_t a_rs, int64_t a_cs, const float *b
   // edge quads). The 128x64 tile (the attention products with a 64-wide right
   // operand) measured faster on the register-staged kernel.
   const bool dma = vector && (lk || m >= 4) && (rk || n >= 4);
+  // 16-byte output stores: every batch's and split's base and every row
+  // start 16-byte aligned.
+  const bool vector_out = target_ld % 4 == 0 && reinterpret_cast<uintptr_t>(target) % 16 == 0 &&
+                          (batch.count == 1 || (target_bs % 4 == 0 && target_bs2 % 4 == 0)) &&
+                          (splits == 1 || split_stride % 4 == 0);
   if (dma && shape.bm == 256)
-    dispatch_dma<256, 128>(lk, rk, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, target, target_ld, (int)gm, (int)gn, batch, target_bs, target_bs2, split_len, split_stride, epilogue, gemm_mode);
+    dispatch_dma<256, 128>(lk, rk, vector_out, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, target, target_ld, (int)gm, (int)gn, batch, target_bs, target_bs2, split_len, split_stride, epilogue, gemm_mode);
   else if (dma && shape.bm == 64)
-    dispatch_dma<64, 128>(lk, rk, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, target, target_ld, (int)gm, (int)gn, batch, target_bs, target_bs2, split_len, split_stride, epilogue, gemm_mode);
+    dispatch_dma<64, 128>(lk, rk, vector_out, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, target, target_ld, (int)gm, (int)gn, batch, target_bs, target_bs2, split_len, split_stride, epilogue, gemm_mode);
   else if (dma && shape.bn == 128)
-    dispatch_dma<128, 128>(lk, rk, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, target, target_ld, (int)gm, (int)gn, batch, target_bs, target_bs2, split_len, split_stride, epilogue, gemm_mode);
+    dispatch_dma<128, 128>(lk, rk, vector_out, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, target, target_ld, (int)gm, (int)gn, batch, target_bs, target_bs2, split_len, split_stride, epilogue, gemm_mode);
   else if (shape.bm == 256)
     dispatch_orientation<256, 128>(lk, rk, vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, target, target_ld, (int)gm, (int)gn, batch, target_bs, target_bs2, split_len, split_stride, epilogue, gemm_mode);
   else if (shape.bn == 64)
