@@ -117,7 +117,67 @@ struct Slab {
 // The 256x128 tile (eight waves) with 16-byte loads is held to 128
 // registers per lane so that two of its workgroups share a CU (four waves
 // per SIMD); at the compiler's own choice (129) a CU held one.
-template <int BM, int BN, int WM, bool kLeftInnerK, bool kRightInnerK, bool kVector>
+// A wave's block of the output tile at (m0, n0) into c, with the bias
+// epilogue (bias_mode 0 none, 1 product + bias[col], 2 bias[col] + product).
+// kT: block (i, j) holds, for lane l, row 32i + l % 32 and columns
+// 32j + 8g + 4(l / 32) + {0..3} in elements 4g..4g+3, stored 16 bytes at a
+// time (the caller guarantees c and ldc allow it). Otherwise column
+// 32j + l % 32 and rows 32i + 8(r / 4) + 4(l / 32) + r % 4 in element r.
+template <int WM, bool kT>
+__device__ __forceinline__ void store_block(const floatx16 (&acc)[WM / 32][2], float *__restrict__ c, int64_t ldc,
+                                                int64_t m, int64_t n, int64_t m0, int64_t n0, int wm, int wn, int lane,
+                                                const float *__restrict__ bias, int64_t bias_cs, int bias_mode) {
+  constexpr int WI = WM / 32;
+  if (!kT) {
+#pragma unroll
+    for (int i = 0; i < WI; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int64_t col = n0 + wn + 32 * j + (lane % 32);
+        if (col >= n) continue;
+        const float add = bias_mode != 0 ? bias[col * bias_cs] : 0.0f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int64_t row = m0 + wm + 32 * i + 8 * (r / 4) + 4 * (lane / 32) + (r % 4);
+          float v = acc[i][j][r];
+          if (bias_mode == 1) v = v + add;
+          if (bias_mode == 2) v = add + v;
+          if (row < m) c[row * ldc + col] = v;
+        }
+      }
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < WI; ++i) {
+    const int64_t row = m0 + wm + 32 * i + (lane % 32);
+    if (row >= m) continue;
+    float *out = c + row * ldc;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int64_t col = n0 + wn + 32 * j + 8 * g + 4 * (lane / 32);
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          v[e] = acc[i][j][4 * g + e];
+          if (bias_mode != 0 && col + e < n) {
+            const float add = bias[(col + e) * bias_cs];
+            v[e] = bias_mode == 1 ? v[e] + add : add + v[e];
+          }
+        }
+        if (col + 3 < n) {
+          *reinterpret_cast<float4 *>(out + col) = make_float4(v[0], v[1], v[2], v[3]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (col + e < n) out[col + e] = v[e];
+        }
+      }
+  }
+}
+
+template <int BM, int BN, int WM, bool kLeftInnerK, bool kRightInnerK, bool kVector, bool kT>
 __global__ __launch_bounds__(BM / WM * BN, BM == 256 && kVector ? 4 : 1) void gemm_mfma_kernel(
     const float *__restrict__ a, int64_t a_rs, int64_t a_cs, const float *__restrict__ b,
     int64_t b_rs, int64_t b_cs, int64_t m, int64_t k, int64_t n, float *__restrict__ c, int64_t ldc,
@@ -205,9 +265,11 @@ __global__ __launch_bounds__(BM / WM * BN, BM == 256 && kVector ? 4 : 1) void ge
       const float b0 = right[cur][kr][wn + (lane % 32)];
       const float b1 = right[cur][kr][wn + 32 + (lane % 32)];
 #pragma unroll
-      for (int i = 0; i < WI; ++i) {
-        acc[i][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i], b0, acc[i][0], 0, 0, 0);
-        acc[i][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i], b1, acc[i][1], 0, 0, 0);
+      for (int i = 0; i < WI; ++i) {  // kT: transposed blocks (store_block)
+        acc[i][0] = kT ? __builtin_amdgcn_mfma_f32_32x32x2f32(b0, av[i], acc[i][0], 0, 0, 0)
+                       : __builtin_amdgcn_mfma_f32_32x32x2f32(av[i], b0, acc[i][0], 0, 0, 0);
+        acc[i][1] = kT ? __builtin_amdgcn_mfma_f32_32x32x2f32(b1, av[i], acc[i][1], 0, 0, 0)
+                       : __builtin_amdgcn_mfma_f32_32x32x2f32(av[i], b1, acc[i][1], 0, 0, 0);
       }
     }
     if (more) {
@@ -217,25 +279,7 @@ __global__ __launch_bounds__(BM / WM * BN, BM == 256 && kVector ? 4 : 1) void ge
     __syncthreads();
   }
 
-  // 32x32 accumulator layout: register r of lane l holds
-  // row 8 * (r / 4) + 4 * (l / 32) + r % 4, column l % 32.
-#pragma unroll
-  for (int i = 0; i < WI; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int64_t col = n0 + wn + 32 * j + (lane % 32);
-      if (col >= n) continue;
-      // bias_mode: 0 the product, 1 product + bias[col], 2 bias[col] + product.
-      const float add = bias_mode != 0 ? bias[col * bias_cs] : 0.0f;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int64_t row = m0 + wm + 32 * i + 8 * (r / 4) + 4 * (lane / 32) + (r % 4);
-        float v = acc[i][j][r];
-        if (bias_mode == 1) v = v + add;
-        if (bias_mode == 2) v = add + v;
-        if (row < m) c[row * ldc + col] = v;
-      }
-    }
+  store_block<WM, kT>(acc, c, ldc, m, n, m0, n0, wm, wn, lane, bias, bias_cs, bias_mode);
 }
 
 // ---- the LDS-DMA variant ----
@@ -408,66 +452,6 @@ __device__ __forceinline__ void dma_mfma_slab(const float *sa, const float *sb, 
   }
 }
 
-// A wave's block of the output tile at (m0, n0) into c, with the bias
-// epilogue (bias_mode 0 none, 1 product + bias[col], 2 bias[col] + product).
-// kT: block (i, j) holds, for lane l, row 32i + l % 32 and columns
-// 32j + 8g + 4(l / 32) + {0..3} in elements 4g..4g+3, stored 16 bytes at a
-// time (the caller guarantees c and ldc allow it). Otherwise column
-// 32j + l % 32 and rows 32i + 8(r / 4) + 4(l / 32) + r % 4 in element r.
-template <int WM, bool kT>
-__device__ __forceinline__ void dma_store_block(const floatx16 (&acc)[WM / 32][2], float *__restrict__ c, int64_t ldc,
-                                                int64_t m, int64_t n, int64_t m0, int64_t n0, int wm, int wn, int lane,
-                                                const float *__restrict__ bias, int64_t bias_cs, int bias_mode) {
-  constexpr int WI = WM / 32;
-  if (!kT) {
-#pragma unroll
-    for (int i = 0; i < WI; ++i)
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int64_t col = n0 + wn + 32 * j + (lane % 32);
-        if (col >= n) continue;
-        const float add = bias_mode != 0 ? bias[col * bias_cs] : 0.0f;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int64_t row = m0 + wm + 32 * i + 8 * (r / 4) + 4 * (lane / 32) + (r % 4);
-          float v = acc[i][j][r];
-          if (bias_mode == 1) v = v + add;
-          if (bias_mode == 2) v = add + v;
-          if (row < m) c[row * ldc + col] = v;
-        }
-      }
-    return;
-  }
-#pragma unroll
-  for (int i = 0; i < WI; ++i) {
-    const int64_t row = m0 + wm + 32 * i + (lane % 32);
-    if (row >= m) continue;
-    float *out = c + row * ldc;
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int64_t col = n0 + wn + 32 * j + 8 * g + 4 * (lane / 32);
-        float v[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          v[e] = acc[i][j][4 * g + e];
-          if (bias_mode != 0 && col + e < n) {
-            const float add = bias[(col + e) * bias_cs];
-            v[e] = bias_mode == 1 ? v[e] + add : add + v[e];
-          }
-        }
-        if (col + 3 < n) {
-          *reinterpret_cast<float4 *>(out + col) = make_float4(v[0], v[1], v[2], v[3]);
-        } else {
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (col + e < n) out[col + e] = v[e];
-        }
-      }
-  }
-}
-
 template <int BM, int BN, int WM, bool kLeftInnerK, bool kRightInnerK, bool kT>
 __global__ __launch_bounds__(BM / WM * BN) void gemm_dma_kernel(
     const float *__restrict__ a, int64_t a_rs, int64_t a_cs, const float *__restrict__ b, int64_t b_rs,
@@ -556,7 +540,7 @@ __global__ __launch_bounds__(BM / WM * BN) void gemm_dma_kernel(
     }
   }
 
-  dma_store_block<WM, kT>(acc, c, ldc, m, n, m0, n0, wm, wn, lane, bias, bias_cs, bias_mode);
+  store_block<WM, kT>(acc, c, ldc, m, n, m0, n0, wm, wn, lane, bias, bias_cs, bias_mode);
 }
 
 // The tile shape for an m x n product (over `batches`): 128x64 or 64x128
@@ -583,38 +567,38 @@ TileShape tile_shape(int64_t m, int64_t n, int64_t batches) {
 constexpr int wave_rows(int bm, int bn) { return bm == 64 || bn == 64 ? 32 : 64; }
 
 template <int BM, int BN, bool kL, bool kR>
-void dispatch_vector(bool vector, dim3 grid, hipStream_t stream, const float *a, int64_t a_rs,
+void dispatch_vector(bool vector, bool vector_out, dim3 grid, hipStream_t stream, const float *a, int64_t a_rs,
                      int64_t a_cs, const float *b, int64_t b_rs, int64_t b_cs, int64_t m, int64_t k,
                      int64_t n, float *c, int64_t ldc, int gm, int gn, const Batch &batch, int64_t c_bs,
                      int64_t c_bs2, int64_t split_len, int64_t split_stride, const Epilogue &e, int mode) {
   constexpr int WM = wave_rows(BM, BN);
   constexpr int T = BM / WM * BN;
-  if (vector)
-    gemm_mfma_kernel<BM, BN, WM, kL, kR, true><<<grid, T, 0, stream>>>(a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, gm,
-                                                                   gn, batch.a_stride, batch.b_stride, c_bs,
-                                                                   split_len, split_stride, e.bias, e.bias_stride, mode,
-                                                                   batch.inner, batch.a_inner, batch.b_inner, c_bs2);
+#define TOPOS_MFMA_ARGS                                                                                        \
+  a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, gm, gn, batch.a_stride, batch.b_stride, c_bs, split_len,    \
+      split_stride, e.bias, e.bias_stride, mode, batch.inner, batch.a_inner, batch.b_inner, c_bs2
+  if (vector && vector_out)
+    gemm_mfma_kernel<BM, BN, WM, kL, kR, true, true><<<grid, T, 0, stream>>>(TOPOS_MFMA_ARGS);
+  else if (vector)
+    gemm_mfma_kernel<BM, BN, WM, kL, kR, true, false><<<grid, T, 0, stream>>>(TOPOS_MFMA_ARGS);
   else
-    gemm_mfma_kernel<BM, BN, WM, kL, kR, false><<<grid, T, 0, stream>>>(a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, gm,
-                                                                    gn, batch.a_stride, batch.b_stride, c_bs,
-                                                                    split_len, split_stride, e.bias, e.bias_stride, mode,
-                                                                   batch.inner, batch.a_inner, batch.b_inner, c_bs2);
+    gemm_mfma_kernel<BM, BN, WM, kL, kR, false, false><<<grid, T, 0, stream>>>(TOPOS_MFMA_ARGS);
+#undef TOPOS_MFMA_ARGS
 }
 
 template <int BM, int BN>
-void dispatch_orientation(bool lk, bool rk, bool vector, dim3 grid, hipStream_t stream, const float *a,
+void dispatch_orientation(bool lk, bool rk, bool vector, bool vector_out, dim3 grid, hipStream_t stream, const float *a,
                           int64_t a_rs, int64_t a_cs, const float *b, int64_t b_rs, int64_t b_cs, int64_t m,
                           int64_t k, int64_t n, float *c, int64_t ldc, int gm, int gn, const Batch &batch,
                           int64_t c_bs, int64_t c_bs2, int64_t split_len, int64_t split_stride, const Epilogue &e,
                           int mode) {
   if (lk && rk)
-    dispatch_vector<BM, BN, true, true>(vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, gm, gn, batch, c_bs, c_bs2, split_len, split_stride, e, mode);
+    dispatch_vector<BM, BN, true, true>(vector, vector_out, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, gm, gn, batch, c_bs, c_bs2, split_len, split_stride, e, mode);
   else if (lk)
-    dispatch_vector<BM, BN, true, false>(vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, gm, gn, batch, c_bs, c_bs2, split_len, split_stride, e, mode);
+    dispatch_vector<BM, BN, true, false>(vector, vector_out, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, gm, gn, batch, c_bs, c_bs2, split_len, split_stride, e, mode);
   else if (rk)
-    dispatch_vector<BM, BN, false, true>(vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, gm, gn, batch, c_bs, c_bs2, split_len, split_stride, e, mode);
+    dispatch_vector<BM, BN, false, true>(vector, vector_out, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, gm, gn, batch, c_bs, c_bs2, split_len, split_stride, e, mode);
   else
-    dispatch_vector<BM, BN, false, false>(vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, gm, gn, batch, c_bs, c_bs2, split_len, split_stride, e, mode);
+    dispatch_vector<BM, BN, false, false>(vector, vector_out, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, gm, gn, batch, c_bs, c_bs2, split_len, split_stride, e, mode);
 }
 
 template <int BM, int BN>
@@ -784,13 +768,13 @@ bool launch_gemm_mfma(const float *a, int64_t a_rs, int64_t a_cs, const float *b
   else if (dma && shape.bn == 128)
     dispatch_dma<128, 128>(lk, rk, vector_out, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, target, target_ld, (int)gm, (int)gn, batch, target_bs, target_bs2, split_len, split_stride, epilogue, gemm_mode);
   else if (shape.bm == 256)
-    dispatch_orientation<256, 128>(lk, rk, vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, target, target_ld, (int)gm, (int)gn, batch, target_bs, target_bs2, split_len, split_stride, epilogue, gemm_mode);
+    dispatch_orientation<256, 128>(lk, rk, vector, vector_out, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, target, target_ld, (int)gm, (int)gn, batch, target_bs, target_bs2, split_len, split_stride, epilogue, gemm_mode);
   else if (shape.bn == 64)
-    dispatch_orientation<128, 64>(lk, rk, vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, target, target_ld, (int)gm, (int)gn, batch, target_bs, target_bs2, split_len, split_stride, epilogue, gemm_mode);
+    dispatch_orientation<128, 64>(lk, rk, vector, vector_out, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, target, target_ld, (int)gm, (int)gn, batch, target_bs, target_bs2, split_len, split_stride, epilogue, gemm_mode);
   else if (shape.bm == 64)
-    dispatch_orientation<64, 128>(lk, rk, vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, target, target_ld, (int)gm, (int)gn, batch, target_bs, target_bs2, split_len, split_stride, epilogue, gemm_mode);
+    dispatch_orientation<64, 128>(lk, rk, vector, vector_out, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, target, target_ld, (int)gm, (int)gn, batch, target_bs, target_bs2, split_len, split_stride, epilogue, gemm_mode);
   else
-    dispatch_orientation<128, 128>(lk, rk, vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, target, target_ld, (int)gm, (int)gn, batch, target_bs, target_bs2, split_len, split_stride, epilogue, gemm_mode);
+    dispatch_orientation<128, 128>(lk, rk, vector, vector_out, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, target, target_ld, (int)gm, (int)gn, batch, target_bs, target_bs2, split_len, split_stride, epilogue, gemm_mode);
   check_launch("gemm_mfma_kernel launch");
   if (splits > 1) {
     const int64_t quads = split_stride / 4;
