@@ -1199,12 +1199,25 @@ Generated generate_row_resident(const RowProgram &p, const RowLayout &l, const R
     for (int j = 0; j < V; ++j) lanes.push_back("r" + std::to_string(i) + "_" + std::to_string(j));
     return lanes;
   };
+  // Point i of lane t. Four rows of quads in multiples of 64: a wave's
+  // point covers all four rows over 16 consecutive quads (lanes 16j..16j+15
+  // on row j), so a wave's operands share one column range: a per-column
+  // condition (a causal mask) then splits few waves. Otherwise points run
+  // row-major over the block.
+  const bool banded = G == 4 && V == 4 && CV % 64 == 0;
   for (int i = 0; i < P; ++i) {
     const std::string I = std::to_string(i);
-    s << "  const int q" << I << " = t + " << 256 * i << ";\n";
-    s << "  const int r" << I << " = q" << I << " / " << CV << ";\n";
-    s << "  const long long col" << I << " = (long long)(q" << I << " % " << CV << ") * " << V << ";\n";
-    s << "  const bool ok" << I << " = q" << I << " < " << (int64_t)G * CV << " && row0 + r" << I << " < " << ll(R) << ";\n";
+    if (banded) {
+      s << "  const int r" << I << " = (t % 64) / 16;\n";
+      s << "  const long long col" << I << " = (long long)(" << 64 * i << " + (t / 64) * 16 + t % 16) * 4;\n";
+      s << "  const bool ok" << I << " = row0 + r" << I << " < " << ll(R) << ";\n";
+    } else {
+      s << "  const int q" << I << " = t + " << 256 * i << ";\n";
+      s << "  const int r" << I << " = q" << I << " / " << CV << ";\n";
+      s << "  const long long col" << I << " = (long long)(q" << I << " % " << CV << ") * " << V << ";\n";
+      s << "  const bool ok" << I << " = q" << I << " < " << (int64_t)G * CV << " && row0 + r" << I << " < " << ll(R)
+        << ";\n";
+    }
     const std::vector<std::string> lanes = lanes_of(i);
     for (size_t k = 0; k < p.inputs.size(); ++k) {
       if (!inputs_all[k]) continue;
