@@ -593,6 +593,47 @@ def test_joined_chains_exact(hip):
         assert_bitwise(got[r.id], want[r.id], f"node {r.id}")
 
 
+@pytest.mark.parametrize("columns", [1024, 768])
+def test_row_sums_with_zero_tails_exact(hip, columns):
+    """Row sums over resident four-row blocks whose rows end in zeros: +0,
+    -0 and mixed zero tails, all -0 rows (the sum is -0), a -0 run meeting a
+    +0 (+0), cancellations to +0, NaN and infinities before a zero tail, and
+    a causal softmax (exp of masked terms is +0): bit-identical to the
+    interpreter's ordered folds."""
+    banner(f"program row sums zero tails {columns}")
+    rng = np.random.default_rng(53)
+    rows = 48
+    x = rng.standard_normal((rows, columns)).astype(np.float32)
+    pz, nz = np.float32(0.0), np.float32(-0.0)
+    x[0, 5:] = pz
+    x[1, 5:] = nz
+    x[2, :] = nz
+    x[3, :] = nz; x[3, -1] = pz
+    x[4, :] = nz; x[4, 700 % columns] = pz
+    x[5, :] = pz
+    x[6, :2] = [1.0, -1.0]; x[6, 2:] = nz
+    x[7, :2] = [-1.0, 1.0]; x[7, 2:] = nz; x[7, 40] = pz
+    x[8, :] = nz; x[8, 33] = 2.5; x[8, 34:] = pz
+    x[9, 10] = np.nan; x[9, 11:] = pz
+    x[10, 3] = np.inf; x[10, 4:] = nz
+    x[11, 31] = 1e-30; x[11, 32:] = nz; x[11, 63] = pz
+    for r in range(12, rows):
+        tail = int(rng.integers(0, columns))
+        x[r, tail:] = np.where(rng.random(columns - tail) < 0.5, pz, nz)
+    causal = np.where(np.arange(columns)[None, :] <= (np.arange(rows) * (columns // rows))[:, None], 0.0,
+                      -np.inf).astype(np.float32)
+    tape = t.Tape()
+    xi = tape.input((rows, columns))
+    mask = tape.leaf(t.Dense(causal))
+    roots = [xi.sum_along(1), (xi + mask).softmax(1), (xi * xi + mask).logsumexp(1)]
+    dense = {xi.node.slot: x}
+    want = run_oracle(tape, roots, [], dense)
+    got, program = run_device(tape, roots, [], dense)
+    assert ": rows [" in program.describe
+    for r in roots:
+        assert_bitwise(got[r.id], want[r.id], f"node {r.id} {r.shape}")
+
+
 @pytest.mark.parametrize("form", ["plain", "left_transposed", "right_transposed"])
 def test_fast_batched_products_with_edges(hip, form):
     """Batched fast products whose tiles overhang m and n (the LDS-DMA
