@@ -21,7 +21,9 @@ Measured beside it, each in its own section of the JSON line:
   gaps open between them and the operands start outside the last-level cache);
 * ``llama``: the Llama-style decoder's forward + backward (8
   layers, d_model 2048, 16 heads of 128, SwiGLU 5632, seq 2048, batch 2,
-  vocab 32000), ms per step and product TFLOP/s.
+  vocab 32000), ms per step and product TFLOP/s;
+* ``gpt2_exact`` (configs[3], exact posture): the same program with
+  bit-identical kernels, ms per forward + backward.
 
 The roofline object describes the step's dominant kernel class (most time in
 a profiled step, HIP events around every launch on the library's stream);
@@ -29,7 +31,7 @@ a profiled step, HIP events around every launch on the library's stream);
 topos interpreter — on a bounded sample of the same step.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--quick]
-       python bench.py --only {mlp,gemm,chains,llama} [--steps K] [--warmup W]   (one section alone)
+       python bench.py --only {mlp,gemm,chains,llama,gpt2_exact} [--steps K] [--warmup W]   (one section alone)
 """
 from __future__ import annotations
 
@@ -77,7 +79,7 @@ def parse() -> argparse.Namespace:
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU oracle leg")
     p.add_argument("--quick", action="store_true", help="the GPT-2 step only (no side sections)")
-    p.add_argument("--only", choices=["mlp", "gemm", "chains", "llama"],
+    p.add_argument("--only", choices=["mlp", "gemm", "chains", "llama", "gpt2_exact"],
                    help="run one side section alone and print its JSON (a diagnostic, not the bench line)")
     p.add_argument("--profile-out", help="write the profiled step's launches (one line each) to this file")
     p.add_argument("--calibration-copy-mib", type=int, default=0,
@@ -260,6 +262,34 @@ def mlp_section(torch, n, steps: int, warmup: int) -> dict:
             "gflop_per_step": round(3 * matmul_flops(w.tape, [w.loss]) / 1e9, 4)}
 
 
+def gpt2_exact_section(torch, n, steps: int, warmup: int) -> dict:
+    """configs[3] in the exact posture: the same recorded-gradients program
+    planned with bit-identical kernels (fixed-k-order products, ordered
+    folds), forward + backward without the optimizer. Two runs must give the
+    same loss bits."""
+    from poorgrad_amd import workloads
+    from poorgrad_amd.program import DeviceProgram
+
+    w = workloads.gpt2()
+    program = DeviceProgram(w.tape, w.roots, numerics=n.EXACT)
+    params = [torch.from_numpy(a).cuda() for a in w.initial]
+    for slot, p in enumerate(params):
+        program.bind_parameter(slot, p)
+    for slot, (indices, one) in w.selection_inputs.items():
+        program.bind_selection(slot, indices, one)
+    program.run()
+    torch.cuda.synchronize()
+    first = program.read(w.loss)
+    reps = max(1, min(steps, 3))
+    wall = time_steps(torch, program.run, reps, min(warmup, 1))
+    again = program.read(w.loss)
+    flops = matmul_flops(w.tape, w.roots)
+    ms = wall / reps * 1e3
+    return {"ms_per_step": round(ms, 2), "products_TFLOP/s": round(flops / (ms / 1e3) / 1e12, 2),
+            "loss": float(first), "loss_bits_repeat": bool(first.tobytes() == again.tobytes()),
+            "launches_per_step": program.info["launches"], "posture": "exact (bit-identical)"}
+
+
 def llama_section(torch, n, steps: int, warmup: int) -> dict:
     """the Llama-style decoder's forward + backward (loss and every
     gradient; no optimizer) through the fast-posture program. Weights are drawn
@@ -429,7 +459,8 @@ def main() -> int:
         torch.cuda.synchronize()
         del source
     if args.only:
-        sections = {"mlp": mlp_section, "gemm": gemm_section, "chains": chains_section, "llama": llama_section}
+        sections = {"mlp": mlp_section, "gemm": gemm_section, "chains": chains_section, "llama": llama_section,
+                    "gpt2_exact": gpt2_exact_section}
         print(json.dumps({args.only: sections[args.only](torch, n, args.steps, args.warmup)}), flush=True)
         return 0
     g = gpt2_section(torch, n, args)
@@ -476,6 +507,8 @@ def main() -> int:
         line["chains"] = chains_section(torch, n, args.steps, args.warmup)
         log("llama forward + backward (configs[4])")
         line["llama"] = llama_section(torch, n, args.steps, args.warmup)
+        log("gpt2 step, exact posture (configs[3])")
+        line["gpt2_exact"] = gpt2_exact_section(torch, n, args.steps, args.warmup)
     if not args.no_cpu_baseline:
         log("cpu baseline: the oracle interpreter on one core")
         line["cpu_baseline"] = cpu_leg(full_flops)
