@@ -21,110 +21,116 @@ constexpr int kTileN = 128;
 constexpr int kTileK = 8;
 constexpr int kThreads = 256;
 
-// Loads a kTileK x kTileM slab of the left operand (rows m0.., inner k0..)
-// into lds[k][m]. `unit_inner` picks the lane mapping that reads contiguous
+// Loads a kTileK x E slab of the left operand (rows m0.., inner k0..) into
+// lds[k][m]. `unit_inner` picks the lane mapping that reads contiguous
 // memory: along k when the column stride is one, along m otherwise.
-template <bool kUnitInner>
-__device__ inline void stage_left(float (*lds)[kTileM + 4], const float *__restrict__ a, int64_t rs,
+template <int E, bool kUnitInner>
+__device__ inline void stage_left(float (*lds)[E + 4], const float *__restrict__ a, int64_t rs,
                                   int64_t cs, int64_t m, int64_t k, int64_t m0, int64_t k0) {
   const int t = threadIdx.x;
 #pragma unroll
-  for (int e = 0; e < (kTileM * kTileK) / kThreads; ++e) {
+  for (int e = 0; e < (E * kTileK) / kThreads; ++e) {
     const int flat = e * kThreads + t;
     int mm, kk;
     if (kUnitInner) {
       kk = flat % kTileK;
       mm = flat / kTileK;
     } else {
-      mm = flat % kTileM;
-      kk = flat / kTileM;
+      mm = flat % E;
+      kk = flat / E;
     }
     const int64_t gm = m0 + mm, gk = k0 + kk;
     lds[kk][mm] = (gm < m && gk < k) ? a[gm * rs + gk * cs] : 0.0f;
   }
 }
 
-// Loads a kTileK x kTileN slab of the right operand (inner k0.., columns n0..)
+// Loads a kTileK x E slab of the right operand (inner k0.., columns n0..)
 // into lds[k][n].
-template <bool kUnitInner>
-__device__ inline void stage_right(float (*lds)[kTileN + 4], const float *__restrict__ b, int64_t rs,
+template <int E, bool kUnitInner>
+__device__ inline void stage_right(float (*lds)[E + 4], const float *__restrict__ b, int64_t rs,
                                    int64_t cs, int64_t k, int64_t n, int64_t k0, int64_t n0) {
   const int t = threadIdx.x;
 #pragma unroll
-  for (int e = 0; e < (kTileN * kTileK) / kThreads; ++e) {
+  for (int e = 0; e < (E * kTileK) / kThreads; ++e) {
     const int flat = e * kThreads + t;
     int nn, kk;
     if (kUnitInner) {
       kk = flat % kTileK;
       nn = flat / kTileK;
     } else {
-      nn = flat % kTileN;
-      kk = flat / kTileN;
+      nn = flat % E;
+      kk = flat / E;
     }
     const int64_t gk = k0 + kk, gn = n0 + nn;
     lds[kk][nn] = (gk < k && gn < n) ? b[gk * rs + gn * cs] : 0.0f;
   }
 }
 
-template <bool kLeftUnitInner, bool kRightUnitInner>
+// E x E output tiles (E = 128: 8x8 accumulators a lane; E = 64: 4x4, for
+// products with too few 128-wide tiles to give every CU several workgroups).
+// Lane (tx, ty) owns rows ty*4 + {0..3} (and E/2 + ty*4 + {0..3} when E =
+// 128), and the same pattern of columns, so each lane's LDS reads are float4s.
+template <int E, bool kLeftUnitInner, bool kRightUnitInner>
 __global__ __launch_bounds__(kThreads) void gemm_exact_kernel(
     const float *__restrict__ a, int64_t a_rs, int64_t a_cs, const float *__restrict__ b,
     int64_t b_rs, int64_t b_cs, int64_t m, int64_t k, int64_t n, float *__restrict__ c, int64_t ldc,
     int64_t a_bs, int64_t b_bs, int64_t c_bs) {
-  __shared__ float left[kTileK][kTileM + 4];
+  constexpr int H = E / 64;  // float4 groups a lane owns per dimension
+  constexpr int A = 4 * H;   // accumulators a lane owns per dimension
+  __shared__ float left[kTileK][E + 4];
+  __shared__ float right[kTileK][E + 4];
   a += (int64_t)blockIdx.z * a_bs;
   b += (int64_t)blockIdx.z * b_bs;
   c += (int64_t)blockIdx.z * c_bs;
-  __shared__ float right[kTileK][kTileN + 4];
-  const int64_t m0 = (int64_t)blockIdx.y * kTileM;
-  const int64_t n0 = (int64_t)blockIdx.x * kTileN;
+  const int64_t m0 = (int64_t)blockIdx.y * E;
+  const int64_t n0 = (int64_t)blockIdx.x * E;
   const int tx = threadIdx.x % 16;
   const int ty = threadIdx.x / 16;
-  // Lane (tx, ty) owns rows ty*4 + {0..3} and 64 + ty*4 + {0..3}, and the
-  // same pattern of columns, so each lane's LDS reads are two float4s.
-  float acc[8][8];
+  float acc[A][A];
 
   for (int64_t k0 = 0; k0 < k; k0 += kTileK) {
     __syncthreads();
-    stage_left<kLeftUnitInner>(left, a, a_rs, a_cs, m, k, m0, k0);
-    stage_right<kRightUnitInner>(right, b, b_rs, b_cs, k, n, k0, n0);
+    stage_left<E, kLeftUnitInner>(left, a, a_rs, a_cs, m, k, m0, k0);
+    stage_right<E, kRightUnitInner>(right, b, b_rs, b_cs, k, n, k0, n0);
     __syncthreads();
     const int steps = (k - k0) < kTileK ? (int)(k - k0) : kTileK;
     for (int s = 0; s < steps; ++s) {
-      const float4 a_lo = *reinterpret_cast<const float4 *>(&left[s][ty * 4]);
-      const float4 a_hi = *reinterpret_cast<const float4 *>(&left[s][64 + ty * 4]);
-      const float4 b_lo = *reinterpret_cast<const float4 *>(&right[s][tx * 4]);
-      const float4 b_hi = *reinterpret_cast<const float4 *>(&right[s][64 + tx * 4]);
-      const float av[8] = {a_lo.x, a_lo.y, a_lo.z, a_lo.w, a_hi.x, a_hi.y, a_hi.z, a_hi.w};
-      const float bv[8] = {b_lo.x, b_lo.y, b_lo.z, b_lo.w, b_hi.x, b_hi.y, b_hi.z, b_hi.w};
+      float av[A], bv[A];
+#pragma unroll
+      for (int h = 0; h < H; ++h) {
+        const float4 a4 = *reinterpret_cast<const float4 *>(&left[s][64 * h + ty * 4]);
+        const float4 b4 = *reinterpret_cast<const float4 *>(&right[s][64 * h + tx * 4]);
+        av[4 * h] = a4.x; av[4 * h + 1] = a4.y; av[4 * h + 2] = a4.z; av[4 * h + 3] = a4.w;
+        bv[4 * h] = b4.x; bv[4 * h + 1] = b4.y; bv[4 * h + 2] = b4.z; bv[4 * h + 3] = b4.w;
+      }
       if (k0 == 0 && s == 0) {
         // The seed: the first term itself (gemm.rs:151-160).
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
+        for (int i = 0; i < A; ++i)
 #pragma unroll
-          for (int j = 0; j < 8; ++j) acc[i][j] = __fmul_rn(av[i], bv[j]);
+          for (int j = 0; j < A; ++j) acc[i][j] = __fmul_rn(av[i], bv[j]);
       } else {
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
+        for (int i = 0; i < A; ++i)
 #pragma unroll
-          for (int j = 0; j < 8; ++j) acc[i][j] = __fadd_rn(acc[i][j], __fmul_rn(av[i], bv[j]));
+          for (int j = 0; j < A; ++j) acc[i][j] = __fadd_rn(acc[i][j], __fmul_rn(av[i], bv[j]));
       }
     }
   }
 
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int64_t row = m0 + (i < 4 ? ty * 4 + i : 64 + ty * 4 + (i - 4));
+  for (int i = 0; i < A; ++i) {
+    const int64_t row = m0 + 64 * (i / 4) + ty * 4 + i % 4;
     if (row >= m) continue;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int64_t col = n0 + (j < 4 ? tx * 4 + j : 64 + tx * 4 + (j - 4));
+    for (int j = 0; j < A; ++j) {
+      const int64_t col = n0 + 64 * (j / 4) + tx * 4 + j % 4;
       if (col < n) c[row * ldc + col] = acc[i][j];
     }
   }
 }
 
-// Products with too few 128x128 tiles to occupy the chip (the MLP's
+// Products with too few 64x64 tiles to occupy the chip (the MLP's
 // [64, 784] x [784, 128], a 512-cube): one output per lane, 16x16 outputs per
 // workgroup, k staged through LDS 64 at a time (the next slab's loads in
 // flight during the current one's chain). Each lane runs its element's
@@ -212,9 +218,10 @@ void launch_gemm_exact(const float *a, int64_t a_rs, int64_t a_cs, const float *
   const int64_t a_bs = batch.a_stride, b_bs = batch.b_stride, c_bs = batch.c_stride;
   const bool left_unit = a_cs == 1;
   const bool right_unit = b_rs == 1 && b_cs != 1;
-  // Fewer 128x128 tiles than CUs: one output per lane instead.
+  // Fewer 64x64 tiles than CUs: one output per lane instead.
   const int64_t small_m = (m + kSmall - 1) / kSmall, small_n = (n + kSmall - 1) / kSmall;
-  if (grid_m * grid_n * batch.count < 256 && small_m <= 65535 && small_n <= 0x7fffffff) {
+  const int64_t tiles64 = ((m + 63) / 64) * ((n + 63) / 64) * batch.count;
+  if (tiles64 < 256 && small_m <= 65535 && small_n <= 0x7fffffff) {
     const dim3 small_grid((unsigned)small_n, (unsigned)small_m, (unsigned)batch.count);
 #define TOPOS_SMALL_ARGS a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, a_bs, b_bs, c_bs
     if (left_unit && right_unit)
@@ -229,14 +236,28 @@ void launch_gemm_exact(const float *a, int64_t a_rs, int64_t a_cs, const float *
     check_launch("gemm_exact_small_kernel launch");
     return;
   }
-  if (left_unit && right_unit)
-    gemm_exact_kernel<true, true><<<grid, kThreads, 0, stream>>>(a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, a_bs, b_bs, c_bs);
-  else if (left_unit)
-    gemm_exact_kernel<true, false><<<grid, kThreads, 0, stream>>>(a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, a_bs, b_bs, c_bs);
-  else if (right_unit)
-    gemm_exact_kernel<false, true><<<grid, kThreads, 0, stream>>>(a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, a_bs, b_bs, c_bs);
-  else
-    gemm_exact_kernel<false, false><<<grid, kThreads, 0, stream>>>(a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, a_bs, b_bs, c_bs);
+  // Fewer than four 128-wide tiles a CU: 64-wide tiles (four times as many).
+  const int64_t tiles = grid_m * grid_n * batch.count;
+  const int64_t grid_n64 = (n + 63) / 64, grid_m64 = (m + 63) / 64;
+  const bool narrow = tiles < 1024 && grid_m64 <= 65535 && grid_n64 <= 0x7fffffff;
+#define TOPOS_EXACT_ARGS a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, a_bs, b_bs, c_bs
+#define TOPOS_EXACT_LAUNCH(E, g)                                                        \
+  if (left_unit && right_unit)                                                          \
+    gemm_exact_kernel<E, true, true><<<g, kThreads, 0, stream>>>(TOPOS_EXACT_ARGS);     \
+  else if (left_unit)                                                                   \
+    gemm_exact_kernel<E, true, false><<<g, kThreads, 0, stream>>>(TOPOS_EXACT_ARGS);    \
+  else if (right_unit)                                                                  \
+    gemm_exact_kernel<E, false, true><<<g, kThreads, 0, stream>>>(TOPOS_EXACT_ARGS);    \
+  else                                                                                  \
+    gemm_exact_kernel<E, false, false><<<g, kThreads, 0, stream>>>(TOPOS_EXACT_ARGS);
+  if (narrow) {
+    const dim3 grid64((unsigned)grid_n64, (unsigned)grid_m64, (unsigned)batch.count);
+    TOPOS_EXACT_LAUNCH(64, grid64)
+  } else {
+    TOPOS_EXACT_LAUNCH(128, grid)
+  }
+#undef TOPOS_EXACT_LAUNCH
+#undef TOPOS_EXACT_ARGS
   check_launch("gemm_exact_kernel launch");
 }
 
