@@ -21,48 +21,44 @@ constexpr int kTileN = 128;
 constexpr int kTileK = 8;
 constexpr int kThreads = 256;
 
-// Loads a kTileK x E slab of the left operand (rows m0.., inner k0..) into
-// lds[k][m]. `unit_inner` picks the lane mapping that reads contiguous
-// memory: along k when the column stride is one, along m otherwise.
+// Loads a kTileK x E slab of an operand (outer index o0.., inner k0..) into
+// lds[k][o]. With k contiguous (kUnitInner: k_stride is 1) a lane loads four
+// consecutive k values at once (16-byte loads serve any 4-byte alignment);
+// otherwise consecutive lanes read consecutive outer elements.
 template <int E, bool kUnitInner>
-__device__ inline void stage_left(float (*lds)[E + 4], const float *__restrict__ a, int64_t rs,
-                                  int64_t cs, int64_t m, int64_t k, int64_t m0, int64_t k0) {
+__device__ inline void stage(float (*lds)[E + 4], const float *__restrict__ p, int64_t outer_stride,
+                             int64_t k_stride, int64_t outer_extent, int64_t k, int64_t o0, int64_t k0) {
   const int t = threadIdx.x;
+  if (kUnitInner) {
+    constexpr int kQuads = E * kTileK / 4;
 #pragma unroll
-  for (int e = 0; e < (E * kTileK) / kThreads; ++e) {
-    const int flat = e * kThreads + t;
-    int mm, kk;
-    if (kUnitInner) {
-      kk = flat % kTileK;
-      mm = flat / kTileK;
-    } else {
-      mm = flat % E;
-      kk = flat / E;
+    for (int e = 0; e < (kQuads + kThreads - 1) / kThreads; ++e) {
+      const int flat = e * kThreads + t;
+      if (flat >= kQuads) break;
+      const int kq = flat % (kTileK / 4), o = flat / (kTileK / 4);
+      const int64_t go = o0 + o, gk = k0 + 4 * kq;
+      float v[4];
+      if (go < outer_extent && gk + 3 < k) {
+        const float4 w = *reinterpret_cast<const float4 *>(p + go * outer_stride + gk);
+        v[0] = w.x;
+        v[1] = w.y;
+        v[2] = w.z;
+        v[3] = w.w;
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = (go < outer_extent && gk + j < k) ? p[go * outer_stride + gk + j] : 0.0f;
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) lds[4 * kq + j][o] = v[j];
     }
-    const int64_t gm = m0 + mm, gk = k0 + kk;
-    lds[kk][mm] = (gm < m && gk < k) ? a[gm * rs + gk * cs] : 0.0f;
+    return;
   }
-}
-
-// Loads a kTileK x E slab of the right operand (inner k0.., columns n0..)
-// into lds[k][n].
-template <int E, bool kUnitInner>
-__device__ inline void stage_right(float (*lds)[E + 4], const float *__restrict__ b, int64_t rs,
-                                   int64_t cs, int64_t k, int64_t n, int64_t k0, int64_t n0) {
-  const int t = threadIdx.x;
 #pragma unroll
   for (int e = 0; e < (E * kTileK) / kThreads; ++e) {
     const int flat = e * kThreads + t;
-    int nn, kk;
-    if (kUnitInner) {
-      kk = flat % kTileK;
-      nn = flat / kTileK;
-    } else {
-      nn = flat % E;
-      kk = flat / E;
-    }
-    const int64_t gk = k0 + kk, gn = n0 + nn;
-    lds[kk][nn] = (gk < k && gn < n) ? b[gk * rs + gn * cs] : 0.0f;
+    const int o = flat % E, kk = flat / E;
+    const int64_t go = o0 + o, gk = k0 + kk;
+    lds[kk][o] = (go < outer_extent && gk < k) ? p[go * outer_stride + gk * k_stride] : 0.0f;
   }
 }
 
@@ -90,8 +86,8 @@ __global__ __launch_bounds__(kThreads) void gemm_exact_kernel(
 
   for (int64_t k0 = 0; k0 < k; k0 += kTileK) {
     __syncthreads();
-    stage_left<E, kLeftUnitInner>(left, a, a_rs, a_cs, m, k, m0, k0);
-    stage_right<E, kRightUnitInner>(right, b, b_rs, b_cs, k, n, k0, n0);
+    stage<E, kLeftUnitInner>(left, a, a_rs, a_cs, m, k, m0, k0);
+    stage<E, kRightUnitInner>(right, b, b_cs, b_rs, n, k, n0, k0);
     __syncthreads();
     const int steps = (k - k0) < kTileK ? (int)(k - k0) : kTileK;
     for (int s = 0; s < steps; ++s) {
