@@ -62,6 +62,72 @@ __device__ inline void stage(float (*lds)[E + 4], const float *__restrict__ p, i
   }
 }
 
+// One kTileK x E slab of an operand (outer index o0.., inner k0..) in a
+// lane's registers (fetch), then into lds[k][o] (deposit): the next slab's
+// loads are in flight while the current slab is multiplied. With k
+// contiguous (kUnitInner: k_stride is 1) a lane loads four consecutive k
+// values at once (16-byte loads serve any 4-byte alignment); otherwise
+// consecutive lanes read consecutive outer elements.
+template <int E, bool kUnitInner>
+struct Stage {
+  static constexpr int kQuads = E * kTileK / 4;                      // quads a slab (k contiguous)
+  static constexpr int kQ = (kQuads + kThreads - 1) / kThreads;      // quads a lane
+  static constexpr int kS = E * kTileK / kThreads;                   // elements a lane (otherwise)
+  float v[kUnitInner ? 4 * kQ : kS];
+
+  __device__ void fetch(const float *__restrict__ p, int64_t outer_stride, int64_t k_stride, int64_t outer_extent,
+                        int64_t k, int64_t o0, int64_t k0) {
+    const int t = threadIdx.x;
+    if (kUnitInner) {
+#pragma unroll
+      for (int e = 0; e < kQ; ++e) {
+        const int flat = e * kThreads + t;
+        const int kq = flat % (kTileK / 4), o = flat / (kTileK / 4);
+        const int64_t go = o0 + o, gk = k0 + 4 * kq;
+        if (flat < kQuads && go < outer_extent && gk + 3 < k) {
+          const float4 w = *reinterpret_cast<const float4 *>(p + go * outer_stride + gk);
+          v[4 * e] = w.x;
+          v[4 * e + 1] = w.y;
+          v[4 * e + 2] = w.z;
+          v[4 * e + 3] = w.w;
+        } else {
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            v[4 * e + j] = (flat < kQuads && go < outer_extent && gk + j < k) ? p[go * outer_stride + gk + j] : 0.0f;
+        }
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < kS; ++e) {
+        const int flat = e * kThreads + t;
+        const int o = flat % E, kk = flat / E;
+        const int64_t go = o0 + o, gk = k0 + kk;
+        v[e] = (go < outer_extent && gk < k) ? p[go * outer_stride + gk * k_stride] : 0.0f;
+      }
+    }
+  }
+
+  __device__ void deposit(float (*lds)[E + 4]) const {
+    const int t = threadIdx.x;
+    if (kUnitInner) {
+#pragma unroll
+      for (int e = 0; e < kQ; ++e) {
+        const int flat = e * kThreads + t;
+        if (flat >= kQuads) break;
+        const int kq = flat % (kTileK / 4), o = flat / (kTileK / 4);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) lds[4 * kq + j][o] = v[4 * e + j];
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < kS; ++e) {
+        const int flat = e * kThreads + t;
+        lds[flat / E][flat % E] = v[e];
+      }
+    }
+  }
+};
+
 // E x E output tiles (E = 128: 8x8 accumulators a lane; E = 64: 4x4, for
 // products with too few 128-wide tiles to give every CU several workgroups).
 // Lane (tx, ty) owns rows ty*4 + {0..3} (and E/2 + ty*4 + {0..3} when E =
@@ -84,6 +150,52 @@ __global__ __launch_bounds__(kThreads) void gemm_exact_kernel(
   const int ty = threadIdx.x / 16;
   float acc[A][A];
 
+  if constexpr (E == 64) {
+    // 64-wide tiles have the registers to prefetch: the next slab's loads
+    // are in flight (Stage) while this slab is multiplied from the other
+    // LDS buffer.
+    __shared__ float left2[2][kTileK][E + 4];
+    __shared__ float right2[2][kTileK][E + 4];
+    Stage<E, kLeftUnitInner> sa;
+    Stage<E, kRightUnitInner> sb;
+    sa.fetch(a, a_rs, a_cs, m, k, m0, 0);
+    sb.fetch(b, b_cs, b_rs, n, k, n0, 0);
+    sa.deposit(left2[0]);
+    sb.deposit(right2[0]);
+    __syncthreads();
+    int cur = 0;
+    for (int64_t k0 = 0; k0 < k; k0 += kTileK) {
+      const bool more = k0 + kTileK < k;
+      if (more) {
+        sa.fetch(a, a_rs, a_cs, m, k, m0, k0 + kTileK);
+        sb.fetch(b, b_cs, b_rs, n, k, n0, k0 + kTileK);
+      }
+      const int steps = (k - k0) < kTileK ? (int)(k - k0) : kTileK;
+      for (int s = 0; s < steps; ++s) {
+        const float4 a4 = *reinterpret_cast<const float4 *>(&left2[cur][s][ty * 4]);
+        const float4 b4 = *reinterpret_cast<const float4 *>(&right2[cur][s][tx * 4]);
+        const float av[4] = {a4.x, a4.y, a4.z, a4.w};
+        const float bv[4] = {b4.x, b4.y, b4.z, b4.w};
+        if (k0 == 0 && s == 0) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[i][j] = __fmul_rn(av[i], bv[j]);  // the seed (gemm.rs:151-160)
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[i][j] = __fadd_rn(acc[i][j], __fmul_rn(av[i], bv[j]));
+        }
+      }
+      if (more) {
+        sa.deposit(left2[cur ^ 1]);
+        sb.deposit(right2[cur ^ 1]);
+      }
+      __syncthreads();
+      cur ^= 1;
+    }
+  } else
   for (int64_t k0 = 0; k0 < k; k0 += kTileK) {
     __syncthreads();
     stage<E, kLeftUnitInner>(left, a, a_rs, a_cs, m, k, m0, k0);
