@@ -6,61 +6,19 @@
 // the sign of an all negative-zero sum, src/payload/tests/gemm_tests.rs:130-139),
 // then acc = RN(acc + RN(a[i,s] * b[s,j])) for s = 1..k-1: a separately rounded
 // multiply and add, never a fused multiply-add, never a split of k. That is
-// VALU work (two instructions per term) and the kernel is shaped for it:
-// 128x128 output tiles per 256-lane workgroup, 8x8 accumulators per lane,
-// operands staged k-major through LDS so each lane reads its eight rows and
-// eight columns as two 128-bit LDS loads each.
+// VALU work (two instructions per term) and the kernels are shaped for it:
+// 64x64 output tiles per 256-lane workgroup, 4x4 accumulators per lane,
+// operands staged k-major through LDS so each lane reads its four rows and
+// four columns as two 128-bit LDS loads; small products run one output per
+// lane.
 #pragma clang fp contract(off)
 #include "backend.hpp"
 
 namespace topos_hip {
 namespace {
 
-constexpr int kTileM = 128;
-constexpr int kTileN = 128;
 constexpr int kTileK = 8;
 constexpr int kThreads = 256;
-
-// Loads a kTileK x E slab of an operand (outer index o0.., inner k0..) into
-// lds[k][o]. With k contiguous (kUnitInner: k_stride is 1) a lane loads four
-// consecutive k values at once (16-byte loads serve any 4-byte alignment);
-// otherwise consecutive lanes read consecutive outer elements.
-template <int E, bool kUnitInner>
-__device__ inline void stage(float (*lds)[E + 4], const float *__restrict__ p, int64_t outer_stride,
-                             int64_t k_stride, int64_t outer_extent, int64_t k, int64_t o0, int64_t k0) {
-  const int t = threadIdx.x;
-  if (kUnitInner) {
-    constexpr int kQuads = E * kTileK / 4;
-#pragma unroll
-    for (int e = 0; e < (kQuads + kThreads - 1) / kThreads; ++e) {
-      const int flat = e * kThreads + t;
-      if (flat >= kQuads) break;
-      const int kq = flat % (kTileK / 4), o = flat / (kTileK / 4);
-      const int64_t go = o0 + o, gk = k0 + 4 * kq;
-      float v[4];
-      if (go < outer_extent && gk + 3 < k) {
-        const float4 w = *reinterpret_cast<const float4 *>(p + go * outer_stride + gk);
-        v[0] = w.x;
-        v[1] = w.y;
-        v[2] = w.z;
-        v[3] = w.w;
-      } else {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) v[j] = (go < outer_extent && gk + j < k) ? p[go * outer_stride + gk + j] : 0.0f;
-      }
-#pragma unroll
-      for (int j = 0; j < 4; ++j) lds[4 * kq + j][o] = v[j];
-    }
-    return;
-  }
-#pragma unroll
-  for (int e = 0; e < (E * kTileK) / kThreads; ++e) {
-    const int flat = e * kThreads + t;
-    const int o = flat % E, kk = flat / E;
-    const int64_t go = o0 + o, gk = k0 + kk;
-    lds[kk][o] = (go < outer_extent && gk < k) ? p[go * outer_stride + gk * k_stride] : 0.0f;
-  }
-}
 
 // One kTileK x E slab of an operand (outer index o0.., inner k0..) in a
 // lane's registers (fetch), then into lds[k][o] (deposit): the next slab's
@@ -128,19 +86,18 @@ struct Stage {
   }
 };
 
-// E x E output tiles (E = 128: 8x8 accumulators a lane; E = 64: 4x4, for
-// products with too few 128-wide tiles to give every CU several workgroups).
-// Lane (tx, ty) owns rows ty*4 + {0..3} (and E/2 + ty*4 + {0..3} when E =
-// 128), and the same pattern of columns, so each lane's LDS reads are float4s.
+// 64x64 output tiles, 4x4 accumulators a lane: lane (tx, ty) owns rows
+// ty*4 + {0..3} and columns tx*4 + {0..3}, so its LDS reads are two float4s
+// per k step. The next slab's loads are in flight (Stage) while this slab is
+// multiplied from the other LDS buffer. (Measured on MI355X against 128x128
+// tiles of 8x8 accumulators: those need about 160 registers a lane, three
+// waves a SIMD and no room to prefetch; 4096-cubes went 30-34 -> 43 TFLOP/s.)
 template <int E, bool kLeftUnitInner, bool kRightUnitInner>
 __global__ __launch_bounds__(kThreads) void gemm_exact_kernel(
     const float *__restrict__ a, int64_t a_rs, int64_t a_cs, const float *__restrict__ b,
     int64_t b_rs, int64_t b_cs, int64_t m, int64_t k, int64_t n, float *__restrict__ c, int64_t ldc,
     int64_t a_bs, int64_t b_bs, int64_t c_bs) {
-  constexpr int H = E / 64;  // float4 groups a lane owns per dimension
-  constexpr int A = 4 * H;   // accumulators a lane owns per dimension
-  __shared__ float left[kTileK][E + 4];
-  __shared__ float right[kTileK][E + 4];
+  static_assert(E == 64, "64x64 tiles");
   a += (int64_t)blockIdx.z * a_bs;
   b += (int64_t)blockIdx.z * b_bs;
   c += (int64_t)blockIdx.z * c_bs;
@@ -148,12 +105,9 @@ __global__ __launch_bounds__(kThreads) void gemm_exact_kernel(
   const int64_t n0 = (int64_t)blockIdx.x * E;
   const int tx = threadIdx.x % 16;
   const int ty = threadIdx.x / 16;
-  float acc[A][A];
+  float acc[4][4];
 
-  if constexpr (E == 64) {
-    // 64-wide tiles have the registers to prefetch: the next slab's loads
-    // are in flight (Stage) while this slab is multiplied from the other
-    // LDS buffer.
+  {
     __shared__ float left2[2][kTileK][E + 4];
     __shared__ float right2[2][kTileK][E + 4];
     Stage<E, kLeftUnitInner> sa;
@@ -195,44 +149,15 @@ __global__ __launch_bounds__(kThreads) void gemm_exact_kernel(
       __syncthreads();
       cur ^= 1;
     }
-  } else
-  for (int64_t k0 = 0; k0 < k; k0 += kTileK) {
-    __syncthreads();
-    stage<E, kLeftUnitInner>(left, a, a_rs, a_cs, m, k, m0, k0);
-    stage<E, kRightUnitInner>(right, b, b_cs, b_rs, n, k, n0, k0);
-    __syncthreads();
-    const int steps = (k - k0) < kTileK ? (int)(k - k0) : kTileK;
-    for (int s = 0; s < steps; ++s) {
-      float av[A], bv[A];
-#pragma unroll
-      for (int h = 0; h < H; ++h) {
-        const float4 a4 = *reinterpret_cast<const float4 *>(&left[s][64 * h + ty * 4]);
-        const float4 b4 = *reinterpret_cast<const float4 *>(&right[s][64 * h + tx * 4]);
-        av[4 * h] = a4.x; av[4 * h + 1] = a4.y; av[4 * h + 2] = a4.z; av[4 * h + 3] = a4.w;
-        bv[4 * h] = b4.x; bv[4 * h + 1] = b4.y; bv[4 * h + 2] = b4.z; bv[4 * h + 3] = b4.w;
-      }
-      if (k0 == 0 && s == 0) {
-        // The seed: the first term itself (gemm.rs:151-160).
-#pragma unroll
-        for (int i = 0; i < A; ++i)
-#pragma unroll
-          for (int j = 0; j < A; ++j) acc[i][j] = __fmul_rn(av[i], bv[j]);
-      } else {
-#pragma unroll
-        for (int i = 0; i < A; ++i)
-#pragma unroll
-          for (int j = 0; j < A; ++j) acc[i][j] = __fadd_rn(acc[i][j], __fmul_rn(av[i], bv[j]));
-      }
-    }
   }
 
 #pragma unroll
-  for (int i = 0; i < A; ++i) {
-    const int64_t row = m0 + 64 * (i / 4) + ty * 4 + i % 4;
+  for (int i = 0; i < 4; ++i) {
+    const int64_t row = m0 + ty * 4 + i;
     if (row >= m) continue;
 #pragma unroll
-    for (int j = 0; j < A; ++j) {
-      const int64_t col = n0 + 64 * (j / 4) + tx * 4 + j % 4;
+    for (int j = 0; j < 4; ++j) {
+      const int64_t col = n0 + tx * 4 + j;
       if (col < n) c[row * ldc + col] = acc[i][j];
     }
   }
@@ -318,11 +243,7 @@ __global__ __launch_bounds__(kThreads) void gemm_exact_small_kernel(
 void launch_gemm_exact(const float *a, int64_t a_rs, int64_t a_cs, const float *b, int64_t b_rs,
                        int64_t b_cs, int64_t m, int64_t k, int64_t n, float *c, int64_t ldc,
                        hipStream_t stream, const Batch &batch) {
-  const int64_t grid_n = (n + kTileN - 1) / kTileN;
-  const int64_t grid_m = (m + kTileM - 1) / kTileM;
-  if (grid_m > 65535 || grid_n > 0x7fffffff || batch.count > 65535 || batch.count < 1)
-    throw Unsupported{"exact gemm: product too tall for one launch"};
-  const dim3 grid((unsigned)grid_n, (unsigned)grid_m, (unsigned)batch.count);
+  if (batch.count > 65535 || batch.count < 1) throw Unsupported{"exact gemm: too many batches for one launch"};
   const int64_t a_bs = batch.a_stride, b_bs = batch.b_stride, c_bs = batch.c_stride;
   const bool left_unit = a_cs == 1;
   const bool right_unit = b_rs == 1 && b_cs != 1;
@@ -344,10 +265,8 @@ void launch_gemm_exact(const float *a, int64_t a_rs, int64_t a_cs, const float *
     check_launch("gemm_exact_small_kernel launch");
     return;
   }
-  // Fewer than four 128-wide tiles a CU: 64-wide tiles (four times as many).
-  const int64_t tiles = grid_m * grid_n * batch.count;
   const int64_t grid_n64 = (n + 63) / 64, grid_m64 = (m + 63) / 64;
-  const bool narrow = tiles < 1024 && grid_m64 <= 65535 && grid_n64 <= 0x7fffffff;
+  if (grid_m64 > 65535 || grid_n64 > 0x7fffffff) throw Unsupported{"exact gemm: product too tall for one launch"};
 #define TOPOS_EXACT_ARGS a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, a_bs, b_bs, c_bs
 #define TOPOS_EXACT_LAUNCH(E, g)                                                        \
   if (left_unit && right_unit)                                                          \
@@ -358,12 +277,8 @@ void launch_gemm_exact(const float *a, int64_t a_rs, int64_t a_cs, const float *
     gemm_exact_kernel<E, false, true><<<g, kThreads, 0, stream>>>(TOPOS_EXACT_ARGS);    \
   else                                                                                  \
     gemm_exact_kernel<E, false, false><<<g, kThreads, 0, stream>>>(TOPOS_EXACT_ARGS);
-  if (narrow) {
-    const dim3 grid64((unsigned)grid_n64, (unsigned)grid_m64, (unsigned)batch.count);
-    TOPOS_EXACT_LAUNCH(64, grid64)
-  } else {
-    TOPOS_EXACT_LAUNCH(128, grid)
-  }
+  const dim3 grid64((unsigned)grid_n64, (unsigned)grid_m64, (unsigned)batch.count);
+  TOPOS_EXACT_LAUNCH(64, grid64)
 #undef TOPOS_EXACT_LAUNCH
 #undef TOPOS_EXACT_ARGS
   check_launch("gemm_exact_kernel launch");
