@@ -17,7 +17,7 @@
 namespace topos_hip {
 namespace {
 
-constexpr int kTileK = 8;
+constexpr int kTileK = 32;
 constexpr int kThreads = 256;
 
 // One kTileK x E slab of an operand (outer index o0.., inner k0..) in a
