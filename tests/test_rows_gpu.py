@@ -90,6 +90,33 @@ def test_exact_rows_special_values(hip):
         assert_bitwise(got, expected_rows(kind_code(kind), x), f"special {kind}")
 
 
+@pytest.mark.parametrize("columns", [8, 1024])
+def test_fast_rows_special_values(hip, columns):
+    """The fast posture on rows with NaN, infinities and signed zeros (the
+    register-resident kernel at 1024 columns, the streaming one at 8): the
+    maximum is bitwise the ordered max_f32 fold, and every other reduction
+    puts NaN and infinities where the interpreter does."""
+    banner(f"fast rows special values {columns}")
+    x = np.full((6, columns), 0.5, dtype=np.float32)
+    x[0, :] = -0.0
+    x[1, 0], x[1, -1] = np.nan, np.nan
+    x[2, 1], x[2, -2] = np.inf, -np.inf
+    x[3, :] = -np.inf
+    x[4, 3] = 1e38; x[4, 4] = 1e38
+    x[5, :] = np.nan
+    for kind in KINDS:
+        got = device.rows(kind_code(kind), to_device(x), hip.FAST).cpu().numpy()
+        want = expected_rows(kind_code(kind), x)
+        if kind == "max":
+            assert_bitwise(got, want, f"fast special {kind}")
+            continue
+        assert np.array_equal(np.isnan(got), np.isnan(want)), f"fast special {kind}: NaN positions"
+        finite = ~np.isnan(want)
+        assert np.array_equal(np.isinf(got[finite]), np.isinf(want[finite])), f"fast special {kind}: infinities"
+        inf = np.isinf(want) & finite
+        assert np.array_equal(np.sign(got[inf]), np.sign(want[inf])), f"fast special {kind}: infinity signs"
+
+
 @pytest.mark.parametrize("rows, columns", [(3, 5), (64, 768), (257, 1000), (96, 4096)])
 def test_layer_norm_exact_and_fast(hip, rows, columns):
     banner(f"layer norm {rows}x{columns}")
