@@ -245,6 +245,11 @@ int topos_hip_rows_f32_device(int reduction, const float *x, int64_t rows, int64
   if (status != TOPOS_HIP_OK) return status;
   if (reduction < TOPOS_HIP_ROWS_SUM || reduction > TOPOS_HIP_ROWS_LOG_SUM_EXP) return TOPOS_HIP_INVALID_ARGUMENT;
   return guarded([&] {
+    // The row maximum is exact in both postures: rows that fit one wave's
+    // registers take the one-read kernel.
+    if (reduction == TOPOS_HIP_ROWS_MAX &&
+        launch_rows_max_exact(x, rows, columns, out, static_cast<hipStream_t>(stream)))
+      return;
     if (numerics == TOPOS_HIP_EXACT)
       launch_rows_program(reduction, x, rows, columns, out, static_cast<hipStream_t>(stream));
     else

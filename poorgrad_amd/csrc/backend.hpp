@@ -190,6 +190,10 @@ void launch_layer_norm(const float *x, int64_t rows, int64_t columns, const floa
 
 // rows_device.cpp: the exact posture of the two above as generated row
 // programs (cached per shape).
+// The exact row maximum over rows of at most 4096 columns (a multiple of
+// four, 16-byte aligned) held in registers; false when the shape is not
+// served (the caller then runs the row program).
+bool launch_rows_max_exact(const float *x, int64_t rows, int64_t columns, float *out, hipStream_t stream);
 void launch_rows_program(int reduction, const float *x, int64_t rows, int64_t columns, float *out,
                          hipStream_t stream);
 void launch_layer_norm_program(const float *x, int64_t rows, int64_t columns, const float *scale,

@@ -339,6 +339,61 @@ __global__ __launch_bounds__(kThreads) void rows_fast_resident_kernel(const floa
     }
 }
 
+// The exact row maximum with the row in one wave's registers: the ordered
+// max_f32 fold (src/payload/tensor.rs:1104-1124) is the first occurrence of
+// the largest non-NaN term, or the last term when every term is NaN, which
+// any partition recovers: each lane keeps its first largest term and that
+// term's column, and the butterfly keeps the largest, earliest (so a -0
+// before a +0 of the same row wins, as in the fold).
+template <int kQ>
+__global__ __launch_bounds__(kThreads) void rows_max_exact_resident_kernel(const float *__restrict__ x, int64_t rows,
+                                                                           int64_t columns, float *__restrict__ out) {
+  const int lane = threadIdx.x % 64;
+  const int64_t row = (int64_t)blockIdx.x * (kThreads / 64) + threadIdx.x / 64;
+  if (row >= rows) return;
+  const int quads = (int)(columns / 4);
+  const float4 *src = reinterpret_cast<const float4 *>(x + row * columns);
+  float v[kQ][4];
+#pragma unroll
+  for (int i = 0; i < kQ; ++i) {
+    const int q = lane + 64 * i;
+    const float4 w = q < quads ? src[q] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    v[i][0] = w.x;
+    v[i][1] = w.y;
+    v[i][2] = w.z;
+    v[i][3] = w.w;
+  }
+  float mv = 0.0f;
+  int mi = -1;
+#pragma unroll
+  for (int i = 0; i < kQ; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float value = v[i][j];
+      if (lane + 64 * i < quads && value == value && (mi < 0 || value > mv)) {
+        mv = value;
+        mi = 4 * (lane + 64 * i) + j;
+      }
+    }
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const float ov = __shfl_xor(mv, off, 64);
+    const int oi = __shfl_xor(mi, off, 64);
+    if (oi >= 0 && (mi < 0 || ov > mv || (!(mv > ov) && oi < mi))) {
+      mv = ov;
+      mi = oi;
+    }
+  }
+  if (lane == 0) out[row] = mi < 0 ? x[row * columns + columns - 1] : mv;
+}
+
+template <int kQ>
+bool try_max_exact(const float *x, int64_t rows, int64_t columns, float *out, hipStream_t stream) {
+  if (columns > 256 * kQ) return false;
+  rows_max_exact_resident_kernel<kQ><<<(unsigned)((rows + 3) / 4), kThreads, 0, stream>>>(x, rows, columns, out);
+  return true;
+}
+
 template <int kReduction, int kQ>
 bool try_resident(const float *x, int64_t rows, int64_t columns, const float *scale, const float *shift,
                   float epsilon, float *out, hipStream_t stream) {
@@ -394,6 +449,16 @@ void launch_rows(int reduction, const float *x, int64_t rows, int64_t columns, i
     case TOPOS_HIP_ROWS_LOG_SUM_EXP: launch_one<TOPOS_HIP_ROWS_LOG_SUM_EXP>(x, rows, columns, numerics, nullptr, nullptr, 0.0f, out, stream); break;
     default: throw InvalidArgument{"unknown row reduction"};
   }
+}
+
+bool launch_rows_max_exact(const float *x, int64_t rows, int64_t columns, float *out, hipStream_t stream) {
+  if (rows <= 0 || columns <= 0 || columns % 4 != 0 || reinterpret_cast<uintptr_t>(x) % 16 != 0 ||
+      rows > 0x7fffffffLL * 4)
+    return false;
+  const bool served = try_max_exact<2>(x, rows, columns, out, stream) || try_max_exact<4>(x, rows, columns, out, stream) ||
+                      try_max_exact<8>(x, rows, columns, out, stream) || try_max_exact<16>(x, rows, columns, out, stream);
+  if (served) check_launch("row maximum launch");
+  return served;
 }
 
 void launch_layer_norm(const float *x, int64_t rows, int64_t columns, const float *scale,
