@@ -99,19 +99,16 @@ static const LogRow kLogTableHost[16] = {
 // 1.5 * 2^52 shift; 2^(k/32) = table[k mod 32] with k/32 added to the exponent
 // field; 2^(r/32) by a cubic. The product x * 32/ln2 is fused into both the
 // shift addition and the remainder subtraction, as the FMA build of glibc does.
+// glibc's special cases (NaN, e^+-inf, overflow above 0x1.62e42ep6, underflow
+// below -0x1.9fe368p6) are applied as selects after the common arithmetic, so
+// the common path has no branch; on those inputs the arithmetic is harmless
+// (the table index is still k mod 32) and its value is discarded.
 TOPOS_HD float exp_f32_table(float x, const uint64_t *table) {
   const double inv_ln2_scaled = 0x1.71547652b82fep+0 * 32;
   const double shift = 0x1.8p+52;
   const double c0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32;
   const double c1 = 0x1.ebfce50fac4f3p-3 / 32 / 32;
   const double c2 = 0x1.62e42ff0c52d6p-1 / 32;
-  const uint32_t top = (bits_of(x) >> 20) & 0x7ff;
-  if (top >= (0x42b00000u >> 20)) {  // |x| >= 88 or NaN
-    if (bits_of(x) == 0xff800000u) return 0.0f;  // e^-inf
-    if (top >= 0x7f8u) return x + x;             // +inf, NaN
-    if (x > 0x1.62e42ep6f) return float_of(0x7f800000u);
-    if (x < -0x1.9fe368p6f) return 0.0f;
-  }
   const double xd = (double)x;
   double kd = __builtin_fma(inv_ln2_scaled, xd, shift);
   const uint64_t ki = bits_of(kd);
@@ -125,7 +122,10 @@ TOPOS_HD float exp_f32_table(float x, const uint64_t *table) {
   double y = __builtin_fma(c2, r, 1.0);
   y = __builtin_fma(z, r2, y);
   y = y * s;
-  return (float)y;
+  float result = (float)y;
+  result = x < -0x1.9fe368p6f ? 0.0f : result;                  // underflow, e^-inf = +0
+  result = x > 0x1.62e42ep6f ? float_of(0x7f800000u) : result;  // overflow, e^inf = inf
+  return x != x ? x + x : result;                               // NaN
 }
 
 // e^x with the built-in table (a kernel may pass a copy it keeps in LDS).
