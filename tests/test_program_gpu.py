@@ -30,7 +30,7 @@ def test_mlp_train_step_exact_is_bit_identical(hip):
     want, got, program = check_workload(w, hip.EXACT, hip)
     for r in w.roots:
         assert_bitwise(got[r.id], want[r.id], f"mlp node {r.id}")
-    assert abs(float(want[w.loss.id]) - math.log(10)) < 0.5
+    assert abs(want[w.loss.id].item() - math.log(10)) < 0.5
 
 
 def test_mlp_train_step_fast_within_envelope(hip):
@@ -58,7 +58,7 @@ def test_small_gpt2_fast_within_envelope(hip):
     banner("program gpt2 small fast")
     w = workloads.gpt2(batch=2, context=32, vocab=61, width=64, heads=4, layers=2, positions=32)
     want, got, _ = check_workload(w, hip.FAST, hip)
-    loss_exact, loss_fast = float(want[w.loss.id]), float(got[w.loss.id])
+    loss_exact, loss_fast = want[w.loss.id].item(), got[w.loss.id].item()
     assert abs(loss_fast - loss_exact) <= 1e-4 * max(abs(loss_exact), 1.0)
     for r in w.gradients:
         g, e = got[r.id].astype(np.float64), want[r.id].astype(np.float64)
@@ -82,7 +82,7 @@ def test_small_llama_fast_within_envelope(hip):
     banner("program llama small fast")
     w = workloads.llama(batch=2, context=32, vocab=61, width=64, heads=4, hidden=96, layers=2)
     want, got, _ = check_workload(w, hip.FAST, hip)
-    loss_exact, loss_fast = float(want[w.loss.id]), float(got[w.loss.id])
+    loss_exact, loss_fast = want[w.loss.id].item(), got[w.loss.id].item()
     assert abs(loss_fast - loss_exact) <= 1e-4 * max(abs(loss_exact), 1.0)
     for r in w.gradients:
         g, e = got[r.id].astype(np.float64), want[r.id].astype(np.float64)

@@ -138,7 +138,7 @@ def test_mlp_workload_loss_and_gradient_shapes():
     w = workloads.mlp()
     assert [g.shape for g in w.gradients] == [(784, 128), (128,), (128, 10), (10,)]
     out = run_oracle(w.tape, w.roots, w.initial, w.dense_inputs, w.selection_inputs)
-    assert 1.5 < float(out[w.loss.id]) < 3.5
+    assert 1.5 < out[w.loss.id].item() < 3.5
     assert np.isfinite(out[w.gradients[0].id]).all()
 
 
@@ -148,7 +148,7 @@ def test_gpt2_workload_records_the_configured_graph():
     assert ops.count(t.GATHER) == 2 and ops.count(t.LOG_SOFTMAX) == 1 and ops.count(t.SCATTER) == 2
     assert len(w.gradients) == len(w.parameters) == 2 + 12 * 1 + 2
     out = run_oracle(w.tape, w.roots, w.initial, {}, w.selection_inputs)
-    assert abs(float(out[w.loss.id]) - math.log(11)) < 0.5
+    assert abs(out[w.loss.id].item() - math.log(11)) < 0.5
 
 
 def test_synthetic_uniform_is_the_reference_stream():
