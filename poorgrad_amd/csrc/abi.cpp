@@ -85,6 +85,17 @@ struct Borrowed {
 
 bool fits_i32(size_t value) { return value <= 0x7fffffffu; }
 
+// The elements a strided rows x columns view spans, 1 + (rows - 1) * row_stride
+// + (columns - 1) * column_stride; false when that overflows size_t.
+bool span(size_t rows, size_t columns, size_t row_stride, size_t column_stride, size_t *out) {
+  size_t along_rows = 0, along_columns = 0, sum = 0;
+  if (__builtin_mul_overflow(rows - 1, row_stride, &along_rows)) return false;
+  if (__builtin_mul_overflow(columns - 1, column_stride, &along_columns)) return false;
+  if (__builtin_add_overflow(along_rows, along_columns, &sum)) return false;
+  if (__builtin_add_overflow(sum, size_t(1), out)) return false;
+  return true;
+}
+
 // Enqueues the product with the posture's kernel: the matrix cores under
 // Fast when their loaders cover the strides, else the exact kernel (a
 // bit-identical result meets every posture, src/backend/coverage.rs:35-44).
@@ -97,8 +108,7 @@ void enqueue_gemm(const float *a, int64_t a_rs, int64_t a_cs, const float *b, in
     return;
   }
   if (numerics == TOPOS_HIP_FAST) {
-    const int splits = mfma_splits(m, n, k, 1);
-    const int64_t floats = splits > 1 ? (int64_t)splits * m * n : 0;
+    const int64_t floats = mfma_serves(a_rs, a_cs, b_rs, b_cs, m, k, n) ? mfma_split_floats(m, n, k, Batch()) : 0;
     float *workspace = floats ? context.workspace(floats) : nullptr;
     if (launch_gemm_mfma(a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, stream, Batch(), workspace, floats)) return;
   }
@@ -167,8 +177,9 @@ int topos_hip_gemm_f32(const float *a, size_t a_len, size_t a_row_stride, size_t
   if (!a || !b || !product || m == 0 || k == 0 || n == 0) return TOPOS_HIP_INVALID_ARGUMENT;
   if (numerics != TOPOS_HIP_EXACT && numerics != TOPOS_HIP_FAST) return TOPOS_HIP_INVALID_ARGUMENT;
   if (!fits_i32(m) || !fits_i32(n) || !fits_i32(k)) return TOPOS_HIP_DECLINED;
-  const size_t a_span = 1 + (m - 1) * a_row_stride + (k - 1) * a_col_stride;
-  const size_t b_span = 1 + (k - 1) * b_row_stride + (n - 1) * b_col_stride;
+  size_t a_span = 0, b_span = 0;
+  if (!span(m, k, a_row_stride, a_col_stride, &a_span) || !span(k, n, b_row_stride, b_col_stride, &b_span))
+    return TOPOS_HIP_INVALID_ARGUMENT;  // the reference's span arithmetic overflows (gemm.rs:57-89)
   if (a_len < a_span || b_len < b_span) return TOPOS_HIP_INVALID_ARGUMENT;
   // Declines that need no device (src/backend/cuda/kernels/mod.rs:69-89).
   if (m == 1 || n == 1) return TOPOS_HIP_DECLINED;

@@ -703,6 +703,16 @@ int mfma_splits(int64_t m, int64_t n, int64_t k, int64_t batches) {
   return (int)std::max<int64_t>(splits, 1);
 }
 
+int64_t mfma_split_floats(int64_t m, int64_t n, int64_t k, const Batch &batch) {
+  // The reduction walks one flat batch axis in quads of one row (n % 4 == 0)
+  // with 32-bit quad indices.
+  if (batch.inner != 1 || batch.count < 1 || n % 4 != 0) return 0;
+  const int splits = mfma_splits(m, n, k, batch.count);
+  const int64_t split_stride = batch.count * m * n;
+  if (splits <= 1 || splits > 16 || split_stride / 4 >= (int64_t(1) << 31)) return 0;
+  return splits * split_stride;
+}
+
 bool mfma_serves(int64_t a_rs, int64_t a_cs, int64_t b_rs, int64_t b_cs, int64_t m, int64_t k, int64_t n) {
   // Orientation: each operand needs a unit stride along k or along its outer
   // axis; an extent-1 axis leaves its stride unused (any value serves).
@@ -727,13 +737,12 @@ bool launch_gemm_mfma(const float *a, int64_t a_rs, int64_t a_cs, const float *b
   const int64_t gm = (m + shape.bm - 1) / shape.bm;
   const int64_t gn = (n + shape.bn - 1) / shape.bn;
   if (gm * gn > 0x7fffffff || batch.count > 65535 || batch.count < 1) throw Unsupported{"mfma gemm: grid too large"};
-  int splits = mfma_splits(m, n, k, batch.count);
   if (batch.inner < 1) throw Unsupported{"mfma gemm: batch inner extent below one"};
-  if (batch.inner > 1) splits = 1;  // the reduction walks one flat batch axis
   const int64_t split_stride = batch.count * m * n;
-  if (splits > 1 && (!workspace || workspace_floats < splits * split_stride || n % 4 != 0 ||
-                     reinterpret_cast<uintptr_t>(workspace) % 16 != 0 || splits > 16 ||
-                     split_stride / 4 >= (int64_t(1) << 31)))
+  const int64_t split_floats = mfma_split_floats(m, n, k, batch);
+  int splits = split_floats > 0 ? (int)(split_floats / split_stride) : 1;
+  if (splits > 1 && (!workspace || workspace_floats < split_floats ||
+                     reinterpret_cast<uintptr_t>(workspace) % 16 != 0))
     splits = 1;
   int64_t split_len = k;
   if (splits > 1) {

@@ -91,7 +91,8 @@ def test_negative_zero_seed_survives_on_device(hip):
     assert got.view(np.uint32)[0, 0] == np.float32(-0.0).view(np.uint32)
 
 
-@pytest.mark.parametrize("m, k, n", [(1024, 1024, 4096), (512, 512, 512), (8192, 3072, 768), (768, 8192, 768),
+@pytest.mark.parametrize("m, k, n", [(1024, 1024, 4096), (512, 512, 512), (4096, 4096, 4096), (8192, 3072, 768),
+                                     (768, 8192, 768),
                                      (1025, 1027, 1029), (1000, 512, 1020), (300, 64, 260)])
 @pytest.mark.parametrize("product", ["forward", "a_transposed", "b_transposed"])
 def test_sweep_shapes_sampled_rows(hip, m, k, n, product):

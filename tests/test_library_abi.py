@@ -55,6 +55,21 @@ def test_task_face_declines_need_no_device():
         tasks.gemm_f32(np.ones(3), (2, 1), np.ones(4), (2, 1), 2, 2, 2)
 
 
+def test_task_face_span_overflow_is_a_contract_violation():
+    import ctypes
+
+    from poorgrad_amd import _native as n
+
+    # Strides whose span 1 + (m-1)*rs + (k-1)*cs wraps size_t must not pass the
+    # length check (the reference's span arithmetic panics on overflow).
+    buf = (ctypes.c_float * 16)()
+    out = (ctypes.c_float * 4)()
+    huge = 1 << 63
+    for a_rs, a_cs in ((huge, huge), (1, (1 << 64) - 1), ((1 << 64) - 1, 2)):
+        code = n.lib.topos_hip_gemm_f32(buf, 16, a_rs, a_cs, buf, 16, 2, 1, 2, 2, 2, n.EXACT, out)
+        assert code == n.INVALID_ARGUMENT, (a_rs, a_cs, code)
+
+
 def _run_isolated(code: str) -> str:
     # Setup and poison are process-wide and sticky: each scenario runs in a
     # fresh interpreter.

@@ -117,6 +117,38 @@ def test_fast_rows_special_values(hip, columns):
         assert np.array_equal(np.sign(got[inf]), np.sign(want[inf])), f"fast special {kind}: infinity signs"
 
 
+@pytest.mark.parametrize("columns", [1024, 4096])
+def test_row_max_signed_zero_ties_and_nan_payloads(hip, columns):
+    """The ordered max_f32 fold keeps the earlier of two tied signed zeros
+    and, over a row of NaNs only, ends on the last term. Rows wide enough to
+    spread over every lane and quad of the register-resident kernel put the
+    competing zeros in other lanes and quads than column 0; the NaN rows
+    carry a distinct payload per column, compared by raw bits."""
+    banner(f"row max ties {columns}")
+    from poorgrad_amd import _native as n
+
+    x = np.full((8, columns), -1.0, dtype=np.float32)
+    x[0, 0] = -0.0; x[0, [1, 5, 67, columns // 2, columns - 1]] = 0.0    # -0 first, +0 in other lanes
+    x[1, 0] = 0.0; x[1, [1, 5, 67, columns // 2, columns - 1]] = -0.0    # +0 first, -0 elsewhere
+    x[2, 300] = -0.0; x[2, [4, 260, columns - 3]] = 0.0                   # +0 earlier in another quad
+    x[3, 4] = -0.0; x[3, [260, columns - 3]] = 0.0                        # -0 in quad 1, +0 later
+    nan_bits = (np.uint32(0x7FC00000) | np.arange(1, columns + 1, dtype=np.uint32))
+    x[4] = nan_bits.view(np.float32)                                       # every term a distinct quiet NaN
+    x[5] = (nan_bits | np.uint32(0x80000000)).view(np.float32)             # negative NaN payloads
+    x[6] = nan_bits.view(np.float32); x[6, columns // 3] = -0.0           # one number among NaNs
+    x[7, :] = -0.0; x[7, columns - 1] = 0.0
+    want = oracle.max_along(x, 1)
+    for numerics in (hip.EXACT, hip.FAST):
+        got = device.rows(n.ROWS_MAX, to_device(x), numerics).cpu().numpy()
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (
+            f"posture {numerics}: {got.view(np.uint32)} vs {want.view(np.uint32)}")
+    # The oracle's own fold fixes the answers these rows are built around.
+    assert want.view(np.uint32)[0] == np.float32(-0.0).view(np.uint32)
+    assert want.view(np.uint32)[1] == np.float32(0.0).view(np.uint32)
+    assert want.view(np.uint32)[4] == nan_bits[-1]
+    assert want.view(np.uint32)[6] == np.float32(-0.0).view(np.uint32)
+
+
 @pytest.mark.parametrize("rows, columns", [(3, 5), (64, 768), (257, 1000), (96, 4096)])
 def test_layer_norm_exact_and_fast(hip, rows, columns):
     banner(f"layer norm {rows}x{columns}")
