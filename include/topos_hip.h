@@ -129,6 +129,23 @@ int topos_hip_gemm_f32_device(const float *a, int64_t a_row_stride, int64_t a_co
                               int64_t m, int64_t k, int64_t n, int numerics, float *product,
                               int64_t ldc, void *stream);
 
+/* The same product as topos_hip_gemm_f32_device, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). No counterpart in the reference: it calls
+ * no hipMalloc/hipFree on any call. The split-k partials of a Fast product go
+ * to a fixed device array of 64 MiB (16 Mi floats) that each GPU holds from
+ * library load until the process ends, instead of
+ * the library's grow-only workspace; results are bit-identical to
+ * topos_hip_gemm_f32_device's. A product whose partials exceed the array
+ * returns TOPOS_HIP_INVALID_ARGUMENT (topos_hip_last_refusal() says why).
+ * Every call on one GPU shares that GPU's array: calls that overlap on one
+ * GPU (other streams, other threads) race and must be serialised by the
+ * caller. */
+int topos_hip_gemm_f32_device_noalloc(const float *a, int64_t a_row_stride, int64_t a_col_stride,
+                                      const float *b, int64_t b_row_stride, int64_t b_col_stride,
+                                      int64_t m, int64_t k, int64_t n, int numerics, float *product,
+                                      int64_t ldc, void *stream);
+
 /* Elementwise unary map over `count` contiguous elements (MapOperation). */
 int topos_hip_map_f32_device(int operation, const float *x, int64_t count, float *y, void *stream);
 

@@ -85,6 +85,8 @@ PROTOTYPES = {
     "topos_hip_map_f32": (c_int, [c_int, FLOAT_P, c_size_t, c_int, FLOAT_P]),
     "topos_hip_gemm_f32_device": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_int64, c_int64, c_int64,
                                           c_int64, c_int64, c_int, c_void_p, c_int64, c_void_p]),
+    "topos_hip_gemm_f32_device_noalloc": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_int64, c_int64,
+                                                  c_int64, c_int64, c_int64, c_int, c_void_p, c_int64, c_void_p]),
     "topos_hip_map_f32_device": (c_int, [c_int, c_void_p, c_int64, c_void_p, c_void_p]),
     "topos_hip_rows_f32_device": (c_int, [c_int, c_void_p, c_int64, c_int64, c_int, c_void_p, c_void_p]),
     "topos_hip_layer_norm_f32_device": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_float,
