@@ -38,6 +38,7 @@ from __future__ import annotations
 import argparse
 import json
 import math
+import os
 import sys
 import time
 from pathlib import Path
@@ -201,10 +202,11 @@ def roofline(profile) -> dict:
             "kernel": f"{dominant}: the step's {len(launches)} launches", "ms_per_step": round(ms, 3)}
 
 
-def cpu_leg(full_flops: float) -> dict:
-    """The oracle interpreter on one 64-token sequence of the same model
-    (full width, depth and vocabulary), one core; extrapolated to the full
-    step by the ratio of product flops (97% of the step's arithmetic)."""
+def cpu_sample() -> dict:
+    """The oracle interpreter on one 64-token sequence of the GPT-2-small
+    train step (full width, depth and vocabulary), in this process, which the
+    caller has pinned to one core. Returns the seconds and the sample's
+    product flops."""
     import numpy as np
 
     from oracle import interpreter
@@ -218,13 +220,33 @@ def cpu_leg(full_flops: float) -> dict:
     with np.errstate(all="ignore"):
         interpreter.run(w.tape, w.roots, w.initial, inputs)
     seconds = time.perf_counter() - start
-    sample_flops = matmul_flops(w.tape, w.roots)
+    return {"seconds": seconds, "flops": matmul_flops(w.tape, w.roots)}
+
+
+def cpu_leg(full_flops: float) -> dict:
+    """Times cpu_sample() in a child process pinned to one core (the
+    reference interpreter is single-threaded), then extrapolates to the full
+    step by the ratio of product flops (97% of the step's arithmetic)."""
+    import subprocess
+
+    allowed = sorted(os.sched_getaffinity(0))
+    core = allowed[0]
+    code = ("import json, os, sys; sys.path.insert(0, %r); os.sched_setaffinity(0, {%d}); "
+            "import bench; r = bench.cpu_sample(); r['affinity'] = sorted(os.sched_getaffinity(0)); "
+            "print(json.dumps(r))" % (str(Path(__file__).resolve().parent), core))
+    env = dict(os.environ, OMP_NUM_THREADS="1", OPENBLAS_NUM_THREADS="1", MKL_NUM_THREADS="1")
+    child = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, env=env, timeout=900)
+    if child.returncode != 0:
+        raise RuntimeError(f"cpu leg failed: {child.stderr[-2000:]}")
+    sample = json.loads(child.stdout.strip().splitlines()[-1])
+    seconds, sample_flops = sample["seconds"], sample["flops"]
     step_seconds = seconds * full_flops / sample_flops
     return {"value": round(1.0 / step_seconds, 8), "unit": "steps/s", "cores": 1, "kind": "port",
+            "host_cpus": os.cpu_count(), "allowed_cpus": len(allowed), "pinned_core": sample["affinity"],
             "sample": f"the interpreter restatement (oracle/) on the same GPT-2-small train step at batch 1, "
-                      f"context 64 ({sample_flops / 1e9:.1f} GFLOP of products, {seconds:.1f} s on one core), "
-                      f"scaled by product flops to the full step ({full_flops / 1e12:.2f} TFLOP): "
-                      f"{step_seconds / 60:.1f} min per step"}
+                      f"context 64 ({sample_flops / 1e9:.1f} GFLOP of products, {seconds:.1f} s on core "
+                      f"{core} of {os.cpu_count()} host CPUs, one thread), scaled by product flops to the full "
+                      f"step ({full_flops / 1e12:.2f} TFLOP): {step_seconds / 60:.1f} min per step"}
 
 
 def mlp_section(torch, n, steps: int, warmup: int) -> dict:

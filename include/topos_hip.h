@@ -67,6 +67,11 @@ enum {                                                         /* Formula (formu
   TOPOS_HIP_FORMULA_BATCH_NORM_INFERENCE = 5
 };
 enum { TOPOS_HIP_PRECISION_F32 = 1u, TOPOS_HIP_PRECISION_F64 = 2u }; /* Precision bits */
+enum {                                                         /* Dispatch (coverage.rs:87-98) */
+  TOPOS_HIP_DISPATCH_OFFERED = 0,
+  TOPOS_HIP_DISPATCH_ELECTED = 1,
+  TOPOS_HIP_DISPATCH_TRANSLATED = 2
+};
 enum {                                                         /* MapOperation (elementary.rs:13-22) */
   TOPOS_HIP_MAP_EXP = 0,
   TOPOS_HIP_MAP_LN = 1,
@@ -78,6 +83,10 @@ enum {                                                         /* MapOperation (
 
 /* ABI version of the loaded library; a binding refuses a mismatch. */
 int topos_hip_abi_version(void);
+/* How the member's kernels are reached (Manifest::DISPATCH, manifest.rs:17-18):
+ * TOPOS_HIP_DISPATCH_OFFERED, buffer tasks offered down the chains at run time,
+ * as the CUDA rung (src/backend/cuda/mod.rs:20). */
+int topos_hip_dispatch(void);
 /* Build facts only, no device probe (Manifest::compiled, manifest.rs:30-32). */
 int topos_hip_compiled(void);
 /* The coverage cell for one formula (Manifest::coverage, manifest.rs:22-28).

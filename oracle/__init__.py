@@ -1,4 +1,5 @@
-"""ctypes binding of the CPU oracle (oracle/oracle.c, oracle/program.c).
+"""ctypes binding of the CPU oracle (oracle/oracle.c); oracle/interpreter.py plays
+recorded tapes over it.
 
 TEST INFRASTRUCTURE ONLY: the parity tests, ``__graft_entry__.smoke()`` and
 the ``cpu_baseline`` leg of ``bench.py`` use it as the checker. Product code

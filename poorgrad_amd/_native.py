@@ -33,6 +33,7 @@ BIT_IDENTICAL, ENVELOPE = 0, 1
 FORMULA_GEMM, FORMULA_MAP, FORMULA_WINDOW_PRODUCT, FORMULA_REDUCE_WINDOW = 0, 1, 2, 3
 FORMULA_BATCH_NORM_TRAINING, FORMULA_BATCH_NORM_INFERENCE = 4, 5
 PRECISION_F32, PRECISION_F64 = 1, 2
+DISPATCH_OFFERED, DISPATCH_ELECTED, DISPATCH_TRANSLATED = 0, 1, 2
 MAP_EXP, MAP_LN, MAP_SQRT, MAP_TANH = 0, 1, 2, 3
 ROWS_SUM, ROWS_MAX, ROWS_LOG_SOFTMAX, ROWS_SOFTMAX, ROWS_LOG_SUM_EXP = 0, 1, 2, 3, 4
 CHAIN_NEG, CHAIN_EXP, CHAIN_LN, CHAIN_SQRT, CHAIN_TANH = 0, 1, 2, 3, 4
@@ -75,6 +76,7 @@ class Leaf(ctypes.Structure):
 # that each one resolves.
 PROTOTYPES = {
     "topos_hip_abi_version": (c_int, []),
+    "topos_hip_dispatch": (c_int, []),
     "topos_hip_compiled": (c_int, []),
     "topos_hip_coverage": (c_int, [c_int, POINTER(c_int), POINTER(c_uint)]),
     "topos_hip_status": (c_int, []),

@@ -126,6 +126,8 @@ extern "C" {
 
 int topos_hip_abi_version(void) { return TOPOS_HIP_ABI_VERSION; }
 
+int topos_hip_dispatch(void) { return TOPOS_HIP_DISPATCH_OFFERED; }
+
 int topos_hip_compiled(void) { return 1; }
 
 int topos_hip_coverage(int formula, int *fidelity, unsigned *precisions) {

@@ -18,8 +18,17 @@
 //   tanhf — fdlibm `tanhf` over fdlibm `expm1f` (s_tanhf.c, s_expm1f.c), pure
 //           single precision, built without FMA in glibc.
 //
+// Notices of the restated sources. ARM optimized-routines (the expf/logf
+// algorithms and their tables) is Copyright (c) 2017-2018 Arm Limited,
+// distributed under the MIT License or the Apache License 2.0 with LLVM
+// exception (SPDX: MIT OR Apache-2.0 WITH LLVM-exception), as contributed to
+// glibc. fdlibm (tanhf, expm1f): "Copyright (C) 1993 by Sun Microsystems, Inc.
+// All rights reserved. Developed at SunPro, a Sun Microsystems, Inc. business.
+// Permission to use, copy, modify, and distribute this software is freely
+// granted, provided that this notice is preserved."
+//
 // Each function is checked against the host glibc on every one of the 2^32
-// single-precision inputs (oracle/faithful_check.cpp, run by the CPU tests),
+// single-precision inputs (tests/native/faithful_check.cpp, run by the CPU tests),
 // and the device build is checked the same way on the GPU.
 #pragma once
 #if defined(__HIPCC_RTC__)
@@ -49,7 +58,7 @@ TOPOS_HD uint64_t bits_of(double value) { return __builtin_bit_cast(uint64_t, va
 TOPOS_HD double double_of(uint64_t bits) { return __builtin_bit_cast(double, bits); }
 
 // exp: bits(RN(2^(i/32))) - (i << 52) / 32 for i in 0..32. Derivable from the
-// definition alone (oracle/faithful_check.cpp recomputes every entry in
+// definition alone (tests/native/faithful_check.cpp recomputes every entry in
 // extended precision and compares).
 #if defined(__HIPCC__)
 static __device__ __constant__ uint64_t kExpTableDevice[32] = {

@@ -1,5 +1,6 @@
 """The C ABI library loads, exports every symbol include/topos_hip.h declares,
 and answers its manifest and device-free declines without a GPU."""
+import ctypes
 import re
 import subprocess
 import sys
@@ -40,6 +41,35 @@ def test_manifest_answers_without_a_device():
     for formula in (n.FORMULA_WINDOW_PRODUCT, n.FORMULA_REDUCE_WINDOW, n.FORMULA_BATCH_NORM_TRAINING,
                     n.FORMULA_BATCH_NORM_INFERENCE):
         assert n.lib.topos_hip_coverage(formula, None, None) == 0
+
+
+def test_coverage_matches_the_integration_table():
+    """The Rust manifest written out for topos (the coverage table of the
+    binding's documentation) and the library's own answers agree cell by cell,
+    as formula_tests.rs checks the chains against the matrix for every member."""
+    from poorgrad_amd import _native as n
+
+    text = (ROOT / "INTEGRATION.md").read_text()
+    table = text[text.index("| Formula | Coverage | Fidelity | Precisions |"):]
+    rows = []
+    for line in table.splitlines()[2:]:
+        if not line.startswith("|"):
+            break
+        rows.append([cell.strip() for cell in line.strip("|").split("|")])
+    codes = {"Gemm": n.FORMULA_GEMM, "Map": n.FORMULA_MAP, "WindowProduct": n.FORMULA_WINDOW_PRODUCT,
+             "ReduceWindow": n.FORMULA_REDUCE_WINDOW, "BatchNormTraining": n.FORMULA_BATCH_NORM_TRAINING,
+             "BatchNormInference": n.FORMULA_BATCH_NORM_INFERENCE}
+    assert sorted(r[0] for r in rows) == sorted(codes), "the table names every Formula variant once"
+    for formula, coverage, fidelity, precisions in rows:
+        f, p = ctypes.c_int(-1), ctypes.c_uint(0)
+        served = n.lib.topos_hip_coverage(codes[formula], ctypes.byref(f), ctypes.byref(p))
+        assert served == (coverage == "Serves"), formula
+        if served:
+            assert f.value == {"BitIdentical": n.BIT_IDENTICAL, "Envelope": n.ENVELOPE}[fidelity], formula
+            want = sum({"F32": n.PRECISION_F32, "F64": n.PRECISION_F64}[x.strip()] for x in precisions.split(","))
+            assert p.value == want, formula
+    assert n.lib.topos_hip_dispatch() == n.DISPATCH_OFFERED
+    assert "const DISPATCH: Dispatch = Dispatch::Offered;" in text
 
 
 def test_task_face_declines_need_no_device():
