@@ -333,6 +333,26 @@ int topos_hip_program_create(const topos_hip_node *nodes, int64_t n_nodes, const
                              int64_t n_leaves, const float *leaf_data, int64_t leaf_data_len,
                              const int32_t *leaf_indices, int64_t leaf_indices_len, int numerics,
                              topos_hip_program **program);
+/* The engine-backward route (Run::backward, src/engine/run.rs:229-318) for a
+ * plan compiled with Request::backward(): the library appends the reverse
+ * scan from the scalar node `target` to the forward table itself — one_like
+ * seed, zero_like-seeded accumulation in reverse scan order, only ancestors
+ * running their derivative rules (src/function/*.rs `backward`), only present
+ * cotangents marking ancestors — and plans forward and backward as one
+ * program whose arena keeps every forward value a rule reads. `wrt` lists the
+ * nodes whose gradients the caller will read (Run::backward answers every
+ * value; a device program keeps those asked for). Gradients equal
+ * Tape::differentiate's recorded gradients bit for bit under
+ * TOPOS_HIP_EXACT. TOPOS_HIP_INVALID_ARGUMENT for a non-scalar target. */
+int topos_hip_program_create_backward(const topos_hip_node *nodes, int64_t n_nodes, const topos_hip_leaf *leaves,
+                                      int64_t n_leaves, const float *leaf_data, int64_t leaf_data_len,
+                                      const int32_t *leaf_indices, int64_t leaf_indices_len, int numerics,
+                                      int64_t target, const int64_t *wrt, int64_t n_wrt,
+                                      topos_hip_program **program);
+/* The node of an engine-backward program holding the target's gradient with
+ * respect to node `node` (one of its `wrt`): read it after a run with
+ * topos_hip_program_output / topos_hip_program_read (Gradients::of). */
+int topos_hip_program_gradient(const topos_hip_program *program, int64_t node, int64_t *gradient_node);
 /* Bytes of the program's HBM arena (liveness-packed), and the number of
  * kernel launches one run enqueues. */
 int topos_hip_program_info(const topos_hip_program *program, uint64_t *arena_bytes, int64_t *launches,

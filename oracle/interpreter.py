@@ -159,10 +159,22 @@ def run(tape: t.Tape, readable, parameters: list, inputs: list) -> dict:
         if wanted[i]:
             for link in tape.nodes[i].operands:
                 wanted[link] = True
+    # A value is dropped after its last wanted consumer (the releases of a
+    # forward-only plan, src/engine/plan.rs:612-621), so full-width graphs fit
+    # in host memory; numpy views keep their bases alive as long as needed.
+    keep = set(targets)
+    last_use = [-1] * len(tape.nodes)
+    for i, node in enumerate(tape.nodes):
+        if wanted[i]:
+            for link in node.operands:
+                last_use[link] = i
     values: list = [None] * len(tape.nodes)
     for i, node in enumerate(tape.nodes):
         if wanted[i]:
             values[i] = forward(node, [values[link] for link in node.operands], parameters, inputs)
+            for link in node.operands:
+                if last_use[link] == i and link not in keep:
+                    values[link] = None
     out = {}
     for i in targets:
         v = values[i]

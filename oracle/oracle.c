@@ -51,23 +51,44 @@ void oracle_normal_f64(uint64_t *state, double deviation, size_t count, double *
 
 /* ---- src/payload/gemm.rs:140-211 ---- */
 
+/* Every output element keeps its own accumulator, seeded with its first
+ * term and advanced in ascending k, exactly as seed_row/accumulate_row do;
+ * the loops only visit the elements in a cache-friendlier order (column
+ * blocks whose slab of b stays in cache across rows, four rows per pass over
+ * a k step), which changes no element's sequence of roundings. */
 void oracle_gemm_rows_f32(const float *a, int64_t a_row_stride, int64_t a_col_stride,
                           const float *b, int64_t b_row_stride, int64_t b_col_stride, int64_t m,
                           int64_t n, int64_t k, int64_t row_begin, int64_t row_end, float *product) {
   (void)m;
-  for (int64_t row = row_begin; row < row_end; ++row) {
-    const int64_t a_row = row * a_row_stride;
-    float *out = product + row * n;
-    /* seed_row (gemm.rs:166-183): the first term, never a zero. */
-    const float a_first = a[a_row];
-    for (int64_t column = 0; column < n; ++column) out[column] = a_first * b[column * b_col_stride];
-    /* accumulate_row (gemm.rs:193-211): ascending inner steps. */
-    for (int64_t step = 1; step < k; ++step) {
-      const float a_value = a[a_row + step * a_col_stride];
-      const float *b_row = b + step * b_row_stride;
-      for (int64_t column = 0; column < n; ++column) {
-        const float term = a_value * b_row[column * b_col_stride];
-        out[column] = out[column] + term;
+  enum { kColumns = 512, kRows = 4 };
+  for (int64_t c0 = 0; c0 < n; c0 += kColumns) {
+    const int64_t c1 = c0 + kColumns < n ? c0 + kColumns : n;
+    for (int64_t r0 = row_begin; r0 < row_end; r0 += kRows) {
+      const int64_t rows = r0 + kRows <= row_end ? kRows : row_end - r0;
+      /* seed_row (gemm.rs:166-183): the first term, never a zero. */
+      for (int64_t r = 0; r < rows; ++r) {
+        const float a_first = a[(r0 + r) * a_row_stride];
+        float *out = product + (r0 + r) * n;
+        for (int64_t column = c0; column < c1; ++column) out[column] = a_first * b[column * b_col_stride];
+      }
+      /* accumulate_row (gemm.rs:193-211): ascending inner steps. */
+      for (int64_t step = 1; step < k; ++step) {
+        const float *b_row = b + step * b_row_stride;
+        for (int64_t r = 0; r < rows; ++r) {
+          const float a_value = a[(r0 + r) * a_row_stride + step * a_col_stride];
+          float *out = product + (r0 + r) * n;
+          if (b_col_stride == 1) {
+            for (int64_t column = c0; column < c1; ++column) {
+              const float term = a_value * b_row[column];
+              out[column] = out[column] + term;
+            }
+          } else {
+            for (int64_t column = c0; column < c1; ++column) {
+              const float term = a_value * b_row[column * b_col_stride];
+              out[column] = out[column] + term;
+            }
+          }
+        }
       }
     }
   }

@@ -100,6 +100,10 @@ PROTOTYPES = {
     "topos_hip_fake_runtime": (c_int, [c_int]),
     "topos_hip_program_create": (c_int, [POINTER(Node), c_int64, POINTER(Leaf), c_int64, FLOAT_P, c_int64,
                                          INT32_P, c_int64, c_int, POINTER(c_void_p)]),
+    "topos_hip_program_create_backward": (c_int, [POINTER(Node), c_int64, POINTER(Leaf), c_int64, FLOAT_P, c_int64,
+                                                  INT32_P, c_int64, c_int, c_int64, POINTER(c_int64), c_int64,
+                                                  POINTER(c_void_p)]),
+    "topos_hip_program_gradient": (c_int, [c_void_p, c_int64, POINTER(c_int64)]),
     "topos_hip_program_info": (c_int, [c_void_p, POINTER(ctypes.c_uint64), POINTER(c_int64), POINTER(c_int64)]),
     "topos_hip_program_bind": (c_int, [c_void_p, c_int, c_int32, c_void_p]),
     "topos_hip_program_bind_selection": (c_int, [c_void_p, c_int32, INT32_P, c_int64, c_float]),

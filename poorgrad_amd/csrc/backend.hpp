@@ -6,6 +6,7 @@
 #include <atomic>
 #include <cstddef>
 #include <cstdint>
+#include <map>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -164,6 +165,12 @@ bool launch_gemm_mfma(const float *a, int64_t a_rs, int64_t a_cs, const float *b
                       int64_t b_cs, int64_t m, int64_t k, int64_t n, float *c, int64_t ldc,
                       hipStream_t stream, const Batch &batch = Batch(), float *workspace = nullptr,
                       int64_t workspace_floats = 0, const Epilogue &epilogue = Epilogue());
+
+// backward.cpp: appends Run::backward's reverse scan from the scalar
+// `target` to a forward node table, and maps each node of `wrt` to the node
+// holding the target's gradient with respect to it (flagged readable).
+void append_engine_backward(std::vector<topos_hip_node> &nodes, std::vector<topos_hip_leaf> &leaves, int64_t target,
+                            const std::vector<int64_t> &wrt, std::map<int64_t, int64_t> &gradient_of);
 
 // index.hip
 void launch_gather(const float *table, int64_t row_stride, int64_t column_stride, const int32_t *indices,

@@ -292,6 +292,9 @@ struct topos_hip_program {
   std::vector<int32_t> leaf_indices;
   int numerics = TOPOS_HIP_EXACT;
   bool device = true;  // false under the fake runtime: plan and compile only
+  // The engine-backward route: node -> the node holding the target's
+  // gradient with respect to it (topos_hip_program_create_backward).
+  std::map<int64_t, int64_t> gradient_of;
 
   // ---- the plan ----
   std::vector<bool> wanted, readable;
@@ -2453,27 +2456,17 @@ struct topos_hip_program {
   }
 };
 
-extern "C" {
+namespace {
 
-int topos_hip_program_create(const topos_hip_node *nodes, int64_t n_nodes, const topos_hip_leaf *leaves,
-                             int64_t n_leaves, const float *leaf_data, int64_t leaf_data_len,
-                             const int32_t *leaf_indices, int64_t leaf_indices_len, int numerics,
-                             topos_hip_program **program) {
-  if (!program || n_nodes <= 0 || !nodes || (n_leaves > 0 && !leaves) || (leaf_data_len > 0 && !leaf_data) ||
-      (leaf_indices_len > 0 && !leaf_indices) || n_leaves < 0 || leaf_data_len < 0 || leaf_indices_len < 0)
-    return TOPOS_HIP_INVALID_ARGUMENT;
-  if (numerics != TOPOS_HIP_EXACT && numerics != TOPOS_HIP_FAST) return TOPOS_HIP_INVALID_ARGUMENT;
-  *program = nullptr;
-  const int status = Context::get().status();
-  if (status != TOPOS_HIP_OK) return status;
-  auto p = std::make_unique<topos_hip_program>();
-  p->nodes.assign(nodes, nodes + n_nodes);
-  p->leaves.assign(leaves, leaves + n_leaves);
+// Validates the table's buffers, then plans the program over `p`'s node
+// table (shared by the forward and the engine-backward entry points).
+int plan_program(std::unique_ptr<topos_hip_program> p, const float *leaf_data, int64_t leaf_data_len,
+                 const int32_t *leaf_indices, int64_t leaf_indices_len, int numerics,
+                 topos_hip_program **program) {
   p->leaf_data.assign(leaf_data, leaf_data + leaf_data_len);
   p->leaf_indices.assign(leaf_indices, leaf_indices + leaf_indices_len);
   p->numerics = numerics;
   p->device = Context::get().runtime().launches_kernels;
-  last_refusal().clear();
   const int code = guarded([&] {
     try {
       p->plan();
@@ -2488,6 +2481,76 @@ int topos_hip_program_create(const topos_hip_node *nodes, int64_t n_nodes, const
   });
   if (code == TOPOS_HIP_OK) *program = p.release();
   return code;
+}
+
+bool table_arguments_valid(const topos_hip_node *nodes, int64_t n_nodes, const topos_hip_leaf *leaves,
+                           int64_t n_leaves, const float *leaf_data, int64_t leaf_data_len,
+                           const int32_t *leaf_indices, int64_t leaf_indices_len, int numerics,
+                           topos_hip_program **program) {
+  if (!program || n_nodes <= 0 || !nodes || (n_leaves > 0 && !leaves) || (leaf_data_len > 0 && !leaf_data) ||
+      (leaf_indices_len > 0 && !leaf_indices) || n_leaves < 0 || leaf_data_len < 0 || leaf_indices_len < 0)
+    return false;
+  return numerics == TOPOS_HIP_EXACT || numerics == TOPOS_HIP_FAST;
+}
+
+}  // namespace
+
+extern "C" {
+
+int topos_hip_program_create(const topos_hip_node *nodes, int64_t n_nodes, const topos_hip_leaf *leaves,
+                             int64_t n_leaves, const float *leaf_data, int64_t leaf_data_len,
+                             const int32_t *leaf_indices, int64_t leaf_indices_len, int numerics,
+                             topos_hip_program **program) {
+  if (!table_arguments_valid(nodes, n_nodes, leaves, n_leaves, leaf_data, leaf_data_len, leaf_indices,
+                             leaf_indices_len, numerics, program))
+    return TOPOS_HIP_INVALID_ARGUMENT;
+  *program = nullptr;
+  const int status = Context::get().status();
+  if (status != TOPOS_HIP_OK) return status;
+  last_refusal().clear();
+  auto p = std::make_unique<topos_hip_program>();
+  p->nodes.assign(nodes, nodes + n_nodes);
+  p->leaves.assign(leaves, leaves + n_leaves);
+  return plan_program(std::move(p), leaf_data, leaf_data_len, leaf_indices, leaf_indices_len, numerics, program);
+}
+
+int topos_hip_program_create_backward(const topos_hip_node *nodes, int64_t n_nodes, const topos_hip_leaf *leaves,
+                                      int64_t n_leaves, const float *leaf_data, int64_t leaf_data_len,
+                                      const int32_t *leaf_indices, int64_t leaf_indices_len, int numerics,
+                                      int64_t target, const int64_t *wrt, int64_t n_wrt,
+                                      topos_hip_program **program) {
+  if (!table_arguments_valid(nodes, n_nodes, leaves, n_leaves, leaf_data, leaf_data_len, leaf_indices,
+                             leaf_indices_len, numerics, program) ||
+      n_wrt < 0 || (n_wrt > 0 && !wrt))
+    return TOPOS_HIP_INVALID_ARGUMENT;
+  *program = nullptr;
+  const int status = Context::get().status();
+  if (status != TOPOS_HIP_OK) return status;
+  last_refusal().clear();
+  auto p = std::make_unique<topos_hip_program>();
+  p->nodes.assign(nodes, nodes + n_nodes);
+  p->leaves.assign(leaves, leaves + n_leaves);
+  const int code = guarded([&] {
+    try {
+      append_engine_backward(p->nodes, p->leaves, target, std::vector<int64_t>(wrt, wrt + n_wrt), p->gradient_of);
+    } catch (const InvalidArgument &e) {
+      last_refusal() = e.message;
+      throw;
+    } catch (const Unsupported &e) {
+      last_refusal() = e.message;
+      throw;
+    }
+  });
+  if (code != TOPOS_HIP_OK) return code;
+  return plan_program(std::move(p), leaf_data, leaf_data_len, leaf_indices, leaf_indices_len, numerics, program);
+}
+
+int topos_hip_program_gradient(const topos_hip_program *program, int64_t node, int64_t *gradient_node) {
+  if (!program || !gradient_node) return TOPOS_HIP_INVALID_ARGUMENT;
+  const auto it = program->gradient_of.find(node);
+  if (it == program->gradient_of.end()) return TOPOS_HIP_INVALID_ARGUMENT;
+  *gradient_node = it->second;
+  return TOPOS_HIP_OK;
 }
 
 int topos_hip_program_info(const topos_hip_program *program, uint64_t *arena_bytes, int64_t *launches,

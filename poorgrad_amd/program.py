@@ -18,12 +18,41 @@ from .topos import ProgramTable, Tape, Value
 class DeviceProgram:
     """topos_hip_program_*: create once, bind, run many times."""
 
-    def __init__(self, tape: Tape, roots: Sequence[Value], observe: Sequence[Value] = (), numerics: int = n.EXACT):
+    def __init__(self, tape: Tape, roots: Sequence[Value], observe: Sequence[Value] = (), numerics: int = n.EXACT,
+                 backward: tuple | None = None):
         self.tape = tape
         self.table: ProgramTable = tape.program(roots, observe)
         self.numerics = numerics
-        self.handle = self.table.create(numerics)
+        self.handle = self.table.create(numerics) if backward is None else self.table.create_backward(numerics, *backward)
         self._held = {}  # keeps bound tensors alive
+
+    @classmethod
+    def engine_backward(cls, tape: Tape, target: Value, wrt: Sequence[Value], observe: Sequence[Value] = (),
+                        numerics: int = n.EXACT) -> "DeviceProgram":
+        """The engine-backward route (Request::backward() plan, then
+        Run::backward(target), src/engine/run.rs:229-318): the tape holds the
+        forward graph only, and the library appends the reverse scan itself.
+        Read gradients with read_gradient / gradient_pointer."""
+        return cls(tape, [target], observe, numerics, backward=(target.id, [v.id for v in wrt]))
+
+    def _gradient_node(self, value: Value) -> int:
+        node = ctypes.c_int64()
+        n.checked(n.lib.topos_hip_program_gradient(self.handle, value.id, ctypes.byref(node)), "program gradient")
+        return node.value
+
+    def read_gradient(self, value: Value) -> np.ndarray:
+        """The target's gradient with respect to `value` after a run
+        (Gradients::of)."""
+        out = np.empty(value.shape, dtype=np.float32)
+        n.checked(n.lib.topos_hip_program_read(self.handle, self._gradient_node(value),
+                                               out.ctypes.data_as(n.FLOAT_P), out.size), "program read gradient")
+        return out
+
+    def gradient_pointer(self, value: Value) -> int:
+        p = ctypes.c_void_p()
+        n.checked(n.lib.topos_hip_program_output(self.handle, self._gradient_node(value), ctypes.byref(p)),
+                  "program gradient output")
+        return p.value
 
     @property
     def describe(self) -> str:

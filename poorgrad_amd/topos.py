@@ -522,6 +522,22 @@ class ProgramTable:
         self.leaf_indices = np.concatenate(indices).astype(np.int32) if indices else np.zeros(1, np.int32)
         self.leaf_indices_len = index_len
 
+    def create_backward(self, numerics: int, target: int, wrt: Sequence[int]):
+        """topos_hip_program_create_backward: this forward table plus the
+        library's own reverse scan from `target`; returns the native handle."""
+        from . import _native as n
+
+        handle = ctypes.c_void_p()
+        wanted = (ctypes.c_int64 * max(1, len(wrt)))(*wrt)
+        code = n.lib.topos_hip_program_create_backward(
+            self.nodes, self.count, self.leaves, self.n_leaves,
+            self.leaf_data.ctypes.data_as(n.FLOAT_P), self.leaf_data_len,
+            self.leaf_indices.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), self.leaf_indices_len,
+            numerics, int(target), wanted, len(wrt), ctypes.byref(handle))
+        if code != n.OK:
+            raise n.HipError(code, "program create backward: " + n.lib.topos_hip_last_refusal().decode())
+        return handle
+
     def create(self, numerics: int):
         """topos_hip_program_create; returns the native handle."""
         from . import _native as n

@@ -92,7 +92,7 @@ class Workload:
 
 
 def mlp(batch: int = 64, sizes=(784, 128, 10), weight_seeds=(7, 8), input_seed: int = 11,
-        label_seed: int = 13) -> Workload:
+        label_seed: int = 13, record_gradients: bool = True) -> Workload:
     """Linear -> ReLU -> Linear, cross_entropy over
     one-hot targets; inputs U[0,1), Kaiming-uniform weights
     U(-sqrt(6/fan_in), +sqrt(6/fan_in)), zero biases."""
@@ -111,7 +111,9 @@ def mlp(batch: int = 64, sizes=(784, 128, 10), weight_seeds=(7, 8), input_seed: 
         if layer < len(sizes) - 2:
             h = h.relu()
     loss = cross_entropy(h, targets)
-    gradients = tape.differentiate(loss, params)
+    # Without recorded gradients the tape is the forward graph alone: the
+    # engine-backward route appends the reverse scan on the device.
+    gradients = tape.differentiate(loss, params) if record_gradients else []
     feeds = unit(input_seed, batch * sizes[0]).astype(np.float32).reshape(batch, sizes[0])
     return Workload(tape, params, initial, loss, gradients, dense_inputs={x.node.slot: feeds},
                     selection_inputs={targets.node.slot: (labels(label_seed, batch, sizes[-1]), 1.0)},
@@ -125,8 +127,21 @@ def _gelu(x: Value, half: Value, one: Value, root: Value, coefficient: Value) ->
     return x * (inner + one.broadcast_like(inner)) * half.broadcast_like(x)
 
 
+def _weights(init: str):
+    """The weight draw: init::normal(seed, 0.02) (the configs' N(0, 0.02)), or
+    init::uniform(seed, 0.02 * sqrt(3)) of the same deviation, whose draws use
+    integer and correctly rounded f64 arithmetic only, so every machine draws
+    the same bits (the full-shape parity fixtures use it)."""
+    if init == "normal":
+        return lambda seed, shape: normal(seed, 0.02, shape)
+    if init == "uniform":
+        return lambda seed, shape: uniform(seed, 0.02 * math.sqrt(3.0), shape)
+    raise ValueError(f"unknown weight init {init!r}")
+
+
 def gpt2(batch: int = 8, context: int = 1024, vocab: int = 50257, width: int = 768, heads: int = 12,
-         layers: int = 12, positions: int = 1024, weight_seed: int = 7, token_seed: int = 13) -> Workload:
+         layers: int = 12, positions: int = 1024, weight_seed: int = 7, token_seed: int = 13,
+         init: str = "normal", record_gradients: bool = True) -> Workload:
     """BASELINE configs[3] (or the same graph at other dimensions): GPT-2 with
     pre-LayerNorm blocks, causal attention, GELU MLP, tied embeddings."""
     assert width % heads == 0 and context <= positions
@@ -136,10 +151,12 @@ def gpt2(batch: int = 8, context: int = 1024, vocab: int = 50257, width: int = 7
     params, initial = [], []
     seed = [weight_seed]
 
+    draw = _weights(init)
+
     def weight(shape):
         p = tape.parameter(shape)
         params.append(p)
-        initial.append(normal(seed[0], 0.02, shape))
+        initial.append(draw(seed[0], shape))
         seed[0] += 1
         return p
 
@@ -193,7 +210,9 @@ def gpt2(batch: int = 8, context: int = 1024, vocab: int = 50257, width: int = 7
         x = x + linear(_gelu(linear(h, *b["fc"]), half, one, root, coefficient), *b["out"])
     logits = layer_norm(x, *ln_f, epsilon).matmul(wte.transpose())
     loss = cross_entropy(logits, targets)
-    gradients = tape.differentiate(loss, params)
+    # Without recorded gradients the tape is the forward graph alone: the
+    # engine-backward route appends the reverse scan on the device.
+    gradients = tape.differentiate(loss, params) if record_gradients else []
 
     stream = labels(token_seed, rows + batch, vocab).reshape(batch, context + 1)
     token_ids = stream[:, :-1].reshape(-1)
@@ -217,7 +236,8 @@ def rope_tables(context: int, head: int, base: float = 10000.0):
 
 def llama(batch: int = 2, context: int = 2048, vocab: int = 32000, width: int = 2048, heads: int = 16,
           hidden: int = 5632, layers: int = 8, epsilon: float = 1e-6, weight_seed: int = 7,
-          token_seed: int = 13, host_weights: bool = True) -> Workload:
+          token_seed: int = 13, host_weights: bool = True, init: str = "normal",
+          record_gradients: bool = True) -> Workload:
     """BASELINE configs[4] (or the same graph at other dimensions): a Llama-style
     decoder, forward and backward (the loss and every parameter's gradient).
     Blocks follow examples/llama/model.rs: pre-norm RMSNorm (:280-300), q/k/v/o
@@ -234,10 +254,12 @@ def llama(batch: int = 2, context: int = 2048, vocab: int = 32000, width: int = 
     params, initial = [], []
     seed = [weight_seed]
 
+    draw = _weights(init)
+
     def weight(shape):
         p = tape.parameter(shape)
         params.append(p)
-        initial.append(normal(seed[0], 0.02, shape) if host_weights else shape)
+        initial.append(draw(seed[0], shape) if host_weights else shape)
         seed[0] += 1
         return p
 
@@ -296,7 +318,9 @@ def llama(batch: int = 2, context: int = 2048, vocab: int = 32000, width: int = 
         x = x + (activated * h.matmul(b["up"])).matmul(b["down"])
     logits = rms_norm(x, final_norm, eps).matmul(lm_head)
     loss = cross_entropy(logits, targets)
-    gradients = tape.differentiate(loss, params)
+    # Without recorded gradients the tape is the forward graph alone: the
+    # engine-backward route appends the reverse scan on the device.
+    gradients = tape.differentiate(loss, params) if record_gradients else []
 
     stream = labels(token_seed, rows + batch, vocab).reshape(batch, context + 1)
     token_ids = stream[:, :-1].reshape(-1)

@@ -12,7 +12,7 @@ from poorgrad_amd import topos as t
 from poorgrad_amd import workloads
 from tests.conftest import banner
 from tests.gpu_util import assert_bitwise
-from tests.program_util import run_device, run_oracle
+from tests.program_util import adamw_reference, adamw_state, paper_adam_trace, run_device, run_oracle
 
 pytestmark = pytest.mark.gpu
 
@@ -279,20 +279,30 @@ def test_adamw_steps_match_the_rule(hip):
             assert_bitwise(device[i], params[i], f"adamw step {step} param {i}")
 
 
-def _adamw_reference(params, grads, state, f=np.float32):
-    """AdamW::step (src/neural/adam.rs:62-171) restated in numpy f32."""
-    b1, b2, eps, decay, lr = f(0.9), f(0.999), f(1e-8), f(0.01), f(3e-4)
-    state["p1"], state["p2"] = f(state["p1"] * b1), f(state["p2"] * b2)
-    c1, c2 = f(1) - state["p1"], f(1) - state["p2"]
-    out = []
-    for i, (p, g) in enumerate(zip(params, grads)):
-        m = state["m"][i] * b1 + g * (f(1) - b1)
-        v = state["v"][i] * b2 + (g * g) * (f(1) - b2)
-        state["m"][i], state["v"][i] = m, v
-        direction = (m / c1) / (np.sqrt(v / c2) + eps)
-        stepped = p - direction * lr
-        out.append(stepped - (p * decay) * lr if p.ndim >= 2 else stepped)
-    return out
+def test_device_adamw_follows_the_paper_trace(hip):
+    """The reference's two-step Adam trace (src/neural/tests/adam_tests.rs:15-53:
+    loss = w * w from w = 1, rate 0.1, betas 0.9 / 0.999, epsilon 1e-8, traced
+    in f64 from the paper's rule) through the device kernel, with the gradient
+    2w formed in f32 each step: within f32 rounding of the f64 trace, and
+    bitwise equal to the numpy restatement."""
+    import torch
+
+    from poorgrad_amd.program import AdamW
+
+    banner("adamw paper trace")
+    w = torch.ones(1, device="cuda")
+    opt = AdamW([w], decay=0.0)
+    host = [np.ones(1, np.float32)]
+    state = adamw_state(host)
+    trace = paper_adam_trace(2)
+    for step in range(2):
+        gradient = (np.float32(2) * w.cpu().numpy()).astype(np.float32)
+        g = torch.from_numpy(gradient).cuda()
+        opt.step([w], [g.data_ptr()], 0.1)
+        torch.cuda.synchronize()
+        host = adamw_reference(host, [gradient], state, rate=0.1, decay=0.0)
+        assert_bitwise(w, host[0], f"paper trace step {step}: device vs restatement")
+        assert abs(float(w.cpu()[0]) - trace[step]) <= 1e-6 * abs(trace[step]), (step, float(w.cpu()[0]), trace[step])
 
 
 def test_small_gpt2_adamw_steps_exact(hip):
@@ -315,8 +325,7 @@ def test_small_gpt2_adamw_steps_exact(hip):
         program.bind_selection(slot, indices, one)
     optimizer = AdamW(device)
     host = [a.copy() for a in w.initial]
-    state = {"p1": np.float32(1), "p2": np.float32(1), "m": [np.zeros_like(a) for a in host],
-             "v": [np.zeros_like(a) for a in host]}
+    state = adamw_state(host)
     pointers = None
     for step in range(3):
         want = run_oracle(w.tape, w.roots, host, {}, w.selection_inputs)
@@ -325,7 +334,7 @@ def test_small_gpt2_adamw_steps_exact(hip):
             pointers = [program.pointer(g) for g in w.gradients]
         optimizer.step(device, pointers, 3e-4)
         torch.cuda.synchronize()
-        host = _adamw_reference(host, [want[g.id] for g in w.gradients], state)
+        host = adamw_reference(host, [want[g.id] for g in w.gradients], state)
         for i, (d, h) in enumerate(zip(device, host)):
             assert_bitwise(d, h, f"step {step} parameter {i}")
 

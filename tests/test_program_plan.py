@@ -186,3 +186,43 @@ print(p.describe)
     lines = out.splitlines()
     assert lines[0] == "2", out
     assert "chain Add+Mul+Exp [48,48]" in out and ", 3 outputs" in out, out
+
+
+def test_engine_backward_plans_the_recorded_gradients_program():
+    """The engine-backward route (the library's own reverse scan,
+    Run::backward of src/engine/run.rs:229-318, over a forward-only table)
+    records the same nodes, in the same order, as Tape::differentiate's
+    recorded route (src/graph/tape.rs:335-411): the two programs plan to the
+    same launches, descriptions and arena."""
+    out = run(r'''
+cases = [
+    lambda g: workloads.mlp(record_gradients=g),
+    lambda g: workloads.gpt2(batch=2, context=16, vocab=37, width=32, heads=4, layers=2, positions=24,
+                             record_gradients=g),
+    lambda g: workloads.llama(batch=2, context=16, vocab=37, width=32, heads=4, hidden=48, layers=2,
+                              record_gradients=g),
+]
+for make in cases:
+    for numerics in (n.EXACT, n.FAST):
+        recorded = make(True)
+        forward = make(False)
+        a = DeviceProgram(recorded.tape, recorded.roots, numerics=numerics)
+        b = DeviceProgram.engine_backward(forward.tape, forward.loss, forward.parameters, numerics=numerics)
+        assert a.describe == b.describe, (a.describe[:2000], b.describe[:2000])
+        assert a.info == b.info, (a.info, b.info)
+        print(a.info["launches"])
+''')
+    assert len(out.split()) == 6, out
+
+
+def test_engine_backward_refuses_a_non_scalar_target():
+    out = run(r'''
+tape = t.Tape()
+x = tape.parameter((4, 3))
+y = (x * x).sum_along(1)
+try:
+    DeviceProgram.engine_backward(tape, y, [x])
+except n.HipError as e:
+    print(e.code, "scalar" in str(e))
+''')
+    assert out.split() == ["5", "True"], out

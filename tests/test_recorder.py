@@ -170,3 +170,25 @@ def test_synthetic_normal_follows_the_reference_stream():
     want = oracle.Generator(7).normal(2000, 0.02)
     assert np.mean(got == want) > 0.99
     assert np.allclose(got, want, rtol=1e-6, atol=1e-9)
+
+
+def test_adamw_restatement_follows_the_paper_trace():
+    """The f32 AdamW restatement the GPU tests hold the device kernel to,
+    against the reference's two-step f64 paper trace
+    (src/neural/tests/adam_tests.rs:15-53), with no decay as for its
+    scalar-shaped parameter: within f32 rounding (1e-6 relative, about a
+    dozen ulps of the result; the restatement lands 3.8e-7 away at step 2)
+    at each step. A dropped bias correction moves step 1 by 24%, and swapped
+    betas move step 2 by 7e-4."""
+    from tests.program_util import adamw_reference, adamw_state, paper_adam_trace
+
+    params = [np.ones((), np.float32)]
+    state = adamw_state(params)
+    trace = paper_adam_trace(2)
+    for step in range(2):
+        gradient = (np.float32(2) * params[0]).astype(np.float32)
+        params = adamw_reference(params, [gradient], state, rate=0.1, decay=0.0)
+        assert abs(float(params[0]) - trace[step]) <= 1e-6 * abs(trace[step]), (step, float(params[0]), trace[step])
+    # The trace itself: after one step Adam moves w by the rate exactly
+    # (m / c1 = g and sqrt(v / c2) = |g|), up to epsilon.
+    assert abs(trace[0] - (1.0 - 0.1 * 2.0 / (2.0 + 1e-8))) < 1e-15
