@@ -198,7 +198,8 @@ enum {
   TOPOS_HIP_CHAIN_MUL = 18,
   TOPOS_HIP_CHAIN_DIV = 19,
   TOPOS_HIP_CHAIN_MAX = 20,  /* f32::max */
-  TOPOS_HIP_CHAIN_STEP = 21  /* x >= y ? 1 : 0 */
+  TOPOS_HIP_CHAIN_STEP = 21, /* x >= y ? 1 : 0 */
+  TOPOS_HIP_CHAIN_POWF = 22  /* f32::powf: the host libm's powf */
 };
 #define TOPOS_HIP_MAX_RANK 4
 /* A strided view of `rank` axes (the Layout of src/payload/layout.rs:23-31):
@@ -287,7 +288,7 @@ enum {
   TOPOS_HIP_OP_LOG_SOFTMAX = 25,   /* axis = params[0] */
   TOPOS_HIP_OP_LOG_SUM_EXP = 26,   /* axis = params[0] */
   TOPOS_HIP_OP_SQRT = 27,
-  TOPOS_HIP_OP_POWF = 28,          /* served for constant operands only */
+  TOPOS_HIP_OP_POWF = 28,
   TOPOS_HIP_OP_MAXIMUM = 29,
   TOPOS_HIP_OP_RELU = 30,
   TOPOS_HIP_OP_STEP = 31
@@ -327,8 +328,8 @@ typedef struct topos_hip_program topos_hip_program;
 
 /* Validates and plans the program (shape inference per node, views, fusion
  * groups, launch order, arena offsets) and compiles its generated kernels.
- * TOPOS_HIP_UNSUPPORTED names a node outside the kernels (Unfold, Fold, Powf
- * of non-constant operands); TOPOS_HIP_INVALID_ARGUMENT a malformed table. */
+ * TOPOS_HIP_UNSUPPORTED names a node outside the kernels (Unfold, Fold);
+ * TOPOS_HIP_INVALID_ARGUMENT a malformed table. */
 int topos_hip_program_create(const topos_hip_node *nodes, int64_t n_nodes, const topos_hip_leaf *leaves,
                              int64_t n_leaves, const float *leaf_data, int64_t leaf_data_len,
                              const int32_t *leaf_indices, int64_t leaf_indices_len, int numerics,

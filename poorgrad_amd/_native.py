@@ -37,7 +37,7 @@ DISPATCH_OFFERED, DISPATCH_ELECTED, DISPATCH_TRANSLATED = 0, 1, 2
 MAP_EXP, MAP_LN, MAP_SQRT, MAP_TANH = 0, 1, 2, 3
 ROWS_SUM, ROWS_MAX, ROWS_LOG_SOFTMAX, ROWS_SOFTMAX, ROWS_LOG_SUM_EXP = 0, 1, 2, 3, 4
 CHAIN_NEG, CHAIN_EXP, CHAIN_LN, CHAIN_SQRT, CHAIN_TANH = 0, 1, 2, 3, 4
-CHAIN_ADD, CHAIN_SUB, CHAIN_MUL, CHAIN_DIV, CHAIN_MAX, CHAIN_STEP = 16, 17, 18, 19, 20, 21
+CHAIN_ADD, CHAIN_SUB, CHAIN_MUL, CHAIN_DIV, CHAIN_MAX, CHAIN_STEP, CHAIN_POWF = 16, 17, 18, 19, 20, 21, 22
 MAX_RANK = 4
 
 FLOAT_P = POINTER(c_float)

@@ -50,6 +50,7 @@ const char *binary_pattern(int op) {
     case TOPOS_HIP_CHAIN_DIV: return "(%a / %b)";
     case TOPOS_HIP_CHAIN_MAX: return "topos_faithful::max_f32(%a, %b)";
     case TOPOS_HIP_CHAIN_STEP: return "topos_faithful::step_f32(%a, %b)";
+    case TOPOS_HIP_CHAIN_POWF: return "topos_pow(%a, %b)";
   }
   return nullptr;
 }
@@ -216,17 +217,24 @@ std::string preamble() {
        "  __builtin_amdgcn_s_barrier();\n"
        "  __atomic_signal_fence(__ATOMIC_SEQ_CST);\n"
        "}\n";
-  // The exp and ln tables, copied into LDS by every generated kernel on
-  // entry: a per-lane table index then costs an LDS read, not a global load.
+  // The exp, ln and log2 tables, copied into LDS by every generated kernel
+  // on entry: a per-lane table index then costs an LDS read, not a global
+  // load.
   s += "__shared__ uint64_t topos_exp_lds[32];\n"
        "__shared__ topos_faithful::LogRow topos_log_lds[16];\n"
+       "__shared__ topos_faithful::LogRow topos_log2_lds[16];\n"
        "__device__ __forceinline__ void topos_tables_init() {\n"
        "  if (threadIdx.x < 32) topos_exp_lds[threadIdx.x] = topos_faithful::kExpTableDevice[threadIdx.x];\n"
        "  if (threadIdx.x < 16) topos_log_lds[threadIdx.x] = topos_faithful::kLogTableDevice[threadIdx.x];\n"
+       "  if (threadIdx.x >= 32 && threadIdx.x < 48)\n"
+       "    topos_log2_lds[threadIdx.x - 32] = topos_faithful::kLog2TableDevice[threadIdx.x - 32];\n"
        "  __syncthreads();\n"
        "}\n"
        "__device__ __forceinline__ float topos_exp(float x) { return topos_faithful::exp_f32_table(x, topos_exp_lds); }\n"
-       "__device__ __forceinline__ float topos_ln(float x) { return topos_faithful::ln_f32_table(x, topos_log_lds); }\n";
+       "__device__ __forceinline__ float topos_ln(float x) { return topos_faithful::ln_f32_table(x, topos_log_lds); }\n"
+       "__device__ __forceinline__ float topos_pow(float x, float y) {\n"
+       "  return topos_faithful::pow_f32_tables(x, y, topos_log2_lds, topos_exp_lds);\n"
+       "}\n";
   return s;
 }
 

@@ -15,6 +15,9 @@
 //           since 2.27): 2^(k/32) table lookup plus a cubic in double.
 //   logf  — ARM optimized-routines `logf` (e_logf.c): 16-interval table of
 //           (1/c, log c) plus a cubic in double.
+//   powf  — ARM optimized-routines `powf` (e_powf.c since 2.27): log2 x from the
+//           same 16 subintervals (1/c, log2 c) and a quintic in double, times
+//           y in double, then 2^(y log2 x) from the exp table and a cubic.
 //   tanhf — fdlibm `tanhf` over fdlibm `expm1f` (s_tanhf.c, s_expm1f.c), pure
 //           single precision, built without FMA in glibc.
 //
@@ -96,12 +99,31 @@ static const LogRow kLogTableHost[16] = {
     {0x1.886e6037841edp-1, 0x1.1058bc8a07ee1p-2},  {0x1.767dcf5534862p-1, 0x1.4043057b6ee09p-2},
 };
 
+// powf's log2: the same 1/c column, and RN(log2 c) = RN(-log2(invc)) (the check
+// recomputes it).
+#if defined(__HIPCC__)
+static __device__ __constant__ LogRow kLog2TableDevice[16] = {
+#else
+static const LogRow kLog2TableHost[16] = {
+#endif
+    {0x1.661ec79f8f3bep+0, -0x1.efec65b963019p-2}, {0x1.571ed4aaf883dp+0, -0x1.b0b6832d4fca4p-2},
+    {0x1.49539f0f010bp+0, -0x1.7418b0a1fb77bp-2},  {0x1.3c995b0b80385p+0, -0x1.39de91a6dcf7bp-2},
+    {0x1.30d190c8864a5p+0, -0x1.01d9bf3f2b631p-2}, {0x1.25e227b0b8eap+0, -0x1.97c1d1b3b7afp-3},
+    {0x1.1bb4a4a1a343fp+0, -0x1.2f9e393af3c9fp-3}, {0x1.12358f08ae5bap+0, -0x1.960cbbf788d5cp-4},
+    {0x1.0953f419900a7p+0, -0x1.a6f9db6475fcep-5}, {0x1p+0, 0x0p+0},
+    {0x1.e608cfd9a47acp-1, 0x1.338ca9f24f53dp-4},  {0x1.ca4b31f026aap-1, 0x1.476a9543891bap-3},
+    {0x1.b2036576afce6p-1, 0x1.e840b4ac4e4d2p-3},  {0x1.9c2d163a1aa2dp-1, 0x1.40645f0c6651cp-2},
+    {0x1.886e6037841edp-1, 0x1.88e9c2c1b9ff8p-2},  {0x1.767dcf5534862p-1, 0x1.ce0a44eb17bccp-2},
+};
+
 #if defined(__HIPCC__)
 #define TOPOS_EXP_TABLE kExpTableDevice
 #define TOPOS_LOG_TABLE kLogTableDevice
+#define TOPOS_LOG2_TABLE kLog2TableDevice
 #else
 #define TOPOS_EXP_TABLE kExpTableHost
 #define TOPOS_LOG_TABLE kLogTableHost
+#define TOPOS_LOG2_TABLE kLog2TableHost
 #endif
 
 // e^x. Reduction x * 32/ln2 = k + r, |r| <= 1/2, with k rounded by the
@@ -281,6 +303,112 @@ TOPOS_HD float tanh_f32(float x) {
   }
   return jx >= 0 ? z : -z;
 }
+
+// Whether a non-zero finite f32 (by its bits) is an integer: 0 if not, 1 if
+// odd, 2 if even.
+TOPOS_HD int pow_integer_class(uint32_t iy) {
+  const int e = (int)(iy >> 23 & 0xff);
+  if (e < 0x7f) return 0;
+  if (e > 0x7f + 23) return 2;
+  if (iy & ((1u << (0x7f + 23 - e)) - 1)) return 0;
+  if (iy & (1u << (0x7f + 23 - e))) return 1;
+  return 2;
+}
+
+// Whether an f32 (by its bits) is zero, infinite or NaN.
+TOPOS_HD bool pow_zero_inf_nan(uint32_t i) { return 2 * i - 1 >= 2u * 0x7f800000u - 1; }
+
+// x^y. log2 x = k + log2 c + log1p(z/c - 1)/ln 2 (x = 2^k z, z in
+// [0x3f330000, 2 * 0x3f330000), c from the top four mantissa bits of z) with a
+// quintic for log1p(r)/ln 2; y log2 x rounded to double; 2^(y log2 x) =
+// 2^(k'/32) 2^r by the exp table and a cubic, the result's sign folded into
+// the table entry's exponent. The multiply-adds are fused as in glibc's FMA
+// build. Special cases follow glibc: y = +-0 or x = 1 give 1 (NaN included);
+// NaN operands propagate; |x| = 1 with y = +-inf gives 1; 0 and inf bases
+// square through; a finite negative base needs an integer exponent (else
+// NaN), an odd one carrying the sign; overflow gives +-inf and underflow
+// +-0, with the sign of the result.
+TOPOS_HD float pow_f32_tables(float x, float y, const LogRow *log2_table, const uint64_t *exp_table) {
+  const double a0 = 0x1.27616c9496e0bp-2, a1 = -0x1.71969a075c67ap-2, a2 = 0x1.ec70a6ca7baddp-2,
+               a3 = -0x1.7154748bef6c8p-1, a4 = 0x1.71547652ab82bp0;
+  const double c0 = 0x1.c6af84b912394p-5, c1 = 0x1.ebfce50fac4f3p-3, c2 = 0x1.62e42ff0c52d6p-1;
+  const double shift = 0x1.8p+52 / 32;
+  uint32_t sign_bias = 0;
+  uint32_t ix = bits_of(x);
+  const uint32_t iy = bits_of(y);
+  if (ix - 0x00800000u >= 0x7f800000u - 0x00800000u || pow_zero_inf_nan(iy)) {
+    // x subnormal, zero, negative, infinite or NaN; or y zero, infinite or NaN.
+    if (pow_zero_inf_nan(iy)) {
+      if (2 * iy == 0) return (ix & 0x7fc00000u) == 0x7f800000u && (ix & 0x003fffffu) ? x + y : 1.0f;
+      if (ix == 0x3f800000u) return (iy & 0x7fc00000u) == 0x7f800000u && (iy & 0x003fffffu) ? x + y : 1.0f;
+      if (2 * ix > 2u * 0x7f800000u || 2 * iy > 2u * 0x7f800000u) return x + y;
+      if (2 * ix == 2u * 0x3f800000u) return 1.0f;
+      if ((2 * ix < 2u * 0x3f800000u) == !(iy & 0x80000000u)) return 0.0f;  // |x| < 1, y = inf; |x| > 1, y = -inf
+      return y * y;
+    }
+    if (pow_zero_inf_nan(ix)) {
+      float x2 = x * x;
+      if ((ix & 0x80000000u) && pow_integer_class(iy) == 1) x2 = -x2;
+      return (iy & 0x80000000u) ? 1.0f / x2 : x2;
+    }
+    // x and y are non-zero finite.
+    if (ix & 0x80000000u) {
+      const int yint = pow_integer_class(iy);
+      if (yint == 0) {
+        const float d = x - x;  // the invalid result, (x - x) / (x - x)
+        return d / d;
+      }
+      if (yint == 1) sign_bias = 1u << (5 + 11);
+      ix &= 0x7fffffffu;
+    }
+    if (ix < 0x00800000u) {  // subnormal x: normalise, the exponent goes negative
+      ix = bits_of(x * 0x1p23f);
+      ix &= 0x7fffffffu;
+      ix -= 23u << 23;
+    }
+  }
+  // log2 x.
+  const uint32_t tmp = ix - 0x3f330000u;
+  const int i = (int)((tmp >> (23 - 4)) % 16);
+  const uint32_t top = tmp & 0xff800000u;
+  const uint32_t iz = ix - top;
+  const int k = (int32_t)top >> 23;
+  const double invc = log2_table[i].invc;
+  const double logc = log2_table[i].logc;
+  const double z = (double)float_of(iz);
+  const double r = __builtin_fma(z, invc, -1.0);
+  const double y0 = logc + (double)k;
+  const double r2 = r * r;
+  double p = __builtin_fma(a0, r, a1);
+  const double q0 = __builtin_fma(a2, r, a3);
+  const double r4 = r2 * r2;
+  double q = __builtin_fma(a4, r, y0);
+  q = __builtin_fma(q0, r2, q);
+  const double logx = __builtin_fma(p, r4, q);
+  const double ylogx = (double)y * logx;
+  if ((bits_of(ylogx) >> 47 & 0xffff) >= bits_of(126.0) >> 47) {
+    // |y log2 x| >= 126.
+    if (ylogx > 0x1.fffffffd1d571p+6) return sign_bias ? -float_of(0x7f800000u) : float_of(0x7f800000u);
+    if (ylogx <= -150.0) return sign_bias ? -0.0f : 0.0f;
+  }
+  // 2^ylogx.
+  double kd = ylogx + shift;
+  const uint64_t ki = bits_of(kd);
+  kd -= shift;
+  const double rr = ylogx - kd;
+  uint64_t t = exp_table[ki % 32];
+  const uint64_t ski = ki + sign_bias;
+  t += ski << (52 - 5);
+  const double s = double_of(t);
+  const double zz = __builtin_fma(c0, rr, c1);
+  const double rr2 = rr * rr;
+  double yy = __builtin_fma(c2, rr, 1.0);
+  yy = __builtin_fma(zz, rr2, yy);
+  yy = yy * s;
+  return (float)yy;
+}
+
+TOPOS_HD float pow_f32(float x, float y) { return pow_f32_tables(x, y, TOPOS_LOG2_TABLE, TOPOS_EXP_TABLE); }
 
 // Rust's f32::max as compiled for x86-64 (llvm.maxnum): a NaN operand loses
 // to the other, and a tie between +0 and -0 answers the first operand.

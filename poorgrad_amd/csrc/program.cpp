@@ -238,7 +238,7 @@ float fold_scalar(int op, float a, float b) {
     case TOPOS_HIP_OP_EXP: return exp_f32(a);
     case TOPOS_HIP_OP_LN: return ln_f32(a);
     case TOPOS_HIP_OP_SQRT: return std::sqrt(a);
-    case TOPOS_HIP_OP_POWF: return powf(a, b);
+    case TOPOS_HIP_OP_POWF: return pow_f32(a, b);
     case TOPOS_HIP_OP_MAXIMUM: return max_f32(a, b);
     case TOPOS_HIP_OP_RELU: return max_f32(a, 0.0f);
     case TOPOS_HIP_OP_STEP: return step_f32(a, b);
@@ -274,6 +274,7 @@ int chain_op(int op) {
     case TOPOS_HIP_OP_SQRT: return TOPOS_HIP_CHAIN_SQRT;
     case TOPOS_HIP_OP_MAXIMUM: return TOPOS_HIP_CHAIN_MAX;
     case TOPOS_HIP_OP_STEP: return TOPOS_HIP_CHAIN_STEP;
+    case TOPOS_HIP_OP_POWF: return TOPOS_HIP_CHAIN_POWF;
   }
   throw Unsupported{std::string("no device kernel computes ") + op_name(op) + " of a non-constant operand"};
 }
@@ -665,7 +666,7 @@ struct topos_hip_program {
     if (!wanted[i] || group_of[i] >= 0 || alias_of[i] >= 0) return false;
     if (x.op == TOPOS_HIP_OP_SUM_ALONG && is_selection_node(x.operands[0])) return false;
     const int last = g.rank - 1;
-    if (is_elementwise(x.op)) return x.op != TOPOS_HIP_OP_POWF && (group_full(x, g) || group_row(x, g));
+    if (is_elementwise(x.op)) return group_full(x, g) || group_row(x, g);
     switch (x.op) {
       case TOPOS_HIP_OP_BROADCAST_ALONG: return x.params[0] == last && group_full(x, g);
       case TOPOS_HIP_OP_SUM_ALONG:
@@ -1619,8 +1620,6 @@ struct topos_hip_program {
       values[i] = host_constant(x, fold_scalar(x.op, a, b));
       return;
     }
-    if (x.op == TOPOS_HIP_OP_POWF)
-      throw Unsupported{"node " + std::to_string(i) + ": Powf is served for host-known constant operands only"};
     // +0 + v (or v + +0) of a value with no -0 element is v itself: the
     // addition only maps -0 to +0. Matrix-core products are never -0, nor are
     // views of them (the zero-seeded gradient accumulation behind every

@@ -122,6 +122,119 @@ void host_libm_range(int function, uint64_t begin, uint64_t count, uint32_t *out
   spread(function, begin, begin + count, threads, 2, out);
 }
 
+// splitmix64, for reproducible input streams.
+static uint64_t mix(uint64_t *state) {
+  uint64_t z = (*state += 0x9E3779B97F4A7C15ull);
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+// The (x, y) pair number `index` of input family `family` for powf:
+//   0: both operands uniform over all 2^32 bit patterns (specials, subnormals);
+//   1: x = 2^u with u uniform in [-150, 128), y uniform in [-40, 40];
+//   2: x negative with an integer or half-integer y in [-64, 64];
+//   3: x within 2^-10 of 1, |y| up to 2^20;
+//   4: y log2 x near the overflow and underflow edges (126, 128, -126, -149, -150);
+//   5: y an integer or a small dyadic in [-8, 8], x uniform in [2^-4, 2^4].
+void pow_pair(int family, uint64_t seed, uint64_t index, float *x, float *y) {
+  uint64_t state = seed * 0x100000001B3ull + index * 0x9E3779B97F4A7C15ull + (uint64_t)family;
+  const uint64_t a = mix(&state), b = mix(&state);
+  const double ua = (double)(a >> 11) / 9007199254740992.0, ub = (double)(b >> 11) / 9007199254740992.0;
+  switch (family) {
+    case 0:
+      *x = float_of((uint32_t)a);
+      *y = float_of((uint32_t)b);
+      return;
+    case 1:
+      *x = (float)exp2(-150.0 + 278.0 * ua);
+      *y = (float)(-40.0 + 80.0 * ub);
+      return;
+    case 2: {
+      *x = -(float)exp2(-20.0 + 40.0 * ua);
+      const int64_t n = (int64_t)(b % 257) - 128;
+      *y = (float)n * ((b >> 32) & 1 ? 0.5f : 1.0f);
+      return;
+    }
+    case 3:
+      *x = (float)(1.0 + (ua - 0.5) * 0x1p-9);
+      *y = (float)((ub - 0.5) * 0x1p21);
+      return;
+    case 4: {
+      static const double edges[5] = {126.0, 128.0, -126.0, -149.0, -150.0};
+      const double edge = edges[b % 5] + ((double)((b >> 8) % 2001) - 1000.0) * 1e-7;
+      float xf = (float)exp2(-8.0 + 16.0 * ua);
+      if (xf == 1.0f) xf = 2.0f;
+      *x = xf;
+      *y = (float)(edge / log2((double)xf));
+      return;
+    }
+    default:
+      *x = (float)exp2(-4.0 + 8.0 * ua);
+      *y = (float)((int64_t)(b % 1025) - 512) / 64.0f;
+      return;
+  }
+}
+
+struct PowWork {
+  int family;
+  uint64_t seed, begin, end;
+  int64_t mismatches;
+  float bad_x, bad_y;
+};
+
+void *run_pow(void *arg) {
+  PowWork *w = static_cast<PowWork *>(arg);
+  for (uint64_t i = w->begin; i < w->end; ++i) {
+    float x, y;
+    pow_pair(w->family, w->seed, i, &x, &y);
+    if (canonical(powf(x, y)) != canonical(pow_f32(x, y))) {
+      if (w->mismatches == 0) {
+        w->bad_x = x;
+        w->bad_y = y;
+      }
+      ++w->mismatches;
+    }
+  }
+  return nullptr;
+}
+
+// Counts pairs 0..count-1 of a family where the restated powf differs from
+// the host libm's (NaN as a class); the first differing pair goes to bad[0..2).
+int64_t pow_check(int family, uint64_t seed, uint64_t count, int threads, float *bad) {
+  if (threads < 1) threads = 1;
+  std::vector<PowWork> work(threads);
+  std::vector<pthread_t> ids(threads);
+  const uint64_t span = (count + threads - 1) / threads;
+  for (int t = 0; t < threads; ++t) {
+    const uint64_t b = span * t < count ? span * t : count;
+    const uint64_t e = b + span < count ? b + span : count;
+    work[t] = PowWork{family, seed, b, e, 0, 0.0f, 0.0f};
+    pthread_create(&ids[t], nullptr, run_pow, &work[t]);
+  }
+  int64_t total = 0;
+  bool seen = false;
+  for (int t = 0; t < threads; ++t) {
+    pthread_join(ids[t], nullptr);
+    if (work[t].mismatches && !seen) {
+      bad[0] = work[t].bad_x;
+      bad[1] = work[t].bad_y;
+      seen = true;
+    }
+    total += work[t].mismatches;
+  }
+  return total;
+}
+
+// Writes pairs 0..count-1 of a family and the host libm's powf of each (NaN
+// canonicalised), for comparison with the device build.
+void pow_pairs(int family, uint64_t seed, uint64_t count, float *x, float *y, uint32_t *host) {
+  for (uint64_t i = 0; i < count; ++i) {
+    pow_pair(family, seed, i, &x[i], &y[i]);
+    host[i] = canonical(powf(x[i], y[i]));
+  }
+}
+
 // Recomputes the exp table (bits(RN(2^(i/32))) - (i << 52)/32) and the log
 // table's logc = RN(-log(invc)) in extended precision; returns the number of
 // entries that disagree with faithful_math.h.
@@ -135,6 +248,10 @@ int faithful_tables_check(void) {
   for (int i = 0; i < 16; ++i) {
     const double logc = (double)logl(1.0L / (long double)kLogTableHost[i].invc);
     if (logc != kLogTableHost[i].logc) ++bad;
+    // powf's log2 table: the same 1/c, and RN(log2 c).
+    if (kLog2TableHost[i].invc != kLogTableHost[i].invc) ++bad;
+    const double log2c = (double)log2l(1.0L / (long double)kLog2TableHost[i].invc);
+    if (log2c != kLog2TableHost[i].logc) ++bad;
   }
   return bad;
 }

@@ -50,6 +50,35 @@ def test_map_every_f32_input_matches_host_libm(hip, host_libm, operation, name):
                                  f"inputs {[hex(start + int(i)) for i in bad]}")
 
 
+POW_FAMILIES = ["random bits", "positive bases", "negative bases", "bases near one", "overflow edges", "dyadic"]
+
+
+@pytest.mark.parametrize("family", range(len(POW_FAMILIES)), ids=POW_FAMILIES)
+def test_chain_powf_matches_host_libm_on_dense_samples(hip, host_libm, family):
+    """powf in a generated chain against the box host's glibc powf on 2^24
+    seeded pairs per input family (the families of the CPU check of the
+    restated source), NaN as a class."""
+    from poorgrad_amd import _native as n
+
+    banner(f"chain powf {POW_FAMILIES[family]}")
+    count = 1 << 24
+    host_libm.pow_pairs.argtypes = [ctypes.c_int, ctypes.c_uint64, ctypes.c_uint64, ctypes.POINTER(ctypes.c_float),
+                                    ctypes.POINTER(ctypes.c_float), ctypes.POINTER(ctypes.c_uint32)]
+    x = np.empty(count, np.float32)
+    y = np.empty(count, np.float32)
+    expected = np.empty(count, np.uint32)
+    host_libm.pow_pairs(family, 11, count, x.ctypes.data_as(ctypes.POINTER(ctypes.c_float)),
+                        y.ctypes.data_as(ctypes.POINTER(ctypes.c_float)),
+                        expected.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)))
+    chain = device.Chain((count,), [((1,), 0), ((1,), 0)], [(n.CHAIN_POWF, -1, -2)], [0])
+    got = chain(to_device(x), to_device(y))[0].cpu().numpy().view(np.uint32).copy()
+    got[np.isnan(got.view(np.float32))] = 0x7FC00000
+    if not np.array_equal(got, expected):
+        bad = np.flatnonzero(got != expected)
+        raise AssertionError(f"{len(bad)} pairs differ, e.g. powf({x[bad[0]]!r}, {y[bad[0]]!r}): "
+                             f"0x{got[bad[0]]:08x} vs host 0x{expected[bad[0]]:08x}")
+
+
 def compose(steps, inputs, outputs, shape):
     """The oracle's op-by-op evaluation of a chain over materialised views."""
     from poorgrad_amd import _native as n
@@ -57,7 +86,8 @@ def compose(steps, inputs, outputs, shape):
     unary = {n.CHAIN_NEG: oracle.NEG, n.CHAIN_EXP: oracle.EXP, n.CHAIN_LN: oracle.LN,
              n.CHAIN_SQRT: oracle.SQRT, n.CHAIN_TANH: oracle.TANH}
     binary = {n.CHAIN_ADD: oracle.ADD, n.CHAIN_SUB: oracle.SUB, n.CHAIN_MUL: oracle.MUL,
-              n.CHAIN_DIV: oracle.DIV, n.CHAIN_MAX: oracle.MAX, n.CHAIN_STEP: oracle.STEP}
+              n.CHAIN_DIV: oracle.DIV, n.CHAIN_MAX: oracle.MAX, n.CHAIN_STEP: oracle.STEP,
+              n.CHAIN_POWF: oracle.POWF}
     values = []
 
     def ref(r):

@@ -279,6 +279,31 @@ def test_adamw_steps_match_the_rule(hip):
             assert_bitwise(device[i], params[i], f"adamw step {step} param {i}")
 
 
+@pytest.mark.parametrize("posture", ["exact", "fast"])
+def test_powf_of_tensors_forward_and_backward(hip, posture):
+    """f32::powf of two recorded tensors (src/payload/elementary.rs:133-135)
+    and its rule (src/function/powf.rs:48-54: g * exponent * base^(exponent - 1)
+    and g * output * ln(base)), in a chain and inside a row program (a
+    softmax over powf values): bit-identical to the interpreter in both
+    postures (no product in the graph)."""
+    banner(f"program powf {posture}")
+    rng = np.random.default_rng(41)
+    tape = t.Tape()
+    base = tape.parameter((24, 40))
+    exponent = tape.parameter((24, 40))
+    powered = base.powf(exponent)
+    loss = (powered.log_softmax(1) * powered).sum()
+    (gb, ge) = tape.differentiate(loss, [base, exponent])
+    base0 = np.abs(rng.standard_normal((24, 40))).astype(np.float32) * np.float32(2) + np.float32(0.05)
+    exponent0 = rng.standard_normal((24, 40)).astype(np.float32) * np.float32(1.5)
+    params = [base0, exponent0]
+    want = run_oracle(tape, [loss, gb, ge], params)
+    got, program = run_device(tape, [loss, gb, ge], params, numerics=hip.EXACT if posture == "exact" else hip.FAST)
+    assert "Powf" in program.describe
+    for r in (loss, gb, ge):
+        assert_bitwise(got[r.id], want[r.id], f"powf node {r.id}")
+
+
 def test_device_adamw_follows_the_paper_trace(hip):
     """The reference's two-step Adam trace (src/neural/tests/adam_tests.rs:15-53:
     loss = w * w from w = 1, rate 0.1, betas 0.9 / 0.999, epsilon 1e-8, traced

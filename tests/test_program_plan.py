@@ -226,3 +226,19 @@ except n.HipError as e:
     print(e.code, "scalar" in str(e))
 ''')
     assert out.split() == ["5", "True"], out
+
+
+def test_powf_of_tensors_plans_into_a_chain_and_a_row_program():
+    """Powf of recorded tensors is a chain step (and a row-program step), its
+    generated code compiled for gfx950 through hipRTC with the restated powf."""
+    out = run(r'''
+tape = t.Tape()
+x = tape.input((16, 24))
+y = tape.input((16, 24))
+z = x.powf(y)
+p = DeviceProgram(tape, [(z + x).exp(), z.log_softmax(1)])
+d = p.describe
+print("Powf" in d, p.info["launches"])
+''')
+    ok, launches = out.split()
+    assert ok == "True" and int(launches) >= 1, out
