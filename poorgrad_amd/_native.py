@@ -6,10 +6,13 @@ this module without it raises ImportError: there is no fallback path.
 from __future__ import annotations
 
 import ctypes
+import os
 from ctypes import POINTER, c_char_p, c_float, c_int, c_int32, c_int64, c_size_t, c_uint, c_void_p
 from pathlib import Path
 
-LIBRARY_PATH = Path(__file__).resolve().parent / "libtopos_hip.so"
+# TOPOS_HIP_LIBRARY names another build of the same library (the sanitized
+# host build the CPU tests load under the fake runtime).
+LIBRARY_PATH = Path(os.environ.get("TOPOS_HIP_LIBRARY", Path(__file__).resolve().parent / "libtopos_hip.so"))
 
 if not LIBRARY_PATH.exists():
     raise ImportError(f"{LIBRARY_PATH} is not built; run `python -m poorgrad_amd.build` "

@@ -107,10 +107,17 @@ void enqueue_gemm(const float *a, int64_t a_rs, int64_t a_cs, const float *b, in
     context.tick("gemm launch");
     return;
   }
-  if (numerics == TOPOS_HIP_FAST) {
-    const int64_t floats = mfma_serves(a_rs, a_cs, b_rs, b_cs, m, k, n) ? mfma_split_floats(m, n, k, Batch()) : 0;
-    float *workspace = floats ? context.workspace(floats) : nullptr;
-    if (launch_gemm_mfma(a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, stream, Batch(), workspace, floats)) return;
+  if (numerics == TOPOS_HIP_FAST && mfma_serves(a_rs, a_cs, b_rs, b_cs, m, k, n)) {
+    const int64_t floats = mfma_split_floats(m, n, k, Batch());
+    if (floats == 0) {
+      if (launch_gemm_mfma(a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, stream)) return;
+    } else {
+      bool served = false;
+      context.with_workspace(floats, stream, [&](float *workspace) {
+        served = launch_gemm_mfma(a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, stream, Batch(), workspace, floats);
+      });
+      if (served) return;
+    }
   }
   launch_gemm_exact(a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, stream);
 }

@@ -44,6 +44,9 @@ struct Unsupported {
   std::string message;
 };
 
+// Throws RuntimeFailure on a HIP error, naming the call.
+void check(hipError_t status, const char *what);
+
 class Context {
  public:
   // The process-wide context, set up on first use (OnceLock semantics).
@@ -60,10 +63,20 @@ class Context {
   // RuntimeFailure when the countdown reaches the failing call.
   void tick(const char *what);
 
-  // A grow-only device buffer of at least `floats` floats for the device
-  // face's split products. Calls that use it are ordered on one stream;
-  // device-face calls on different streams must not overlap while using it.
-  float *workspace(int64_t floats);
+  // Runs `enqueue(workspace)` with a grow-only device buffer of at least
+  // `floats` floats for one device-face split product on `stream`. The
+  // buffer's users are serialised: the lock is held from the buffer's
+  // choice to the launch, each use is ordered on the GPU after the previous
+  // one (on any stream) by an event, and a regrow waits for the last use
+  // before freeing the old buffer.
+  template <class Enqueue>
+  void with_workspace(int64_t floats, hipStream_t stream, Enqueue enqueue) {
+    std::lock_guard<std::mutex> guard(workspace_lock_);
+    float *buffer = workspace_for(floats, stream);
+    enqueue(buffer);
+    if (runtime_.launches_kernels) check(hipEventRecord(workspace_used_, stream), "hipEventRecord(workspace)");
+    workspace_in_use_ = runtime_.launches_kernels;
+  }
 
   int device_count() const { return device_count_; }
   int architecture_major() const { return arch_major_; }
@@ -84,9 +97,12 @@ class Context {
   int device_count_ = 0;
   int arch_major_ = 0;
   std::mutex task_lock_;
+  float *workspace_for(int64_t floats, hipStream_t stream);
   std::mutex workspace_lock_;
   float *workspace_ = nullptr;
   int64_t workspace_floats_ = 0;
+  hipEvent_t workspace_used_ = nullptr;
+  bool workspace_in_use_ = false;
 };
 
 // Runs `body`, mapping the library's exceptions to status codes; a runtime
@@ -113,8 +129,6 @@ int guarded(Body body) {
 // on this thread (for diagnostics; status codes stay the contract).
 std::string &last_refusal();
 
-// Throws RuntimeFailure on a HIP error, naming the call.
-void check(hipError_t status, const char *what);
 // Checks the launch status of the kernel just enqueued.
 void check_launch(const char *what);
 

@@ -112,19 +112,23 @@ void Context::tick(const char *what) {
   if (left == 0) throw RuntimeFailure{std::string("fake runtime failure injected at ") + what};
 }
 
-float *Context::workspace(int64_t floats) {
-  std::lock_guard<std::mutex> guard(workspace_lock_);
-  if (floats <= workspace_floats_) return workspace_;
-  if (workspace_) {
-    check(hipDeviceSynchronize(), "hipDeviceSynchronize(workspace)");
-    runtime_.free(workspace_);
-    workspace_ = nullptr;
-    workspace_floats_ = 0;
+float *Context::workspace_for(int64_t floats, hipStream_t stream) {
+  if (runtime_.launches_kernels && !workspace_used_)
+    check(hipEventCreateWithFlags(&workspace_used_, hipEventDisableTiming), "hipEventCreate(workspace)");
+  if (floats > workspace_floats_) {
+    if (workspace_) {
+      if (workspace_in_use_) check(hipEventSynchronize(workspace_used_), "hipEventSynchronize(workspace)");
+      runtime_.free(workspace_);
+      workspace_ = nullptr;
+      workspace_floats_ = 0;
+      workspace_in_use_ = false;
+    }
+    void *p = nullptr;
+    check(runtime_.malloc(&p, (size_t)floats * sizeof(float)), "hipMalloc(workspace)");
+    workspace_ = static_cast<float *>(p);
+    workspace_floats_ = floats;
   }
-  void *p = nullptr;
-  check(runtime_.malloc(&p, (size_t)floats * sizeof(float)), "hipMalloc(workspace)");
-  workspace_ = static_cast<float *>(p);
-  workspace_floats_ = floats;
+  if (workspace_in_use_) check(hipStreamWaitEvent(stream, workspace_used_, 0), "hipStreamWaitEvent(workspace)");
   return workspace_;
 }
 

@@ -387,9 +387,31 @@ struct topos_hip_program {
   hipGraph_t graph = nullptr;
   hipGraphExec_t graph_exec = nullptr;
 
+  // One program, many host threads (a Plan is Send + Sync,
+  // src/engine/plan.rs:20): every entry point that enqueues, binds or reads
+  // holds `lock`, and each run first waits (on the GPU, not the host) for the
+  // previous run's completion, recorded in `run_done` on that run's stream,
+  // so runs on different streams never overlap on the one arena. A value a
+  // run leaves in the arena is valid until the next run of the program.
+  mutable std::mutex lock;
+  hipEvent_t run_done = nullptr;
+  hipStream_t last_stream = nullptr;
+  bool ran = false;
+
+  // Orders a run enqueued on `stream` after the previous run.
+  void serialize_before(hipStream_t stream) {
+    if (ran && stream != last_stream) check(hipStreamWaitEvent(stream, run_done, 0), "hipStreamWaitEvent(run)");
+  }
+  void record_after(hipStream_t stream) {
+    check(hipEventRecord(run_done, stream), "hipEventRecord(run done)");
+    last_stream = stream;
+    ran = true;
+  }
+
   ~topos_hip_program() {
     if (!device) return;
     drop_graph();
+    if (run_done) hipEventDestroy(run_done);
     if (capture_stream) hipStreamDestroy(capture_stream);
     for (auto &kv : signal_events) hipEventDestroy(kv.second);
     if (side_done) hipEventDestroy(side_done);
@@ -2368,6 +2390,7 @@ struct topos_hip_program {
       allocations.push_back(p);
       arena = (char *)p;
     }
+    if (!run_done) check(hipEventCreateWithFlags(&run_done, hipEventDisableTiming), "hipEventCreate(run done)");
     if (side_launches > 0 && !side_stream) {
       check(hipStreamCreateWithFlags(&side_stream, hipStreamNonBlocking), "hipStreamCreate(side)");
       check(hipEventCreateWithFlags(&side_done, hipEventDisableTiming), "hipEventCreate(side)");
@@ -2563,6 +2586,7 @@ int topos_hip_program_info(const topos_hip_program *program, uint64_t *arena_byt
 
 int topos_hip_program_bind(topos_hip_program *program, int is_input, int32_t slot, const float *device) {
   if (!program || !device || slot < 0) return TOPOS_HIP_INVALID_ARGUMENT;
+  std::lock_guard<std::mutex> guard(program->lock);
   auto &bound = (is_input ? program->inputs : program->parameters);
   auto old = bound.find(slot);
   if (old == bound.end() || old->second != device) program->drop_graph();
@@ -2583,6 +2607,7 @@ int topos_hip_program_bind_selection(topos_hip_program *program, int32_t slot, c
     if (indices[r] < 0 || indices[r] >= declared->vocab) return TOPOS_HIP_INVALID_ARGUMENT;
   if (!program->device) return TOPOS_HIP_OK;
   const int64_t vocab = declared->vocab;
+  std::lock_guard<std::mutex> guard(program->lock);
   program->drop_graph();
   return guarded([&] {
     auto old = program->selection_inputs.find(slot);
@@ -2601,21 +2626,42 @@ int topos_hip_program_run(topos_hip_program *program, void *stream) {
   if (!program) return TOPOS_HIP_INVALID_ARGUMENT;
   const int status = Context::get().status();
   if (status != TOPOS_HIP_OK) return status;
-  return guarded([&] { program->run(static_cast<hipStream_t>(stream)); });
+  std::lock_guard<std::mutex> guard(program->lock);
+  return guarded([&] {
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    program->prepare();
+    program->serialize_before(s);
+    program->run(s);
+    program->record_after(s);
+  });
 }
 
 int topos_hip_program_replay(topos_hip_program *program, void *stream) {
   if (!program) return TOPOS_HIP_INVALID_ARGUMENT;
   const int status = Context::get().status();
   if (status != TOPOS_HIP_OK) return status;
-  return guarded([&] { program->replay(static_cast<hipStream_t>(stream)); });
+  std::lock_guard<std::mutex> guard(program->lock);
+  return guarded([&] {
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    program->prepare();
+    program->serialize_before(s);
+    program->replay(s);
+    program->record_after(s);
+  });
 }
 
 int topos_hip_program_run_profiled(topos_hip_program *program, void *stream, float *milliseconds) {
   if (!program || !milliseconds) return TOPOS_HIP_INVALID_ARGUMENT;
   const int status = Context::get().status();
   if (status != TOPOS_HIP_OK) return status;
-  return guarded([&] { program->run(static_cast<hipStream_t>(stream), milliseconds); });
+  std::lock_guard<std::mutex> guard(program->lock);
+  return guarded([&] {
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    program->prepare();
+    program->serialize_before(s);
+    program->run(s, milliseconds);
+    program->record_after(s);
+  });
 }
 
 int topos_hip_program_launch(const topos_hip_program *program, int64_t launch, const char **kind, double *flops,
@@ -2628,7 +2674,8 @@ int topos_hip_program_launch(const topos_hip_program *program, int64_t launch, c
   return TOPOS_HIP_OK;
 }
 
-int topos_hip_program_output(const topos_hip_program *program, int64_t node, const float **device) {
+namespace {
+int program_output(const topos_hip_program *program, int64_t node, const float **device) {
   if (!program || !device) return TOPOS_HIP_INVALID_ARGUMENT;
   auto it = program->output_storage.find(node);
   if (it == program->output_storage.end()) return TOPOS_HIP_INVALID_ARGUMENT;
@@ -2639,12 +2686,20 @@ int topos_hip_program_output(const topos_hip_program *program, int64_t node, con
   });
   return code;
 }
+}  // namespace
+
+int topos_hip_program_output(const topos_hip_program *program, int64_t node, const float **device) {
+  if (!program) return TOPOS_HIP_INVALID_ARGUMENT;
+  std::lock_guard<std::mutex> guard(program->lock);
+  return program_output(program, node, device);
+}
 
 int topos_hip_program_read(const topos_hip_program *program, int64_t node, float *host, int64_t count) {
   if (!program || !host || node < 0 || node >= (int64_t)program->nodes.size()) return TOPOS_HIP_INVALID_ARGUMENT;
   if (count != topos_hip_program::volume_of(program->nodes[node])) return TOPOS_HIP_INVALID_ARGUMENT;
+  std::lock_guard<std::mutex> guard(program->lock);
   const float *device = nullptr;
-  const int code = topos_hip_program_output(program, node, &device);
+  const int code = program_output(program, node, &device);
   if (code != TOPOS_HIP_OK) return code;
   return guarded([&] {
     check(hipDeviceSynchronize(), "hipDeviceSynchronize(read)");
