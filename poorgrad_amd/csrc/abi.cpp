@@ -108,7 +108,7 @@ void enqueue_gemm(const float *a, int64_t a_rs, int64_t a_cs, const float *b, in
     return;
   }
   if (numerics == TOPOS_HIP_FAST && mfma_serves(a_rs, a_cs, b_rs, b_cs, m, k, n)) {
-    const int64_t floats = mfma_split_floats(m, n, k, Batch());
+    const int64_t floats = mfma_split_floats(m, n, k, Batch(), ldc);
     if (floats == 0) {
       if (launch_gemm_mfma(a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, stream)) return;
     } else {

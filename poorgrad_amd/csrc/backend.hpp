@@ -168,9 +168,10 @@ void launch_gemm_exact(const float *a, int64_t a_rs, int64_t a_cs, const float *
 // along k into that many partial products, reduced in a fixed order
 // (deterministic; envelope fidelity like the unsplit kernel).
 int mfma_splits(int64_t m, int64_t n, int64_t k, int64_t batches);
-// The workspace floats launch_gemm_mfma uses for this product: the split
-// partials, splits * count * m * n, or 0 when the product runs unsplit.
-int64_t mfma_split_floats(int64_t m, int64_t n, int64_t k, const Batch &batch);
+// The workspace floats launch_gemm_mfma uses for this product (output
+// leading dimension ldc): the split partials, splits * count * m * n, or 0
+// when the product runs unsplit.
+int64_t mfma_split_floats(int64_t m, int64_t n, int64_t k, const Batch &batch, int64_t ldc);
 // Whether launch_gemm_mfma takes operands with these strides (else the
 // caller's exact fallback runs). Its products are never -0: every
 // accumulator starts at +0, and a sum of +0 with any zero is +0.

@@ -685,6 +685,50 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float4 *__restr
   }
 }
 
+// split_reduce_kernel over a contiguous output in quads of the flat
+// [count][m][n] array (n need not be a multiple of four; the caller
+// guarantees count * m * n is): the same fixed-order sum of the partials,
+// then the bias of each element's own column.
+__global__ __launch_bounds__(256) void split_reduce_flat_kernel(const float4 *__restrict__ partials, int splits,
+                                                                uint32_t split_quads, uint32_t n,
+                                                                float *__restrict__ c, const float *__restrict__ bias,
+                                                                int64_t bias_cs, int bias_mode, bool aligned) {
+  constexpr int kMax = 16;
+  for (uint32_t e = blockIdx.x * blockDim.x + threadIdx.x; e < split_quads; e += gridDim.x * blockDim.x) {
+    float4 v[kMax];
+#pragma unroll
+    for (int s = 0; s < kMax; ++s)
+      if (s < splits) v[s] = partials[(size_t)s * split_quads + e];
+    float4 acc = v[0];
+#pragma unroll
+    for (int s = 1; s < kMax; ++s)
+      if (s < splits) {
+        acc.x = acc.x + v[s].x;
+        acc.y = acc.y + v[s].y;
+        acc.z = acc.z + v[s].z;
+        acc.w = acc.w + v[s].w;
+      }
+    float out[4] = {acc.x, acc.y, acc.z, acc.w};
+    if (bias_mode != 0) {
+      const uint64_t first = (uint64_t)e * 4;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float b = bias[(int64_t)((first + q) % n) * bias_cs];
+        out[q] = bias_mode == 1 ? out[q] + b : b + out[q];
+      }
+    }
+    float *dst = c + (size_t)e * 4;
+    if (aligned) {
+      *reinterpret_cast<float4 *>(dst) = make_float4(out[0], out[1], out[2], out[3]);
+    } else {
+      dst[0] = out[0];
+      dst[1] = out[1];
+      dst[2] = out[2];
+      dst[3] = out[3];
+    }
+  }
+}
+
 }  // namespace
 
 int mfma_splits(int64_t m, int64_t n, int64_t k, int64_t batches) {
@@ -696,19 +740,44 @@ int mfma_splits(int64_t m, int64_t n, int64_t k, int64_t batches) {
   const TileShape shape = tile_shape(m, n, batches);
   const int64_t tiles = ((m + shape.bm - 1) / shape.bm) * ((n + shape.bn - 1) / shape.bn) * batches;
   const int64_t full = 256 * shape.per_cu;
-  if (tiles >= full || k < 512) return 1;
+  if (tiles >= full) {
+    // Enough tiles to fill the chip, but the last round of workgroups may
+    // run mostly empty (1179 tiles over 512 slots run as three rounds, the
+    // last 30% full). Splitting k multiplies the workgroups and shortens
+    // each, so the rounds fill better; it pays when the slab rounds saved
+    // outweigh writing and re-reading the partials. Cost model, in rounds of
+    // one 16-deep slab on every slot: rounds x slabs, plus the partials'
+    // (splits + 1) passes over m x n at 6 TB/s. A split must save 10% and
+    // stay 512 deep.
+    const double slab_round_s = 2.0 * shape.bm * shape.bn * kTileK * full / (0.7 * 157.3e12);
+    const double partial_bytes = 4.0 * (double)batches * (double)m * (double)n;
+    auto cost = [&](int64_t s) {
+      const int64_t rounds = (tiles * s + full - 1) / full;
+      const int64_t slabs = ((k + s - 1) / s + kTileK - 1) / kTileK;
+      const double partials = s > 1 ? (double)(s + 1) * partial_bytes / 6e12 / slab_round_s : 0.0;
+      return (double)rounds * (double)slabs + partials;
+    };
+    int64_t best = 1;
+    for (int64_t s = 2; s <= 8 && k / s >= 512; ++s)
+      if (cost(s) < cost(best)) best = s;
+    return cost(best) < 0.9 * cost(1) ? (int)best : 1;
+  }
+  if (k < 512) return 1;
   int64_t splits = std::min<int64_t>((full + tiles - 1) / tiles, k / 256);
   while (splits * 2 * tiles <= 2048 && k / (splits * 2) >= 512) splits *= 2;
   splits = std::min<int64_t>(splits, 16);
   return (int)std::max<int64_t>(splits, 1);
 }
 
-int64_t mfma_split_floats(int64_t m, int64_t n, int64_t k, const Batch &batch) {
-  // The reduction walks one flat batch axis in quads of one row (n % 4 == 0)
-  // with 32-bit quad indices.
-  if (batch.inner != 1 || batch.count < 1 || n % 4 != 0) return 0;
-  const int splits = mfma_splits(m, n, k, batch.count);
+int64_t mfma_split_floats(int64_t m, int64_t n, int64_t k, const Batch &batch, int64_t ldc) {
+  // The reduction walks one flat batch axis with 32-bit quad indices, in
+  // quads of one row (n % 4 == 0), or in quads of the whole output when it
+  // is contiguous (ldc == n, batches back to back) and holds whole quads.
+  if (batch.inner != 1 || batch.count < 1) return 0;
   const int64_t split_stride = batch.count * m * n;
+  const bool flat = ldc == n && (batch.count == 1 || batch.c_stride == m * n) && split_stride % 4 == 0;
+  if (n % 4 != 0 && !flat) return 0;
+  const int splits = mfma_splits(m, n, k, batch.count);
   if (splits <= 1 || splits > 16 || split_stride / 4 >= (int64_t(1) << 31)) return 0;
   return splits * split_stride;
 }
@@ -739,7 +808,7 @@ bool launch_gemm_mfma(const float *a, int64_t a_rs, int64_t a_cs, const float *b
   if (gm * gn > 0x7fffffff || batch.count > 65535 || batch.count < 1) throw Unsupported{"mfma gemm: grid too large"};
   if (batch.inner < 1) throw Unsupported{"mfma gemm: batch inner extent below one"};
   const int64_t split_stride = batch.count * m * n;
-  const int64_t split_floats = mfma_split_floats(m, n, k, batch);
+  const int64_t split_floats = mfma_split_floats(m, n, k, batch, ldc);
   int splits = split_floats > 0 ? (int)(split_floats / split_stride) : 1;
   if (splits > 1 && (!workspace || workspace_floats < split_floats ||
                      reinterpret_cast<uintptr_t>(workspace) % 16 != 0))
@@ -789,10 +858,19 @@ bool launch_gemm_mfma(const float *a, int64_t a_rs, int64_t a_cs, const float *b
     const int64_t quads = split_stride / 4;
     int64_t blocks = (quads + 255) / 256;
     if (blocks > 256 * 32) blocks = 256 * 32;
-    const bool aligned = reinterpret_cast<uintptr_t>(c) % 16 == 0 && ldc % 4 == 0 && batch.c_stride % 4 == 0;
-    split_reduce_kernel<<<(unsigned)blocks, 256, 0, stream>>>(
-        reinterpret_cast<const float4 *>(workspace), splits, (uint32_t)quads, (uint32_t)m, (uint32_t)(n / 4), c, ldc,
-        batch.c_stride, epilogue.bias, epilogue.bias_stride, bias_mode, aligned);
+    if (n % 4 == 0) {
+      const bool aligned = reinterpret_cast<uintptr_t>(c) % 16 == 0 && ldc % 4 == 0 && batch.c_stride % 4 == 0;
+      split_reduce_kernel<<<(unsigned)blocks, 256, 0, stream>>>(
+          reinterpret_cast<const float4 *>(workspace), splits, (uint32_t)quads, (uint32_t)m, (uint32_t)(n / 4), c,
+          ldc, batch.c_stride, epilogue.bias, epilogue.bias_stride, bias_mode, aligned);
+    } else {
+      // A contiguous output whose rows are not whole quads (the 50257-wide
+      // products): quads of the flat output.
+      const bool aligned = reinterpret_cast<uintptr_t>(c) % 16 == 0;
+      split_reduce_flat_kernel<<<(unsigned)blocks, 256, 0, stream>>>(
+          reinterpret_cast<const float4 *>(workspace), splits, (uint32_t)quads, (uint32_t)n, c, epilogue.bias,
+          epilogue.bias_stride, bias_mode, aligned);
+    }
     check_launch("split_reduce_kernel launch");
   }
   return true;

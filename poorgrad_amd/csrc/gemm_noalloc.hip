@@ -53,7 +53,7 @@ void enqueue_gemm_noalloc(const float *a, int64_t a_rs, int64_t a_cs, const floa
   if (numerics == TOPOS_HIP_FAST && mfma_serves(a_rs, a_cs, b_rs, b_cs, m, k, n)) {
     // The same split choice as the allocating entry point, so both give the
     // same bits; a split whose partials exceed the scratch is refused.
-    const int64_t floats = mfma_split_floats(m, n, k, Batch());
+    const int64_t floats = mfma_split_floats(m, n, k, Batch(), ldc);
     if (floats > (int64_t)(kScratchBytes / sizeof(float)))
       throw InvalidArgument{"no-allocation product: its split-k partials need " + std::to_string(floats * 4) +
                             " bytes; the fixed scratch holds " + std::to_string(kScratchBytes) + " bytes"};

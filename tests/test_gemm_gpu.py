@@ -92,7 +92,7 @@ def test_negative_zero_seed_survives_on_device(hip):
 
 
 @pytest.mark.parametrize("m, k, n", [(1024, 1024, 4096), (512, 512, 512), (4096, 4096, 4096), (8192, 3072, 768),
-                                     (768, 8192, 768),
+                                     (768, 8192, 768), (768, 4096, 20001),
                                      (1025, 1027, 1029), (1000, 512, 1020), (300, 64, 260)])
 @pytest.mark.parametrize("product", ["forward", "a_transposed", "b_transposed"])
 def test_sweep_shapes_sampled_rows(hip, m, k, n, product):

@@ -6,6 +6,7 @@ interpreter bitwise), and within the stated envelope in the fast posture
 import math
 
 import numpy as np
+import oracle
 import pytest
 
 from poorgrad_amd import topos as t
@@ -277,6 +278,30 @@ def test_adamw_steps_match_the_rule(hip):
         torch.cuda.synchronize()
         for i in range(2):
             assert_bitwise(device[i], params[i], f"adamw step {step} param {i}")
+
+
+def test_split_product_with_odd_width_and_fused_bias(hip):
+    """A Linear layer whose product has enough tiles to fill the chip but
+    fills its last round poorly, so it splits along k, with a width of 20001
+    (rows that are not whole quads: the partials are reduced in quads of the
+    flat output) and the bias added by that reduction: within the envelope
+    |c - exact| <= 1e-5 * sum_k |x_ik w_kj| + 1 ulp for the bias addition."""
+    banner("program split product, odd width, fused bias")
+    tape = t.Tape()
+    x = tape.input((640, 1024))
+    w = tape.parameter((1024, 20001))
+    b = tape.parameter((20001,))
+    y = t.linear(x, w, b)
+    g = oracle.Generator(23)
+    xs = g.normal(640 * 1024, 1.0).reshape(640, 1024)
+    ws = g.normal(1024 * 20001, 1.0).reshape(1024, 20001)
+    bs = g.normal(20001, 1.0)
+    want = run_oracle(tape, [y], [ws, bs], {x.node.slot: xs})[y.id].astype(np.float64)
+    got, program = run_device(tape, [y], [ws, bs], {x.node.slot: xs}, numerics=hip.FAST)
+    assert "+bias" in program.describe
+    bound = 1e-5 * (np.abs(xs.astype(np.float64)) @ np.abs(ws.astype(np.float64)))
+    bound += np.spacing(np.abs(want).astype(np.float32)).astype(np.float64)
+    assert (np.abs(got[y.id].astype(np.float64) - want) <= bound).all()
 
 
 @pytest.mark.parametrize("posture", ["exact", "fast"])
