@@ -49,6 +49,7 @@ if str(ROOT) not in sys.path:
 
 METRIC = "GPT-2-small train steps/s; fp32 GEMM TFLOP/s + fused-op GB/s as % of peak"
 FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense fp32 matrix, published
+BF16_MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 matrix, published
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, published
 SWEEP = [(512, 512, 512), (1024, 4096, 1024), (4096, 4096, 4096), (8192, 768, 3072)]
 CHAIN_ROWS, CHAIN_COLUMNS = 16384, 4096
@@ -80,7 +81,7 @@ def parse() -> argparse.Namespace:
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU oracle leg")
     p.add_argument("--quick", action="store_true", help="the GPT-2 step only (no side sections)")
-    p.add_argument("--only", choices=["mlp", "gemm", "chains", "llama", "gpt2_exact"],
+    p.add_argument("--only", choices=["mlp", "gemm", "bf16", "chains", "llama", "gpt2_exact"],
                    help="run one side section alone and print its JSON (a diagnostic, not the bench line)")
     p.add_argument("--profile-out", help="write the profiled step's launches (one line each) to this file")
     p.add_argument("--calibration-copy-mib", type=int, default=0,
@@ -411,6 +412,39 @@ def gemm_section(torch, n, steps: int, warmup: int) -> dict:
     return result
 
 
+def bf16_section(torch, n, steps: int, warmup: int) -> dict:
+    """The sweep's products on bf16 operands (Bf16::gemm's contract: f32
+    accumulation, one rounding), fast posture on the bf16 matrix cores,
+    against MI355X's dense bf16 peak."""
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(7)
+    stream = torch.cuda.current_stream().cuda_stream
+    products = []
+    for (M, N, K) in SWEEP:
+        A = torch.randn(M, K, device="cuda", generator=gen).to(torch.bfloat16)
+        B = torch.randn(K, N, device="cuda", generator=gen).to(torch.bfloat16)
+        G = torch.randn(M, N, device="cuda", generator=gen).to(torch.bfloat16)
+        shape = f"{M}x{N}x{K}"
+        for label, a, ast, b, bst, m, k, n_ in (
+                (f"forward {shape}", A, (K, 1), B, (N, 1), M, K, N),
+                (f"a_t_g {shape}", A, (1, K), G, (N, 1), K, M, N),
+                (f"g_b_t {shape}", G, (N, 1), B, (1, N), M, N, K)):
+            out = torch.empty(m, n_, device="cuda", dtype=torch.bfloat16)
+            products.append((label, 2.0 * m * n_ * k, a, ast, b, bst, m, k, n_, out))
+    launches = []
+    for label, _, a, ast, b, bst, m, k, n_, out in products:
+        def fn(a=a, ast=ast, b=b, bst=bst, m=m, k=k, n_=n_, out=out):
+            n.checked(n.lib.topos_hip_gemm_bf16_device(a.data_ptr(), ast[0], ast[1], b.data_ptr(), bst[0], bst[1],
+                                                       m, k, n_, n.FAST, out.data_ptr(), n_, stream), "bf16 gemm")
+        launches.append((label, fn))
+    per = event_times(torch, launches, steps, 1)
+    total_flops = sum(p[1] for p in products)
+    total_s = sum(per.values())
+    return {"sweep_TFLOP/s": round(total_flops / total_s / 1e12, 2),
+            "frac_of_bf16_peak": round(total_flops / total_s / 1e12 / BF16_MFMA_PEAK_TFLOPS, 4),
+            "products": {p[0]: round(p[1] / per[p[0]] / 1e12, 2) for p in products}}
+
+
 def chains_section(torch, n, steps: int, warmup: int) -> dict:
     import ctypes
 
@@ -481,8 +515,8 @@ def main() -> int:
         torch.cuda.synchronize()
         del source
     if args.only:
-        sections = {"mlp": mlp_section, "gemm": gemm_section, "chains": chains_section, "llama": llama_section,
-                    "gpt2_exact": gpt2_exact_section}
+        sections = {"mlp": mlp_section, "gemm": gemm_section, "bf16": bf16_section, "chains": chains_section,
+                    "llama": llama_section, "gpt2_exact": gpt2_exact_section}
         print(json.dumps({args.only: sections[args.only](torch, n, args.steps, args.warmup)}), flush=True)
         return 0
     g = gpt2_section(torch, n, args)
@@ -525,6 +559,8 @@ def main() -> int:
         line["mlp"] = mlp_section(torch, n, args.steps, args.warmup)
         log("gemm sweep (configs[1])")
         line["gemm_sweep"] = gemm_section(torch, n, args.steps, args.warmup)
+        log("bf16 products (configs[1] shapes on bf16 operands)")
+        line["gemm_sweep_bf16"] = bf16_section(torch, n, args.steps, args.warmup)
         log("chains (configs[2])")
         line["chains"] = chains_section(torch, n, args.steps, args.warmup)
         log("llama forward + backward (configs[4])")

@@ -155,6 +155,20 @@ int topos_hip_gemm_f32_device_noalloc(const float *a, int64_t a_row_stride, int6
                                       int64_t m, int64_t k, int64_t n, int numerics, float *product,
                                       int64_t ldc, void *stream);
 
+/* A bf16 product, the matmul contract of the bf16 payload (Bf16::gemm,
+ * src/payload/bf16.rs:235-262): `a`, `b` and `product` hold bf16 bit patterns
+ * (the top half of an f32); the operands widen to f32 exactly, the f32
+ * product is taken, and every output rounds once to bf16, to nearest with
+ * ties to even (Bf16::from_f32, :38-46). TOPOS_HIP_EXACT: the f32 product is
+ * gemm::multiply's (bit-identical). TOPOS_HIP_FAST: bf16 matrix cores with
+ * f32 accumulation, within |c - exact| <= 1e-5 * sum_k |a_ik b_kj| before the
+ * rounding, when each operand has a unit stride along one axis (else the
+ * exact path). Strides are in elements; the product is row-major with
+ * leading dimension `ldc`. */
+int topos_hip_gemm_bf16_device(const uint16_t *a, int64_t a_row_stride, int64_t a_col_stride, const uint16_t *b,
+                               int64_t b_row_stride, int64_t b_col_stride, int64_t m, int64_t k, int64_t n,
+                               int numerics, uint16_t *product, int64_t ldc, void *stream);
+
 /* Elementwise unary map over `count` contiguous elements (MapOperation). */
 int topos_hip_map_f32_device(int operation, const float *x, int64_t count, float *y, void *stream);
 

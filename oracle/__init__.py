@@ -44,6 +44,9 @@ _PROTOTYPES = {
     "oracle_softmax_rows_f32": (None, [_F, c_int64, c_int64, _F]),
     "oracle_log_sum_exp_rows_f32": (None, [_F, c_int64, c_int64, _F]),
     "oracle_layer_norm_rows_f32": (None, [_F, c_int64, c_int64, _F, _F, c_float, _F]),
+    "oracle_bf16_from_f32": (ctypes.c_uint16, [c_float]),
+    "oracle_bf16_round": (None, [_F, c_size_t, POINTER(ctypes.c_uint16)]),
+    "oracle_bf16_widen": (None, [POINTER(ctypes.c_uint16), c_size_t, _F]),
 }
 for _name, (_res, _args) in _PROTOTYPES.items():
     _fn = getattr(lib, _name)
@@ -169,3 +172,27 @@ def layer_norm_rows(x: np.ndarray, scale: np.ndarray, shift: np.ndarray, epsilon
     out = np.empty_like(x)
     lib.oracle_layer_norm_rows_f32(_f(x), x.shape[0], x.shape[1], _f(scale), _f(shift), epsilon, _f(out))
     return out
+
+
+# ---- the bf16 payload (src/payload/bf16.rs) ----
+
+def bf16_round(x: np.ndarray) -> np.ndarray:
+    """Bf16::from_f32 elementwise: uint16 bit patterns."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, dtype=np.uint16)
+    lib.oracle_bf16_round(_f(x), x.size, out.ctypes.data_as(POINTER(ctypes.c_uint16)))
+    return out
+
+
+def bf16_widen(h: np.ndarray) -> np.ndarray:
+    """Bf16::to_f32 elementwise."""
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    out = np.empty(h.shape, dtype=np.float32)
+    lib.oracle_bf16_widen(h.ctypes.data_as(POINTER(ctypes.c_uint16)), h.size, _f(out))
+    return out
+
+
+def gemm_bf16(a: np.ndarray, a_strides, b: np.ndarray, b_strides, m: int, k: int, n: int) -> np.ndarray:
+    """Bf16::gemm (src/payload/bf16.rs:235-262): widen both operands, the f32
+    gemm::multiply, one rounding per output."""
+    return bf16_round(gemm(bf16_widen(a), a_strides, bf16_widen(b), b_strides, m, k, n))

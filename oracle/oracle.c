@@ -232,3 +232,24 @@ void oracle_layer_norm_rows_f32(const float *x, int64_t rows, int64_t columns, c
     }
   }
 }
+
+/* ---- src/payload/bf16.rs:38-53 ---- */
+
+uint16_t oracle_bf16_from_f32(float x) {
+  uint32_t bits;
+  memcpy(&bits, &x, sizeof bits);
+  if (x != x) return (uint16_t)((bits >> 16) | 0x0040u);
+  const uint32_t rounding_bias = 0x7FFFu + ((bits >> 16) & 1u);
+  return (uint16_t)((bits + rounding_bias) >> 16);
+}
+
+void oracle_bf16_round(const float *x, size_t count, uint16_t *out) {
+  for (size_t i = 0; i < count; ++i) out[i] = oracle_bf16_from_f32(x[i]);
+}
+
+void oracle_bf16_widen(const uint16_t *x, size_t count, float *out) {
+  for (size_t i = 0; i < count; ++i) {
+    const uint32_t bits = (uint32_t)x[i] << 16;
+    memcpy(&out[i], &bits, sizeof bits);
+  }
+}

@@ -81,6 +81,14 @@ void oracle_log_sum_exp_rows_f32(const float *x, int64_t rows, int64_t columns, 
 void oracle_layer_norm_rows_f32(const float *x, int64_t rows, int64_t columns, const float *scale,
                                 const float *shift, float epsilon, float *out);
 
+/* ---- the bf16 payload (src/payload/bf16.rs) ----
+ * Bf16::from_f32 (:38-46): round to nearest, ties to even, by adding the
+ * rounding bias to the bits; a NaN keeps its top half with bit 0x40 set. */
+uint16_t oracle_bf16_from_f32(float x);
+void oracle_bf16_round(const float *x, size_t count, uint16_t *out);
+/* Bf16::to_f32 (:50-53): the bits shifted into the top half of a single. */
+void oracle_bf16_widen(const uint16_t *x, size_t count, float *out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -92,6 +92,8 @@ PROTOTYPES = {
                                           c_int64, c_int64, c_int, c_void_p, c_int64, c_void_p]),
     "topos_hip_gemm_f32_device_noalloc": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_int64, c_int64,
                                                   c_int64, c_int64, c_int64, c_int, c_void_p, c_int64, c_void_p]),
+    "topos_hip_gemm_bf16_device": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_int64, c_int64, c_int64, c_int64,
+                                           c_int64, c_int, c_void_p, c_int64, c_void_p]),
     "topos_hip_map_f32_device": (c_int, [c_int, c_void_p, c_int64, c_void_p, c_void_p]),
     "topos_hip_rows_f32_device": (c_int, [c_int, c_void_p, c_int64, c_int64, c_int, c_void_p, c_void_p]),
     "topos_hip_layer_norm_f32_device": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_float,

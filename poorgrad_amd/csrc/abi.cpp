@@ -249,6 +249,44 @@ int topos_hip_gemm_f32_device(const float *a, int64_t a_row_stride, int64_t a_co
   });
 }
 
+int topos_hip_gemm_bf16_device(const uint16_t *a, int64_t a_row_stride, int64_t a_col_stride, const uint16_t *b,
+                               int64_t b_row_stride, int64_t b_col_stride, int64_t m, int64_t k, int64_t n,
+                               int numerics, uint16_t *product, int64_t ldc, void *stream) {
+  if (!a || !b || !product || m <= 0 || k <= 0 || n <= 0 || ldc < n) return TOPOS_HIP_INVALID_ARGUMENT;
+  if (a_row_stride < 0 || a_col_stride < 0 || b_row_stride < 0 || b_col_stride < 0)
+    return TOPOS_HIP_INVALID_ARGUMENT;
+  if (numerics != TOPOS_HIP_EXACT && numerics != TOPOS_HIP_FAST) return TOPOS_HIP_INVALID_ARGUMENT;
+  size_t a_span = 0, b_span = 0;
+  if (!span((size_t)m, (size_t)k, (size_t)a_row_stride, (size_t)a_col_stride, &a_span) ||
+      !span((size_t)k, (size_t)n, (size_t)b_row_stride, (size_t)b_col_stride, &b_span) ||
+      a_span > ((size_t)1 << 40) || b_span > ((size_t)1 << 40))
+    return TOPOS_HIP_INVALID_ARGUMENT;
+  const int status = ready_for_device_face();
+  if (status != TOPOS_HIP_OK) return status;
+  Context &context = Context::get();
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  return guarded([&] {
+    if (!context.runtime().launches_kernels) {
+      context.tick("bf16 gemm launch");
+      return;
+    }
+    if (numerics == TOPOS_HIP_FAST && bf16_mfma_serves(a_row_stride, a_col_stride, b_row_stride, b_col_stride)) {
+      launch_gemm_bf16_mfma(a, a_row_stride, a_col_stride, b, b_row_stride, b_col_stride, m, k, n, product, ldc, s);
+      return;
+    }
+    // The exact contract step by step: widen both spans, the bit-identical
+    // f32 product, one rounding per output.
+    const int64_t a_floats = ((int64_t)a_span + 63) / 64 * 64, b_floats = ((int64_t)b_span + 63) / 64 * 64;
+    context.with_workspace(a_floats + b_floats + m * n, s, [&](float *w) {
+      launch_widen_bf16(a, (int64_t)a_span, w, s);
+      launch_widen_bf16(b, (int64_t)b_span, w + a_floats, s);
+      float *wc = w + a_floats + b_floats;
+      launch_gemm_exact(w, a_row_stride, a_col_stride, w + a_floats, b_row_stride, b_col_stride, m, k, n, wc, n, s);
+      launch_narrow_bf16(wc, m, n, product, ldc, s);
+    });
+  });
+}
+
 int topos_hip_map_f32_device(int operation, const float *x, int64_t count, float *y, void *stream) {
   if (operation < TOPOS_HIP_MAP_EXP || operation > TOPOS_HIP_MAP_TANH || count < 0) return TOPOS_HIP_INVALID_ARGUMENT;
   if (count > 0 && (!x || !y)) return TOPOS_HIP_INVALID_ARGUMENT;

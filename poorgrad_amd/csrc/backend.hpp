@@ -187,6 +187,14 @@ bool launch_gemm_mfma(const float *a, int64_t a_rs, int64_t a_cs, const float *b
 void append_engine_backward(std::vector<topos_hip_node> &nodes, std::vector<topos_hip_leaf> &leaves, int64_t target,
                             const std::vector<int64_t> &wrt, std::map<int64_t, int64_t> &gradient_of);
 
+// gemm_bf16.hip: bf16 products (operands and product as bf16 bit patterns).
+bool bf16_mfma_serves(int64_t a_rs, int64_t a_cs, int64_t b_rs, int64_t b_cs);
+void launch_gemm_bf16_mfma(const uint16_t *a, int64_t a_rs, int64_t a_cs, const uint16_t *b, int64_t b_rs,
+                           int64_t b_cs, int64_t m, int64_t k, int64_t n, uint16_t *c, int64_t ldc,
+                           hipStream_t stream);
+void launch_widen_bf16(const uint16_t *in, int64_t count, float *out, hipStream_t stream);
+void launch_narrow_bf16(const float *in, int64_t m, int64_t n, uint16_t *out, int64_t ldc, hipStream_t stream);
+
 // index.hip
 void launch_gather(const float *table, int64_t row_stride, int64_t column_stride, const int32_t *indices,
                    int64_t rows, int64_t row_size, float *out, hipStream_t stream);

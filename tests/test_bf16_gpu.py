@@ -1,0 +1,79 @@
+"""bf16 products on the device (topos_hip_gemm_bf16_device) against the
+oracle's Bf16::gemm (src/payload/bf16.rs:235-262: widen, f32 product, one
+rounding): bit-identical under Exact; under Fast (bf16 matrix cores, f32
+accumulation) within |c - exact| <= 1e-5 * sum_k |a_ik b_kj| before the
+rounding, so within that plus one bf16 spacing of the rounded exact
+result. Shapes and stride forms as the f32 grid (forward, both transposed
+operands, a narrowed window, and rows not 16-byte aligned)."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from tests.conftest import banner
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [(2, 3, 4), (5, 8, 13), (16, 16, 16), (63, 64, 65), (100, 127, 3), (129, 257, 131), (256, 384, 512),
+          (1024, 1024, 1024), (777, 1000, 515)]
+FORMS = ["contiguous", "a_transposed", "b_transposed", "narrowed"]
+
+
+def _operands(m, k, n, form, seed):
+    g = oracle.Generator(seed)
+    a = oracle.bf16_round(g.normal(m * k, 1.0).reshape(m, k))
+    b = oracle.bf16_round(g.normal(k * n, 1.0).reshape(k, n))
+    a_buf, a_st, a_off = a.ravel(), (k, 1), 0
+    b_buf, b_st = b.ravel(), (n, 1)
+    if form == "a_transposed":
+        a_buf, a_st = np.ascontiguousarray(a.T).ravel(), (1, m)
+    if form == "b_transposed":
+        b_buf, b_st = np.ascontiguousarray(b.T).ravel(), (1, k)
+    if form == "narrowed":
+        wide = np.zeros((m, k + 3), np.uint16)
+        wide[:, 1:1 + k] = a
+        a_buf, a_st, a_off = wide.ravel(), (k + 3, 1), 1
+    return a, b, (a_buf, a_st, a_off), (b_buf, b_st)
+
+
+def _device(a_view, b_view, m, k, n, numerics):
+    from poorgrad_amd import _native as nat
+
+    (a_buf, a_st, a_off), (b_buf, b_st) = a_view, b_view
+    da = torch.from_numpy(a_buf.view(np.int16).copy()).cuda()
+    db = torch.from_numpy(b_buf.view(np.int16).copy()).cuda()
+    out = torch.zeros((m, n), dtype=torch.int16, device="cuda")
+    nat.checked(nat.lib.topos_hip_gemm_bf16_device(da.data_ptr() + 2 * a_off, a_st[0], a_st[1], db.data_ptr(), b_st[0],
+                                                   b_st[1], m, k, n, numerics, out.data_ptr(), n,
+                                                   torch.cuda.current_stream().cuda_stream), "bf16 gemm")
+    torch.cuda.synchronize()
+    return out.cpu().numpy().view(np.uint16)
+
+
+@pytest.mark.parametrize("form", FORMS)
+@pytest.mark.parametrize("m, k, n", SHAPES)
+def test_bf16_gemm_exact_and_fast(hip, m, k, n, form):
+    banner(f"bf16 gemm {m}x{k}x{n} {form}")
+    a, b, a_view, b_view = _operands(m, k, n, form, seed=m + 3 * k + 7 * n)
+    want = oracle.gemm_bf16(a, (k, 1), b, (n, 1), m, k, n)
+    exact = _device(a_view, b_view, m, k, n, hip.EXACT)
+    assert np.array_equal(exact, want), f"exact: {int((exact != want).sum())} differ"
+    fast = _device(a_view, b_view, m, k, n, hip.FAST)
+    wa, wb = oracle.bf16_widen(a).astype(np.float64), oracle.bf16_widen(b).astype(np.float64)
+    bound = 1e-5 * (np.abs(wa) @ np.abs(wb))
+    w = oracle.bf16_widen(want).astype(np.float64)
+    spacing = np.abs(w) * 2.0**-7 + 1e-38  # one bf16 step at the exact result
+    assert (np.abs(oracle.bf16_widen(fast).astype(np.float64) - w) <= bound + spacing).all()
+    again = _device(a_view, b_view, m, k, n, hip.FAST)
+    assert np.array_equal(again, fast), "fast bf16 products repeat bit for bit"
+
+
+def test_bf16_product_accumulates_in_f32(hip):
+    """src/payload/tests/bf16_tests.rs:117-127 on the device, both postures:
+    [256, 1, 1] . [1, 1, 1] = 258, per-op bf16 accumulation would say 256."""
+    banner("bf16 gemm 258")
+    a = oracle.bf16_round(np.array([[256.0, 1.0, 1.0]] * 2, np.float32))
+    b = oracle.bf16_round(np.array([[1.0, 1.0], [1.0, 1.0], [1.0, 1.0]], np.float32))
+    for numerics in (hip.EXACT, hip.FAST):
+        got = _device((a.ravel(), (3, 1), 0), (b.ravel(), (2, 1)), 2, 3, 2, numerics)
+        assert (oracle.bf16_widen(got) == 258.0).all(), got

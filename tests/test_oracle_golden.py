@@ -165,3 +165,36 @@ def test_layer_norm_closed_form():
     assert np.allclose(out, expected, atol=1e-6)
     shifted = oracle.layer_norm_rows(x, np.full(4, 2.0, np.float32), np.full(4, 1.0, np.float32), 0.0)
     assert np.allclose(shifted, 2.0 * expected + 1.0, atol=1e-6)
+
+
+def test_bf16_rounding_golden_cases():
+    """Bf16::from_f32 against the reference's own cases
+    (src/payload/tests/bf16_tests.rs:6-52): ties to even, the carry into the
+    extremes, signed zeros, NaN kept a NaN, and every bit pattern
+    round-tripping through f32."""
+    f = np.float32
+
+    def h(x):
+        return int(oracle.lib.oracle_bf16_from_f32(f(x)))
+
+    assert h(1.003_906_25) == h(1.0) == 0x3F80            # 1 + 2^-8 ties to the even 1.0
+    assert h(1.011_718_75) == h(1.015_625) == 0x3F82      # 1 + 3 * 2^-8 ties to the even neighbour
+    assert h(1.006) == h(1.007_812_5) == 0x3F81           # off a tie: the nearest
+    assert h(np.finfo(np.float32).max) == 0x7F80          # carries into infinity
+    assert h(-np.finfo(np.float32).max) == 0xFF80
+    assert h(-0.0) == 0x8000 and h(0.0) == 0x0000
+    assert np.isnan(oracle.bf16_widen(np.array([h(np.nan)], np.uint16))[0])
+    every = np.arange(1 << 16, dtype=np.uint16)
+    back = oracle.bf16_round(oracle.bf16_widen(every))
+    nan = np.isnan(oracle.bf16_widen(every))
+    assert np.array_equal(back[~nan], every[~nan])
+    assert np.isnan(oracle.bf16_widen(back[nan])).all()
+
+
+def test_bf16_matmul_accumulates_in_f32_and_rounds_once():
+    """src/payload/tests/bf16_tests.rs:117-127: [256, 1, 1] . [1, 1, 1] is 258
+    (per-op bf16 accumulation would answer 256)."""
+    left = oracle.bf16_round(np.array([[256.0, 1.0, 1.0]], np.float32))
+    right = oracle.bf16_round(np.array([[1.0], [1.0], [1.0]], np.float32))
+    product = oracle.gemm_bf16(left, (3, 1), right, (1, 1), 1, 3, 1)
+    assert oracle.bf16_widen(product)[0, 0] == 258.0
