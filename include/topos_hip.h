@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define TOPOS_HIP_ABI_VERSION 1
+#define TOPOS_HIP_ABI_VERSION 2
 
 /* ---- status codes ---- */
 enum {
@@ -215,7 +215,7 @@ enum {
   TOPOS_HIP_CHAIN_STEP = 21, /* x >= y ? 1 : 0 */
   TOPOS_HIP_CHAIN_POWF = 22  /* f32::powf: the host libm's powf */
 };
-#define TOPOS_HIP_MAX_RANK 4
+#define TOPOS_HIP_MAX_RANK 6
 /* A strided view of `rank` axes (the Layout of src/payload/layout.rs:23-31):
  * element (i0..) lives at offset + sum i_d * strides[d], in elements. */
 typedef struct {
@@ -295,8 +295,8 @@ enum {
   TOPOS_HIP_OP_PERMUTE = 18,       /* order = params[0..rank) */
   TOPOS_HIP_OP_NARROW = 19,        /* axis, start, len = params[0..3) */
   TOPOS_HIP_OP_PAD = 20,           /* axis, start, full_extent = params[0..3) */
-  TOPOS_HIP_OP_UNFOLD = 21,        /* not served: the program is refused */
-  TOPOS_HIP_OP_FOLD = 22,          /* not served: the program is refused */
+  TOPOS_HIP_OP_UNFOLD = 21,        /* axis, size, step, dilation = params[0..4): a strided view */
+  TOPOS_HIP_OP_FOLD = 22,          /* axis, size, step, dilation, extent = params[0..5) */
   TOPOS_HIP_OP_GATHER = 23,        /* [table, selection] */
   TOPOS_HIP_OP_SCATTER = 24,       /* [gradient, selection], rows = params[0] */
   TOPOS_HIP_OP_LOG_SOFTMAX = 25,   /* axis = params[0] */

@@ -15,7 +15,7 @@ import numpy as np
 
 _PATH = Path(__file__).resolve().parent / "liboracle.so"
 if not _PATH.exists():
-    raise ImportError(f"{_PATH} is not built; run `python -m poorgrad_amd.build`")
+    raise ImportError(f"{_PATH} is not built; run `python poorgrad_amd/build.py`")
 lib = ctypes.CDLL(str(_PATH))
 
 _F = POINTER(c_float)

@@ -76,6 +76,38 @@ def _scatter(g: np.ndarray, selection: Sel, rows: int) -> np.ndarray:
     return acc
 
 
+def _unfold(x: np.ndarray, axis: int, size: int, step: int, dilation: int) -> np.ndarray:
+    """Tensor::unfold, the strided window view of Layout::unfold
+    (src/payload/layout.rs:299-331): (count, size) at `axis`, window starts
+    `step` apart, window elements `dilation` apart."""
+    x = _dense(x)
+    count = (x.shape[axis] - dilation * (size - 1) - 1) // step + 1
+    shape = x.shape[:axis] + (count, size) + x.shape[axis + 1:]
+    # An extent-1 axis never advances, so its stride is 0 (layout.rs:311-329):
+    # a single window takes any step.
+    along = x.strides[axis]
+    strides = x.strides[:axis] + (0 if count == 1 else along * step, 0 if size == 1 else along * dilation) \
+        + x.strides[axis + 1:]
+    return np.lib.stride_tricks.as_strided(x, shape, strides, writeable=False)
+
+
+def _fold(x: np.ndarray, axis: int, size: int, step: int, dilation: int, extent: int) -> np.ndarray:
+    """Tensor::fold (src/payload/tensor.rs:1392-1462): each position sums, from
+    +0 and in ascending window-element order k, the terms of the windows w
+    with w * step + k * dilation == position."""
+    x = _dense(x)
+    count = x.shape[axis]
+    out = np.zeros(x.shape[:axis] + (extent,) + x.shape[axis + 2:], dtype=np.float32)
+    positions = np.arange(extent)
+    lead = (slice(None),) * axis
+    for k in range(size):
+        rest = positions - k * dilation
+        valid = (rest >= 0) & (rest % step == 0) & (rest // step < count)
+        target, window = positions[valid], rest[valid] // step
+        out[lead + (target,)] = out[lead + (target,)] + x[lead + (window, k)]
+    return out
+
+
 def forward(node: t.Node, operands: list, parameters: list, inputs: list):
     """Function::forward of one node."""
     op = node.op
@@ -137,6 +169,10 @@ def forward(node: t.Node, operands: list, parameters: list, inputs: list):
         index[axis] = slice(start, start + x.shape[axis])
         out[tuple(index)] = x
         return out
+    if op == t.UNFOLD:
+        return _unfold(a, *node.params[:4])
+    if op == t.FOLD:
+        return _fold(a, *node.params[:5])
     if op == t.GATHER:
         return _dense(a)[b.indices]
     if op == t.SCATTER:

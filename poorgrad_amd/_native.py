@@ -1,6 +1,6 @@
 """ctypes binding of libtopos_hip.so (include/topos_hip.h).
 
-The library is built in-tree by ``python -m poorgrad_amd.build``. Importing
+The library is built in-tree by ``python poorgrad_amd/build.py``. Importing
 this module without it raises ImportError: there is no fallback path.
 """
 from __future__ import annotations
@@ -15,7 +15,7 @@ from pathlib import Path
 LIBRARY_PATH = Path(os.environ.get("TOPOS_HIP_LIBRARY", Path(__file__).resolve().parent / "libtopos_hip.so"))
 
 if not LIBRARY_PATH.exists():
-    raise ImportError(f"{LIBRARY_PATH} is not built; run `python -m poorgrad_amd.build` "
+    raise ImportError(f"{LIBRARY_PATH} is not built; run `python poorgrad_amd/build.py` "
                       "(the HIP backend has no CPU fallback)")
 
 # One HIP runtime per process. torch carries its own libamdhip64.so.7; the
@@ -41,7 +41,7 @@ MAP_EXP, MAP_LN, MAP_SQRT, MAP_TANH = 0, 1, 2, 3
 ROWS_SUM, ROWS_MAX, ROWS_LOG_SOFTMAX, ROWS_SOFTMAX, ROWS_LOG_SUM_EXP = 0, 1, 2, 3, 4
 CHAIN_NEG, CHAIN_EXP, CHAIN_LN, CHAIN_SQRT, CHAIN_TANH = 0, 1, 2, 3, 4
 CHAIN_ADD, CHAIN_SUB, CHAIN_MUL, CHAIN_DIV, CHAIN_MAX, CHAIN_STEP, CHAIN_POWF = 16, 17, 18, 19, 20, 21, 22
-MAX_RANK = 4
+MAX_RANK = 6
 
 FLOAT_P = POINTER(c_float)
 
@@ -131,6 +131,12 @@ for _name, (_restype, _argtypes) in PROTOTYPES.items():
     _function = getattr(lib, _name)
     _function.restype = _restype
     _function.argtypes = _argtypes
+
+# The structures above follow include/topos_hip.h at this version.
+ABI_VERSION = 2
+if lib.topos_hip_abi_version() != ABI_VERSION:
+    raise ImportError(f"{LIBRARY_PATH} has ABI version {lib.topos_hip_abi_version()}, this binding "
+                      f"{ABI_VERSION}; rebuild with `python poorgrad_amd/build.py`")
 
 
 class HipError(RuntimeError):

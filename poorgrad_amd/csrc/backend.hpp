@@ -195,6 +195,21 @@ void launch_gemm_bf16_mfma(const uint16_t *a, int64_t a_rs, int64_t a_cs, const 
 void launch_widen_bf16(const uint16_t *in, int64_t count, float *out, hipStream_t stream);
 void launch_narrow_bf16(const float *in, int64_t m, int64_t n, uint16_t *out, int64_t ldc, hipStream_t stream);
 
+// window.hip: Fold (src/payload/tensor.rs:1392-1462). The operand is read
+// through its layout: output element (outer, position, inner) sums, from +0
+// in ascending k, source[outer + window * window_stride + k * element_stride
+// + inner] over the windows covering the position. The output is contiguous
+// [outer..., extent, inner...].
+struct FoldGeometry {
+  int outer_rank = 0, inner_rank = 0;
+  int64_t outer_shape[TOPOS_HIP_MAX_RANK] = {}, outer_strides[TOPOS_HIP_MAX_RANK] = {};
+  int64_t inner_shape[TOPOS_HIP_MAX_RANK] = {}, inner_strides[TOPOS_HIP_MAX_RANK] = {};
+  int64_t window_stride = 0, element_stride = 0;
+  int64_t count = 1, size = 1, step = 1, dilation = 1, extent = 1;
+  int64_t inner_volume = 1, total = 0;
+};
+void launch_fold(const float *source, const FoldGeometry &geometry, float *out, hipStream_t stream);
+
 // index.hip
 void launch_gather(const float *table, int64_t row_stride, int64_t column_stride, const int32_t *indices,
                    int64_t rows, int64_t row_size, float *out, hipStream_t stream);

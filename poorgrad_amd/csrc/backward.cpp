@@ -33,7 +33,7 @@ namespace {
 
 struct Shape {
   int rank = 0;
-  int64_t axes[TOPOS_HIP_MAX_RANK] = {0, 0, 0, 0};
+  int64_t axes[TOPOS_HIP_MAX_RANK] = {};
   int64_t volume() const {
     int64_t v = 1;
     for (int d = 0; d < rank; ++d) v *= axes[d];
@@ -143,6 +143,25 @@ class Recorder {
     Shape out = shape(x);
     out.axes[axis] = full;
     return record(TOPOS_HIP_OP_PAD, x, -1, out, {axis, start, full});
+  }
+  int64_t unfold(int64_t x, int64_t axis, int64_t size, int64_t step, int64_t dilation) {
+    const Shape s = shape(x);
+    Shape out;
+    out.rank = s.rank + 1;
+    for (int d = 0; d < out.rank; ++d)
+      out.axes[d] = d < axis ? s.axes[d]
+                    : d == axis ? (s.axes[axis] - dilation * (size - 1) - 1) / step + 1
+                    : d == axis + 1 ? size
+                                    : s.axes[d - 1];
+    if (out.rank > TOPOS_HIP_MAX_RANK) throw InvalidArgument{"backward: unfold beyond the library's axes"};
+    return record(TOPOS_HIP_OP_UNFOLD, x, -1, out, {axis, size, step, dilation});
+  }
+  int64_t fold(int64_t x, int64_t axis, int64_t size, int64_t step, int64_t dilation, int64_t extent) {
+    const Shape s = shape(x);
+    Shape out;
+    out.rank = s.rank - 1;
+    for (int d = 0; d < out.rank; ++d) out.axes[d] = d < axis ? s.axes[d] : d == axis ? extent : s.axes[d + 1];
+    return record(TOPOS_HIP_OP_FOLD, x, -1, out, {axis, size, step, dilation, extent});
   }
   int64_t gather(int64_t table, int64_t selection) {
     Shape out = shape(table);
@@ -280,9 +299,11 @@ std::vector<Cotangent> rule(Recorder &r, int64_t index, int64_t g) {
       const int64_t probabilities = r.unary(TOPOS_HIP_OP_EXP, r.sub(a, r.broadcast_along(index, axis, a)));
       return {r.mul(r.broadcast_along(g, axis, a), probabilities)};
     }
-    case TOPOS_HIP_OP_UNFOLD:
-    case TOPOS_HIP_OP_FOLD:
-      throw Unsupported{"backward: Unfold/Fold programs are not served"};
+    case TOPOS_HIP_OP_UNFOLD:  // unfold.rs:77-87: the fold onto the operand's extent
+      return {r.fold(g, node.params[0], node.params[1], node.params[2], node.params[3],
+                     r.shape(a).axes[node.params[0]])};
+    case TOPOS_HIP_OP_FOLD:  // fold.rs:91-98: the unfold by the same parameters
+      return {r.unfold(g, node.params[0], node.params[1], node.params[2], node.params[3])};
   }
   throw InvalidArgument{"backward: unknown node kind " + std::to_string(node.op)};
 }

@@ -24,6 +24,7 @@
 namespace topos_hip {
 
 constexpr int kMaxRank = TOPOS_HIP_MAX_RANK;
+static_assert(kMaxRank == 6, "the shape initialisers below list six axes");
 
 struct ExprInput {
   // kLiteral: the constant `one` everywhere, embedded in the source (its
@@ -34,7 +35,7 @@ struct ExprInput {
   // (kPadded: with the pad axis coordinate shifted by -pad_start, and +0
   // outside the window).
   int64_t offset = 0;
-  int64_t strides[kMaxRank] = {0, 0, 0, 0};
+  int64_t strides[kMaxRank] = {};
   // kSelection: the expression is [rows, vocab]; the element is `one` where
   // indices[c0] == c1, else +0.
   float one = 1.0f;
@@ -53,7 +54,7 @@ struct ExprStep {
 
 struct Expr {
   int rank = 0;
-  int64_t shape[kMaxRank] = {1, 1, 1, 1};
+  int64_t shape[kMaxRank] = {1, 1, 1, 1, 1, 1};
   std::vector<ExprInput> inputs;
   std::vector<ExprStep> steps;
   std::vector<int> outputs;  // references; a fold reads outputs[0]
@@ -122,7 +123,7 @@ struct RowNode {
 
 struct RowProgram {
   int rank = 0;
-  int64_t shape[kMaxRank] = {1, 1, 1, 1};
+  int64_t shape[kMaxRank] = {1, 1, 1, 1, 1, 1};
   std::vector<ExprInput> inputs;   // layouts over the full shape (row inputs: stride 0 on the last axis)
   std::vector<RowNode> nodes;      // in evaluation order
   std::vector<int> full_outputs;   // full nodes written [rows, columns]

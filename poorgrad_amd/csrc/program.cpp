@@ -51,8 +51,8 @@ namespace {
 
 struct Layout {
   int rank = 0;
-  int64_t shape[kMaxRank] = {1, 1, 1, 1};
-  int64_t strides[kMaxRank] = {0, 0, 0, 0};
+  int64_t shape[kMaxRank] = {1, 1, 1, 1, 1, 1};
+  int64_t strides[kMaxRank] = {};
   int64_t offset = 0;
   int64_t volume() const {
     int64_t v = 1;
@@ -454,7 +454,7 @@ struct topos_hip_program {
     for (int64_t i = 0; i < n; ++i) {
       const topos_hip_node &x = nodes[i];
       if (x.op < 0 || x.op > TOPOS_HIP_OP_STEP) refuse(i, "unknown operation");
-      if (x.rank < 0 || x.rank > kMaxRank) refuse(i, "rank beyond the library's four axes");
+      if (x.rank < 0 || x.rank > kMaxRank) refuse(i, "rank beyond the library's six axes");
       for (int d = 0; d < x.rank; ++d)
         if (x.shape[d] <= 0) refuse(i, "empty axis");
       const int k = arity(x.op);
@@ -541,7 +541,7 @@ struct topos_hip_program {
           break;
         case TOPOS_HIP_OP_PERMUTE: {
           expect(x.rank == a->rank, "permute rank");
-          bool seen[kMaxRank] = {false, false, false, false};
+          bool seen[kMaxRank] = {};
           for (int d = 0; d < x.rank; ++d) {
             const int64_t o = x.params[d];
             expect(o >= 0 && o < a->rank && !seen[o], "permute order");
@@ -577,9 +577,33 @@ struct topos_hip_program {
                  "scatter shapes");
           for (int d = 1; d < x.rank; ++d) expect(x.shape[d] == a->shape[d], "scattered rows");
           break;
-        case TOPOS_HIP_OP_UNFOLD:
-        case TOPOS_HIP_OP_FOLD:
-          break;  // refused when reached (only if wanted)
+        case TOPOS_HIP_OP_UNFOLD: {  // Unfold::infer_shape (src/function/unfold.rs:40-70)
+          const int64_t axis = x.params[0], size = x.params[1], step = x.params[2], dilation = x.params[3];
+          expect(axis >= 0 && axis < a->rank && x.rank == a->rank + 1 && size > 0 && step > 0 && dilation > 0,
+                 "unfold parameters");
+          int64_t span = 0;
+          expect(!__builtin_mul_overflow(dilation, size - 1, &span) && span < a->shape[axis], "unfold window span");
+          for (int d = 0; d < x.rank; ++d) {
+            const int64_t want = d < axis ? a->shape[d]
+                                 : d == axis ? (a->shape[axis] - span - 1) / step + 1
+                                 : d == axis + 1 ? size
+                                                 : a->shape[d - 1];
+            expect(x.shape[d] == want, "unfolded shape");
+          }
+          break;
+        }
+        case TOPOS_HIP_OP_FOLD: {  // Fold::infer_shape (src/function/fold.rs:42-82)
+          const int64_t axis = x.params[0], size = x.params[1], step = x.params[2], dilation = x.params[3],
+                        extent = x.params[4];
+          expect(axis >= 0 && axis + 1 < a->rank && x.rank == a->rank - 1 && size > 0 && step > 0 && dilation > 0,
+                 "fold parameters");
+          int64_t span = 0;
+          expect(!__builtin_mul_overflow(dilation, size - 1, &span) && span < extent, "fold window span");
+          expect(a->shape[axis] == (extent - span - 1) / step + 1 && a->shape[axis + 1] == size, "fold window pair");
+          for (int d = 0; d < x.rank; ++d)
+            expect(x.shape[d] == (d < axis ? a->shape[d] : d == axis ? extent : a->shape[d + 1]), "folded shape");
+          break;
+        }
       }
     }
   }
@@ -659,7 +683,7 @@ struct topos_hip_program {
   struct RowGroup {
     std::vector<int64_t> members;  // ascending
     int rank = 0;
-    int64_t shape[kMaxRank] = {1, 1, 1, 1};
+    int64_t shape[kMaxRank] = {1, 1, 1, 1, 1, 1};
   };
   std::vector<RowGroup> row_groups;
   std::vector<int> group_of;
@@ -1603,10 +1627,28 @@ struct topos_hip_program {
         out = view_of(copied, contiguous(x.rank, x.shape));
         return;
       }
-      case TOPOS_HIP_OP_UNFOLD:
-      case TOPOS_HIP_OP_FOLD:
-        throw Unsupported{std::string("node ") + std::to_string(i) + ": " + op_name(x.op) +
-                          " (the window patterns) has no device kernel"};
+      case TOPOS_HIP_OP_UNFOLD: {
+        // Layout::unfold (src/payload/layout.rs:299-331): the axis becomes
+        // (count, size) with window starts `step` and window elements
+        // `dilation` source steps apart; an extent-1 axis gets stride 0.
+        const Value &a = dense_operand(x.operands[0]);
+        const int axis = (int)x.params[0];
+        const int64_t along = a.layout.strides[axis];
+        Layout l;
+        l.rank = x.rank;
+        l.offset = a.layout.offset;
+        for (int d = 0; d < x.rank; ++d) {
+          l.shape[d] = x.shape[d];
+          if (d < axis) l.strides[d] = a.layout.strides[d];
+          if (d > axis + 1) l.strides[d] = a.layout.strides[d - 1];
+        }
+        if (x.shape[axis] > 1 && __builtin_mul_overflow(x.params[2], along, &l.strides[axis]))
+          refuse(i, "unfold stride overflows");
+        if (x.shape[axis + 1] > 1 && __builtin_mul_overflow(x.params[3], along, &l.strides[axis + 1]))
+          refuse(i, "unfold stride overflows");
+        out = view_of(a, l);
+        return;
+      }
       default:
         break;
     }
@@ -1623,6 +1665,7 @@ struct topos_hip_program {
       case TOPOS_HIP_OP_LOG_SUM_EXP: plan_rows(i); return;
       case TOPOS_HIP_OP_GATHER: plan_gather(i); return;
       case TOPOS_HIP_OP_SCATTER: plan_scatter(i); return;
+      case TOPOS_HIP_OP_FOLD: plan_fold(i); return;
     }
     refuse(i, "no plan for this operation");
   }
@@ -2100,6 +2143,47 @@ struct topos_hip_program {
       if (l.shape[d + 1] != 1 && l.strides[d] != l.shape[d + 1] * l.strides[d + 1]) return false;
     column_stride = l.strides[l.rank - 1];
     return true;
+  }
+
+  // Fold (src/payload/tensor.rs:1392-1462): one kernel reading the operand
+  // through its layout, writing the folded value contiguous.
+  void plan_fold(int64_t i) {
+    const topos_hip_node &x = nodes[i];
+    const Value a = dense_operand(x.operands[0]);
+    const Layout &l = a.layout;
+    const int axis = (int)x.params[0];
+    FoldGeometry g;
+    g.outer_rank = axis;
+    for (int d = 0; d < axis; ++d) {
+      g.outer_shape[d] = l.shape[d];
+      g.outer_strides[d] = l.strides[d];
+    }
+    g.inner_rank = l.rank - axis - 2;
+    for (int d = 0; d < g.inner_rank; ++d) {
+      g.inner_shape[d] = l.shape[axis + 2 + d];
+      g.inner_strides[d] = l.strides[axis + 2 + d];
+      g.inner_volume *= l.shape[axis + 2 + d];
+    }
+    g.window_stride = l.strides[axis];
+    g.element_stride = l.strides[axis + 1];
+    g.count = l.shape[axis];
+    g.size = x.params[1];
+    g.step = x.params[2];
+    g.dilation = x.params[3];
+    g.extent = x.params[4];
+    g.total = volume_of(x);
+    const int out = arena_storage(g.total * 4);
+    const int source = a.storage;
+    const int64_t offset = l.offset;
+    std::ostringstream what;
+    what << "fold [";
+    for (int d = 0; d < l.rank; ++d) what << (d ? "," : "") << l.shape[d];
+    what << "] axis " << axis << " onto " << g.extent;
+    add_launch(what.str(), {source}, {out}, [this, source, offset, g, out](const Exec &ex) {
+      launch_fold((const float *)base(source) + offset, g, (float *)base(out), ex.stream);
+    });
+    launches.back().bytes = 4.0 * ((double)volume_of(nodes[x.operands[0]]) + (double)g.total);
+    values[i] = dense_value(out, contiguous(x.rank, x.shape));
   }
 
   void plan_gather(int64_t i) {

@@ -39,7 +39,7 @@ NAMES = ["Leaf", "Parameter", "Input", "Add", "Sub", "Mul", "Div", "Neg", "Tanh"
          "Unfold", "Fold", "Gather", "Scatter", "LogSoftmax", "LogSumExp", "Sqrt", "Powf", "Maximum", "Relu",
          "Step"]
 
-MAX_RANK = 4
+MAX_RANK = 6
 
 
 # ---- payloads (src/payload/storage.rs:36-51) ----
@@ -285,6 +285,29 @@ class Value:
         s[axis] = full_extent
         return self._apply(PAD, [self], s, [axis, start, full_extent])
 
+    def unfold(self, axis: int, size: int, step: int, dilation: int) -> "Value":
+        """Unfold::infer_shape (src/function/unfold.rs:40-70): `axis` becomes
+        the (count, size) pair of sliding windows."""
+        s = list(self.shape)
+        assert axis < len(s) and size > 0 and step > 0 and dilation > 0, "unfold parameters"
+        span = dilation * (size - 1) + 1
+        assert span <= s[axis], f"unfold window span {span} exceeds axis {axis} extent {s[axis]}"
+        s[axis] = (s[axis] - span) // step + 1
+        s.insert(axis + 1, size)
+        return self._apply(UNFOLD, [self], s, [axis, size, step, dilation])
+
+    def fold(self, axis: int, size: int, step: int, dilation: int, extent: int) -> "Value":
+        """Fold::infer_shape (src/function/fold.rs:42-82): the (count, size)
+        pair at `axis` folds back onto an axis of `extent`."""
+        s = list(self.shape)
+        assert axis + 1 < len(s) and size > 0 and step > 0 and dilation > 0, "fold parameters"
+        span = dilation * (size - 1) + 1
+        assert span <= extent, f"fold window span {span} exceeds the target extent {extent}"
+        assert s[axis] == (extent - span) // step + 1 and s[axis + 1] == size, "fold window pair"
+        s[axis] = extent
+        del s[axis + 1]
+        return self._apply(FOLD, [self], s, [axis, size, step, dilation, extent])
+
     def gather(self, selection: "Value") -> "Value":
         rows, vocab = selection.shape
         assert vocab == self.shape[0], "gather selection vocabulary must match the table rows"
@@ -409,6 +432,12 @@ def _backward(node: Node, operands: list, output: Value, g: Value) -> list:
     if op == PAD:
         axis, start, _ = node.params
         return [g.narrow(axis, start, operands[0].shape[axis])]
+    if op == UNFOLD:
+        axis, size, step, dilation = node.params[:4]
+        return [g.fold(axis, size, step, dilation, operands[0].shape[axis])]
+    if op == FOLD:
+        axis, size, step, dilation, _ = node.params[:5]
+        return [g.unfold(axis, size, step, dilation)]
     if op == GATHER:
         table, selection = operands
         return [g.scatter(selection, table.shape[0]), None]
@@ -459,6 +488,59 @@ def cross_entropy(logits: Value, targets: Value) -> Value:
     normalizers = (targets.sum_along(1) * logits.logsumexp(1)).sum()
     alignment = (targets * logits).sum()
     return (normalizers - alignment) / targets.sum()
+
+
+def conv2d(x: Value, weights: Value, bias: Value, stride: int, padding: int) -> Value:
+    """conv2d (src/neural/convolution.rs:24-118): pad, two single-axis
+    unfolds, the im2col reshape of the permuted windows, one rank-2 product
+    with the permuted kernel, the bias along the rows, and the NCHW view."""
+    batch, channels, height, width = x.shape
+    filters, kernel_channels, kernel_height, kernel_width = weights.shape
+    assert kernel_channels == channels and bias.shape == (filters,) and stride > 0, "conv2d shapes"
+    padded = x
+    if padding > 0:
+        padded = padded.pad(2, padding, height + 2 * padding)
+        padded = padded.pad(3, padding, width + 2 * padding)
+    windows = padded.unfold(2, kernel_height, stride, 1).unfold(4, kernel_width, stride, 1)
+    out_height, out_width = windows.shape[2], windows.shape[4]
+    patches = windows.permute([0, 2, 4, 1, 3, 5]).reshape(
+        [batch * out_height * out_width, channels * kernel_height * kernel_width])
+    kernel = weights.permute([1, 2, 3, 0]).reshape([channels * kernel_height * kernel_width, filters])
+    product = patches.matmul(kernel)
+    shifted = product + bias.broadcast_along(0, product)
+    return shifted.reshape([batch, out_height, out_width, filters]).permute([0, 3, 1, 2])
+
+
+def window_lanes(x: Value, size: int, stride: int) -> Value:
+    """window_lanes (src/neural/pooling.rs:10-28): [b, c, oh, ow, size*size]."""
+    assert len(x.shape) == 4 and size > 0 and stride > 0, "pooling input must be rank 4"
+    windows = x.unfold(2, size, stride, 1).unfold(4, size, stride, 1)
+    axes = windows.shape
+    return windows.permute([0, 1, 2, 4, 3, 5]).reshape([axes[0], axes[1], axes[2], axes[4], size * size])
+
+
+def max_pool(x: Value, size: int, stride: int) -> Value:
+    """max_pool (src/neural/pooling.rs:30-41): a left-biased fold of `maximum`
+    over the window lanes, then the lane axis squeezed."""
+    lanes = window_lanes(x, size, stride)
+    largest = lanes.narrow(4, 0, 1)
+    for lane in range(1, size * size):
+        largest = largest.maximum(lanes.narrow(4, lane, 1))
+    return largest.squeeze(4)
+
+
+def batch_norm(x: Value, scale: Value, shift: Value, epsilon: Value):
+    """BatchNorm::express (src/neural/batch_norm.rs:104-121, normalize at
+    :149-176): statistics of the batch itself, the biased variance; returns
+    (output, mean, variance). `epsilon` is a single-value leaf."""
+    assert len(x.shape) == 2 and scale.shape == (x.shape[1],), "batch-norm input must be rank 2"
+    mean = x.mean_along(0)
+    centered = x - mean.broadcast_along(0, x)
+    variance = (centered * centered).mean_along(0)
+    deviation = (variance + epsilon.broadcast_like(variance)).sqrt()
+    normalized = centered / deviation.broadcast_along(0, centered)
+    output = normalized * scale.broadcast_along(0, centered) + shift.broadcast_along(0, centered)
+    return output, mean, variance
 
 
 # ---- the program table ----

@@ -11,6 +11,12 @@
   embeddings rotated by narrow/neg/concat, causal attention batched over
   (batch x heads), SwiGLU MLP, bias-free projections, an untied head
   (examples/llama/model.rs:80-330) — forward and backward, no optimizer.
+* ``cnn``: the convolutional examples (examples/mnist/main.rs:59-99,
+  examples/cifar10/main.rs) — conv2d -> ReLU -> max_pool stages over the
+  window views, flatten, an affine head, cross-entropy.
+* ``batch_norm_mlp``: examples/makemore/mlp_batchnorm.rs — embedding gather,
+  a bias-free hidden product, BatchNorm by the batch's own statistics, tanh,
+  an affine head, cross-entropy.
 
 All use the recorded-gradients route (src/graph/tape.rs:335-411;
 examples/makemore/mlp_compiled.rs:142-204): one forward program reads the
@@ -26,7 +32,8 @@ from dataclasses import dataclass, field
 
 import numpy as np
 
-from .topos import Constant, Dense, Selection, Tape, Value, concat, cross_entropy, layer_norm, linear, rms_norm
+from .topos import (Constant, Dense, Selection, Tape, Value, batch_norm, concat, conv2d, cross_entropy, layer_norm,
+                    linear, max_pool, rms_norm)
 
 # ---- synthetic data: src/neural/init.rs:45-102, vectorized ----
 
@@ -118,6 +125,85 @@ def mlp(batch: int = 64, sizes=(784, 128, 10), weight_seeds=(7, 8), input_seed: 
     return Workload(tape, params, initial, loss, gradients, dense_inputs={x.node.slot: feeds},
                     selection_inputs={targets.node.slot: (labels(label_seed, batch, sizes[-1]), 1.0)},
                     config={"model": "mlp", "sizes": list(sizes), "batch": batch})
+
+
+def cnn(batch: int = 64, channels: int = 1, side: int = 28, filters=(8, 16), classes: int = 10,
+        weight_seed: int = 11, input_seed: int = 17, label_seed: int = 19,
+        record_gradients: bool = True) -> Workload:
+    """The MNIST example's model (examples/mnist/main.rs:59-99; with
+    channels=3, side=32, filters=(16, 32, 64) the CIFAR-10 one): per stage
+    conv2d (3x3, stride 1, padding 1, Kaiming-normal kernels
+    sqrt(2 / (c * 9)), zero biases), ReLU, 2x2 max_pool; then the flattened
+    features through an affine head (Kaiming-normal), cross-entropy over
+    one-hot targets. Images are U[0, 1) draws (synthetic data)."""
+    tape = Tape()
+    params, initial = [], []
+    stages = []
+    c = channels
+    for s, f in enumerate(filters):
+        w = tape.parameter((f, c, 3, 3))
+        b = tape.parameter((f,))
+        params += [w, b]
+        initial += [normal(weight_seed + s, math.sqrt(2.0 / (c * 9)), (f, c, 3, 3)), np.zeros(f, np.float32)]
+        stages.append((w, b))
+        c = f
+    reduced = side >> len(filters)
+    flat = c * reduced * reduced
+    head_w = tape.parameter((flat, classes))
+    head_b = tape.parameter((classes,))
+    params += [head_w, head_b]
+    initial += [normal(weight_seed + len(filters), math.sqrt(2.0 / flat), (flat, classes)),
+                normal(weight_seed + len(filters) + 1, math.sqrt(2.0 / classes), (classes,))]
+    images = tape.input((batch, channels, side, side))
+    targets = tape.selection_input(batch, classes)
+    h = images
+    for w, b in stages:
+        h = max_pool(conv2d(h, w, b, 1, 1).relu(), 2, 2)
+    logits = linear(h.reshape([batch, flat]), head_w, head_b)
+    loss = cross_entropy(logits, targets)
+    gradients = tape.differentiate(loss, params) if record_gradients else []
+    pixels = unit(input_seed, batch * channels * side * side).astype(np.float32).reshape(batch, channels, side, side)
+    return Workload(tape, params, initial, loss, gradients, dense_inputs={images.node.slot: pixels},
+                    selection_inputs={targets.node.slot: (labels(label_seed, batch, classes), 1.0)},
+                    config={"model": "cnn", "batch": batch, "channels": channels, "side": side,
+                            "filters": list(filters)})
+
+
+def batch_norm_mlp(batch: int = 64, vocab: int = 27, context: int = 3, embed: int = 10, hidden: int = 100,
+                   weight_seed: int = 7, token_seed: int = 13, record_gradients: bool = True) -> Workload:
+    """examples/makemore/mlp_batchnorm.rs:55-126: embeddings gathered by the
+    context's token ids and flattened, a bias-free hidden product, BatchNorm
+    (scale one, shift zero, epsilon 1e-5; normalized by the batch's own
+    statistics), tanh, an affine output, cross-entropy over the next token.
+    Embeddings N(0, 1), Xavier-uniform weights; token ids are uniform draws
+    (synthetic data)."""
+    tape = Tape()
+    table = tape.parameter((vocab, embed))
+    hidden_w = tape.parameter((context * embed, hidden))
+    scale = tape.parameter((hidden,))
+    shift = tape.parameter((hidden,))
+    out_w = tape.parameter((hidden, vocab))
+    out_b = tape.parameter((vocab,))
+    epsilon = tape.leaf(Constant((), 1e-5))
+    params = [table, hidden_w, scale, shift, out_w, out_b]
+    xavier = lambda seed, fan_in, fan_out, shape: uniform(seed, math.sqrt(6.0 / (fan_in + fan_out)), shape)
+    initial = [normal(weight_seed + 1, 1.0, (vocab, embed)),
+               xavier(weight_seed, context * embed, hidden, (context * embed, hidden)),
+               np.ones(hidden, np.float32), np.zeros(hidden, np.float32),
+               xavier(weight_seed + 2, hidden, vocab, (hidden, vocab)),
+               xavier(weight_seed + 3, hidden, vocab, (vocab,))]
+    contexts = tape.selection_input(batch * context, vocab)
+    targets = tape.selection_input(batch, vocab)
+    preactivation = table.gather(contexts).reshape([batch, context * embed]).matmul(hidden_w)
+    normalized, _, _ = batch_norm(preactivation, scale, shift, epsilon)
+    product = normalized.tanh().matmul(out_w)
+    loss = cross_entropy(product + out_b.broadcast_along(0, product), targets)
+    gradients = tape.differentiate(loss, params) if record_gradients else []
+    return Workload(tape, params, initial, loss, gradients,
+                    selection_inputs={contexts.node.slot: (labels(token_seed, batch * context, vocab), 1.0),
+                                      targets.node.slot: (labels(token_seed + 1, batch, vocab), 1.0)},
+                    config={"model": "batch_norm_mlp", "batch": batch, "vocab": vocab, "context": context,
+                            "embed": embed, "hidden": hidden})
 
 
 def _gelu(x: Value, half: Value, one: Value, root: Value, coefficient: Value) -> Value:

@@ -22,6 +22,8 @@ CASES = {
                                      record_gradients=g),
     "llama": lambda g: workloads.llama(batch=2, context=16, vocab=37, width=32, heads=4, hidden=48, layers=2,
                                        record_gradients=g),
+    "cnn": lambda g: workloads.cnn(batch=4, record_gradients=g),
+    "batch_norm_mlp": lambda g: workloads.batch_norm_mlp(batch=8, record_gradients=g),
 }
 
 

@@ -14,7 +14,7 @@ _LIB = Path(__file__).resolve().parent / "native" / "libfaithful_check.so"
 @pytest.fixture(scope="module")
 def check():
     if not _LIB.exists():
-        pytest.fail(f"{_LIB} is not built; run `python -m poorgrad_amd.build`")
+        pytest.fail(f"{_LIB} is not built; run `python poorgrad_amd/build.py`")
     lib = ctypes.CDLL(str(_LIB))
     lib.faithful_check.restype = ctypes.c_int64
     lib.faithful_check.argtypes = [ctypes.c_int, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_int,

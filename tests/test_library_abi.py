@@ -31,7 +31,7 @@ def test_manifest_answers_without_a_device():
     from poorgrad_amd import _native as n
     import ctypes
 
-    assert n.lib.topos_hip_abi_version() == 1
+    assert n.lib.topos_hip_abi_version() == 2
     assert n.lib.topos_hip_compiled() == 1
     fidelity, precisions = ctypes.c_int(-1), ctypes.c_uint(0)
     assert n.lib.topos_hip_coverage(n.FORMULA_GEMM, ctypes.byref(fidelity), ctypes.byref(precisions)) == 1

@@ -106,20 +106,56 @@ for numerics in (n.EXACT, n.FAST):
         assert ok == "True" and int(launches) > 10 and int(side) > 0, out
 
 
-def test_unserved_variants_are_refused_with_a_reason():
+def test_window_views_launch_nothing_and_fold_is_one_kernel():
+    """Unfold is a strided view (Layout::unfold, src/payload/layout.rs:299-331):
+    a chain reads the overlapping windows directly. Fold
+    (src/payload/tensor.rs:1392-1462) is one kernel."""
     out = run(r'''
-import ctypes
+tape = t.Tape()
+x = tape.input((4, 3, 10, 12))
+windows = x.unfold(2, 3, 2, 1).unfold(4, 3, 2, 1)
+y = (windows * windows).exp()
+folded = y.fold(4, 3, 2, 1, 12).fold(2, 3, 2, 1, 10)
+p = DeviceProgram(tape, [y, folded])
+d = p.describe
+print(p.info["launches"], d.count("fold ["), d.count("chain"))
+''')
+    launches, folds, chains = map(int, out.split())
+    assert launches == 3 and folds == 2 and chains == 1, out
+
+
+def test_wrong_window_shapes_are_invalid_arguments():
+    out = run(r'''
 tape = t.Tape()
 x = tape.input((6,))
-tape._record(t.UNFOLD, [x.id], (2, 3), params=(0, 3, 3, 1))
+tape._record(t.UNFOLD, [x.id], (3, 3), params=(0, 3, 3, 1))   # two windows, not three
 table = tape.program([t.Value(tape, 1)])
 try:
     table.create(n.EXACT)
 except n.HipError as e:
-    print(e.code, n.lib.topos_hip_last_refusal().decode())
+    print(e.code, "unfolded shape" in n.lib.topos_hip_last_refusal().decode())
+tape = t.Tape()
+x = tape.input((3, 3))
+tape._record(t.FOLD, [x.id], (9,), params=(0, 3, 2, 1, 9))    # extent 9 makes four windows
+table = tape.program([t.Value(tape, 1)])
+try:
+    table.create(n.EXACT)
+except n.HipError as e:
+    print(e.code, "fold window pair" in n.lib.topos_hip_last_refusal().decode())
 ''')
-    code, _, reason = out.strip().partition(" ")
-    assert int(code) == 7 and "Unfold" in reason, out  # TOPOS_HIP_UNSUPPORTED
+    assert out.split() == ["5", "True", "5", "True"], out  # TOPOS_HIP_INVALID_ARGUMENT
+
+
+def test_the_convolutional_and_batch_norm_graphs_plan():
+    out = run(r'''
+for make in (lambda: workloads.cnn(batch=4), lambda: workloads.batch_norm_mlp(batch=8)):
+    w = make()
+    for numerics in (n.EXACT, n.FAST):
+        p = DeviceProgram(w.tape, w.roots, numerics=numerics)
+        print(p.info["launches"], p.describe.count("fold ["))
+''')
+    rows = [list(map(int, line.split())) for line in out.strip().splitlines()]
+    assert len(rows) == 4 and rows[0][1] >= 6 and rows[2][1] == 0, out
 
 
 def test_malformed_tables_are_invalid_arguments():
@@ -201,6 +237,8 @@ cases = [
                              record_gradients=g),
     lambda g: workloads.llama(batch=2, context=16, vocab=37, width=32, heads=4, hidden=48, layers=2,
                               record_gradients=g),
+    lambda g: workloads.cnn(batch=4, record_gradients=g),
+    lambda g: workloads.batch_norm_mlp(batch=8, record_gradients=g),
 ]
 for make in cases:
     for numerics in (n.EXACT, n.FAST):
@@ -212,7 +250,7 @@ for make in cases:
         assert a.info == b.info, (a.info, b.info)
         print(a.info["launches"])
 ''')
-    assert len(out.split()) == 6, out
+    assert len(out.split()) == 10, out
 
 
 def test_engine_backward_refuses_a_non_scalar_target():

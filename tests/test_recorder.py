@@ -83,7 +83,7 @@ def finite_difference_check(build, shapes, seed=0, eps=1e-2, tolerance=2e-2, pos
             (up,) = evaluate(tape, [loss], bumped)
             bumped[p_index][index] -= np.float32(2 * eps)
             (down,) = evaluate(tape, [loss], bumped)
-            numeric = (float(up) - float(down)) / (2 * eps)
+            numeric = (float(np.ravel(up)[0]) - float(np.ravel(down)[0])) / (2 * eps)
             a = float(analytic[p_index][index])
             assert abs(a - numeric) <= tolerance * max(1.0, abs(numeric)), (p_index, index, a, numeric)
 
