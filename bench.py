@@ -81,7 +81,7 @@ def parse() -> argparse.Namespace:
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU oracle leg")
     p.add_argument("--quick", action="store_true", help="the GPT-2 step only (no side sections)")
-    p.add_argument("--only", choices=["mlp", "gemm", "bf16", "chains", "llama", "gpt2_exact"],
+    p.add_argument("--only", choices=["mlp", "gemm", "bf16", "chains", "llama", "gpt2_exact", "windows"],
                    help="run one side section alone and print its JSON (a diagnostic, not the bench line)")
     p.add_argument("--profile-out", help="write the profiled step's launches (one line each) to this file")
     p.add_argument("--calibration-copy-mib", type=int, default=0,
@@ -495,6 +495,66 @@ def chains_section(torch, n, steps: int, warmup: int) -> dict:
                     "frac": round(bytes_of[label] / t / 1e9 / HBM_PEAK_GBS, 4)} for label, t in per.items()}
 
 
+def windows_section(torch, n, steps: int, warmup: int) -> dict:
+    """The reference's pattern bench (benches/pattern.rs:22-107) as device
+    programs — max_pool over [64,32,28,28], conv2d [64,16,14,14] x
+    [32,16,3,3] padding 1, BatchNorm over [256,512] — and the MNIST example's
+    convolutional train step (examples/mnist/main.rs, batch 64, forward and
+    recorded gradients), each timed as one program run, in both postures."""
+    import numpy as np
+
+    from poorgrad_amd import topos as t
+    from poorgrad_amd import workloads
+    from poorgrad_amd.program import DeviceProgram
+
+    def fill(count, multiplier, modulus, shift, scale):
+        index = np.arange(count, dtype=np.int64)
+        return (((index * multiplier) % modulus).astype(np.float32) - np.float32(shift)) / np.float32(scale)
+
+    def pattern(kind):
+        tape = t.Tape()
+        if kind == "pool":
+            x = tape.input((64, 32, 28, 28))
+            return tape, [t.max_pool(x, 2, 2)], {x.node.slot: fill(64 * 32 * 28 * 28, 5, 13, 6.0, 4.0).reshape(x.shape)}
+        if kind == "conv":
+            x = tape.input((64, 16, 14, 14))
+            w = tape.input((32, 16, 3, 3))
+            out = t.conv2d(x, w, tape.leaf(t.Constant((32,), 0.01)), 1, 1)
+            return tape, [out], {x.node.slot: fill(64 * 16 * 14 * 14, 7, 23, 11.0, 8.0).reshape(x.shape),
+                                 w.node.slot: fill(32 * 16 * 9, 3, 17, 8.0, 16.0).reshape(w.shape)}
+        x = tape.input((256, 512))
+        out, _, _ = t.batch_norm(x, tape.leaf(t.Constant((512,), 1.0)), tape.leaf(t.Constant((512,), 0.0)),
+                                 tape.leaf(t.Constant((1,), 1e-5)))
+        return tape, [out], {x.node.slot: fill(256 * 512, 11, 29, 14.0, 8.0).reshape(x.shape)}
+
+    result = {}
+    reps = max(20, steps * 10)
+    for posture, numerics in (("exact", n.EXACT), ("fast", n.FAST)):
+        for kind in ("pool", "conv", "batch_norm", "mnist_step"):
+            if kind == "mnist_step":
+                w = workloads.cnn()
+                program = DeviceProgram(w.tape, w.roots, numerics=numerics)
+                held = [torch.from_numpy(a).cuda() for a in w.initial]
+                for slot, p in enumerate(held):
+                    program.bind_parameter(slot, p)
+                feeds = w.dense_inputs
+                for slot, (indices, one) in w.selection_inputs.items():
+                    program.bind_selection(slot, indices, one)
+            else:
+                tape, roots, feeds = pattern(kind)
+                program = DeviceProgram(tape, roots, numerics=numerics)
+                held = []
+            for slot, a in feeds.items():
+                tensor = torch.from_numpy(np.ascontiguousarray(a)).cuda()
+                held.append(tensor)
+                program.bind_input(slot, tensor)
+            program.run()
+            wall = time_steps(torch, program.replay, reps, warmup)
+            result[f"{kind}/{posture}"] = {"us": round(wall / reps * 1e6, 1), "launches": program.info["launches"]}
+            del program, held
+    return result
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1:
@@ -516,7 +576,7 @@ def main() -> int:
         del source
     if args.only:
         sections = {"mlp": mlp_section, "gemm": gemm_section, "bf16": bf16_section, "chains": chains_section,
-                    "llama": llama_section, "gpt2_exact": gpt2_exact_section}
+                    "llama": llama_section, "gpt2_exact": gpt2_exact_section, "windows": windows_section}
         print(json.dumps({args.only: sections[args.only](torch, n, args.steps, args.warmup)}), flush=True)
         return 0
     g = gpt2_section(torch, n, args)
@@ -567,6 +627,8 @@ def main() -> int:
         line["llama"] = llama_section(torch, n, args.steps, args.warmup)
         log("gpt2 step, exact posture (configs[3])")
         line["gpt2_exact"] = gpt2_exact_section(torch, n, args.steps, args.warmup)
+        log("window programs (the reference's pattern bench, the MNIST convolutional step)")
+        line["windows"] = windows_section(torch, n, args.steps, args.warmup)
     if not args.no_cpu_baseline:
         log("cpu baseline: the oracle interpreter on one core")
         line["cpu_baseline"] = cpu_leg(full_flops)
