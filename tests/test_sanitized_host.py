@@ -2,8 +2,9 @@
 face, status and poison paths) under AddressSanitizer and
 UndefinedBehaviorSanitizer: a sanitized build of libtopos_hip.so
 (poorgrad_amd/build.py build_sanitized, host code only) planning the
-benchmark programs and the refusal paths under the fake runtime, in a fresh
-interpreter with the sanitizer runtime preloaded. Any report fails the test."""
+benchmark programs (window programs included), planning from four threads at
+once, and the refusal paths under the fake runtime, in a fresh interpreter
+with the sanitizer runtime preloaded. Any report fails the test."""
 import os
 import subprocess
 import sys
@@ -40,14 +41,43 @@ y = tape.input((16, 24))
 z = x.powf(y)
 print("powf", DeviceProgram(tape, [(z + x).exp(), z.log_softmax(1)]).info["launches"])
 
-# Refusals: an unserved variant, malformed tables, a non-scalar backward target.
+# Window programs: the convolutional and BatchNorm steps, both routes.
+for numerics in (n.EXACT, n.FAST):
+    for make in (lambda g: workloads.cnn(batch=2, side=8, filters=(2, 3), record_gradients=g),
+                 lambda g: workloads.batch_norm_mlp(batch=4, record_gradients=g)):
+        w = make(True)
+        a = DeviceProgram(w.tape, w.roots, numerics=numerics)
+        f = make(False)
+        b = DeviceProgram.engine_backward(f.tape, f.loss, f.parameters, numerics=numerics)
+        assert a.describe == b.describe
+        print("planned", a.info["launches"])
+
+# Planning from four threads at once (the generated-kernel cache and the
+# compile queue are shared): every plan equals the serial one.
+import threading
+def make_program(i):
+    w = workloads.gpt2(batch=2, context=8, vocab=19 + i, width=16, heads=2, layers=1, positions=8)
+    return DeviceProgram(w.tape, w.roots, numerics=n.FAST if i % 2 else n.EXACT).describe
+expected = [make_program(i) for i in range(4)]
+results = [None] * 4
+def worker(i):
+    results[i] = make_program(i)
+threads = [threading.Thread(target=worker, args=(i,)) for i in range(4)]
+for th in threads: th.start()
+for th in threads: th.join()
+assert results == expected
+print("threads", len(results))
+
+# Refusals: a window pair that disagrees with its extent, malformed tables, a
+# non-scalar backward target.
 tape = t.Tape()
 x = tape.input((6,))
-tape._record(t.UNFOLD, [x.id], (2, 3), params=(0, 3, 3, 1))
+tape._record(t.UNFOLD, [x.id], (3, 3), params=(0, 3, 3, 1))
 try:
     tape.program([t.Value(tape, 1)]).create(n.EXACT)
+    raise AssertionError("a wrong unfold shape was accepted")
 except n.HipError as e:
-    assert e.code == n.UNSUPPORTED
+    assert e.code == n.INVALID_ARGUMENT
 tape = t.Tape()
 x = tape.input((4, 3))
 tape.nodes.append(t.Node(t.ADD, (0, 7), (4, 3)))
