@@ -1833,7 +1833,95 @@ struct topos_hip_program {
     return true;
   }
 
+  // A rank-2 product read only through a transpose (the tied embedding's
+  // gradient (h^T dlogits)^T): computed as B^T A^T into [n, m], so the
+  // transpose is the contiguous layout its reader wants instead of a
+  // column-strided one. Every output element is the same chain of the same
+  // products in the same ascending k order (a * b = b * a in IEEE
+  // arithmetic), so the exact posture keeps its bits.
+  // Under Fast the product may also reach the transpose through zero-seeded
+  // accumulations (+0 + product), which are planned as the product itself
+  // because a matrix-core product is never -0.
+  bool read_transposed(int64_t i) const {
+    const topos_hip_node &x = nodes[i];
+    const Value &a = values[x.operands[0]], &b = values[x.operands[1]];
+    if (x.rank != 2 || readable[i] || a.split_inner != 0 || b.split_inner != 0 || a.kind != Value::kDense ||
+        b.kind != Value::kDense)
+      return false;
+    const bool mfma = numerics == TOPOS_HIP_FAST &&
+                      mfma_serves(b.layout.strides[1], b.layout.strides[0], a.layout.strides[1], a.layout.strides[0],
+                                  x.shape[1], nodes[x.operands[0]].shape[1], x.shape[0]);
+    int64_t v = i;
+    for (int hop = 0; hop < 4; ++hop) {
+      if (consumers[v].size() != 1) return false;
+      const int64_t c = consumers[v][0];
+      const topos_hip_node &y = nodes[c];
+      if (y.op == TOPOS_HIP_OP_TRANSPOSE) return true;
+      if (!(mfma && y.op == TOPOS_HIP_OP_ADD && group_of[c] < 0 && alias_of[c] < 0)) return false;
+      const int64_t other = y.operands[0] == v ? y.operands[1] : y.operands[0];
+      if (other == v || !static_plus_zero(other)) return false;
+      v = c;
+    }
+    return false;
+  }
+
+  void plan_transposed_matmul(int64_t i) {
+    const topos_hip_node &x = nodes[i];
+    const int64_t m = x.shape[0], n = x.shape[1], k = nodes[x.operands[0]].shape[1];
+    const Value a = dense_operand(x.operands[0]);
+    const Value b = dense_operand(x.operands[1]);
+    // D = B^T A^T (n x m): its left operand B^T, its right A^T, as views.
+    const int64_t ars = b.layout.strides[1], acs = b.layout.strides[0];
+    const int64_t brs = a.layout.strides[1], bcs = a.layout.strides[0];
+    const int64_t a_offset = b.layout.offset, b_offset = a.layout.offset;
+    const int left = b.storage, right = a.storage;
+    const int out = arena_storage(m * n * 4);
+    const bool mfma = numerics == TOPOS_HIP_FAST && mfma_serves(ars, acs, brs, bcs, n, k, m);
+    int64_t workspace_floats = 0;
+    int workspace = -1;
+    if (numerics == TOPOS_HIP_FAST) {
+      const int splits = mfma_splits(n, m, k, 1);
+      if (splits > 1) {
+        workspace_floats = (int64_t)splits * m * n;
+        workspace = arena_storage(workspace_floats * 4);
+      }
+    }
+    std::ostringstream what;
+    what << "gemm " << (numerics == TOPOS_HIP_FAST ? "mfma" : "exact") << " 1x(" << n << "," << m << "," << k
+         << ") a[" << ars << "," << acs << "] b[" << brs << "," << bcs << "] transposed";
+    std::vector<int> writes = {out};
+    if (workspace >= 0) writes.push_back(workspace);
+    const int numerics_ = numerics;
+    add_launch(what.str(), {left, right}, writes,
+               [this, left, right, out, a_offset, b_offset, ars, acs, brs, bcs, m, n, k, numerics_, workspace,
+                workspace_floats](const Exec &ex) {
+                 const float *pa = (const float *)base(left) + a_offset;
+                 const float *pb = (const float *)base(right) + b_offset;
+                 float *pc = (float *)base(out);
+                 float *pw = workspace >= 0 ? (float *)base(workspace) : nullptr;
+                 if (numerics_ == TOPOS_HIP_FAST &&
+                     launch_gemm_mfma(pa, ars, acs, pb, brs, bcs, n, k, m, pc, m, ex.stream, Batch(), pw,
+                                      workspace_floats))
+                   return;
+                 launch_gemm_exact(pa, ars, acs, pb, brs, bcs, n, k, m, pc, m, ex.stream);
+               });
+    launches.back().flops = 2.0 * (double)m * n * k;
+    launches.back().bytes = 4.0 * ((double)m * k + (double)k * n + (double)m * n);
+    Layout l;
+    l.rank = 2;
+    l.shape[0] = m;
+    l.shape[1] = n;
+    l.strides[0] = 1;
+    l.strides[1] = m;
+    values[i] = dense_value(out, l);
+    values[i].never_minus_zero = mfma;
+  }
+
   void plan_matmul(int64_t i) {
+    if (read_transposed(i)) {
+      plan_transposed_matmul(i);
+      return;
+    }
     const topos_hip_node &x = nodes[i];
     const int r = x.rank, s = r - 2;
     const int64_t m = x.shape[s], n = x.shape[s + 1], k = nodes[x.operands[0]].shape[s + 1];
