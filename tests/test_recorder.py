@@ -134,6 +134,67 @@ def test_view_and_index_rules_match_finite_differences():
     finite_difference_check(build, [(3, 4), (3, 4)])
 
 
+def test_window_rules_match_finite_differences():
+    """Unfold's rule folds and Fold's rule unfolds (src/function/unfold.rs,
+    src/function/fold.rs): checked through conv2d (padding, stride 2), a
+    dilated unfold, a fold of a permuted view, and max_pool over distinct
+    values (every window's maximum is strict)."""
+    def build(tape, v):
+        x, w, b, y = v
+        conv = t.conv2d(x, w, b, 2, 1)                                        # [1, 2, 3, 3]
+        dilated = y.unfold(1, 2, 1, 2)                                        # [2, 3, 2]
+        folded = (dilated * dilated).permute((0, 2, 1)).permute((0, 2, 1)).fold(1, 2, 1, 2, 5)
+        pooled = t.max_pool(x, 2, 2)                                           # [1, 1, 2, 2]
+        return (conv * conv).sum() + (folded * y).sum() + (pooled * pooled).sum()
+    finite_difference_check(build, [(1, 1, 5, 5), (2, 1, 3, 3), (2,), (2, 5)], eps=1e-3)
+
+
+def test_log_softmax_backward_is_the_seed_minus_scaled_probabilities():
+    """src/function/tests/log_softmax_tests.rs:44-66: with a one-hot seed the
+    cotangent is onehot - softmax (f32 against the f64 closed form)."""
+    tape = t.Tape()
+    x = tape.parameter((2, 5))
+    picked = tape.leaf(t.Dense(np.eye(5, dtype=np.float32)[[1, 3]]))
+    loss = (x.log_softmax(1) * picked).sum()
+    (g,) = tape.differentiate(loss, [x])
+    values = np.array([[0.3, -1.2, 2.0, 0.0, 0.7], [-0.5, 0.25, 1.5, -2.0, 0.9]], np.float32)
+    (got,) = evaluate(tape, [g], [values])
+    e = np.exp(values.astype(np.float64) - values.max(1, keepdims=True))
+    want = np.eye(5)[[1, 3]] - e / e.sum(1, keepdims=True)
+    assert np.abs(got - want).max() < 1e-6
+
+
+def test_cross_entropy_zero_target_lanes_contribute_exact_zero():
+    """src/neural/tests/loss_tests.rs:136-147: a dense soft target with a zero
+    lane against an extreme logit: exactly 0, never NaN."""
+    tape = t.Tape()
+    logits = tape.input((1, 2))
+    targets = tape.input((1, 2))
+    loss = t.cross_entropy(logits, targets)
+    (value,) = evaluate(tape, [loss], [], {logits.node.slot: np.array([[-3.0e38, 3.0e38]], np.float32),
+                                           targets.node.slot: np.array([[0.0, 1.0]], np.float32)})
+    assert float(np.ravel(value)[0]) == 0.0 and not np.signbit(np.ravel(value)[0])
+
+
+def test_adamw_decays_weights_and_spares_biases():
+    """src/neural/tests/adam_tests.rs:79-143: the rank-1 bias is spared (AdamW
+    equals Adam bit for bit there); a rank-2 weight differs from Adam by the
+    decoupled term original * decay * rate (f32 rounding); decay 0 is Adam."""
+    from tests.program_util import adamw_reference, adamw_state
+
+    weights = np.array([[1.0, -0.5], [0.25, 2.0]], np.float32)
+    bias = np.array([0.5, -1.0], np.float32)
+    x = np.array([[1.0, -1.0]], np.float32)
+    shifted = x @ weights + bias
+    grads = [(x.T @ (2 * shifted)).astype(np.float32), (2 * shifted).sum(0).astype(np.float32)]
+    plain = adamw_reference([weights, bias], grads, adamw_state([weights, bias]), rate=0.05, decay=0.0)
+    decoupled = adamw_reference([weights, bias], grads, adamw_state([weights, bias]), rate=0.05, decay=0.1)
+    assert plain[1].tobytes() == decoupled[1].tobytes()
+    term = weights.astype(np.float64) * 0.1 * 0.05
+    assert np.abs(plain[0].astype(np.float64) - decoupled[0] - term).max() < 1e-6
+    assert np.abs(plain[0].astype(np.float64) - decoupled[0]).min() > 1e-4   # the decay is applied
+
+
 def test_mlp_workload_loss_and_gradient_shapes():
     w = workloads.mlp()
     assert [g.shape for g in w.gradients] == [(784, 128), (128,), (128, 10), (10,)]
