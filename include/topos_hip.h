@@ -423,11 +423,29 @@ int topos_hip_sgd_step_f32(float *parameter, const float *gradient, int64_t coun
  * optimizer's absent moments, whose Constant-zero scaling gives the same
  * bits). `first_correction`/`second_correction` are 1 - beta^t as the
  * optimizer computes them in f32; `decay` applies when `decayed` != 0 (the
- * rank >= 2 policy of AdamW::step). */
+ * rank >= 2 policy of AdamW::step). An empty parameter (count 0) may pass
+ * null pointers. */
 int topos_hip_adamw_step_f32(float *parameter, const float *gradient, float *first, float *second,
                              int64_t count, float beta1, float beta2, float first_share,
                              float second_share, float first_correction, float second_correction,
                              float epsilon, float rate, float decay, int decayed, void *stream);
+
+/* One parameter of a many-parameter AdamW step. */
+typedef struct {
+  float *parameter;
+  const float *gradient;
+  float *first;
+  float *second;
+  int64_t count;
+  int32_t decayed; /* the rank >= 2 decay policy of AdamW::step */
+} topos_hip_adamw_tensor;
+/* AdamW::step over every parameter of a model (src/neural/adam.rs:62-171,
+ * the loop over Parameters at :120-171) in as few launches as possible: each
+ * element receives exactly the operations of topos_hip_adamw_step_f32 with
+ * the shared scalars, so the two entry points give the same bits. */
+int topos_hip_adamw_step_multi_f32(const topos_hip_adamw_tensor *tensors, int64_t count, float beta1, float beta2,
+                                   float first_share, float second_share, float first_correction,
+                                   float second_correction, float epsilon, float rate, float decay, void *stream);
 
 /* ---- test surface ---- */
 

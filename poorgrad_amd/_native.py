@@ -71,6 +71,11 @@ class Node(ctypes.Structure):
                 ("params", c_int64 * MAX_RANK), ("slot", c_int32), ("flags", ctypes.c_uint32)]
 
 
+class AdamwTensor(ctypes.Structure):
+    _fields_ = [("parameter", c_void_p), ("gradient", c_void_p), ("first", c_void_p), ("second", c_void_p),
+                ("count", c_int64), ("decayed", c_int32)]
+
+
 class Leaf(ctypes.Structure):
     _fields_ = [("kind", c_int32), ("value", c_float), ("offset", c_int64), ("count", c_int64)]
 
@@ -125,6 +130,8 @@ PROTOTYPES = {
     "topos_hip_sgd_step_f32": (c_int, [c_void_p, c_void_p, c_int64, c_float, c_void_p]),
     "topos_hip_adamw_step_f32": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_float, c_float, c_float,
                                          c_float, c_float, c_float, c_float, c_float, c_float, c_int, c_void_p]),
+    "topos_hip_adamw_step_multi_f32": (c_int, [POINTER(AdamwTensor), c_int64, c_float, c_float, c_float, c_float,
+                                               c_float, c_float, c_float, c_float, c_float, c_void_p]),
 }
 
 for _name, (_restype, _argtypes) in PROTOTYPES.items():

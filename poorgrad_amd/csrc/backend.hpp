@@ -226,6 +226,22 @@ void launch_adamw(float *parameter, const float *gradient, float *first, float *
                   float second_correction, float epsilon, float rate, float decay, int decayed,
                   hipStream_t stream);
 
+// Up to kAdamTensors parameters of one AdamW step, passed by value as the
+// kernel argument (about 2 KB, within the argument limit).
+constexpr int kAdamTensors = 48;
+struct AdamTable {
+  float *parameter[kAdamTensors];
+  const float *gradient[kAdamTensors];
+  float *first[kAdamTensors];
+  float *second[kAdamTensors];
+  int64_t start[kAdamTensors + 1];
+  int32_t decayed[kAdamTensors];
+  int32_t count;
+};
+void launch_adamw_multi(const AdamTable &table, float beta1, float beta2, float first_share, float second_share,
+                        float first_correction, float second_correction, float epsilon, float rate, float decay,
+                        hipStream_t stream);
+
 // map.hip: host-libm-faithful unary maps over contiguous buffers.
 void launch_map(int operation, const float *x, int64_t count, float *y, hipStream_t stream);
 

@@ -220,25 +220,57 @@ __global__ __launch_bounds__(256) void sgd_kernel(float *__restrict__ parameter,
     parameter[i] = parameter[i] - gradient[i] * rate;
 }
 
+// One element of AdamW::step (src/neural/adam.rs:62-171), in the optimizer's
+// operation order.
+__device__ __forceinline__ void adamw_element(float *__restrict__ parameter, const float *__restrict__ gradient,
+                                              float *__restrict__ first, float *__restrict__ second, int64_t i,
+                                              float beta1, float beta2, float first_share, float second_share,
+                                              float first_correction, float second_correction, float epsilon,
+                                              float rate, float decay, int decayed) {
+  const float g = gradient[i];
+  const float m = first[i] * beta1 + g * first_share;
+  const float squared = g * g;
+  const float v = second[i] * beta2 + squared * second_share;
+  first[i] = m;
+  second[i] = v;
+  const float corrected_first = m / first_correction;
+  const float corrected_second = v / second_correction;
+  const float direction = corrected_first / (__builtin_sqrtf(corrected_second) + epsilon);
+  const float current = parameter[i];
+  const float stepped = current - direction * rate;
+  parameter[i] = decayed ? stepped - (current * decay) * rate : stepped;
+}
+
 __global__ __launch_bounds__(256) void adamw_kernel(float *__restrict__ parameter, const float *__restrict__ gradient,
                                                     float *__restrict__ first, float *__restrict__ second,
                                                     int64_t count, float beta1, float beta2, float first_share,
                                                     float second_share, float first_correction,
                                                     float second_correction, float epsilon, float rate,
                                                     float decay, int decayed) {
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += (int64_t)gridDim.x * blockDim.x) {
-    const float g = gradient[i];
-    const float m = first[i] * beta1 + g * first_share;
-    const float squared = g * g;
-    const float v = second[i] * beta2 + squared * second_share;
-    first[i] = m;
-    second[i] = v;
-    const float corrected_first = m / first_correction;
-    const float corrected_second = v / second_correction;
-    const float direction = corrected_first / (__builtin_sqrtf(corrected_second) + epsilon);
-    const float current = parameter[i];
-    const float stepped = current - direction * rate;
-    parameter[i] = decayed ? stepped - (current * decay) * rate : stepped;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += (int64_t)gridDim.x * blockDim.x)
+    adamw_element(parameter, gradient, first, second, i, beta1, beta2, first_share, second_share, first_correction,
+                  second_correction, epsilon, rate, decay, decayed);
+}
+
+// Many parameters in one launch: the elements of the table's tensors laid
+// end to end (tensor j owns [start[j], start[j + 1])), each lane finding its
+// tensor by binary search over the starts. The table travels as the kernel's
+// argument, so the launch needs no device memory of its own.
+__global__ __launch_bounds__(256) void adamw_multi_kernel(AdamTable table, float beta1, float beta2,
+                                                          float first_share, float second_share,
+                                                          float first_correction, float second_correction,
+                                                          float epsilon, float rate, float decay) {
+  const int64_t total = table.start[table.count];
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (int64_t)gridDim.x * blockDim.x) {
+    int lo = 0, hi = table.count - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) / 2;
+      if (table.start[mid] <= e) lo = mid;
+      else hi = mid - 1;
+    }
+    adamw_element(table.parameter[lo], table.gradient[lo], table.first[lo], table.second[lo], e - table.start[lo],
+                  beta1, beta2, first_share, second_share, first_correction, second_correction, epsilon, rate, decay,
+                  table.decayed[lo]);
   }
 }
 
@@ -280,6 +312,16 @@ void launch_sgd(float *parameter, const float *gradient, int64_t count, float ra
   if (count <= 0) return;
   sgd_kernel<<<blocks_for(count), 256, 0, stream>>>(parameter, gradient, count, rate);
   check_launch("sgd_kernel launch");
+}
+
+void launch_adamw_multi(const AdamTable &table, float beta1, float beta2, float first_share, float second_share,
+                        float first_correction, float second_correction, float epsilon, float rate, float decay,
+                        hipStream_t stream) {
+  const int64_t total = table.start[table.count];
+  if (table.count <= 0 || total <= 0) return;
+  adamw_multi_kernel<<<blocks_for(total), 256, 0, stream>>>(table, beta1, beta2, first_share, second_share,
+                                                            first_correction, second_correction, epsilon, rate, decay);
+  check_launch("adamw_multi_kernel launch");
 }
 
 void launch_adamw(float *parameter, const float *gradient, float *first, float *second, int64_t count, float beta1,

@@ -2898,12 +2898,47 @@ int topos_hip_adamw_step_f32(float *parameter, const float *gradient, float *fir
                              float beta1, float beta2, float first_share, float second_share, float first_correction,
                              float second_correction, float epsilon, float rate, float decay, int decayed,
                              void *stream) {
-  if (!parameter || !gradient || !first || !second || count < 0) return TOPOS_HIP_INVALID_ARGUMENT;
+  if (count < 0 || (count > 0 && (!parameter || !gradient || !first || !second))) return TOPOS_HIP_INVALID_ARGUMENT;
   const int status = Context::get().status();
   if (status != TOPOS_HIP_OK) return status;
   return guarded([&] {
     launch_adamw(parameter, gradient, first, second, count, beta1, beta2, first_share, second_share, first_correction,
                  second_correction, epsilon, rate, decay, decayed, static_cast<hipStream_t>(stream));
+  });
+}
+
+int topos_hip_adamw_step_multi_f32(const topos_hip_adamw_tensor *tensors, int64_t count, float beta1, float beta2,
+                                   float first_share, float second_share, float first_correction,
+                                   float second_correction, float epsilon, float rate, float decay, void *stream) {
+  if (count < 0 || (count > 0 && !tensors)) return TOPOS_HIP_INVALID_ARGUMENT;
+  for (int64_t j = 0; j < count; ++j) {
+    const topos_hip_adamw_tensor &x = tensors[j];
+    if (x.count < 0 || (x.count > 0 && (!x.parameter || !x.gradient || !x.first || !x.second)))
+      return TOPOS_HIP_INVALID_ARGUMENT;
+  }
+  const int status = Context::get().status();
+  if (status != TOPOS_HIP_OK) return status;
+  return guarded([&] {
+    AdamTable table{};
+    auto flush = [&] {
+      launch_adamw_multi(table, beta1, beta2, first_share, second_share, first_correction, second_correction,
+                         epsilon, rate, decay, static_cast<hipStream_t>(stream));
+      table = AdamTable{};
+    };
+    for (int64_t j = 0; j < count; ++j) {
+      const topos_hip_adamw_tensor &x = tensors[j];
+      if (x.count == 0) continue;
+      const int at = table.count;
+      table.parameter[at] = x.parameter;
+      table.gradient[at] = x.gradient;
+      table.first[at] = x.first;
+      table.second[at] = x.second;
+      table.decayed[at] = x.decayed != 0;
+      table.start[at + 1] = table.start[at] + x.count;
+      table.count = at + 1;
+      if (table.count == kAdamTensors) flush();
+    }
+    if (table.count > 0) flush();
   });
 }
 

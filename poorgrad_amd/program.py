@@ -164,6 +164,9 @@ class AdamW:
         self.moments = [(torch.zeros_like(p), torch.zeros_like(p)) for p in parameters]
 
     def step(self, parameters, gradient_pointers, rate: float) -> None:
+        """One AdamW::step over every parameter: the host bookkeeping, then one
+        many-parameter launch per 48 parameters (topos_hip_adamw_step_multi_f32,
+        the same per-element operations as the single-parameter entry)."""
         import torch
 
         f = np.float32
@@ -171,12 +174,13 @@ class AdamW:
         self.beta2_power = f(self.beta2_power * self.beta2)
         first_correction = f(1) - self.beta1_power
         second_correction = f(1) - self.beta2_power
-        stream = torch.cuda.current_stream().cuda_stream
-        for p, g, (m, v) in zip(parameters, gradient_pointers, self.moments):
-            decayed = 1 if p.dim() >= 2 else 0  # AdamW::step's rank >= 2 policy
-            n.checked(n.lib.topos_hip_adamw_step_f32(p.data_ptr(), g, m.data_ptr(), v.data_ptr(), p.numel(),
-                                                     float(self.beta1), float(self.beta2), float(self.first_share),
-                                                     float(self.second_share), float(first_correction),
-                                                     float(second_correction), float(self.epsilon), rate,
-                                                     float(self.decay), decayed, stream),
-                      "adamw step")
+        table = (n.AdamwTensor * len(parameters))()
+        for j, (p, g, (m, v)) in enumerate(zip(parameters, gradient_pointers, self.moments)):
+            table[j] = n.AdamwTensor(p.data_ptr(), g, m.data_ptr(), v.data_ptr(), p.numel(),
+                                     1 if p.dim() >= 2 else 0)  # AdamW::step's rank >= 2 policy
+        n.checked(n.lib.topos_hip_adamw_step_multi_f32(table, len(parameters), float(self.beta1), float(self.beta2),
+                                                       float(self.first_share), float(self.second_share),
+                                                       float(first_correction), float(second_correction),
+                                                       float(self.epsilon), rate, float(self.decay),
+                                                       torch.cuda.current_stream().cuda_stream),
+                  "adamw step")

@@ -1,0 +1,59 @@
+"""The many-parameter AdamW entry (topos_hip_adamw_step_multi_f32) against the
+single-parameter one, which the program tests hold to the oracle's
+restatement of AdamW::step (src/neural/adam.rs:62-171): the same bits for
+every parameter and moment, over three steps, with empty, one-element and
+large tensors, decayed and spared ones, and more tensors than one launch
+takes (48)."""
+import ctypes
+
+import numpy as np
+import pytest
+
+from tests.conftest import banner
+from tests.gpu_util import assert_bitwise
+
+pytestmark = pytest.mark.gpu
+
+
+def test_multi_tensor_adamw_equals_single_tensor_steps(hip):
+    import torch
+
+    banner("adamw multi-tensor vs single-tensor")
+    rng = np.random.default_rng(3)
+    sizes = [0, 1, 5, 768, 1000, 100003, 2304 * 768] + [int(s) for s in rng.integers(1, 5000, 60)]
+    make = lambda s: torch.from_numpy(rng.standard_normal(s).astype(np.float32)).cuda()
+    params = [make(s) for s in sizes]
+    grads = [make(s) for s in sizes]
+    decayed = [i % 3 != 0 for i in range(len(sizes))]
+    single = [(p.clone(), torch.zeros_like(p), torch.zeros_like(p)) for p in params]
+    multi = [(p.clone(), torch.zeros_like(p), torch.zeros_like(p)) for p in params]
+    f = np.float32
+    beta1, beta2, eps, decay, rate = f(0.9), f(0.999), f(1e-8), f(0.01), 3e-4
+    p1 = p2 = f(1)
+    stream = torch.cuda.current_stream().cuda_stream
+    for _ in range(3):
+        p1, p2 = f(p1 * beta1), f(p2 * beta2)
+        c1, c2 = f(1) - p1, f(1) - p2
+        scalars = (float(beta1), float(beta2), float(f(1) - beta1), float(f(1) - beta2), float(c1), float(c2),
+                   float(eps), rate, float(decay))
+        for (p, m, v), g, d in zip(single, grads, decayed):
+            hip.checked(hip.lib.topos_hip_adamw_step_f32(p.data_ptr(), g.data_ptr(), m.data_ptr(), v.data_ptr(),
+                                                         p.numel(), *scalars[:-1], scalars[-1], int(d), stream),
+                        "adamw single")
+        table = (hip.AdamwTensor * len(sizes))()
+        for j, ((p, m, v), g, d) in enumerate(zip(multi, grads, decayed)):
+            table[j] = hip.AdamwTensor(p.data_ptr(), g.data_ptr(), m.data_ptr(), v.data_ptr(), p.numel(), int(d))
+        hip.checked(hip.lib.topos_hip_adamw_step_multi_f32(table, len(sizes), *scalars, stream), "adamw multi")
+    torch.cuda.synchronize()
+    for j, (a, b) in enumerate(zip(single, multi)):
+        for name, x, y in zip(("parameter", "first", "second"), a, b):
+            assert_bitwise(y.cpu().numpy(), x.cpu().numpy(), f"tensor {j} ({sizes[j]}) {name}")
+
+
+def test_multi_tensor_adamw_refuses_bad_tables(hip):
+    table = (hip.AdamwTensor * 1)()
+    table[0] = hip.AdamwTensor(0, 0, 0, 0, 4, 1)
+    assert hip.lib.topos_hip_adamw_step_multi_f32(table, 1, 0.9, 0.999, 0.1, 0.001, 0.1, 0.001, 1e-8, 1e-3, 0.01,
+                                                  None) == hip.INVALID_ARGUMENT
+    assert hip.lib.topos_hip_adamw_step_multi_f32(None, 0, 0.9, 0.999, 0.1, 0.001, 0.1, 0.001, 1e-8, 1e-3, 0.01,
+                                                  None) == hip.OK
