@@ -2888,7 +2888,7 @@ const char *topos_hip_program_describe(const topos_hip_program *program) {
 void topos_hip_program_destroy(topos_hip_program *program) { delete program; }
 
 int topos_hip_sgd_step_f32(float *parameter, const float *gradient, int64_t count, float rate, void *stream) {
-  if (!parameter || !gradient || count < 0) return TOPOS_HIP_INVALID_ARGUMENT;
+  if (count < 0 || (count > 0 && (!parameter || !gradient))) return TOPOS_HIP_INVALID_ARGUMENT;
   const int status = Context::get().status();
   if (status != TOPOS_HIP_OK) return status;
   return guarded([&] { launch_sgd(parameter, gradient, count, rate, static_cast<hipStream_t>(stream)); });
