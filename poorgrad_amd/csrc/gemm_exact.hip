@@ -20,23 +20,27 @@ namespace {
 constexpr int kTileK = 32;
 constexpr int kThreads = 256;
 
+// How an operand is read: kGeneric element by element at any strides;
+// kInnerUnit with k contiguous (a lane loads four consecutive k values at
+// once); kOuterUnit with the outer axis contiguous (a lane loads four
+// consecutive outer elements at once). 16-byte loads serve any 4-byte
+// alignment on gfx950.
+enum { kGeneric = 0, kInnerUnit = 1, kOuterUnit = 2 };
+
 // One kTileK x E slab of an operand (outer index o0.., inner k0..) in a
 // lane's registers (fetch), then into lds[k][o] (deposit): the next slab's
-// loads are in flight while the current slab is multiplied. With k
-// contiguous (kUnitInner: k_stride is 1) a lane loads four consecutive k
-// values at once (16-byte loads serve any 4-byte alignment); otherwise
-// consecutive lanes read consecutive outer elements.
-template <int E, bool kUnitInner>
+// loads are in flight while the current slab is multiplied.
+template <int E, int kMode>
 struct Stage {
-  static constexpr int kQuads = E * kTileK / 4;                      // quads a slab (k contiguous)
+  static constexpr int kQuads = E * kTileK / 4;                      // quads a slab
   static constexpr int kQ = (kQuads + kThreads - 1) / kThreads;      // quads a lane
-  static constexpr int kS = E * kTileK / kThreads;                   // elements a lane (otherwise)
-  float v[kUnitInner ? 4 * kQ : kS];
+  static constexpr int kS = E * kTileK / kThreads;                   // elements a lane (generic)
+  float v[kMode == kGeneric ? kS : 4 * kQ];
 
   __device__ void fetch(const float *__restrict__ p, int64_t outer_stride, int64_t k_stride, int64_t outer_extent,
                         int64_t k, int64_t o0, int64_t k0) {
     const int t = threadIdx.x;
-    if (kUnitInner) {
+    if constexpr (kMode == kInnerUnit) {
 #pragma unroll
       for (int e = 0; e < kQ; ++e) {
         const int flat = e * kThreads + t;
@@ -54,6 +58,24 @@ struct Stage {
             v[4 * e + j] = (flat < kQuads && go < outer_extent && gk + j < k) ? p[go * outer_stride + gk + j] : 0.0f;
         }
       }
+    } else if constexpr (kMode == kOuterUnit) {
+#pragma unroll
+      for (int e = 0; e < kQ; ++e) {
+        const int flat = e * kThreads + t;
+        const int oq = flat % (E / 4), kk = flat / (E / 4);
+        const int64_t go = o0 + 4 * oq, gk = k0 + kk;
+        if (flat < kQuads && go + 3 < outer_extent && gk < k) {
+          const float4 w = *reinterpret_cast<const float4 *>(p + gk * k_stride + go);
+          v[4 * e] = w.x;
+          v[4 * e + 1] = w.y;
+          v[4 * e + 2] = w.z;
+          v[4 * e + 3] = w.w;
+        } else {
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            v[4 * e + j] = (flat < kQuads && go + j < outer_extent && gk < k) ? p[gk * k_stride + go + j] : 0.0f;
+        }
+      }
     } else {
 #pragma unroll
       for (int e = 0; e < kS; ++e) {
@@ -67,7 +89,7 @@ struct Stage {
 
   __device__ void deposit(float (*lds)[E + 4]) const {
     const int t = threadIdx.x;
-    if (kUnitInner) {
+    if constexpr (kMode == kInnerUnit) {
 #pragma unroll
       for (int e = 0; e < kQ; ++e) {
         const int flat = e * kThreads + t;
@@ -75,6 +97,14 @@ struct Stage {
         const int kq = flat % (kTileK / 4), o = flat / (kTileK / 4);
 #pragma unroll
         for (int j = 0; j < 4; ++j) lds[4 * kq + j][o] = v[4 * e + j];
+      }
+    } else if constexpr (kMode == kOuterUnit) {
+#pragma unroll
+      for (int e = 0; e < kQ; ++e) {
+        const int flat = e * kThreads + t;
+        if (flat >= kQuads) break;
+        const int oq = flat % (E / 4), kk = flat / (E / 4);
+        *reinterpret_cast<float4 *>(&lds[kk][4 * oq]) = make_float4(v[4 * e], v[4 * e + 1], v[4 * e + 2], v[4 * e + 3]);
       }
     } else {
 #pragma unroll
@@ -92,26 +122,28 @@ struct Stage {
 // multiplied from the other LDS buffer. (Measured on MI355X against 128x128
 // tiles of 8x8 accumulators: those need about 160 registers a lane, three
 // waves a SIMD and no room to prefetch; 4096-cubes went 30-34 -> 43 TFLOP/s.)
-template <int E, bool kLeftUnitInner, bool kRightUnitInner>
+template <int EM, int EN, int kLeftMode, int kRightMode>
 __global__ __launch_bounds__(kThreads) void gemm_exact_kernel(
     const float *__restrict__ a, int64_t a_rs, int64_t a_cs, const float *__restrict__ b,
     int64_t b_rs, int64_t b_cs, int64_t m, int64_t k, int64_t n, float *__restrict__ c, int64_t ldc,
     int64_t a_bs, int64_t b_bs, int64_t c_bs) {
-  static_assert(E == 64, "64x64 tiles");
+  // RM x RN accumulators a lane, 16 x 16 lanes over the EM x EN tile.
+  constexpr int RM = EM / 16, RN = EN / 16;
+  static_assert(EM * EN == 16 * 16 * RM * RN && (RM == 4 || RM == 2) && (RN == 4 || RN == 2), "tile shape");
   a += (int64_t)blockIdx.z * a_bs;
   b += (int64_t)blockIdx.z * b_bs;
   c += (int64_t)blockIdx.z * c_bs;
-  const int64_t m0 = (int64_t)blockIdx.y * E;
-  const int64_t n0 = (int64_t)blockIdx.x * E;
+  const int64_t m0 = (int64_t)blockIdx.y * EM;
+  const int64_t n0 = (int64_t)blockIdx.x * EN;
   const int tx = threadIdx.x % 16;
   const int ty = threadIdx.x / 16;
-  float acc[4][4];
+  float acc[RM][RN];
 
   {
-    __shared__ float left2[2][kTileK][E + 4];
-    __shared__ float right2[2][kTileK][E + 4];
-    Stage<E, kLeftUnitInner> sa;
-    Stage<E, kRightUnitInner> sb;
+    __shared__ __attribute__((aligned(16))) float left2[2][kTileK][EM + 4];
+    __shared__ __attribute__((aligned(16))) float right2[2][kTileK][EN + 4];
+    Stage<EM, kLeftMode> sa;
+    Stage<EN, kRightMode> sb;
     sa.fetch(a, a_rs, a_cs, m, k, m0, 0);
     sb.fetch(b, b_cs, b_rs, n, k, n0, 0);
     sa.deposit(left2[0]);
@@ -126,20 +158,31 @@ __global__ __launch_bounds__(kThreads) void gemm_exact_kernel(
       }
       const int steps = (k - k0) < kTileK ? (int)(k - k0) : kTileK;
       for (int s = 0; s < steps; ++s) {
-        const float4 a4 = *reinterpret_cast<const float4 *>(&left2[cur][s][ty * 4]);
-        const float4 b4 = *reinterpret_cast<const float4 *>(&right2[cur][s][tx * 4]);
-        const float av[4] = {a4.x, a4.y, a4.z, a4.w};
-        const float bv[4] = {b4.x, b4.y, b4.z, b4.w};
+        float av[RM], bv[RN];
+        if constexpr (RM == 4) {
+          const float4 a4 = *reinterpret_cast<const float4 *>(&left2[cur][s][ty * 4]);
+          av[0] = a4.x, av[1] = a4.y, av[2] = a4.z, av[3] = a4.w;
+        } else {
+          const float2 a2 = *reinterpret_cast<const float2 *>(&left2[cur][s][ty * 2]);
+          av[0] = a2.x, av[1] = a2.y;
+        }
+        if constexpr (RN == 4) {
+          const float4 b4 = *reinterpret_cast<const float4 *>(&right2[cur][s][tx * 4]);
+          bv[0] = b4.x, bv[1] = b4.y, bv[2] = b4.z, bv[3] = b4.w;
+        } else {
+          const float2 b2 = *reinterpret_cast<const float2 *>(&right2[cur][s][tx * 2]);
+          bv[0] = b2.x, bv[1] = b2.y;
+        }
         if (k0 == 0 && s == 0) {
 #pragma unroll
-          for (int i = 0; i < 4; ++i)
+          for (int i = 0; i < RM; ++i)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) acc[i][j] = __fmul_rn(av[i], bv[j]);  // the seed (gemm.rs:151-160)
+            for (int j = 0; j < RN; ++j) acc[i][j] = __fmul_rn(av[i], bv[j]);  // the seed (gemm.rs:151-160)
         } else {
 #pragma unroll
-          for (int i = 0; i < 4; ++i)
+          for (int i = 0; i < RM; ++i)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) acc[i][j] = __fadd_rn(acc[i][j], __fmul_rn(av[i], bv[j]));
+            for (int j = 0; j < RN; ++j) acc[i][j] = __fadd_rn(acc[i][j], __fmul_rn(av[i], bv[j]));
         }
       }
       if (more) {
@@ -152,12 +195,12 @@ __global__ __launch_bounds__(kThreads) void gemm_exact_kernel(
   }
 
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int64_t row = m0 + ty * 4 + i;
+  for (int i = 0; i < RM; ++i) {
+    const int64_t row = m0 + ty * RM + i;
     if (row >= m) continue;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int64_t col = n0 + tx * 4 + j;
+    for (int j = 0; j < RN; ++j) {
+      const int64_t col = n0 + tx * RN + j;
       if (col < n) c[row * ldc + col] = acc[i][j];
     }
   }
@@ -240,6 +283,40 @@ __global__ __launch_bounds__(kThreads) void gemm_exact_small_kernel(
 
 }  // namespace
 
+namespace {
+
+template <int EM, int EN, int L>
+void launch_exact_right(int right_mode, dim3 grid, hipStream_t stream, const float *a, int64_t a_rs, int64_t a_cs,
+                        const float *b, int64_t b_rs, int64_t b_cs, int64_t m, int64_t k, int64_t n, float *c,
+                        int64_t ldc, int64_t a_bs, int64_t b_bs, int64_t c_bs) {
+  if (right_mode == kInnerUnit)
+    gemm_exact_kernel<EM, EN, L, kInnerUnit><<<grid, kThreads, 0, stream>>>(a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c,
+                                                                            ldc, a_bs, b_bs, c_bs);
+  else if (right_mode == kOuterUnit)
+    gemm_exact_kernel<EM, EN, L, kOuterUnit><<<grid, kThreads, 0, stream>>>(a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c,
+                                                                            ldc, a_bs, b_bs, c_bs);
+  else
+    gemm_exact_kernel<EM, EN, L, kGeneric><<<grid, kThreads, 0, stream>>>(a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c,
+                                                                          ldc, a_bs, b_bs, c_bs);
+}
+
+template <int EM, int EN>
+void launch_exact_tile(int left_mode, int right_mode, dim3 grid, hipStream_t stream, const float *a, int64_t a_rs,
+                       int64_t a_cs, const float *b, int64_t b_rs, int64_t b_cs, int64_t m, int64_t k, int64_t n,
+                       float *c, int64_t ldc, int64_t a_bs, int64_t b_bs, int64_t c_bs) {
+  if (left_mode == kInnerUnit)
+    launch_exact_right<EM, EN, kInnerUnit>(right_mode, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc,
+                                           a_bs, b_bs, c_bs);
+  else if (left_mode == kOuterUnit)
+    launch_exact_right<EM, EN, kOuterUnit>(right_mode, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc,
+                                           a_bs, b_bs, c_bs);
+  else
+    launch_exact_right<EM, EN, kGeneric>(right_mode, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc,
+                                         a_bs, b_bs, c_bs);
+}
+
+}  // namespace
+
 void launch_gemm_exact(const float *a, int64_t a_rs, int64_t a_cs, const float *b, int64_t b_rs,
                        int64_t b_cs, int64_t m, int64_t k, int64_t n, float *c, int64_t ldc,
                        hipStream_t stream, const Batch &batch) {
@@ -265,21 +342,25 @@ void launch_gemm_exact(const float *a, int64_t a_rs, int64_t a_cs, const float *
     check_launch("gemm_exact_small_kernel launch");
     return;
   }
-  const int64_t grid_n64 = (n + 63) / 64, grid_m64 = (m + 63) / 64;
-  if (grid_m64 > 65535 || grid_n64 > 0x7fffffff) throw Unsupported{"exact gemm: product too tall for one launch"};
+  // The tile: 64x64 (4x4 accumulators a lane, the fewest LDS bytes per
+  // term) while that gives at least four workgroups a CU; narrower tiles
+  // (4x2, then 2x2 a lane) otherwise, trading LDS reads for occupancy on
+  // products with few outputs and long k (the weight gradients, k = 8192).
+  const int64_t tiles64x32 = ((m + 63) / 64) * ((n + 31) / 32) * batch.count;
+  const int shape = tiles64 >= 1024 ? 0 : tiles64x32 >= 768 ? 1 : 2;
+  const int em = shape == 2 ? 32 : 64, en = shape == 0 ? 64 : 32;
+  const int64_t grid_n = (n + en - 1) / en, grid_m = (m + em - 1) / em;
+  if (grid_m > 65535 || grid_n > 0x7fffffff) throw Unsupported{"exact gemm: product too tall for one launch"};
 #define TOPOS_EXACT_ARGS a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, a_bs, b_bs, c_bs
-#define TOPOS_EXACT_LAUNCH(E, g)                                                        \
-  if (left_unit && right_unit)                                                          \
-    gemm_exact_kernel<E, true, true><<<g, kThreads, 0, stream>>>(TOPOS_EXACT_ARGS);     \
-  else if (left_unit)                                                                   \
-    gemm_exact_kernel<E, true, false><<<g, kThreads, 0, stream>>>(TOPOS_EXACT_ARGS);    \
-  else if (right_unit)                                                                  \
-    gemm_exact_kernel<E, false, true><<<g, kThreads, 0, stream>>>(TOPOS_EXACT_ARGS);    \
-  else                                                                                  \
-    gemm_exact_kernel<E, false, false><<<g, kThreads, 0, stream>>>(TOPOS_EXACT_ARGS);
-  const dim3 grid64((unsigned)grid_n64, (unsigned)grid_m64, (unsigned)batch.count);
-  TOPOS_EXACT_LAUNCH(64, grid64)
-#undef TOPOS_EXACT_LAUNCH
+  const int left_mode = left_unit ? kInnerUnit : a_rs == 1 ? kOuterUnit : kGeneric;
+  const int right_mode = right_unit ? kInnerUnit : b_cs == 1 ? kOuterUnit : kGeneric;
+  const dim3 grid((unsigned)grid_n, (unsigned)grid_m, (unsigned)batch.count);
+  if (shape == 0)
+    launch_exact_tile<64, 64>(left_mode, right_mode, grid, stream, TOPOS_EXACT_ARGS);
+  else if (shape == 1)
+    launch_exact_tile<64, 32>(left_mode, right_mode, grid, stream, TOPOS_EXACT_ARGS);
+  else
+    launch_exact_tile<32, 32>(left_mode, right_mode, grid, stream, TOPOS_EXACT_ARGS);
 #undef TOPOS_EXACT_ARGS
   check_launch("gemm_exact_kernel launch");
 }
