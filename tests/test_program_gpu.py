@@ -419,6 +419,28 @@ def test_long_column_folds_exact(hip):
         assert_bitwise(got[r.id], want[r.id], f"node {r.id} {r.shape}")
 
 
+@pytest.mark.parametrize("steps, columns", [(5000, 24), (8192, 768), (2048, 12), (600, 4096), (4099, 8), (300, 16384)])
+def test_column_fold_shapes_exact(hip, steps, columns):
+    """Column folds over several whole and partial tiles, at 16 and 64
+    outputs a workgroup, the bias-gradient shape [8192, 768], an all -0
+    column, a zero-seeded accumulation of the fold and a fused operand:
+    bit-identical to the ordered fold."""
+    banner(f"program column fold widths {steps}x{columns}")
+    rng = np.random.default_rng(steps + columns)
+    tape = t.Tape()
+    x = tape.input((steps, columns))
+    y = tape.input((steps, columns))
+    folded = (x * y - x).sum_along(0)
+    roots = [x.sum_along(0), folded + folded.zero_like(), (x * x).maximum(y).sum_along(0)]
+    dense = {x.node.slot: rng.standard_normal((steps, columns)).astype(np.float32),
+             y.node.slot: rng.standard_normal((steps, columns)).astype(np.float32)}
+    dense[x.node.slot][:, 0] = -0.0   # an all -0 column: -0 from the fold, +0 after the seed
+    want = run_oracle(tape, roots, [], dense)
+    got, _ = run_device(tape, roots, [], dense, numerics=hip.EXACT)
+    for r in roots:
+        assert_bitwise(got[r.id], want[r.id], f"node {r.id} {r.shape}")
+
+
 @pytest.mark.parametrize("rows, columns", [(37, 1100), (24, 1028), (130, 40), (9, 3), (5, 9001), (70, 3000)])
 def test_row_groups_exact(hip, rows, columns):
     """Row programs (groups of row-local nodes with last-axis reductions):
