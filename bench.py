@@ -478,8 +478,19 @@ def chains_section(torch, n, steps: int, warmup: int) -> dict:
                                                                      g.data_ptr(), b.data_ptr(), 1e-5, numerics,
                                                                      y.data_ptr(), stream), "layer norm")
 
-    launches = [("silu_bias", run_silu)]
-    bytes_of = {"silu_bias": CHAIN_BYTES["silu_bias"]}
+    # Reference points for what this device moves on the same tensor: a plain
+    # read + write (torch's copy) and a generated chain with one addition
+    # (x + b), against which the SiLU + bias chain, also one read and one
+    # write per element, is measured; the fast row sum is the read-only one.
+    add_bias = device.Chain((CHAIN_ROWS, CHAIN_COLUMNS), [((CHAIN_COLUMNS, 1), 0), ((0, 1), 0)],
+                            [(n.CHAIN_ADD, -1, -2)], [0])
+
+    def run_add_bias():
+        n.checked(lib.topos_hip_chain_launch(add_bias._handle, ins, outs, stream), "add chain")
+
+    launches = [("silu_bias", run_silu), ("reference_copy", lambda: y.copy_(x)), ("reference_add_bias", run_add_bias)]
+    bytes_of = {"silu_bias": CHAIN_BYTES["silu_bias"], "reference_copy": 8 * CHAIN_ROWS * CHAIN_COLUMNS,
+                "reference_add_bias": CHAIN_BYTES["silu_bias"]}
     for posture, numerics in (("exact", n.EXACT), ("fast", n.FAST)):
         for name, fn in (("layer_norm", layer_norm(numerics)), ("row_sum", rows(n.ROWS_SUM, stats, numerics)),
                          ("row_max", rows(n.ROWS_MAX, stats, numerics)),

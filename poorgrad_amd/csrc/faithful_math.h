@@ -130,33 +130,48 @@ static const LogRow kLog2TableHost[16] = {
 // 1.5 * 2^52 shift; 2^(k/32) = table[k mod 32] with k/32 added to the exponent
 // field; 2^(r/32) by a cubic. The product x * 32/ln2 is fused into both the
 // shift addition and the remainder subtraction, as the FMA build of glibc does.
-// glibc's special cases (NaN, e^+-inf, overflow above 0x1.62e42ep6, underflow
-// below -0x1.9fe368p6) are applied as selects after the common arithmetic, so
-// the common path has no branch; on those inputs the arithmetic is harmless
-// (the table index is still k mod 32) and its value is discarded.
+// glibc's special cases need no branch and no select but NaN's: the argument
+// is clamped to [-104, 89] first, and the arithmetic itself gives glibc's
+// values beyond its thresholds. Above 0x1.62e42ep6 (the largest f32 whose
+// e^x stays below 2^128) the next f32 already has e^x > 2^128 (1 + 2.4e-7),
+// and e^89, so the double rounds to +inf (e^+inf = +inf). Below -0x1.9fe368p6
+// the next f32 has e^x < 2^-150 (1 - 7e-6), and e^-104 < 2^-150, so it rounds
+// to +0 (e^-inf = +0). The double's relative error (below 2^-40) is far inside
+// both margins. A NaN argument gives x + x, the quieted NaN, as glibc does;
+// the arithmetic on it stays harmless (the table index is still k mod 32).
 TOPOS_HD float exp_f32_table(float x, const uint64_t *table) {
   const double inv_ln2_scaled = 0x1.71547652b82fep+0 * 32;
   const double shift = 0x1.8p+52;
   const double c0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32;
   const double c1 = 0x1.ebfce50fac4f3p-3 / 32 / 32;
   const double c2 = 0x1.62e42ff0c52d6p-1 / 32;
-  const double xd = (double)x;
+#if defined(__HIP_DEVICE_COMPILE__) || defined(__HIPCC_RTC__)
+  const float clamped = __builtin_amdgcn_fmed3f(x, -104.0f, 89.0f);
+#else
+  const float clamped = x < -104.0f ? -104.0f : (x > 89.0f ? 89.0f : x);
+#endif
+  const double xd = (double)clamped;
   double kd = __builtin_fma(inv_ln2_scaled, xd, shift);
-  const uint64_t ki = bits_of(kd);
+  const uint32_t k = (uint32_t)bits_of(kd);  // k mod 2^32: the low word of the shifted sum
   kd -= shift;
   const double r = __builtin_fma(inv_ln2_scaled, xd, -kd);
-  uint64_t t = table[ki % 32];
-  t += ki << (52 - 5);
-  const double s = double_of(t);
+  // table[k mod 32] + (k << 47): the shifted k has a zero low word, so only
+  // the entry's high word changes, by (k << 15) mod 2^32.
+  const uint64_t entry = table[k % 32];
+  const uint32_t s_low = (uint32_t)entry, s_high = (uint32_t)(entry >> 32) + (k << 15);
+#if defined(__HIP_DEVICE_COMPILE__) || defined(__HIPCC_RTC__)
+  typedef uint32_t word_pair __attribute__((ext_vector_type(2)));
+  const double s = __builtin_bit_cast(double, word_pair{s_low, s_high});
+#else
+  const double s = double_of((uint64_t)s_high << 32 | s_low);
+#endif
   const double z = __builtin_fma(c0, r, c1);
   const double r2 = r * r;
   double y = __builtin_fma(c2, r, 1.0);
   y = __builtin_fma(z, r2, y);
   y = y * s;
-  float result = (float)y;
-  result = x < -0x1.9fe368p6f ? 0.0f : result;                  // underflow, e^-inf = +0
-  result = x > 0x1.62e42ep6f ? float_of(0x7f800000u) : result;  // overflow, e^inf = inf
-  return x != x ? x + x : result;                               // NaN
+  const float result = (float)y, quiet = x + x;
+  return x != x ? quiet : result;
 }
 
 // e^x with the built-in table (a kernel may pass a copy it keeps in LDS).
