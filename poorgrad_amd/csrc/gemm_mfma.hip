@@ -311,6 +311,23 @@ __device__ __forceinline__ int dma_outer_index(int kk, int o) {
 
 #define TOPOS_COMPILER_FENCE() __atomic_signal_fence(__ATOMIC_SEQ_CST)
 
+// One wave-wide global_load_lds_dwordx4: each lane's 16 bytes at `src` land
+// in LDS at `lds` + 16 * lane (M0 holds the wave's LDS byte address). Issued
+// as inline assembly: the compiler's wait insertion treats a DMA issued
+// through the builtin as a pending LDS write that every later LDS read must
+// wait for, which put a vmcnt(0) before each slab's fragment reads and so
+// waited for the slab two ahead as well; the kernel orders its DMA itself
+// (dma_wait, then a barrier).
+__device__ __forceinline__ void dma_load16(const float *src, uint32_t lds_byte) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds_byte)
+               : "memory", "m0");
+}
+
+// The LDS byte address of an LDS location.
+__device__ __forceinline__ uint32_t lds_byte_address(const float *p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) float *)p;
+}
+
 // One slab (16 deep) of an operand with outer extent O into `lds`.
 template <int O, int W, bool kInnerK>
 __device__ __forceinline__ void dma_slab(const float *__restrict__ p, int64_t outer_stride, int64_t k_stride,
@@ -335,7 +352,7 @@ __device__ __forceinline__ void dma_slab(const float *__restrict__ p, int64_t ou
       src = p + (k0 + kk) * k_stride + col;
     }
     TOPOS_COMPILER_FENCE();
-    __builtin_amdgcn_global_load_lds(src, lds + c * 256, 16, 0, 0);
+    dma_load16(src, lds_byte_address(lds) + 1024 * c);
     TOPOS_COMPILER_FENCE();
   }
 }
@@ -453,7 +470,7 @@ __device__ __forceinline__ void dma_mfma_slab(const float *sa, const float *sb, 
 }
 
 template <int BM, int BN, int WM, bool kLeftInnerK, bool kRightInnerK, bool kT>
-__global__ __launch_bounds__(BM / WM * BN) void gemm_dma_kernel(
+__global__ __launch_bounds__(BM / WM * BN, BM == 256 ? 4 : 1) void gemm_dma_kernel(
     const float *__restrict__ a, int64_t a_rs, int64_t a_cs, const float *__restrict__ b, int64_t b_rs,
     int64_t b_cs, int64_t m, int64_t k, int64_t n, float *__restrict__ c, int64_t ldc, int grid_m, int grid_n,
     int64_t a_bs, int64_t b_bs, int64_t c_bs, int64_t split_len, int64_t split_stride,
@@ -488,7 +505,9 @@ __global__ __launch_bounds__(BM / WM * BN) void gemm_dma_kernel(
   const int64_t n0 = (int64_t)tile_n * BN;
 
   const int lane = threadIdx.x % 64;
-  const int wave = threadIdx.x / 64;
+  // Wave-uniform (a scalar register): the DMA's LDS addresses, the waves'
+  // block origins and the stage offsets stay scalar arithmetic.
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
   const int wm = (wave / WN) * WM;
   const int wn = (wave % WN) * 64;
   const int half = lane / 32, l32 = lane % 32;
