@@ -744,13 +744,13 @@ def test_fast_batched_products_with_edges(hip, form):
 
 
 @pytest.mark.parametrize("form", ["plain", "left_transposed", "right_transposed"])
-@pytest.mark.parametrize("shape", [(256, 257, 72, 130), (200, 61, 40, 998)])
+@pytest.mark.parametrize("shape", [(256, 257, 72, 130), (200, 61, 40, 998), (64, 520, 64, 700), (130, 300, 24, 257)])
 def test_fast_many_short_products(hip, form, shape):
     """Many short batched products (k at most 128, over a thousand output
     tiles, like the attention scores): 256x128 tiles with a k tail and
-    row/column overhang, and 64x128 tiles with a ragged outer-contiguous
-    edge, in each operand orientation. Within the envelope of the
-    interpreter's exact product."""
+    row/column overhang (k of 72, 64 and 24), and 64x128 tiles with a ragged
+    outer-contiguous edge, in each operand orientation. Within the envelope
+    of the interpreter's exact product."""
     B, M, K, N = shape
     banner(f"program fast many short products {form} {shape}")
     rng = np.random.default_rng(47)
