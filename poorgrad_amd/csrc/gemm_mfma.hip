@@ -469,8 +469,50 @@ __device__ __forceinline__ void dma_mfma_slab(const float *sa, const float *sb, 
   }
 }
 
+// The epilogue of an interior tile through LDS (transposed accumulator
+// blocks of 64-row waves): each half of a wave's 64x64 block (32 rows) goes
+// into the wave's own LDS region, then every store instruction writes four
+// whole 256-byte row segments (16 lanes a row, 16 bytes a lane) instead of
+// 32-byte pieces of 32 rows. `stage` holds 32 x 68 floats for this wave.
+__device__ __forceinline__ void store_block_staged(const floatx16 (&acc)[2][2], float *__restrict__ c, int64_t ldc,
+                                                   int64_t m0, int64_t n0, int wm, int wn, int lane,
+                                                   const float *__restrict__ bias, int64_t bias_cs, int bias_mode,
+                                                   float *stage) {
+  constexpr int kStride = 68;
+  const int h = lane / 32, r = lane % 32;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int col = 32 * j + 8 * g + 4 * h;
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          v[e] = acc[i][j][4 * g + e];
+          if (bias_mode != 0) {
+            const float add = bias[(n0 + wn + col + e) * bias_cs];
+            v[e] = bias_mode == 1 ? v[e] + add : add + v[e];
+          }
+        }
+        *reinterpret_cast<float4 *>(stage + r * kStride + col) = make_float4(v[0], v[1], v[2], v[3]);
+      }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // this wave's LDS writes done (lgkmcnt(0))
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int row = 4 * q + lane / 16, col = 4 * (lane % 16);
+      const float4 v = *reinterpret_cast<const float4 *>(stage + row * kStride + col);
+      *reinterpret_cast<float4 *>(c + (m0 + wm + 32 * i + row) * ldc + n0 + wn + col) = v;
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // the reads are done before the next half overwrites
+  }
+}
+
 template <int BM, int BN, int WM, bool kLeftInnerK, bool kRightInnerK, bool kT>
-__global__ __launch_bounds__(BM / WM * BN, BM == 256 ? 4 : 1) void gemm_dma_kernel(
+// (Register budgets: 128 for the 256-row tiles, two workgroups a CU; 168 for
+// the others, three a CU.)
+__global__ __launch_bounds__(BM / WM * BN, BM == 256 ? 4 : 3) void gemm_dma_kernel(
     const float *__restrict__ a, int64_t a_rs, int64_t a_cs, const float *__restrict__ b, int64_t b_rs,
     int64_t b_cs, int64_t m, int64_t k, int64_t n, float *__restrict__ c, int64_t ldc, int grid_m, int grid_n,
     int64_t a_bs, int64_t b_bs, int64_t c_bs, int64_t split_len, int64_t split_stride,
@@ -559,6 +601,16 @@ __global__ __launch_bounds__(BM / WM * BN, BM == 256 ? 4 : 1) void gemm_dma_kern
     }
   }
 
+  // Interior tiles of 64-row waves store through LDS in whole row segments
+  // (measured on the attention-scores product, which writes 402 MB for 12.9
+  // GFLOP: 198 -> 172 us).
+  if constexpr (kT && WM == 64) {
+    if (m0 + BM <= m && n0 + BN <= n) {
+      dma_barrier();  // every wave's last fragment reads are done before LDS is reused
+      store_block_staged(acc, c, ldc, m0, n0, wm, wn, lane, bias, bias_cs, bias_mode, lds + wave * 32 * 68);
+      return;
+    }
+  }
   store_block<WM, kT>(acc, c, ldc, m, n, m0, n0, wm, wn, lane, bias, bias_cs, bias_mode);
 }
 
