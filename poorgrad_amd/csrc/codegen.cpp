@@ -231,6 +231,18 @@ std::string preamble() {
        "  __syncthreads();\n"
        "}\n"
        "__device__ __forceinline__ float topos_exp(float x) { return topos_faithful::exp_f32_table(x, topos_exp_lds); }\n"
+       // e^x of a lane's four points. When every point of every lane of the
+       // wave is at most -104, each e^x rounds to +0 (e^-104 < 2^-150), and
+       // the wave skips the evaluation: the masked half of a causal softmax.
+       "__device__ __forceinline__ void topos_exp4(float x0, float x1, float x2, float x3, float &y0, float &y1,\n"
+       "                                           float &y2, float &y3) {\n"
+       "  const bool zero = x0 <= -104.0f && x1 <= -104.0f && x2 <= -104.0f && x3 <= -104.0f;\n"
+       "  if (__builtin_amdgcn_ballot_w64(!zero) == 0) {\n"
+       "    y0 = 0.0f; y1 = 0.0f; y2 = 0.0f; y3 = 0.0f;\n"
+       "  } else {\n"
+       "    y0 = topos_exp(x0); y1 = topos_exp(x1); y2 = topos_exp(x2); y3 = topos_exp(x3);\n"
+       "  }\n"
+       "}\n"
        "__device__ __forceinline__ float topos_ln(float x) { return topos_faithful::ln_f32_table(x, topos_log_lds); }\n"
        "__device__ __forceinline__ float topos_pow(float x, float y) {\n"
        "  return topos_faithful::pow_f32_tables(x, y, topos_log2_lds, topos_exp_lds);\n"
@@ -1100,6 +1112,16 @@ struct RowEmit {
     for (int k = 0; k < n; ++k) {
       if (!nodes_needed[k]) continue;
       const RowNode &y = p.nodes[k];
+      if (lanes.size() == 4 && y.kind == RowNode::kFullOp && y.op == TOPOS_HIP_CHAIN_EXP) {
+        std::string args, outs;
+        for (int j = 0; j < 4; ++j) {
+          s << indent << "float f" << k << "_" << lanes[j] << ";\n";
+          args += full_name(y.a, lanes[j], r) + ", ";
+          outs += (j ? ", f" : "f") + std::to_string(k) + "_" + lanes[j];
+        }
+        s << indent << "topos_exp4(" << args << outs << ");\n";
+        continue;
+      }
       for (const std::string &lane : lanes) {
         std::string value;
         const std::string a = full_name(y.a, lane, r);
@@ -1114,6 +1136,26 @@ struct RowEmit {
         s << indent << "const float f" << k << "_" << lane << " = " << value << ";\n";
       }
     }
+  }
+  // The operands of fold f at a point's four lanes, as a make_float4
+  // argument list (a shifted exponential's four go through topos_exp4 first).
+  std::string fold_operands4(std::ostringstream &s, const RowFold &f, const std::vector<std::string> &lanes,
+                             const std::string &r, const std::string &indent, const std::string &tag) const {
+    std::string list;
+    if (!f.shifted_exp) {
+      for (int j = 0; j < 4; ++j) list += (j ? ", " : "") + fold_operand(f, lanes[j], r);
+      return list;
+    }
+    const std::string shift = " - rowv[" + std::to_string(l.max_slot[f.node]) + "][" + r + "]";
+    std::string args;
+    for (int j = 0; j < 4; ++j) {
+      const std::string e = "e" + tag + "_" + std::to_string(j);
+      s << indent << "float " << e << ";\n";
+      args += full_name(p.nodes[f.node].a, lanes[j], r) + shift + ", ";
+      list += (j ? ", " : "") + e;
+    }
+    s << indent << "topos_exp4(" << args << list << ");\n";
+    return list;
   }
   // The operand of fold f at one lane.
   std::string fold_operand(const RowFold &f, const std::string &lane, const std::string &r) const {
@@ -1265,9 +1307,8 @@ Generated generate_row_resident(const RowProgram &p, const RowLayout &l, const R
         s << "  if (ok" << I << ") {\n";
         m.emit_nodes(s, nodes_needed, lanes, "r" + I, "    ");
         if (V == 4) {
-          s << "    *(float4*)&slab[r" << I << "][col" << I << "] = make_float4(";
-          for (int j = 0; j < 4; ++j) s << (j ? ", " : "") << m.fold_operand(f, lanes[j], "r" + I);
-          s << ");\n";
+          const std::string list = m.fold_operands4(s, f, lanes, "r" + I, "    ", I);
+          s << "    *(float4*)&slab[r" << I << "][col" << I << "] = make_float4(" << list << ");\n";
         } else {
           s << "    slab[r" << I << "][col" << I << "] = " << m.fold_operand(f, lanes[0], "r" + I) << ";\n";
         }
@@ -1447,9 +1488,8 @@ Generated generate_row_streaming(const RowProgram &p, const RowLayout &l, const 
       m.emit_nodes(s, nodes_needed, lanes, "r" + I, "      ");
       for (size_t j = 0; j < folds.size(); ++j) {
         if (V == 4) {
-          s << "      *(float4*)&slab[" << j << "][r" << I << "][cu" << I << "] = make_float4(";
-          for (int v = 0; v < 4; ++v) s << (v ? ", " : "") << m.fold_operand(*folds[j], lanes[v], "r" + I);
-          s << ");\n";
+          const std::string list = m.fold_operands4(s, *folds[j], lanes, "r" + I, "      ", I + "_" + std::to_string(j));
+          s << "      *(float4*)&slab[" << j << "][r" << I << "][cu" << I << "] = make_float4(" << list << ");\n";
         } else {
           s << "      slab[" << j << "][r" << I << "][cu" << I << "] = " << m.fold_operand(*folds[j], lanes[0], "r" + I)
             << ";\n";
