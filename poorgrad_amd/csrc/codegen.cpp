@@ -442,34 +442,60 @@ Generated generate_chain(const Expr &e) {
     // An odd innermost extent: quads run along each row from its start
     // (16-byte accesses at any alignment), the row's last partial quad lane
     // by lane.
+    // U quads a lane per iteration, every quad's loads issued before any
+    // use: a partial quad (a row's last) or one past the end loads its row's
+    // first quad instead, which is always whole and in range, and is then
+    // evaluated lane by lane.
     const int64_t quads_per_row = (inner_extent + 3) / 4;
     const int64_t total = volume / inner_extent * quads_per_row;
-    s << "  for (long long qi = (long long)blockIdx.x * 256 + threadIdx.x; qi < " << ll(total)
-      << "; qi += (long long)gridDim.x * 256) {\n";
-    s << "    const long long row = qi / " << ll(quads_per_row) << ";\n";
-    s << "    const long long cq = (qi % " << ll(quads_per_row) << ") * 4;\n";
-    s << "    const long long base = row * " << ll(inner_extent) << " + cq;\n";
-    s << "    if (cq + 4 <= " << ll(inner_extent) << ") {\n";
-    std::vector<std::string> c;
-    if (e.rank > 1) emit_coordinates(s, e.rank - 1, e.shape, "row", "q", c);
-    c.push_back("cq");
-    emit_quad_inputs(s, e, c, "q", lanes, "      ");
-    emit_steps(s, e, lanes);
-    for (size_t o = 0; o < e.outputs.size(); ++o) {
-      s << "      *(topos_f4*)(q" << o << " + base) = topos_f4{";
-      for (int j = 0; j < 4; ++j) s << (j ? ", " : "") << ref(e.outputs[o], lanes[j]);
-      s << "};\n";
+    const int U = chain_unroll(e);
+    s << "  for (long long qb = (long long)blockIdx.x * " << 256 * U << "; qb < " << ll(total)
+      << "; qb += (long long)gridDim.x * " << 256 * U << ") {\n";
+    std::vector<std::string> all_lanes;
+    for (int u = 0; u < U; ++u) {
+      const std::string tag = "q" + std::to_string(u), U_ = std::to_string(u);
+      std::vector<std::string> lanes_u;
+      for (int j = 0; j < 4; ++j) lanes_u.push_back(tag + "_" + std::to_string(j));
+      all_lanes.insert(all_lanes.end(), lanes_u.begin(), lanes_u.end());
+      s << "    const long long qi" << U_ << " = qb + " << 256 * u << " + threadIdx.x;\n";
+      s << "    const bool in" << U_ << " = qi" << U_ << " < " << ll(total) << ";\n";
+      s << "    const long long row" << U_ << " = in" << U_ << " ? qi" << U_ << " / " << ll(quads_per_row) << " : 0;\n";
+      s << "    const long long cq" << U_ << " = in" << U_ << " ? (qi" << U_ << " % " << ll(quads_per_row)
+        << ") * 4 : 0;\n";
+      s << "    const bool whole" << U_ << " = in" << U_ << " && cq" << U_ << " + 4 <= " << ll(inner_extent) << ";\n";
+      s << "    const long long lc" << U_ << " = whole" << U_ << " ? cq" << U_ << " : 0;\n";
+      std::vector<std::string> c;
+      if (e.rank > 1) emit_coordinates(s, e.rank - 1, e.shape, "row" + U_, tag, c);
+      c.push_back("lc" + U_);
+      emit_quad_inputs(s, e, c, tag, lanes_u, "    ");
     }
-    s << "    } else {\n";
-    s << "      for (int j = 0; cq + j < " << ll(inner_extent) << "; ++j) {\n";
-    s << "        const long long f = base + j;\n";
-    std::vector<std::string> cg;
-    emit_coordinates(s, e.rank, e.shape, "f", "g", cg);
-    for (size_t i = 0; i < e.inputs.size(); ++i)
-      s << "        const float in" << i << "_g = " << scalar_value(e, (int)i, cg) << ";\n";
-    emit_steps(s, e, {"g"});
-    for (size_t o = 0; o < e.outputs.size(); ++o) s << "        q" << o << "[f] = " << ref(e.outputs[o], "g") << ";\n";
-    s << "      }\n    }\n  }\n}\n";
+    emit_steps(s, e, all_lanes);
+    for (int u = 0; u < U; ++u) {
+      const std::string tag = "q" + std::to_string(u), U_ = std::to_string(u);
+      s << "    if (whole" << U_ << ") {\n";
+      for (size_t o = 0; o < e.outputs.size(); ++o) {
+        s << "      *(topos_f4*)(q" << o << " + row" << U_ << " * " << ll(inner_extent) << " + cq" << U_
+          << ") = topos_f4{";
+        for (int j = 0; j < 4; ++j) s << (j ? ", " : "") << ref(e.outputs[o], tag + "_" + std::to_string(j));
+        s << "};\n";
+      }
+      s << "    }\n";
+    }
+    for (int u = 0; u < U; ++u) {
+      const std::string U_ = std::to_string(u);
+      s << "    if (in" << U_ << " && !whole" << U_ << ") {\n";
+      s << "      const long long base = row" << U_ << " * " << ll(inner_extent) << " + cq" << U_ << ";\n";
+      s << "      for (int j = 0; cq" << U_ << " + j < " << ll(inner_extent) << "; ++j) {\n";
+      s << "        const long long f = base + j;\n";
+      std::vector<std::string> cg;
+      emit_coordinates(s, e.rank, e.shape, "f", "g", cg);
+      for (size_t i = 0; i < e.inputs.size(); ++i)
+        s << "        const float in" << i << "_g = " << scalar_value(e, (int)i, cg) << ";\n";
+      emit_steps(s, e, {"g"});
+      for (size_t o = 0; o < e.outputs.size(); ++o) s << "        q" << o << "[f] = " << ref(e.outputs[o], "g") << ";\n";
+      s << "      }\n    }\n";
+    }
+    s << "  }\n}\n";
     return make(s.str());
   }
   const bool quads = e.rank > 0 && e.shape[e.rank - 1] % 4 == 0;
@@ -541,7 +567,8 @@ void launch_generated_chain(const Generated &g, const Expr &e, const void *const
   std::vector<void *> arguments;
   for (auto &p : pointers) arguments.push_back(&p);
   const bool quads = e.rank > 0 && e.shape[e.rank - 1] % 4 == 0;
-  const int64_t per_block = quads ? 1024LL * chain_unroll(e) : 1024;
+  const bool odd_rows = e.rank > 0 && e.shape[e.rank - 1] % 4 != 0 && e.shape[e.rank - 1] >= 8;
+  const int64_t per_block = quads || odd_rows ? 1024LL * chain_unroll(e) : 1024;
   int64_t blocks = (e.volume() + per_block - 1) / per_block;
   if (blocks < 1) blocks = 1;
   if (blocks > 256 * 16) blocks = 256 * 16;

@@ -803,3 +803,33 @@ def test_fast_head_merging_views_within_envelope(hip):
     for r in (loss, merged, grad):
         g, e = got[r.id].astype(np.float64), want[r.id].astype(np.float64)
         assert (np.abs(g - e) <= 1e-4 * np.maximum(np.abs(e), 1.0)).all(), f"node {r.id}"
+
+
+@pytest.mark.parametrize("columns", [1024, 768])
+def test_row_softmax_underflow_skip_is_exact(hip, columns):
+    """A row program's exponentials of a point are skipped when every point
+    of the wave lies at or below -104 after the max shift (each e^x then
+    rounds to +0). Rows whose tail columns hold -inf, -1e30, -200, -104 and
+    values just above it (-103.99, -103.97, -103.9: e^x is 0 or the smallest
+    subnormals) beside a normal head: bitwise against the interpreter, in the
+    softmax and log-softmax and in the gradient (src/function/log_softmax.rs:51-72)."""
+    banner(f"program softmax underflow skip {columns}")
+    rng = np.random.default_rng(53)
+    tails = [-np.inf, -1e30, -200.0, -104.0, -103.99, -103.97, -103.9, -50.0]
+    rows = 64
+    x = (-rng.random((rows, columns))).astype(np.float32)  # head values in (-1, 0]
+    for r in range(rows):
+        start = 64 + 64 * (r % 4)
+        x[r, start:] = np.float32(tails[r % len(tails)])
+        x[r, 0] = np.float32(0.0)  # the maximum: a tail's shifted value is the tail itself
+    tape = t.Tape()
+    a = tape.parameter((rows, columns))
+    soft = a.softmax(1)
+    logsoft = a.log_softmax(1)
+    loss = (soft * soft).sum() + logsoft.sum()
+    grads = tape.differentiate(loss, [a])
+    roots = [soft, logsoft, loss] + grads
+    want = run_oracle(tape, roots, [x])
+    got, _ = run_device(tape, roots, [x], numerics=hip.EXACT)
+    for r in roots:
+        assert_bitwise(got[r.id], want[r.id], f"node {r.id} {r.shape}")
