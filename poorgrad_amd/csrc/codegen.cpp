@@ -588,13 +588,19 @@ int64_t fold_width(int64_t outputs) { return outputs / 64 >= 256 ? 64 : 16; }
 namespace {
 
 // Column form with a quad-divisible innermost extent and 16 outputs per
-// workgroup: each lane evaluates the expression on quads (four consecutive
-// outputs at one step, one 16-byte load per unit-stride input) and parks
-// them transposed in LDS as tile[output][step], so lane j < 16 folds output
-// j from 16-byte LDS reads. A tile is kColumnSteps steps; the next tile's
-// quads are loaded before the fold of the current one, so their latency
-// hides behind it. Workgroups are renumbered so that neighbouring column
-// bands (which share cache lines) run on the same XCD.
+// workgroup: each lane loads the expression's inputs at quads (four
+// consecutive outputs at one step, one 16-byte load per unit-stride input),
+// evaluates them, and parks the values transposed in LDS as
+// tile[buffer][output][step], so lane j < 16 folds output j from 16-byte LDS
+// reads. A tile is kColumnSteps steps. Two register sets hold the raw inputs
+// of the next two tiles, their loads in flight while the current tile is
+// folded; a set is evaluated only when it is parked (two folds after its
+// loads were issued), so no load is waited on before a fold. The two LDS
+// buffers alternate, one barrier a tile. Workgroups are renumbered so that
+// neighbouring column bands (which share cache lines) run on the same XCD.
+// (Measured on MI355X, [8192, 768] folds: 45 us with one input and 93 us
+// with three inputs and two steps when the next tile's loads were issued
+// just before the fold and evaluated right after them.)
 constexpr int kColumnQuads = 8;                                // quads per lane per tile
 constexpr int kColumnSteps = kColumnQuads * 256 * 4 / 16;      // 512 steps per tile
 
@@ -605,89 +611,128 @@ Generated generate_column_fold(const Expr &e, int axis, FoldKind kind, const std
   std::ostringstream s;
   s << preamble();
   s << signature(e, "float* __restrict__ out") << " {\n  topos_tables_init();\n";
-  s << "  __shared__ __attribute__((aligned(16))) float tile[" << W << "][" << H + 4 << "];\n";
+  s << "  __shared__ __attribute__((aligned(16))) float tile[2][" << W << "][" << H + 4 << "];\n";
   s << "  const int t = threadIdx.x;\n";
   s << "  const unsigned blocks = gridDim.x;\n";
   s << "  unsigned b = blockIdx.x;\n";
   s << "  if (blocks % 8 == 0) b = (b % 8) * (blocks / 8) + b / 8;\n";
   s << "  const long long first_output = (long long)b * " << W << ";\n";
-  // Quad i of this lane: local step (t + 256 i) / 4, local outputs
-  // ((t + 256 i) % 4) * 4 + 0..3. Out-of-range quads read as zero (their
-  // values are never folded).
-  auto quad = [&](int i, const std::string &k0, const std::string &prefix, bool guarded) {
+  // Quad i of a set: local step (t + 256 i) / 4, local outputs
+  // ((t + 256 i) % 4) * 4 + 0..3. A quad outside the operand is clamped to
+  // the last step or quad (its values are never folded or written), so
+  // every set issues the same loads on every path and the waits before a
+  // set is parked count only that set's loads, not the other set's.
+  // An input broadcast along the innermost axis loads one value a quad; its
+  // three copies are made when the set is parked.
+  const int inner = e.rank - 1;
+  std::vector<bool> loaded_whole(e.inputs.size());
+  for (size_t in = 0; in < e.inputs.size(); ++in)
+    loaded_whole[in] = !(e.inputs[in].kind == ExprInput::kStrided && e.inputs[in].strides[inner] == 0);
+  auto lanes_of = [](const std::string &prefix, int i) {
     const std::string tag = prefix + std::to_string(i);
-    const std::string lk = "((t + " + std::to_string(256 * i) + ") / 4)";
-    const std::string lo = "(((t + " + std::to_string(256 * i) + ") % 4) * 4)";
-    const std::vector<std::string> lanes = {tag + "_0", tag + "_1", tag + "_2", tag + "_3"};
-    s << "      {\n";
-    s << "      const long long o_" << tag << " = first_output + " << lo << ";\n";
-    s << "      const long long k_" << tag << " = " << k0 << " + " << lk << ";\n";
-    if (guarded) s << "      if (o_" << tag << " < " << ll(outputs) << " && k_" << tag << " < " << ll(extent) << ") {\n";
-    std::vector<std::string> rc;
-    emit_coordinates(s, (int)rest.size(), rest.data(), "o_" + tag, tag, rc);
-    std::vector<std::string> c(e.rank);
-    for (size_t q = 0; q < rest_axes.size(); ++q) c[rest_axes[q]] = rc[q];
-    c[axis] = "k_" + tag;
-    emit_quad_inputs(s, e, c, tag, lanes, "        ");
-    emit_steps(s, e, lanes);
-    for (const std::string &l : lanes) s << "        " << prefix << "v_" << l << " = " << ref(e.outputs[0], l) << ";\n";
-    if (guarded) s << "      }\n";
-    s << "      }\n";
+    return std::vector<std::string>{tag + "_0", tag + "_1", tag + "_2", tag + "_3"};
   };
-  // A tile wholly inside the operand (a uniform test) takes the unguarded
-  // path: one straight run of loads, all in flight together.
+  auto declare = [&](const std::string &prefix) {
+    for (int i = 0; i < kColumnQuads; ++i) {
+      const std::vector<std::string> lanes = lanes_of(prefix, i);
+      for (size_t in = 0; in < e.inputs.size(); ++in)
+        for (int j = 0; j < (loaded_whole[in] ? 4 : 1); ++j) s << "  float " << ref(-(int)in - 1, lanes[j]) << " = 0.0f;\n";
+    }
+  };
   auto load = [&](const std::string &k0, const std::string &prefix) {
-    for (int i = 0; i < kColumnQuads; ++i)
-      for (int j = 0; j < 4; ++j) s << "    float " << prefix << "v_" << prefix << i << "_" << j << " = 0.0f;\n";
-    s << "    if (first_output + " << W << " <= " << ll(outputs) << " && " << k0 << " + " << H << " <= " << ll(extent)
-      << ") {\n";
-    for (int i = 0; i < kColumnQuads; ++i) quad(i, k0, prefix, false);
-    s << "    } else {\n";
-    for (int i = 0; i < kColumnQuads; ++i) quad(i, k0, prefix, true);
-    s << "    }\n";
-  };
-  auto store = [&](const std::string &prefix) {
     for (int i = 0; i < kColumnQuads; ++i) {
       const std::string tag = prefix + std::to_string(i);
+      const std::vector<std::string> lanes = lanes_of(prefix, i);
       const std::string lk = "((t + " + std::to_string(256 * i) + ") / 4)";
       const std::string lo = "(((t + " + std::to_string(256 * i) + ") % 4) * 4)";
+      s << "    {\n";
+      s << "      long long o_" << tag << " = first_output + " << lo << ";\n";
+      s << "      if (o_" << tag << " > " << ll(outputs - 4) << ") o_" << tag << " = " << ll(outputs - 4) << ";\n";
+      s << "      long long k_" << tag << " = " << k0 << " + " << lk << ";\n";
+      s << "      if (k_" << tag << " > " << ll(extent - 1) << ") k_" << tag << " = " << ll(extent - 1) << ";\n";
+      std::vector<std::string> rc;
+      emit_coordinates(s, (int)rest.size(), rest.data(), "o_" + tag, tag, rc);
+      std::vector<std::string> c(e.rank);
+      for (size_t q = 0; q < rest_axes.size(); ++q) c[rest_axes[q]] = rc[q];
+      c[axis] = "k_" + tag;
+      emit_quad_inputs(s, e, c, tag, lanes, "      ", &loaded_whole, false);
+      for (size_t in = 0; in < e.inputs.size(); ++in)
+        if (!loaded_whole[in])
+          s << "      " << ref(-(int)in - 1, lanes[0]) << " = p" << in << "[" << address(e, e.inputs[in], c) << "];\n";
+      s << "    }\n";
+    }
+  };
+  // Evaluates a set's quads and parks them in LDS buffer `buffer`.
+  auto park = [&](const std::string &prefix, int buffer) {
+    for (int i = 0; i < kColumnQuads; ++i) {
+      const std::vector<std::string> lanes = lanes_of(prefix, i);
+      const std::string lk = "((t + " + std::to_string(256 * i) + ") / 4)";
+      const std::string lo = "(((t + " + std::to_string(256 * i) + ") % 4) * 4)";
+      s << "    {\n";
+      for (size_t in = 0; in < e.inputs.size(); ++in)
+        if (!loaded_whole[in])
+          for (int j = 1; j < 4; ++j)
+            s << "      const float " << ref(-(int)in - 1, lanes[j]) << " = " << ref(-(int)in - 1, lanes[0]) << ";\n";
+      emit_steps(s, e, lanes);
       for (int j = 0; j < 4; ++j)
-        s << "    tile[" << lo << " + " << j << "][" << lk << "] = " << prefix << "v_" << tag << "_" << j << ";\n";
+        s << "    tile[" << buffer << "][" << lo << " + " << j << "][" << lk << "] = " << ref(e.outputs[0], lanes[j])
+          << ";\n";
+      s << "    }\n";
     }
   };
   const std::string combine = kind == kFoldSum ? "acc + x" : "topos_faithful::max_f32(acc, x)";
+  // Lane t < W folds its output over the tile at k0 in LDS buffer `buffer`.
+  auto fold = [&](int buffer, const std::string &k0) {
+    s << "    if (t < " << W << ") {\n";
+    s << "      const long long k0f = " << k0 << ";\n";
+    s << "      const int steps = " << ll(extent) << " - k0f < " << H << " ? (int)(" << ll(extent) << " - k0f) : " << H
+      << ";\n";
+    // A whole tile: 64 steps at a time, sixteen 16-byte LDS reads then the
+    // 64 dependent additions. (Measured on MI355X: the [8192, 768] chain
+    // runs at about 7.6 cycles a step this way, 9.5 with a ring of 8-14
+    // reads each issued as an earlier one is consumed; a chain fed from
+    // registers runs at 4.6.)
+    s << "      if (steps == " << H << ") {\n";
+    for (int g = 0; g < H / 64; ++g) {
+      s << "        {\n          float r[64];\n";
+      s << "          #pragma unroll\n          for (int j = 0; j < 64; j += 4) { const float4 q = *(const float4*)&tile["
+        << buffer << "][t][" << 64 * g << " + j]; r[j] = q.x; r[j + 1] = q.y; r[j + 2] = q.z; r[j + 3] = q.w; }\n";
+      if (g == 0)
+        s << "          if (k0f == 0) { acc = r[0]; } else { const float x = r[0]; acc = " << combine << "; }\n";
+      else
+        s << "          { const float x = r[0]; acc = " << combine << "; }\n";
+      s << "          #pragma unroll\n          for (int q = 1; q < 64; ++q) { const float x = r[q]; acc = " << combine
+        << "; }\n        }\n";
+    }
+    s << "      } else {\n";
+    s << "        int j = 0;\n";
+    s << "        if (k0f == 0) { acc = tile[" << buffer << "][t][0]; j = 1; }\n";
+    s << "        for (; j < steps; ++j) { const float x = tile[" << buffer << "][t][j]; acc = " << combine << "; }\n";
+    s << "      }\n";
+    s << "    }\n";
+  };
   s << "  float acc = 0.0f;\n";
-  s << "  {\n";
-  load("0LL", "v");
-  store("v");
-  s << "  }\n";
-  s << "  for (long long k0 = 0; k0 < " << ll(extent) << "; k0 += " << H << ") {\n";
+  declare("a");
+  declare("b");
+  // Tile 0 parked in buffer 0; tiles 1 (set a) and 2 (set b) in flight.
+  load("0LL", "a");
+  park("a", 0);
+  load(std::to_string(H) + "LL", "a");
+  load(std::to_string(2 * H) + "LL", "b");
+  // Two tiles an iteration: the barrier before each fold also frees the
+  // other buffer (its fold ended before the barrier).
+  // Both halves park and load on every path (only the second fold is
+  // conditional), so the loop carries set a's loads older than set b's.
+  s << "  for (long long k0 = 0; k0 < " << ll(extent) << "; k0 += " << 2 * H << ") {\n";
   s << "    topos_lds_barrier();\n";
-  s << "    {\n";
-  load("k0 + " + std::to_string(H), "w");  // the next tile, in flight during this fold
-  s << "    if (t < " << W << ") {\n";
-  s << "      const int steps = " << ll(extent) << " - k0 < " << H << " ? (int)(" << ll(extent) << " - k0) : " << H
-    << ";\n";
-  s << "      if (steps == " << H << ") {\n";
-  for (int g = 0; g < H / 64; ++g) {
-    s << "        {\n          float r[64];\n";
-    s << "          #pragma unroll\n          for (int j = 0; j < 64; j += 4) { const float4 q = *(const float4*)&tile[t]["
-      << 64 * g << " + j]; r[j] = q.x; r[j + 1] = q.y; r[j + 2] = q.z; r[j + 3] = q.w; }\n";
-    if (g == 0)
-      s << "          if (k0 == 0) { acc = r[0]; } else { const float x = r[0]; acc = " << combine << "; }\n";
-    else
-      s << "          { const float x = r[0]; acc = " << combine << "; }\n";
-    s << "          #pragma unroll\n          for (int q = 1; q < 64; ++q) { const float x = r[q]; acc = " << combine
-      << "; }\n        }\n";
-  }
-  s << "      } else {\n";
-  s << "        int j = 0;\n";
-  s << "        if (k0 == 0) { acc = tile[t][0]; j = 1; }\n";
-  s << "        for (; j < steps; ++j) { const float x = tile[t][j]; acc = " << combine << "; }\n";
-  s << "      }\n";
-  s << "    }\n";
+  park("a", 1);                                   // tile k0 + H
+  load("k0 + " + std::to_string(3 * H), "a");
+  fold(0, "k0");
   s << "    topos_lds_barrier();\n";
-  store("w");
+  park("b", 0);                                   // tile k0 + 2H
+  load("k0 + " + std::to_string(4 * H), "b");
+  s << "    if (k0 + " << H << " < " << ll(extent) << ") {\n";
+  fold(1, "k0 + " + std::to_string(H));
   s << "    }\n";
   s << "  }\n";
   s << "  if (t < " << W << " && first_output + t < " << ll(outputs) << ") out[first_output + t] = acc;\n";

@@ -421,19 +421,23 @@ def test_long_column_folds_exact(hip):
 
 @pytest.mark.parametrize("steps, columns", [(5000, 24), (8192, 768), (2048, 12), (600, 4096), (4099, 8), (300, 16384)])
 def test_column_fold_shapes_exact(hip, steps, columns):
-    """Column folds over several whole and partial tiles, at 16 and 64
-    outputs a workgroup, the bias-gradient shape [8192, 768], an all -0
-    column, a zero-seeded accumulation of the fold and a fused operand:
-    bit-identical to the ordered fold."""
+    """Column folds over several whole and partial tiles (an odd and an even
+    count), at 16 and 64 outputs a workgroup, the bias-gradient shape
+    [8192, 768], an all -0 column, a zero-seeded accumulation of the fold, a
+    fused operand, and a per-row operand broadcast along the columns (the
+    LayerNorm gain gradient's form): bit-identical to the ordered fold."""
     banner(f"program column fold widths {steps}x{columns}")
     rng = np.random.default_rng(steps + columns)
     tape = t.Tape()
     x = tape.input((steps, columns))
     y = tape.input((steps, columns))
+    r = tape.input((steps,))
     folded = (x * y - x).sum_along(0)
-    roots = [x.sum_along(0), folded + folded.zero_like(), (x * x).maximum(y).sum_along(0)]
+    roots = [x.sum_along(0), folded + folded.zero_like(), (x * x).maximum(y).sum_along(0),
+             (x * y * r.broadcast_along(1, x)).sum_along(0)]
     dense = {x.node.slot: rng.standard_normal((steps, columns)).astype(np.float32),
-             y.node.slot: rng.standard_normal((steps, columns)).astype(np.float32)}
+             y.node.slot: rng.standard_normal((steps, columns)).astype(np.float32),
+             r.node.slot: rng.standard_normal(steps).astype(np.float32)}
     dense[x.node.slot][:, 0] = -0.0   # an all -0 column: -0 from the fold, +0 after the seed
     want = run_oracle(tape, roots, [], dense)
     got, _ = run_device(tape, roots, [], dense, numerics=hip.EXACT)
