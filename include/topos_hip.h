@@ -342,8 +342,10 @@ typedef struct topos_hip_program topos_hip_program;
 
 /* Validates and plans the program (shape inference per node, views, fusion
  * groups, launch order, arena offsets) and compiles its generated kernels.
- * TOPOS_HIP_UNSUPPORTED names a node outside the kernels (Unfold, Fold);
- * TOPOS_HIP_INVALID_ARGUMENT a malformed table. */
+ * Every Function variant of src/function/function.rs:26-59 is planned
+ * (Unfold as a strided view, Fold as one kernel); TOPOS_HIP_UNSUPPORTED names
+ * an operation code no device kernel computes, TOPOS_HIP_INVALID_ARGUMENT a
+ * malformed table. */
 int topos_hip_program_create(const topos_hip_node *nodes, int64_t n_nodes, const topos_hip_leaf *leaves,
                              int64_t n_leaves, const float *leaf_data, int64_t leaf_data_len,
                              const int32_t *leaf_indices, int64_t leaf_indices_len, int numerics,

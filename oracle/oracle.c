@@ -104,7 +104,8 @@ void oracle_gemm_f32(const float *a, int64_t a_row_stride, int64_t a_col_stride,
 /* ---- src/payload/elementary.rs:116-143 ---- */
 
 /* f32::max as compiled for x86-64 (llvm.maxnum): NaN loses, a +-0 tie
- * answers the first operand. */
+ * answers the first operand. Pinned against llvm.maxnum.f32 built by clang on
+ * runtime operands (tests/native/maxnum_probe.c, test_oracle_rows_pinned.py). */
 static float max_f32(float x, float y) {
   if (x != x) return y;
   if (y != y) return x;
