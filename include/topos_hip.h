@@ -143,10 +143,12 @@ int topos_hip_gemm_f32_device(const float *a, int64_t a_row_stride, int64_t a_co
  * harnesses that forbid hipMalloc). No counterpart in the reference: it calls
  * no hipMalloc/hipFree on any call. The split-k partials of a Fast product go
  * to a fixed device array of 64 MiB (16 Mi floats) that each GPU holds from
- * library load until the process ends, instead of
- * the library's grow-only workspace; results are bit-identical to
- * topos_hip_gemm_f32_device's. A product whose partials exceed the array
- * returns TOPOS_HIP_INVALID_ARGUMENT (topos_hip_last_refusal() says why).
+ * library load until the process ends, instead of the library's grow-only
+ * workspace. The array is never exceeded: a product whose chosen split needs
+ * more splits k into as many ranges as fit (or runs unsplit). Results are
+ * bit-identical to topos_hip_gemm_f32_device's whenever its partials fit the
+ * array (and always under TOPOS_HIP_EXACT, which needs no scratch); otherwise
+ * they stay within the same Fast envelope. No size is refused.
  * Every call on one GPU shares that GPU's array: calls that overlap on one
  * GPU (other streams, other threads) race and must be serialised by the
  * caller. */
@@ -444,7 +446,10 @@ typedef struct {
 /* AdamW::step over every parameter of a model (src/neural/adam.rs:62-171,
  * the loop over Parameters at :120-171) in as few launches as possible: each
  * element receives exactly the operations of topos_hip_adamw_step_f32 with
- * the shared scalars, so the two entry points give the same bits. */
+ * the shared scalars, so the two entry points give the same bits. Entries may
+ * share memory (a tied parameter listed twice): an entry whose buffers
+ * overlap what an earlier entry writes starts a new launch, so overlapping
+ * updates apply in table order, as successive one-tensor calls would. */
 int topos_hip_adamw_step_multi_f32(const topos_hip_adamw_tensor *tensors, int64_t count, float beta1, float beta2,
                                    float first_share, float second_share, float first_correction,
                                    float second_correction, float epsilon, float rate, float decay, void *stream);
@@ -457,6 +462,11 @@ int topos_hip_adamw_step_multi_f32(const topos_hip_adamw_tensor *tensors, int64_
  * numbered `fail_after_calls` (0-based) fails, which must poison the library.
  * Returns TOPOS_HIP_INVALID_ARGUMENT once the real runtime is initialised. */
 int topos_hip_fake_runtime(int fail_after_calls);
+
+/* Bytes of the device face's grow-only split-k workspace held now (0 until a
+ * device-face product first needs one). A diagnostic: lets a test show that
+ * topos_hip_gemm_f32_device_noalloc never creates it. */
+int64_t topos_hip_workspace_bytes(void);
 
 #ifdef __cplusplus
 }

@@ -93,6 +93,27 @@ class Generator:
         return lib.oracle_splitmix64(ctypes.byref(self._state))
 
 
+# Host threads a large product's rows are spread over (1: single-threaded, as
+# the reference interpreter runs). Every output row is computed by the same
+# sequential loop whichever thread runs it, so the bits do not depend on this.
+THREADS = 1
+
+
+def _gemm_threaded(a, a_strides, b, b_strides, m, k, n, out) -> None:
+    import concurrent.futures
+
+    chunk = (m + THREADS - 1) // THREADS
+    chunk = (chunk + 3) // 4 * 4
+    ranges = [(r, min(r + chunk, m)) for r in range(0, m, chunk)]
+
+    def run(span):
+        lib.oracle_gemm_rows_f32(_f(a), a_strides[0], a_strides[1], _f(b), b_strides[0], b_strides[1], m, n, k,
+                                 span[0], span[1], _f(out))
+
+    with concurrent.futures.ThreadPoolExecutor(max_workers=THREADS) as pool:
+        list(pool.map(run, ranges))
+
+
 def gemm(a: np.ndarray, a_strides, b: np.ndarray, b_strides, m: int, k: int, n: int,
          rows: tuple[int, int] | None = None) -> np.ndarray:
     """gemm::multiply over flat buffers read through (row, column) strides;
@@ -100,7 +121,9 @@ def gemm(a: np.ndarray, a_strides, b: np.ndarray, b_strides, m: int, k: int, n: 
     a = np.ascontiguousarray(a, dtype=np.float32).ravel()
     b = np.ascontiguousarray(b, dtype=np.float32).ravel()
     out = np.zeros(m * n, dtype=np.float32)
-    if rows is None:
+    if rows is None and THREADS > 1 and m >= 8 * THREADS and m * n * k >= (1 << 27):
+        _gemm_threaded(a, a_strides, b, b_strides, m, k, n, out)
+    elif rows is None:
         lib.oracle_gemm_f32(_f(a), a_strides[0], a_strides[1], _f(b), b_strides[0], b_strides[1], m, n, k, _f(out))
     else:
         lib.oracle_gemm_rows_f32(_f(a), a_strides[0], a_strides[1], _f(b), b_strides[0], b_strides[1], m, n, k,

@@ -108,6 +108,7 @@ PROTOTYPES = {
     "topos_hip_chain_source": (c_char_p, [c_void_p]),
     "topos_hip_chain_destroy": (None, [c_void_p]),
     "topos_hip_fake_runtime": (c_int, [c_int]),
+    "topos_hip_workspace_bytes": (c_int64, []),
     "topos_hip_program_create": (c_int, [POINTER(Node), c_int64, POINTER(Leaf), c_int64, FLOAT_P, c_int64,
                                          INT32_P, c_int64, c_int, POINTER(c_void_p)]),
     "topos_hip_program_create_backward": (c_int, [POINTER(Node), c_int64, POINTER(Leaf), c_int64, FLOAT_P, c_int64,

@@ -179,6 +179,8 @@ int topos_hip_fake_runtime(int fail_after_calls) {
   return Context::get().install_fake(fail_after_calls) ? TOPOS_HIP_OK : TOPOS_HIP_INVALID_ARGUMENT;
 }
 
+int64_t topos_hip_workspace_bytes(void) { return Context::get().workspace_bytes(); }
+
 int topos_hip_gemm_f32(const float *a, size_t a_len, size_t a_row_stride, size_t a_col_stride,
                        const float *b, size_t b_len, size_t b_row_stride, size_t b_col_stride,
                        size_t m, size_t k, size_t n, int numerics, float *product) {
@@ -274,14 +276,27 @@ int topos_hip_gemm_bf16_device(const uint16_t *a, int64_t a_row_stride, int64_t 
       launch_gemm_bf16_mfma(a, a_row_stride, a_col_stride, b, b_row_stride, b_col_stride, m, k, n, product, ldc, s);
       return;
     }
-    // The exact contract step by step: widen both spans, the bit-identical
-    // f32 product, one rounding per output.
-    const int64_t a_floats = ((int64_t)a_span + 63) / 64 * 64, b_floats = ((int64_t)b_span + 63) / 64 * 64;
+    // The exact contract step by step: widen both operands, the bit-identical
+    // f32 product, one rounding per output. Each operand is packed densely
+    // (its unit-stride axis kept innermost), so the workspace is bounded by
+    // the product's own sizes, whatever the views' spans.
+    const int64_t a_floats = (m * k + 63) / 64 * 64, b_floats = (k * n + 63) / 64 * 64;
     context.with_workspace(a_floats + b_floats + m * n, s, [&](float *w) {
-      launch_widen_bf16(a, (int64_t)a_span, w, s);
-      launch_widen_bf16(b, (int64_t)b_span, w + a_floats, s);
+      auto widen = [&](const uint16_t *src, int64_t rows, int64_t cols, int64_t rs, int64_t cs, float *dst,
+                       int64_t *packed_rs, int64_t *packed_cs) {
+        if (rs == 1 && cs != 1) {  // column-contiguous: packed as [cols][rows]
+          launch_widen_bf16(src, cols, rows, cs, rs, dst, s);
+          *packed_rs = 1, *packed_cs = rows;
+        } else {
+          launch_widen_bf16(src, rows, cols, rs, cs, dst, s);
+          *packed_rs = cols, *packed_cs = 1;
+        }
+      };
+      int64_t ars, acs, brs, bcs;
+      widen(a, m, k, a_row_stride, a_col_stride, w, &ars, &acs);
+      widen(b, k, n, b_row_stride, b_col_stride, w + a_floats, &brs, &bcs);
       float *wc = w + a_floats + b_floats;
-      launch_gemm_exact(w, a_row_stride, a_col_stride, w + a_floats, b_row_stride, b_col_stride, m, k, n, wc, n, s);
+      launch_gemm_exact(w, ars, acs, w + a_floats, brs, bcs, m, k, n, wc, n, s);
       launch_narrow_bf16(wc, m, n, product, ldc, s);
     });
   });

@@ -78,6 +78,11 @@ class Context {
     workspace_in_use_ = runtime_.launches_kernels;
   }
 
+  int64_t workspace_bytes() {
+    std::lock_guard<std::mutex> guard(workspace_lock_);
+    return workspace_floats_ * (int64_t)sizeof(float);
+  }
+
   int device_count() const { return device_count_; }
   int architecture_major() const { return arch_major_; }
   std::mutex &task_lock() { return task_lock_; }
@@ -192,7 +197,9 @@ bool bf16_mfma_serves(int64_t a_rs, int64_t a_cs, int64_t b_rs, int64_t b_cs);
 void launch_gemm_bf16_mfma(const uint16_t *a, int64_t a_rs, int64_t a_cs, const uint16_t *b, int64_t b_rs,
                            int64_t b_cs, int64_t m, int64_t k, int64_t n, uint16_t *c, int64_t ldc,
                            hipStream_t stream);
-void launch_widen_bf16(const uint16_t *in, int64_t count, float *out, hipStream_t stream);
+// Widens an [outer, inner] bf16 view into a dense f32 [outer][inner] buffer.
+void launch_widen_bf16(const uint16_t *in, int64_t outer, int64_t inner, int64_t outer_stride, int64_t inner_stride,
+                       float *out, hipStream_t stream);
 void launch_narrow_bf16(const float *in, int64_t m, int64_t n, uint16_t *out, int64_t ldc, hipStream_t stream);
 
 // window.hip: Fold (src/payload/tensor.rs:1392-1462). The operand is read

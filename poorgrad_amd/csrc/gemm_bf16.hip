@@ -28,10 +28,16 @@ __device__ __forceinline__ uint16_t bf16_of(float x) {
 
 __device__ __forceinline__ float f32_of(uint16_t h) { return __builtin_bit_cast(float, (uint32_t)h << 16); }
 
-__global__ __launch_bounds__(256) void widen_kernel(const uint16_t *__restrict__ in, int64_t count,
+// Widens an [outer, inner] view (strides outer_stride, inner_stride) into a
+// dense f32 [outer][inner] buffer.
+__global__ __launch_bounds__(256) void widen_kernel(const uint16_t *__restrict__ in, int64_t outer, int64_t inner,
+                                                    int64_t outer_stride, int64_t inner_stride,
                                                     float *__restrict__ out) {
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += (int64_t)gridDim.x * blockDim.x)
-    out[i] = f32_of(in[i]);
+  const int64_t count = outer * inner;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t o = i / inner, j = i - o * inner;
+    out[i] = f32_of(in[o * outer_stride + j * inner_stride]);
+  }
 }
 
 __global__ __launch_bounds__(256) void narrow_kernel(const float *__restrict__ in, int64_t m, int64_t n,
@@ -260,8 +266,9 @@ void launch_gemm_bf16_mfma(const uint16_t *a, int64_t a_rs, int64_t a_cs, const 
   check_launch("gemm_bf16_mfma_kernel launch");
 }
 
-void launch_widen_bf16(const uint16_t *in, int64_t count, float *out, hipStream_t stream) {
-  widen_kernel<<<blocks_for(count), 256, 0, stream>>>(in, count, out);
+void launch_widen_bf16(const uint16_t *in, int64_t outer, int64_t inner, int64_t outer_stride, int64_t inner_stride,
+                       float *out, hipStream_t stream) {
+  widen_kernel<<<blocks_for(outer * inner), 256, 0, stream>>>(in, outer, inner, outer_stride, inner_stride, out);
   check_launch("widen_kernel launch");
 }
 

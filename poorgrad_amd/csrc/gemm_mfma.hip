@@ -884,9 +884,12 @@ bool launch_gemm_mfma(const float *a, int64_t a_rs, int64_t a_cs, const float *b
   const int64_t split_stride = batch.count * m * n;
   const int64_t split_floats = mfma_split_floats(m, n, k, batch, ldc);
   int splits = split_floats > 0 ? (int)(split_floats / split_stride) : 1;
-  if (splits > 1 && (!workspace || workspace_floats < split_floats ||
-                     reinterpret_cast<uintptr_t>(workspace) % 16 != 0))
-    splits = 1;
+  // A workspace too small for the chosen split takes as many ranges as it
+  // holds (the no-allocation entry's fixed array), down to none.
+  if (splits > 1 && (!workspace || reinterpret_cast<uintptr_t>(workspace) % 16 != 0)) splits = 1;
+  if (splits > 1 && workspace_floats < split_floats)
+    splits = (int)std::min<int64_t>(splits, workspace_floats / split_stride);
+  if (splits < 2) splits = 1;
   int64_t split_len = k;
   if (splits > 1) {
     split_len = ((k + splits - 1) / splits + kTileK - 1) / kTileK * kTileK;

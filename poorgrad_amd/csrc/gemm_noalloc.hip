@@ -42,7 +42,10 @@ float *scratch_on_current_device() {
 }
 
 // Enqueues the product as topos_hip_gemm_f32_device does, with any split-k
-// partials in `scratch`; throws InvalidArgument when they exceed it.
+// partials in `scratch`. A product whose chosen split needs more than the
+// array holds splits into as many ranges as fit (or none), so the array is
+// never exceeded; its result then stays within the Fast envelope but is not
+// the allocating entry's bit pattern.
 void enqueue_gemm_noalloc(const float *a, int64_t a_rs, int64_t a_cs, const float *b, int64_t b_rs, int64_t b_cs,
                           int64_t m, int64_t k, int64_t n, int numerics, float *c, int64_t ldc, hipStream_t stream) {
   Context &context = Context::get();
@@ -52,11 +55,9 @@ void enqueue_gemm_noalloc(const float *a, int64_t a_rs, int64_t a_cs, const floa
   }
   if (numerics == TOPOS_HIP_FAST && mfma_serves(a_rs, a_cs, b_rs, b_cs, m, k, n)) {
     // The same split choice as the allocating entry point, so both give the
-    // same bits; a split whose partials exceed the scratch is refused.
-    const int64_t floats = mfma_split_floats(m, n, k, Batch(), ldc);
-    if (floats > (int64_t)(kScratchBytes / sizeof(float)))
-      throw InvalidArgument{"no-allocation product: its split-k partials need " + std::to_string(floats * 4) +
-                            " bytes; the fixed scratch holds " + std::to_string(kScratchBytes) + " bytes"};
+    // same bits whenever its partials fit the scratch.
+    const int64_t floats = std::min<int64_t>(mfma_split_floats(m, n, k, Batch(), ldc),
+                                             (int64_t)(kScratchBytes / sizeof(float)));
     float *workspace = floats ? scratch_on_current_device() : nullptr;
     if (launch_gemm_mfma(a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, stream, Batch(), workspace, floats)) return;
   }

@@ -2925,9 +2925,33 @@ int topos_hip_adamw_step_multi_f32(const topos_hip_adamw_tensor *tensors, int64_
                          epsilon, rate, decay, static_cast<hipStream_t>(stream));
       table = AdamTable{};
     };
+    // Entries of one launch run concurrently, so an entry whose buffers
+    // overlap what an earlier entry of the launch writes (a tied parameter
+    // listed twice, a gradient aliasing another entry's moment) starts a new
+    // launch: the updates then land in table order, as the one-tensor entry
+    // applied them.
+    auto overlaps = [](const void *p, int64_t n, const void *q, int64_t m) {
+      const char *a = static_cast<const char *>(p), *b = static_cast<const char *>(q);
+      return a < b + m * (int64_t)sizeof(float) && b < a + n * (int64_t)sizeof(float);
+    };
+    auto conflicts = [&](const topos_hip_adamw_tensor &x) {
+      for (int i = 0; i < table.count; ++i) {
+        const int64_t n = table.start[i + 1] - table.start[i];
+        const void *written[3] = {table.parameter[i], table.first[i], table.second[i]};
+        const void *mine[4] = {x.parameter, x.first, x.second, x.gradient};
+        for (const void *w : written)
+          for (const void *q : mine)
+            if (overlaps(w, n, q, x.count)) return true;
+        const void *my_writes[3] = {x.parameter, x.first, x.second};
+        for (const void *q : my_writes)
+          if (overlaps(table.gradient[i], n, q, x.count)) return true;
+      }
+      return false;
+    };
     for (int64_t j = 0; j < count; ++j) {
       const topos_hip_adamw_tensor &x = tensors[j];
       if (x.count == 0) continue;
+      if (table.count > 0 && conflicts(x)) flush();
       const int at = table.count;
       table.parameter[at] = x.parameter;
       table.gradient[at] = x.gradient;

@@ -6,7 +6,17 @@ and configs[4] that one CPU process evaluates in minutes:
   vocabulary 50257, 2 layers (the config's every row, column and product shape
   per sequence, at 2 of its 12 layers);
 * llama_full_width.json: the Llama-style decoder at batch 1, context 2048,
-  width 2048, 16 heads, SwiGLU 5632, vocabulary 32000, 1 layer.
+  width 2048, 16 heads, SwiGLU 5632, vocabulary 32000, 1 layer;
+* gpt2_batch8.json: GPT-2 at the headline batch, 8 x 1024 tokens (products
+  with M = 8192, the 96-way batched attention, the tied-embedding gradient
+  (768, 50257, 8192) with its split along k), full width and vocabulary, 2
+  layers;
+* llama_batch2.json: the Llama-style decoder at its config batch, 2 x 2048
+  tokens (M = 4096, 32-way attention), full width, 1 layer.
+
+The oracle's products spread their rows over the host's cores (at most 8);
+each row is still one sequential loop, so the bits are the single-threaded
+oracle's.
 
 Weights use the uniform draw of the same deviation (integer and correctly
 rounded f64 arithmetic only), so the GPU box re-derives the same parameters
@@ -45,6 +55,12 @@ def configs():
         "llama": (HERE / "llama_full_width.json",
                   lambda: workloads.llama(batch=1, context=2048, vocab=32000, width=2048, heads=16, hidden=5632,
                                           layers=1, init="uniform")),
+        "gpt2_batch8": (HERE / "gpt2_batch8.json",
+                        lambda: workloads.gpt2(batch=8, context=1024, vocab=50257, width=768, heads=12, layers=2,
+                                               positions=1024, init="uniform")),
+        "llama_batch2": (HERE / "llama_batch2.json",
+                         lambda: workloads.llama(batch=2, context=2048, vocab=32000, width=2048, heads=16,
+                                                 hidden=5632, layers=1, init="uniform")),
     }
 
 
@@ -88,7 +104,12 @@ def summarize(w, values: dict) -> dict:
 
 
 def make(name: str) -> None:
+    import os
+
+    import oracle
     from tests.program_util import run_oracle
+
+    oracle.THREADS = max(1, min(8, os.cpu_count() or 1))
 
     path, build = configs()[name]
     start = time.time()
@@ -104,5 +125,5 @@ def make(name: str) -> None:
 
 
 if __name__ == "__main__":
-    for name in sys.argv[1:] or ["gpt2", "llama"]:
+    for name in sys.argv[1:] or list(configs()):
         make(name)

@@ -77,3 +77,35 @@ def test_bf16_product_accumulates_in_f32(hip):
     for numerics in (hip.EXACT, hip.FAST):
         got = _device((a.ravel(), (3, 1), 0), (b.ravel(), (2, 1)), 2, 3, 2, numerics)
         assert (oracle.bf16_widen(got) == 258.0).all(), got
+
+
+@pytest.mark.parametrize("a_transposed", [False, True])
+def test_bf16_narrow_slices_of_wide_buffers(hip, a_transposed):
+    """Column slices of wide buffers (a [512, 48] window of a [512, 30011]
+    buffer, a [48, 80] window of a [48, 30011] one): the exact path packs the
+    operands densely, so its workspace is the product's size, not the
+    views' spans; both postures against the oracle."""
+    banner(f"bf16 gemm narrow slices a_transposed={a_transposed}")
+    m, k, n, wide, start = 512, 48, 80, 30011, 1000
+    g = oracle.Generator(5)
+    a = oracle.bf16_round(g.normal(m * k, 1.0).reshape(m, k))
+    b = oracle.bf16_round(g.normal(k * n, 1.0).reshape(k, n))
+    if a_transposed:
+        a_host = np.zeros((k, wide), np.uint16)
+        a_host[:, start:start + m] = a.T
+        a_view = (a_host.ravel(), (1, wide), start)
+    else:
+        a_host = np.zeros((m, wide), np.uint16)
+        a_host[:, start:start + k] = a
+        a_view = (a_host.ravel(), (wide, 1), start)
+    b_host = np.zeros((k, wide), np.uint16)
+    b_host[:, start:start + n] = b
+    b_buf = b_host.ravel()[start:]
+    want = oracle.gemm_bf16(a, (k, 1), b, (n, 1), m, k, n)
+    exact = _device(a_view, (b_buf, (wide, 1)), m, k, n, hip.EXACT)
+    assert np.array_equal(exact, want), f"exact: {int((exact != want).sum())} differ"
+    fast = _device(a_view, (b_buf, (wide, 1)), m, k, n, hip.FAST)
+    wa, wb = oracle.bf16_widen(a).astype(np.float64), oracle.bf16_widen(b).astype(np.float64)
+    w = oracle.bf16_widen(want).astype(np.float64)
+    bound = 1e-5 * (np.abs(wa) @ np.abs(wb)) + np.abs(w) * 2.0**-7 + 1e-38
+    assert (np.abs(oracle.bf16_widen(fast).astype(np.float64) - w) <= bound).all()

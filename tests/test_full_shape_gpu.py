@@ -1,12 +1,14 @@
-"""Parity at the configs' full widths: the device program of the GPT-2 train
-step (configs[3] per sequence: context 1024, width 768, 12 heads, vocabulary
-50257, at 2 of its 12 layers) and of the Llama-style decoder (configs[4] per
-sequence: context 2048, width 2048, 16 heads, SwiGLU 5632, vocabulary 32000,
-at 1 of its 8 layers) against fixtures the oracle interpreter wrote
+"""Parity at the configs' full widths and batches: the device program of the
+GPT-2 train step (configs[3]: context 1024, width 768, 12 heads, vocabulary
+50257, at 2 of its 12 layers, at batch 1 and at the headline batch 8) and of
+the Llama-style decoder (configs[4]: context 2048, width 2048, 16 heads,
+SwiGLU 5632, vocabulary 32000, at 1 of its 8 layers, at batch 1 and at its
+batch 2) against fixtures the oracle interpreter wrote
 (tests/golden/make_full_shape_fixtures.py). These sizes reach the paths the
 small-size tests cannot: 50257-wide streamed row programs, the gathered
-ordered sum over 51M terms, split-k vocabulary products, and 1024- and
-2048-wide attention row programs.
+ordered sum over 411M terms, split-k vocabulary products, the headline's
+M = 8192 products, 96-way batched attention and the tied-embedding gradient
+(768, 50257, 8192), and 1024- and 2048-wide attention row programs.
 
 Exact posture: the loss bits and every gradient's SHA-256 over its f32 bits
 equal the oracle's (bit-identical, the plan = interpreter contract of
@@ -15,27 +17,16 @@ relative and the sampled gradient elements within 1e-3 of each gradient's
 largest magnitude, the rule of the small-size fast tests."""
 import hashlib
 import json
-from pathlib import Path
 
 import numpy as np
 import pytest
 
-from poorgrad_amd import workloads
 from tests.conftest import banner
-from tests.golden.make_full_shape_fixtures import input_digests
+from tests.golden.make_full_shape_fixtures import configs, input_digests
 
 pytestmark = pytest.mark.gpu
 
-GOLDEN = Path(__file__).resolve().parent / "golden"
-
-CASES = {
-    "gpt2": ("gpt2_full_width.json",
-             lambda: workloads.gpt2(batch=1, context=1024, vocab=50257, width=768, heads=12, layers=2,
-                                    positions=1024, init="uniform")),
-    "llama": ("llama_full_width.json",
-              lambda: workloads.llama(batch=1, context=2048, vocab=32000, width=2048, heads=16, hidden=5632,
-                                      layers=1, init="uniform")),
-}
+CASES = configs()
 
 
 def _run(w, numerics):
@@ -56,11 +47,11 @@ def _run(w, numerics):
     return program
 
 
-@pytest.mark.parametrize("model", ["gpt2", "llama"])
+@pytest.mark.parametrize("model", ["gpt2", "llama", "gpt2_batch8", "llama_batch2"])
 @pytest.mark.parametrize("posture", ["exact", "fast"])
 def test_full_width_train_step_matches_oracle_fixture(hip, model, posture):
-    name, build = CASES[model]
-    fixture = json.loads((GOLDEN / name).read_text())
+    path, build = CASES[model]
+    fixture = json.loads(path.read_text())
     banner(f"full width {model} {posture}: recording")
     w = build()
     assert input_digests(w) == fixture["inputs"], "this host derives other inputs than the fixture's"

@@ -57,3 +57,48 @@ def test_multi_tensor_adamw_refuses_bad_tables(hip):
                                                   None) == hip.INVALID_ARGUMENT
     assert hip.lib.topos_hip_adamw_step_multi_f32(None, 0, 0.9, 0.999, 0.1, 0.001, 0.1, 0.001, 1e-8, 1e-3, 0.01,
                                                   None) == hip.OK
+
+
+def test_multi_tensor_adamw_with_overlapping_entries(hip):
+    """A table whose entries share memory (a tied parameter listed twice with
+    its own moments, and a gradient that is another entry's parameter): the
+    library splits the launch before each overlap, so the result equals the
+    one-tensor entry applied in table order."""
+    import torch
+
+    banner("adamw multi-tensor, overlapping entries")
+    rng = np.random.default_rng(4)
+    make = lambda s: torch.from_numpy(rng.standard_normal(s).astype(np.float32)).cuda()
+    tied, other = make(4096), make(1000)
+    gradients = [make(4096), make(4096), None]
+    f = np.float32
+    scalars = (0.9, 0.999, float(f(1) - f(0.9)), float(f(1) - f(0.999)), float(f(1) - f(0.9)),
+               float(f(1) - f(0.999)), 1e-8, 3e-4, 0.01)
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def entries(state):
+        tied_p, other_p, moments = state
+        # tied twice (each listing with its own moments), then `other`, whose
+        # gradient is a window of the tied parameter the first entries write.
+        return [(tied_p, gradients[0], moments[0], moments[1], 1), (tied_p, gradients[1], moments[2], moments[3], 1),
+                (other_p, tied_p[:1000], moments[4], moments[5], 0)]
+
+    def fresh():
+        return (tied.clone(), other.clone(),
+                [torch.zeros(4096, device="cuda") for _ in range(4)] + [torch.zeros(1000, device="cuda")
+                                                                        for _ in range(2)])
+
+    single, multi = fresh(), fresh()
+    for p, g, m, v, d in entries(single):
+        hip.checked(hip.lib.topos_hip_adamw_step_f32(p.data_ptr(), g.data_ptr(), m.data_ptr(), v.data_ptr(),
+                                                     p.numel(), *scalars[:-1], scalars[-1], d, stream), "single")
+    listed = entries(multi)
+    table = (hip.AdamwTensor * len(listed))()
+    for j, (p, g, m, v, d) in enumerate(listed):
+        table[j] = hip.AdamwTensor(p.data_ptr(), g.data_ptr(), m.data_ptr(), v.data_ptr(), p.numel(), d)
+    hip.checked(hip.lib.topos_hip_adamw_step_multi_f32(table, len(listed), *scalars, stream), "multi")
+    torch.cuda.synchronize()
+    assert_bitwise(multi[0].cpu().numpy(), single[0].cpu().numpy(), "tied parameter")
+    assert_bitwise(multi[1].cpu().numpy(), single[1].cpu().numpy(), "parameter with an aliased gradient")
+    for j, (x, y) in enumerate(zip(single[2], multi[2])):
+        assert_bitwise(y.cpu().numpy(), x.cpu().numpy(), f"moment {j}")
