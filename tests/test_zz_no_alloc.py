@@ -19,11 +19,13 @@ from pathlib import Path
 import numpy as np
 import pytest
 
-import oracle
+ROOT = Path(__file__).resolve().parent.parent
+if str(ROOT) not in sys.path:  # the child process runs this file as a script
+    sys.path.insert(0, str(ROOT))
+
+import oracle  # noqa: E402
 
 pytestmark = pytest.mark.gpu
-
-ROOT = Path(__file__).resolve().parent.parent
 
 # (m, k, n, seed). Under Fast both split k: 16 partials of 512 x 512 (16 MiB)
 # then 8 of 256 x 384, each within the 64 MiB array.
@@ -138,7 +140,6 @@ def test_noalloc_allocates_nothing_in_a_fresh_process_and_under_capture(hip):
 
 
 def _child() -> None:
-    sys.path.insert(0, str(ROOT))
     import torch
 
     from poorgrad_amd import _native as nat
