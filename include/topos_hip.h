@@ -356,7 +356,7 @@ int topos_hip_program_create(const topos_hip_node *nodes, int64_t n_nodes, const
  * plan compiled with Request::backward(): the library appends the reverse
  * scan from the scalar node `target` to the forward table itself — one_like
  * seed, zero_like-seeded accumulation in reverse scan order, only ancestors
- * running their derivative rules (src/function/*.rs `backward`), only present
+ * running their derivative rules (the `backward` of each src/function rule), only present
  * cotangents marking ancestors — and plans forward and backward as one
  * program whose arena keeps every forward value a rule reads. `wrt` lists the
  * nodes whose gradients the caller will read (Run::backward answers every

@@ -142,13 +142,22 @@ int topos_hip_coverage(int formula, int *fidelity, unsigned *precisions) {
   // matrix-core kernel under Fast and the bit-identical kernel under Exact
   // from the posture it is handed, and the envelope is the weaker guarantee
   // the cell may promise. Map is bit-identical: every operation matches the
-  // host libm on all 2^32 inputs. The composed formulas are absent.
+  // host libm on all 2^32 inputs. Three composed formulas are elected onto
+  // device programs, each bit-identical in both postures (the composed
+  // recording's bits, as src/backend/fused.rs:18-50 declares for the
+  // reference's own fused kernels): WindowProduct as window products that
+  // gather the patch matrix, ReduceWindow as lanes viewed from the source in
+  // one launch, BatchNormTraining as one column program. BatchNormInference
+  // stays absent, as in the reference.
   switch (formula) {
     case TOPOS_HIP_FORMULA_GEMM:
       if (fidelity) *fidelity = TOPOS_HIP_ENVELOPE;
       if (precisions) *precisions = TOPOS_HIP_PRECISION_F32;
       return 1;
     case TOPOS_HIP_FORMULA_MAP:
+    case TOPOS_HIP_FORMULA_WINDOW_PRODUCT:
+    case TOPOS_HIP_FORMULA_REDUCE_WINDOW:
+    case TOPOS_HIP_FORMULA_BATCH_NORM_TRAINING:
       if (fidelity) *fidelity = TOPOS_HIP_BIT_IDENTICAL;
       if (precisions) *precisions = TOPOS_HIP_PRECISION_F32;
       return 1;

@@ -166,6 +166,26 @@ struct Epilogue {
 void launch_gemm_exact(const float *a, int64_t a_rs, int64_t a_cs, const float *b, int64_t b_rs,
                        int64_t b_cs, int64_t m, int64_t k, int64_t n, float *c, int64_t ldc,
                        hipStream_t stream, const Batch &batch = Batch());
+
+// The im2col matrix of a convolution, never materialised: row r = (image,
+// out_y, out_x), column q = (channel, kernel_y, kernel_x) of the padded,
+// strided windows of a rank-4 [batch, channels, height, width] source read
+// through any strides; +0 where a window leaves the source (the padding).
+// The patch matrix of src/payload/tensor.rs:1475-1544.
+struct WindowShape {
+  int64_t offset = 0;
+  int64_t s_batch = 0, s_channel = 0, s_height = 0, s_width = 0;
+  int32_t channels = 0, height = 0, width = 0;
+  int32_t kernel_height = 0, kernel_width = 0, out_height = 0, out_width = 0, stride = 1, padding = 0;
+};
+// WindowProduct (src/payload/tensorial.rs:112-122, elected by
+// src/engine/pattern/window.rs:58-150): patches . b ([m, k] . [k, n], m the
+// patch rows) or, transposed, patches^T . b ([m, k] with m the patch columns
+// and k the patch rows: the kernel gradient), bit-identical to
+// gemm::multiply over the materialised patches.
+void launch_window_product(const float *source, const WindowShape &w, bool transposed, const float *b, int64_t b_rs,
+                           int64_t b_cs, int64_t m, int64_t k, int64_t n, float *c, int64_t ldc,
+                           hipStream_t stream);
 // gemm_mfma.hip: fp32 MFMA product within the stated envelope. Returns false
 // when the stride pattern is outside its loaders (caller falls back).
 // With a workspace of at least mfma_splits(m, n, k, count) * count * m * n

@@ -1432,10 +1432,16 @@ Generated generate_row_resident(const RowProgram &p, const RowLayout &l, const R
       const std::vector<std::string> lanes = lanes_of(i);
       s << "  if (ok" << I << ") {\n";
       m.emit_nodes(s, nodes_needed, lanes, "r" + I, "    ");
-      s << "    const long long at = (row0 + r" << I << ") * " << ll(C) << " + col" << I << ";\n";
+      if (p.transposed_outputs)
+        s << "    const long long at = col" << I << " * " << ll(R) << " + row0 + r" << I << ";\n";
+      else
+        s << "    const long long at = (row0 + r" << I << ") * " << ll(C) << " + col" << I << ";\n";
       for (size_t o = 0; o < p.full_outputs.size(); ++o) {
         const int k = p.full_outputs[o];
-        if (V == 4)
+        if (p.transposed_outputs)
+          for (int j = 0; j < V; ++j)
+            s << "    fo" << o << "[at + " << ll(j * R) << "] = f" << k << "_" << lanes[j] << ";\n";
+        else if (V == 4)
           s << "    *(topos_f4*)(fo" << o << " + at) = topos_f4{f" << k << "_" << lanes[0] << ", f" << k << "_" << lanes[1]
             << ", f" << k << "_" << lanes[2] << ", f" << k << "_" << lanes[3] << "};\n";
         else
@@ -1652,10 +1658,16 @@ Generated generate_row_streaming(const RowProgram &p, const RowLayout &l, const 
       const std::vector<std::string> lanes = lanes_of(i);
       s << "    if (row0 + r" << I << " < " << ll(R) << " && c0 + cu" << I << " < " << ll(C) << ") {\n";
       m.emit_nodes(s, nodes_needed, lanes, "r" + I, "      ");
-      s << "      const long long at = (row0 + r" << I << ") * " << ll(C) << " + c0 + cu" << I << ";\n";
+      if (p.transposed_outputs)
+        s << "      const long long at = (c0 + cu" << I << ") * " << ll(R) << " + row0 + r" << I << ";\n";
+      else
+        s << "      const long long at = (row0 + r" << I << ") * " << ll(C) << " + c0 + cu" << I << ";\n";
       for (size_t o = 0; o < p.full_outputs.size(); ++o) {
         const int k = p.full_outputs[o];
-        if (V == 4)
+        if (p.transposed_outputs)
+          for (int j = 0; j < V; ++j)
+            s << "      fo" << o << "[at + " << ll(j * R) << "] = f" << k << "_" << lanes[j] << ";\n";
+        else if (V == 4)
           s << "      *(topos_f4*)(fo" << o << " + at) = topos_f4{f" << k << "_" << lanes[0] << ", f" << k << "_"
             << lanes[1] << ", f" << k << "_" << lanes[2] << ", f" << k << "_" << lanes[3] << "};\n";
         else

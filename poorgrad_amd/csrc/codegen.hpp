@@ -128,6 +128,9 @@ struct RowProgram {
   std::vector<RowNode> nodes;      // in evaluation order
   std::vector<int> full_outputs;   // full nodes written [rows, columns]
   std::vector<int> row_outputs;    // row nodes written [rows]
+  // Rank 2 only: full outputs written [columns, rows] (a column program's
+  // [R, C] nodes, row-major), one element a store.
+  bool transposed_outputs = false;
   int64_t columns() const { return shape[rank - 1]; }
   int64_t rows() const {
     int64_t r = 1;

@@ -24,8 +24,28 @@ constexpr int kThreads = 256;
 // kInnerUnit with k contiguous (a lane loads four consecutive k values at
 // once); kOuterUnit with the outer axis contiguous (a lane loads four
 // consecutive outer elements at once). 16-byte loads serve any 4-byte
-// alignment on gfx950.
-enum { kGeneric = 0, kInnerUnit = 1, kOuterUnit = 2 };
+// alignment on gfx950. kWindowRows / kWindowCols: the left operand is a
+// convolution's patch matrix (outer = patch rows, k = patch columns) or its
+// transpose (outer = patch columns, k = patch rows), each element gathered
+// from the source (window_element).
+enum { kGeneric = 0, kInnerUnit = 1, kOuterUnit = 2, kWindowRows = 3, kWindowCols = 4 };
+
+// Element (row, col) of the patch matrix: row = (image, out_y, out_x),
+// col = (channel, kernel_y, kernel_x), the source element under that window
+// position or +0 in the padding (zero_like of an f32 element, as the padded
+// copy holds).
+__device__ __forceinline__ float window_element(const float *__restrict__ src, const WindowShape &w, uint32_t row,
+                                                uint32_t col) {
+  const uint32_t x = row % (uint32_t)w.out_width, t = row / (uint32_t)w.out_width;
+  const uint32_t y = t % (uint32_t)w.out_height, image = t / (uint32_t)w.out_height;
+  const uint32_t kx = col % (uint32_t)w.kernel_width, u = col / (uint32_t)w.kernel_width;
+  const uint32_t ky = u % (uint32_t)w.kernel_height, channel = u / (uint32_t)w.kernel_height;
+  const int32_t hy = (int32_t)(y * (uint32_t)w.stride + ky) - w.padding;
+  const int32_t wx = (int32_t)(x * (uint32_t)w.stride + kx) - w.padding;
+  if (hy < 0 || hy >= w.height || wx < 0 || wx >= w.width) return 0.0f;
+  return src[w.offset + (int64_t)image * w.s_batch + (int64_t)channel * w.s_channel + (int64_t)hy * w.s_height +
+             (int64_t)wx * w.s_width];
+}
 
 // One kTileK x E slab of an operand (outer index o0.., inner k0..) in a
 // lane's registers (fetch), then into lds[k][o] (deposit): the next slab's
@@ -34,8 +54,26 @@ template <int E, int kMode>
 struct Stage {
   static constexpr int kQuads = E * kTileK / 4;                      // quads a slab
   static constexpr int kQ = (kQuads + kThreads - 1) / kThreads;      // quads a lane
-  static constexpr int kS = E * kTileK / kThreads;                   // elements a lane (generic)
-  float v[kMode == kGeneric ? kS : 4 * kQ];
+  static constexpr int kS = E * kTileK / kThreads;                   // elements a lane (generic, window)
+  float v[(kMode == kInnerUnit || kMode == kOuterUnit) ? 4 * kQ : kS];
+
+  // A patch-matrix slab: consecutive lanes on consecutive patch rows (the
+  // source's x positions), whichever of outer and k that is.
+  __device__ void fetch_window(const float *__restrict__ p, const WindowShape &w, int64_t outer_extent, int64_t k,
+                               int64_t o0, int64_t k0) {
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int e = 0; e < kS; ++e) {
+      const int flat = e * kThreads + t;
+      const int o = kMode == kWindowRows ? flat % E : flat / kTileK;
+      const int kk = kMode == kWindowRows ? flat / E : flat % kTileK;
+      const int64_t go = o0 + o, gk = k0 + kk;
+      v[e] = 0.0f;
+      if (go < outer_extent && gk < k)
+        v[e] = kMode == kWindowRows ? window_element(p, w, (uint32_t)go, (uint32_t)gk)
+                                    : window_element(p, w, (uint32_t)gk, (uint32_t)go);
+    }
+  }
 
   __device__ void fetch(const float *__restrict__ p, int64_t outer_stride, int64_t k_stride, int64_t outer_extent,
                         int64_t k, int64_t o0, int64_t k0) {
@@ -106,6 +144,12 @@ struct Stage {
         const int oq = flat % (E / 4), kk = flat / (E / 4);
         *reinterpret_cast<float4 *>(&lds[kk][4 * oq]) = make_float4(v[4 * e], v[4 * e + 1], v[4 * e + 2], v[4 * e + 3]);
       }
+    } else if constexpr (kMode == kWindowCols) {
+#pragma unroll
+      for (int e = 0; e < kS; ++e) {
+        const int flat = e * kThreads + t;
+        lds[flat % kTileK][flat / kTileK] = v[e];
+      }
     } else {
 #pragma unroll
       for (int e = 0; e < kS; ++e) {
@@ -126,7 +170,7 @@ template <int EM, int EN, int kLeftMode, int kRightMode>
 __global__ __launch_bounds__(kThreads) void gemm_exact_kernel(
     const float *__restrict__ a, int64_t a_rs, int64_t a_cs, const float *__restrict__ b,
     int64_t b_rs, int64_t b_cs, int64_t m, int64_t k, int64_t n, float *__restrict__ c, int64_t ldc,
-    int64_t a_bs, int64_t b_bs, int64_t c_bs) {
+    int64_t a_bs, int64_t b_bs, int64_t c_bs, const WindowShape w) {
   // RM x RN accumulators a lane, 16 x 16 lanes over the EM x EN tile.
   constexpr int RM = EM / 16, RN = EN / 16;
   static_assert(EM * EN == 16 * 16 * RM * RN && (RM == 4 || RM == 2) && (RN == 4 || RN == 2), "tile shape");
@@ -144,7 +188,13 @@ __global__ __launch_bounds__(kThreads) void gemm_exact_kernel(
     __shared__ __attribute__((aligned(16))) float right2[2][kTileK][EN + 4];
     Stage<EM, kLeftMode> sa;
     Stage<EN, kRightMode> sb;
-    sa.fetch(a, a_rs, a_cs, m, k, m0, 0);
+    auto fetch_left = [&](int64_t k0) {
+      if constexpr (kLeftMode == kWindowRows || kLeftMode == kWindowCols)
+        sa.fetch_window(a, w, m, k, m0, k0);
+      else
+        sa.fetch(a, a_rs, a_cs, m, k, m0, k0);
+    };
+    fetch_left(0);
     sb.fetch(b, b_cs, b_rs, n, k, n0, 0);
     sa.deposit(left2[0]);
     sb.deposit(right2[0]);
@@ -153,7 +203,7 @@ __global__ __launch_bounds__(kThreads) void gemm_exact_kernel(
     for (int64_t k0 = 0; k0 < k; k0 += kTileK) {
       const bool more = k0 + kTileK < k;
       if (more) {
-        sa.fetch(a, a_rs, a_cs, m, k, m0, k0 + kTileK);
+        fetch_left(k0 + kTileK);
         sb.fetch(b, b_cs, b_rs, n, k, n0, k0 + kTileK);
       }
       const int steps = (k - k0) < kTileK ? (int)(k - k0) : kTileK;
@@ -214,11 +264,11 @@ __global__ __launch_bounds__(kThreads) void gemm_exact_kernel(
 constexpr int kSmall = 16;
 constexpr int kSmallK = 64;
 
-template <bool kLeftUnitInner, bool kRightUnitInner>
+template <bool kLeftUnitInner, bool kRightUnitInner, int kLeftWindow = kGeneric>
 __global__ __launch_bounds__(kThreads) void gemm_exact_small_kernel(
     const float *__restrict__ a, int64_t a_rs, int64_t a_cs, const float *__restrict__ b,
     int64_t b_rs, int64_t b_cs, int64_t m, int64_t k, int64_t n, float *__restrict__ c, int64_t ldc,
-    int64_t a_bs, int64_t b_bs, int64_t c_bs) {
+    int64_t a_bs, int64_t b_bs, int64_t c_bs, const WindowShape w) {
   __shared__ float left[kSmallK][kSmall + 1];
   __shared__ float right[kSmallK][kSmall + 1];
   a += (int64_t)blockIdx.z * a_bs;
@@ -248,7 +298,12 @@ __global__ __launch_bounds__(kThreads) void gemm_exact_small_kernel(
       int o, kk;
       coords(e, kLeftUnitInner, o, kk);
       const int64_t gm = m0 + o, gk = k0 + kk;
-      va[e] = (gm < m && gk < k) ? a[gm * a_rs + gk * a_cs] : 0.0f;
+      if constexpr (kLeftWindow == kWindowRows)
+        va[e] = (gm < m && gk < k) ? window_element(a, w, (uint32_t)gm, (uint32_t)gk) : 0.0f;
+      else if constexpr (kLeftWindow == kWindowCols)
+        va[e] = (gm < m && gk < k) ? window_element(a, w, (uint32_t)gk, (uint32_t)gm) : 0.0f;
+      else
+        va[e] = (gm < m && gk < k) ? a[gm * a_rs + gk * a_cs] : 0.0f;
       coords(e, kRightUnitInner, o, kk);
       const int64_t gn = n0 + o, gkb = k0 + kk;
       vb[e] = (gkb < k && gn < n) ? b[gkb * b_rs + gn * b_cs] : 0.0f;
@@ -288,41 +343,48 @@ namespace {
 template <int EM, int EN, int L>
 void launch_exact_right(int right_mode, dim3 grid, hipStream_t stream, const float *a, int64_t a_rs, int64_t a_cs,
                         const float *b, int64_t b_rs, int64_t b_cs, int64_t m, int64_t k, int64_t n, float *c,
-                        int64_t ldc, int64_t a_bs, int64_t b_bs, int64_t c_bs) {
+                        int64_t ldc, int64_t a_bs, int64_t b_bs, int64_t c_bs, const WindowShape &w) {
   if (right_mode == kInnerUnit)
     gemm_exact_kernel<EM, EN, L, kInnerUnit><<<grid, kThreads, 0, stream>>>(a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c,
-                                                                            ldc, a_bs, b_bs, c_bs);
+                                                                            ldc, a_bs, b_bs, c_bs, w);
   else if (right_mode == kOuterUnit)
     gemm_exact_kernel<EM, EN, L, kOuterUnit><<<grid, kThreads, 0, stream>>>(a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c,
-                                                                            ldc, a_bs, b_bs, c_bs);
+                                                                            ldc, a_bs, b_bs, c_bs, w);
   else
     gemm_exact_kernel<EM, EN, L, kGeneric><<<grid, kThreads, 0, stream>>>(a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c,
-                                                                          ldc, a_bs, b_bs, c_bs);
+                                                                          ldc, a_bs, b_bs, c_bs, w);
 }
 
 template <int EM, int EN>
 void launch_exact_tile(int left_mode, int right_mode, dim3 grid, hipStream_t stream, const float *a, int64_t a_rs,
                        int64_t a_cs, const float *b, int64_t b_rs, int64_t b_cs, int64_t m, int64_t k, int64_t n,
-                       float *c, int64_t ldc, int64_t a_bs, int64_t b_bs, int64_t c_bs) {
+                       float *c, int64_t ldc, int64_t a_bs, int64_t b_bs, int64_t c_bs, const WindowShape &w) {
   if (left_mode == kInnerUnit)
     launch_exact_right<EM, EN, kInnerUnit>(right_mode, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc,
-                                           a_bs, b_bs, c_bs);
+                                           a_bs, b_bs, c_bs, w);
   else if (left_mode == kOuterUnit)
     launch_exact_right<EM, EN, kOuterUnit>(right_mode, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc,
-                                           a_bs, b_bs, c_bs);
+                                           a_bs, b_bs, c_bs, w);
+  else if (left_mode == kWindowRows)
+    launch_exact_right<EM, EN, kWindowRows>(right_mode, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc,
+                                            a_bs, b_bs, c_bs, w);
+  else if (left_mode == kWindowCols)
+    launch_exact_right<EM, EN, kWindowCols>(right_mode, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc,
+                                            a_bs, b_bs, c_bs, w);
   else
     launch_exact_right<EM, EN, kGeneric>(right_mode, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc,
-                                         a_bs, b_bs, c_bs);
+                                         a_bs, b_bs, c_bs, w);
 }
 
-}  // namespace
-
-void launch_gemm_exact(const float *a, int64_t a_rs, int64_t a_cs, const float *b, int64_t b_rs,
-                       int64_t b_cs, int64_t m, int64_t k, int64_t n, float *c, int64_t ldc,
-                       hipStream_t stream, const Batch &batch) {
+// The exact product with the left operand read as `window_mode` says
+// (kGeneric: through a_rs, a_cs; a window mode: gathered through `w`).
+void enqueue_exact(int window_mode, const WindowShape &w, const float *a, int64_t a_rs, int64_t a_cs, const float *b,
+                   int64_t b_rs, int64_t b_cs, int64_t m, int64_t k, int64_t n, float *c, int64_t ldc,
+                   hipStream_t stream, const Batch &batch) {
   if (batch.count > 65535 || batch.count < 1) throw Unsupported{"exact gemm: too many batches for one launch"};
   const int64_t a_bs = batch.a_stride, b_bs = batch.b_stride, c_bs = batch.c_stride;
-  const bool left_unit = a_cs == 1;
+  const bool window = window_mode != kGeneric;
+  const bool left_unit = !window && a_cs == 1;
   const bool right_unit = b_rs == 1 && b_cs != 1;
   // Fewer 64x64 tiles than CUs: one output per lane instead, unless k is
   // deep and 32x32 tiles still give a workgroup per CU (the [768, 768]
@@ -332,8 +394,18 @@ void launch_gemm_exact(const float *a, int64_t a_rs, int64_t a_cs, const float *
   const int64_t tiles32 = ((m + 31) / 32) * ((n + 31) / 32) * batch.count;
   if (tiles64 < 256 && (k < 2048 || tiles32 < 256) && small_m <= 65535 && small_n <= 0x7fffffff) {
     const dim3 small_grid((unsigned)small_n, (unsigned)small_m, (unsigned)batch.count);
-#define TOPOS_SMALL_ARGS a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, a_bs, b_bs, c_bs
-    if (left_unit && right_unit)
+#define TOPOS_SMALL_ARGS a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, a_bs, b_bs, c_bs, w
+    // Window modes: consecutive lanes on consecutive patch rows (outer for
+    // kWindowRows, k for kWindowCols).
+    if (window_mode == kWindowRows && right_unit)
+      gemm_exact_small_kernel<false, true, kWindowRows><<<small_grid, kThreads, 0, stream>>>(TOPOS_SMALL_ARGS);
+    else if (window_mode == kWindowRows)
+      gemm_exact_small_kernel<false, false, kWindowRows><<<small_grid, kThreads, 0, stream>>>(TOPOS_SMALL_ARGS);
+    else if (window_mode == kWindowCols && right_unit)
+      gemm_exact_small_kernel<true, true, kWindowCols><<<small_grid, kThreads, 0, stream>>>(TOPOS_SMALL_ARGS);
+    else if (window_mode == kWindowCols)
+      gemm_exact_small_kernel<true, false, kWindowCols><<<small_grid, kThreads, 0, stream>>>(TOPOS_SMALL_ARGS);
+    else if (left_unit && right_unit)
       gemm_exact_small_kernel<true, true><<<small_grid, kThreads, 0, stream>>>(TOPOS_SMALL_ARGS);
     else if (left_unit)
       gemm_exact_small_kernel<true, false><<<small_grid, kThreads, 0, stream>>>(TOPOS_SMALL_ARGS);
@@ -356,8 +428,8 @@ void launch_gemm_exact(const float *a, int64_t a_rs, int64_t a_cs, const float *
   const int em = shape == 2 ? 32 : 64, en = shape == 0 ? 64 : 32;
   const int64_t grid_n = (n + en - 1) / en, grid_m = (m + em - 1) / em;
   if (grid_m > 65535 || grid_n > 0x7fffffff) throw Unsupported{"exact gemm: product too tall for one launch"};
-#define TOPOS_EXACT_ARGS a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, a_bs, b_bs, c_bs
-  const int left_mode = left_unit ? kInnerUnit : a_rs == 1 ? kOuterUnit : kGeneric;
+#define TOPOS_EXACT_ARGS a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, a_bs, b_bs, c_bs, w
+  const int left_mode = window ? window_mode : left_unit ? kInnerUnit : a_rs == 1 ? kOuterUnit : kGeneric;
   const int right_mode = right_unit ? kInnerUnit : b_cs == 1 ? kOuterUnit : kGeneric;
   const dim3 grid((unsigned)grid_n, (unsigned)grid_m, (unsigned)batch.count);
   if (shape == 0)
@@ -368,6 +440,28 @@ void launch_gemm_exact(const float *a, int64_t a_rs, int64_t a_cs, const float *
     launch_exact_tile<32, 32>(left_mode, right_mode, grid, stream, TOPOS_EXACT_ARGS);
 #undef TOPOS_EXACT_ARGS
   check_launch("gemm_exact_kernel launch");
+}
+
+}  // namespace
+
+void launch_gemm_exact(const float *a, int64_t a_rs, int64_t a_cs, const float *b, int64_t b_rs,
+                       int64_t b_cs, int64_t m, int64_t k, int64_t n, float *c, int64_t ldc,
+                       hipStream_t stream, const Batch &batch) {
+  enqueue_exact(kGeneric, WindowShape(), a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, stream, batch);
+}
+
+void launch_window_product(const float *source, const WindowShape &w, bool transposed, const float *b, int64_t b_rs,
+                           int64_t b_cs, int64_t m, int64_t k, int64_t n, float *c, int64_t ldc,
+                           hipStream_t stream) {
+  // The patch matrix is [batch * out_height * out_width, channels *
+  // kernel_height * kernel_width]; its indices are taken in 32 bits.
+  const int64_t rows = transposed ? k : m, columns = transposed ? m : k;
+  const int64_t positions = (int64_t)w.out_height * w.out_width;
+  if (positions <= 0 || rows % positions != 0 || columns != (int64_t)w.channels * w.kernel_height * w.kernel_width ||
+      rows > 0x7fffffff || columns > 0x7fffffff)
+    throw Unsupported{"window product: extents outside the patch matrix"};
+  enqueue_exact(transposed ? kWindowCols : kWindowRows, w, source, 0, 0, b, b_rs, b_cs, m, k, n, c, ldc, stream,
+                Batch());
 }
 
 }  // namespace topos_hip

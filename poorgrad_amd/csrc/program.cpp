@@ -49,6 +49,10 @@ std::string &last_refusal() {
 
 namespace {
 
+// The largest reduced extent a column program (a transposed row group) takes:
+// its strided column reads stay within what a workgroup keeps resident.
+constexpr int64_t kColumnProgramRows = 2048;
+
 struct Layout {
   int rank = 0;
   int64_t shape[kMaxRank] = {1, 1, 1, 1, 1, 1};
@@ -150,6 +154,80 @@ bool reshape_view(const Layout &from, int rank, const int64_t *shape, Layout &ou
   return true;
 }
 
+// narrow(axis, start, len) of reshape(`from`, shape) as a view of `from`
+// when the reshape as a whole is none: each group of merged source axes must
+// be contiguous, except the narrowed target axis, whose range may instead lie
+// within one run of its group's innermost source axis (the other axes of the
+// group then take fixed indices). This is how a lane of the max-pool window
+// lanes ([b, c, oh, ow, kh * kw] of a [b, c, oh, ow, kh, kw] window view,
+// src/neural/pooling.rs:10-41) reads the source directly: lane l fixes
+// (l / kw, l % kw). The elements are those the copy would hold, in the same
+// logical order.
+bool narrow_reshape_view(const Layout &from, int rank, const int64_t *shape, int axis, int64_t start, int64_t len,
+                         Layout &out) {
+  if (axis < 0 || axis >= rank || shape[axis] <= 1 || start < 0 || len < 1 || start + len > shape[axis]) return false;
+  std::vector<int64_t> os, ost, ns;
+  std::vector<int> nidx;
+  for (int d = 0; d < from.rank; ++d)
+    if (from.shape[d] != 1) {
+      os.push_back(from.shape[d]);
+      ost.push_back(from.strides[d]);
+    }
+  int narrowed = -1;
+  for (int d = 0; d < rank; ++d)
+    if (shape[d] != 1) {
+      if (d == axis) narrowed = (int)ns.size();
+      ns.push_back(shape[d]);
+      nidx.push_back(d);
+    }
+  std::vector<int64_t> nst(ns.size(), 0);
+  int64_t offset = from.offset;
+  size_t oi = 0, ni = 0;
+  while (oi < os.size() && ni < ns.size()) {
+    int64_t op = os[oi], np = ns[ni];
+    size_t oj = oi + 1, nj = ni + 1;
+    while (op != np) {
+      if (np < op) {
+        if (nj >= ns.size()) return false;
+        np *= ns[nj++];
+      } else {
+        if (oj >= os.size()) return false;
+        op *= os[oj++];
+      }
+    }
+    if ((int)ni <= narrowed && narrowed < (int)nj) {
+      if (nj - ni != 1) return false;  // the narrowed axis must be its group's only target axis
+      const int64_t inner = os[oj - 1];
+      if (start % inner + len > inner) return false;
+      int64_t rest = start / inner;
+      for (size_t k = oj - 1; k-- > oi;) {
+        offset += (rest % os[k]) * ost[k];
+        rest /= os[k];
+      }
+      offset += (start % inner) * ost[oj - 1];
+      nst[ni] = len > 1 ? ost[oj - 1] : 0;
+    } else {
+      for (size_t k = oi; k + 1 < oj; ++k)
+        if (ost[k] != ost[k + 1] * os[k + 1]) return false;
+      nst[nj - 1] = ost[oj - 1];
+      for (size_t k = nj - 1; k-- > ni;) nst[k] = nst[k + 1] * ns[k + 1];
+    }
+    oi = oj;
+    ni = nj;
+  }
+  if (oi != os.size() || ni != ns.size()) return false;
+  Layout l;
+  l.rank = rank;
+  l.offset = offset;
+  for (int d = 0; d < rank; ++d) {
+    l.shape[d] = d == axis ? len : shape[d];
+    l.strides[d] = 0;
+  }
+  for (size_t k = 0; k < ns.size(); ++k) l.strides[nidx[k]] = nst[k];
+  out = l;
+  return true;
+}
+
 enum class StorageKind { kArena, kParameter, kInput, kLeaf, kPool, kSelectionInput, kSelectionLeaf };
 
 struct Storage {
@@ -167,7 +245,9 @@ struct Storage {
 };
 
 struct Value {
-  enum Kind { kNone, kDense, kSelection, kInline, kPadInline } kind = kNone;
+  // kWindow: a convolution's patch matrix (or its transpose) over the dense
+  // source `storage`/`layout`, read only by window products.
+  enum Kind { kNone, kDense, kSelection, kInline, kPadInline, kWindow } kind = kNone;
   int storage = -1;
   Layout layout;
   bool constant = false;
@@ -182,6 +262,12 @@ struct Value {
   // it first.
   int64_t split_inner = 0;
   int64_t split_outer_stride = 0, split_inner_stride = 0;
+  // A reshape that is no view of `layout` as a whole, left unresolved because
+  // only narrows read it and each of them is a view (narrow_reshape_view):
+  // `layout` is the reshape's operand's, the node's shape the reshape's.
+  bool reshape_pending = false;
+  WindowShape window;
+  bool window_transposed = false;
 };
 
 // Device buffers of a bound selection: its indices and their row-sorted
@@ -671,6 +757,169 @@ struct topos_hip_program {
     }
   }
 
+  // ---- window products ----
+
+  // WindowProduct (src/engine/pattern/window.rs:58-150): the canonical
+  // im2col chain reshape(permute(unfold(unfold(pad(pad(x)))))) of conv2d
+  // (src/neural/convolution.rs:24-118). Its interiors (pads, unfolds,
+  // permute) are read only inside the chain, so nothing is launched for
+  // them; the root's value is the patch matrix itself (a kWindow value) and
+  // the products that read it, forward (patches . kernel) and, through the
+  // transpose the MatMul rule records, the kernel gradient (patches^T . g),
+  // gather each element from x. Unlike the reference's election (forward
+  // plans only: there the patches' second reader, the kernel gradient, keeps
+  // the chain materialised), both products read the patch matrix in place.
+  struct WindowRoot {
+    int64_t source = -1;
+    int32_t kernel_height = 0, kernel_width = 0, stride = 1, padding = 0;
+  };
+  std::map<int64_t, WindowRoot> window_roots;
+  std::vector<bool> window_interior;
+
+  bool sole_reader(int64_t i, int64_t reader) const {
+    return wanted[i] && !readable[i] && alias_of[i] < 0 && consumers[i].size() == 1 && consumers[i][0] == reader;
+  }
+
+  // Whether every reader of node i (the patch matrix) is a product taking
+  // it as the left operand, directly or through one transpose.
+  bool window_readers_ok(int64_t i) const {
+    if (consumers[i].empty()) return false;
+    for (int c : consumers[i]) {
+      const topos_hip_node &y = nodes[c];
+      if (y.op == TOPOS_HIP_OP_MATMUL) {
+        if (y.operands[0] != i || y.operands[1] == i || y.rank != 2) return false;
+      } else if (y.op == TOPOS_HIP_OP_TRANSPOSE) {
+        if (readable[c] || consumers[c].empty()) return false;
+        for (int d : consumers[c]) {
+          const topos_hip_node &z = nodes[d];
+          if (z.op != TOPOS_HIP_OP_MATMUL || z.operands[0] != c || z.operands[1] == c || z.rank != 2) return false;
+        }
+      } else {
+        return false;
+      }
+    }
+    return true;
+  }
+
+  void form_window_products() {
+    const int64_t n = (int64_t)nodes.size();
+    window_interior.assign(n, false);
+    for (int64_t i = 0; i < n; ++i) {
+      const topos_hip_node &x = nodes[i];
+      if (!wanted[i] || readable[i] || alias_of[i] >= 0 || x.op != TOPOS_HIP_OP_RESHAPE || x.rank != 2) continue;
+      const int64_t permuted = x.operands[0];
+      const topos_hip_node &p = nodes[permuted];
+      static const int64_t order[6] = {0, 2, 4, 1, 3, 5};
+      if (p.op != TOPOS_HIP_OP_PERMUTE || p.rank != 6 || !sole_reader(permuted, i) ||
+          !std::equal(order, order + 6, p.params))
+        continue;
+      const int64_t across = p.operands[0];
+      const topos_hip_node &uw = nodes[across];
+      if (uw.op != TOPOS_HIP_OP_UNFOLD || !sole_reader(across, permuted) || uw.params[0] != 4 || uw.params[3] != 1)
+        continue;
+      const int64_t down = uw.operands[0];
+      const topos_hip_node &uh = nodes[down];
+      if (uh.op != TOPOS_HIP_OP_UNFOLD || !sole_reader(down, across) || uh.params[0] != 2 || uh.params[3] != 1 ||
+          uh.params[2] != uw.params[2])
+        continue;
+      std::vector<int64_t> interiors = {permuted, across, down};
+      int64_t source = uh.operands[0];
+      int64_t padding = 0;
+      // Symmetric zero pads fold into the gather (a +0 outside the source).
+      if (nodes[source].op == TOPOS_HIP_OP_PAD && sole_reader(source, down) && nodes[source].params[0] == 3) {
+        const int64_t below = nodes[source].operands[0];
+        const topos_hip_node &pw = nodes[source], &ph = nodes[below];
+        if (ph.op == TOPOS_HIP_OP_PAD && sole_reader(below, source) && ph.params[0] == 2) {
+          const topos_hip_node &base = nodes[ph.operands[0]];
+          if (base.rank == 4 && ph.params[1] == pw.params[1] && ph.params[2] == base.shape[2] + 2 * ph.params[1] &&
+              pw.params[2] == base.shape[3] + 2 * pw.params[1]) {
+            interiors.push_back(source);
+            interiors.push_back(below);
+            padding = ph.params[1];
+            source = ph.operands[0];
+          }
+        }
+      }
+      const topos_hip_node &src = nodes[source];
+      if (src.rank != 4 || is_selection_node(source)) continue;
+      const int64_t kh = uh.params[1], kw = uw.params[1], step = uh.params[2];
+      const int64_t ph = src.shape[2] + 2 * padding, pw = src.shape[3] + 2 * padding;
+      if (kh < 1 || kw < 1 || step < 1 || kh > ph || kw > pw) continue;
+      const int64_t oh = (ph - kh) / step + 1, ow = (pw - kw) / step + 1;
+      if (x.shape[0] != src.shape[0] * oh * ow || x.shape[1] != src.shape[1] * kh * kw) continue;
+      if (x.shape[0] > 0x7fffffff || x.shape[1] > 0x7fffffff || ph > 0x7fffffff || pw > 0x7fffffff) continue;
+      if (!window_readers_ok(i)) continue;
+      WindowRoot root;
+      root.source = source;
+      root.kernel_height = (int32_t)kh;
+      root.kernel_width = (int32_t)kw;
+      root.stride = (int32_t)step;
+      root.padding = (int32_t)padding;
+      window_roots[i] = root;
+      for (int64_t j : interiors) window_interior[j] = true;
+    }
+  }
+
+  // The patch-matrix value of window root i over its planned source.
+  Value window_value(int64_t i) {
+    const WindowRoot &root = window_roots.at(i);
+    const Value &src = dense_operand(root.source);
+    if (src.kind != Value::kDense || src.reshape_pending)
+      throw RuntimeFailure{"window product over a source without a dense layout"};
+    const topos_hip_node &s = nodes[root.source];
+    Value v = src;
+    v.kind = Value::kWindow;
+    v.constant = v.host_known = v.never_minus_zero = false;
+    WindowShape &w = v.window;
+    w.offset = src.layout.offset;
+    w.s_batch = src.layout.strides[0];
+    w.s_channel = src.layout.strides[1];
+    w.s_height = src.layout.strides[2];
+    w.s_width = src.layout.strides[3];
+    w.channels = (int32_t)s.shape[1];
+    w.height = (int32_t)s.shape[2];
+    w.width = (int32_t)s.shape[3];
+    w.kernel_height = root.kernel_height;
+    w.kernel_width = root.kernel_width;
+    w.stride = root.stride;
+    w.padding = root.padding;
+    w.out_height = (int32_t)((s.shape[2] + 2 * root.padding - root.kernel_height) / root.stride + 1);
+    w.out_width = (int32_t)((s.shape[3] + 2 * root.padding - root.kernel_width) / root.stride + 1);
+    v.layout = contiguous(nodes[i].rank, nodes[i].shape);
+    return v;
+  }
+
+  // A product whose left operand is a patch matrix: the exact window kernel
+  // in both postures (bit-identical to the product over the materialised
+  // patches, so within the Fast envelope too).
+  void plan_window_matmul(int64_t i) {
+    const topos_hip_node &x = nodes[i];
+    const int64_t m = x.shape[0], n = x.shape[1], k = nodes[x.operands[0]].shape[1];
+    const Value a = values[x.operands[0]];
+    const Value b = dense_operand(x.operands[1]);
+    if (b.kind != Value::kDense || b.reshape_pending) throw RuntimeFailure{"window product operand without a layout"};
+    const int out = arena_storage(m * n * 4);
+    const int64_t brs = b.layout.strides[0], bcs = b.layout.strides[1];
+    const WindowShape w = a.window;
+    const bool transposed = a.window_transposed;
+    const int64_t a_offset = 0, b_offset = b.layout.offset;
+    std::ostringstream what;
+    what << "gemm window " << (transposed ? "patches^T" : "patches") << " (" << m << "," << n << "," << k << ") kernel "
+         << w.kernel_height << "x" << w.kernel_width << " stride " << w.stride << " pad " << w.padding << " b[" << brs
+         << "," << bcs << "]";
+    add_launch(what.str(), {a.storage, b.storage}, {out}, [this, a, b, w, transposed, out, m, n, k, brs, bcs,
+                                                           a_offset, b_offset](const Exec &ex) {
+      launch_window_product((const float *)base(a.storage) + a_offset, w, transposed,
+                            (const float *)base(b.storage) + b_offset, brs, bcs, m, k, n, (float *)base(out), n,
+                            ex.stream);
+    });
+    launches.back().flops = 2.0 * (double)m * n * k;
+    const double source = (double)(w.channels) * w.height * w.width * (double)(transposed ? k : m) /
+                          ((double)w.out_height * w.out_width);
+    launches.back().bytes = 4.0 * (source + (double)k * n + (double)m * n);
+    values[i] = dense_value(out, contiguous(x.rank, x.shape));
+  }
+
   // ---- row groups ----
 
   // A row group: nodes over one [rows, columns] iteration space (full nodes
@@ -680,22 +929,29 @@ struct topos_hip_program {
   // axis, and last-axis SumAlong / LogSumExp / LogSoftmax. The group is
   // launched at its last member; no node outside it consumes a member before
   // that point, and every outside operand is planned before it.
+  // A transposed group (a column program) runs over a rank-2 [R, C] space
+  // whose reductions all run along axis 0, as a row program over [C, R]:
+  // full nodes are read and written through transposed layouts, row nodes
+  // are [C] (BatchNorm's statistics, src/neural/batch_norm.rs:149-176).
   struct RowGroup {
     std::vector<int64_t> members;  // ascending
     int rank = 0;
-    int64_t shape[kMaxRank] = {1, 1, 1, 1, 1, 1};
+    int64_t shape[kMaxRank] = {1, 1, 1, 1, 1, 1};  // the program's space ([C, R] when transposed)
+    bool transposed = false;
   };
   std::vector<RowGroup> row_groups;
   std::vector<int> group_of;
 
   static bool group_full(const topos_hip_node &x, const RowGroup &g) {
     if (x.rank != g.rank) return false;
+    if (g.transposed) return x.shape[0] == g.shape[1] && x.shape[1] == g.shape[0];
     for (int d = 0; d < g.rank; ++d)
       if (x.shape[d] != g.shape[d]) return false;
     return true;
   }
   static bool group_row(const topos_hip_node &x, const RowGroup &g) {
     if (x.rank != g.rank - 1) return false;
+    if (g.transposed) return x.shape[0] == g.shape[0];
     for (int d = 0; d < x.rank; ++d)
       if (x.shape[d] != g.shape[d]) return false;
     return true;
@@ -711,7 +967,14 @@ struct topos_hip_program {
     const topos_hip_node &x = nodes[i];
     if (!wanted[i] || group_of[i] >= 0 || alias_of[i] >= 0) return false;
     if (x.op == TOPOS_HIP_OP_SUM_ALONG && is_selection_node(x.operands[0])) return false;
-    const int last = g.rank - 1;
+    const int last = g.transposed ? 0 : g.rank - 1;  // the reduced axis
+    if (g.transposed) {
+      // Operands a transposed program cannot read: selections and inline pads.
+      for (int j = 0; j < value_links(x.op); ++j) {
+        const int64_t o = x.operands[j];
+        if (is_selection_node(o) || nodes[o].op == TOPOS_HIP_OP_PAD) return false;
+      }
+    }
     if (is_elementwise(x.op)) return group_full(x, g) || group_row(x, g);
     switch (x.op) {
       case TOPOS_HIP_OP_BROADCAST_ALONG: return x.params[0] == last && group_full(x, g);
@@ -731,14 +994,30 @@ struct topos_hip_program {
       RowGroup g;
       if (x.op == TOPOS_HIP_OP_SUM_ALONG || x.op == TOPOS_HIP_OP_LOG_SUM_EXP) {
         const topos_hip_node &a = nodes[x.operands[0]];
-        if (x.params[0] != a.rank - 1) continue;
         if (x.op == TOPOS_HIP_OP_SUM_ALONG && is_selection_node(x.operands[0])) continue;
-        g.rank = a.rank;
-        for (int d = 0; d < a.rank; ++d) g.shape[d] = a.shape[d];
+        if (x.params[0] == a.rank - 1) {
+          g.rank = a.rank;
+          for (int d = 0; d < a.rank; ++d) g.shape[d] = a.shape[d];
+        } else if (x.params[0] == 0 && a.rank == 2 && a.shape[0] <= kColumnProgramRows) {
+          g.rank = 2;
+          g.transposed = true;
+          g.shape[0] = a.shape[1];
+          g.shape[1] = a.shape[0];
+        } else {
+          continue;
+        }
       } else if (x.op == TOPOS_HIP_OP_LOG_SOFTMAX) {
-        if (x.params[0] != x.rank - 1) continue;
-        g.rank = x.rank;
-        for (int d = 0; d < x.rank; ++d) g.shape[d] = x.shape[d];
+        if (x.params[0] == x.rank - 1) {
+          g.rank = x.rank;
+          for (int d = 0; d < x.rank; ++d) g.shape[d] = x.shape[d];
+        } else if (x.params[0] == 0 && x.rank == 2 && x.shape[0] <= kColumnProgramRows) {
+          g.rank = 2;
+          g.transposed = true;
+          g.shape[0] = x.shape[1];
+          g.shape[1] = x.shape[0];
+        } else {
+          continue;
+        }
       } else {
         continue;
       }
@@ -780,6 +1059,22 @@ struct topos_hip_program {
       }
       close_over_operands();
       std::sort(members.begin(), members.end());
+      if (g.transposed) {
+        // A column program reads its columns strided, so it pays only where
+        // it saves launches: statistics broadcast back over the rows (two or
+        // more reductions and a broadcast along axis 0). A lone column sum
+        // stays a column fold.
+        int reductions = 0, broadcasts = 0;
+        for (int64_t m : members) {
+          const int op = nodes[m].op;
+          reductions += op == TOPOS_HIP_OP_SUM_ALONG || op == TOPOS_HIP_OP_LOG_SUM_EXP || op == TOPOS_HIP_OP_LOG_SOFTMAX;
+          broadcasts += op == TOPOS_HIP_OP_BROADCAST_ALONG;
+        }
+        if (reductions < 2 || broadcasts < 1) {
+          for (int64_t m : members) group_of[m] = -1;
+          continue;
+        }
+      }
       g.members = members;
       row_groups.push_back(g);
     }
@@ -788,7 +1083,8 @@ struct topos_hip_program {
   // The input of a row program that reads node o (planned, outside the
   // group) over the group's iteration space: a full node through its layout,
   // a row node through its layout with stride 0 along the last axis.
-  int row_input(RowProgram &p, std::vector<int> &storage_of, std::map<int64_t, int> &input_of, int64_t o) {
+  int row_input(RowProgram &p, std::vector<int> &storage_of, std::map<int64_t, int> &input_of, int64_t o,
+                bool transposed) {
     auto found = input_of.find(o);
     if (found != input_of.end()) return found->second;
     const topos_hip_node &x = nodes[o];
@@ -800,6 +1096,14 @@ struct topos_hip_program {
       in.kind = ExprInput::kLiteral;
       in.one = v.host_value;
       storage = -1;
+    } else if (v.kind == Value::kDense && transposed) {
+      if (v.split_inner > 0 || v.reshape_pending) throw RuntimeFailure{"column program operand without a layout"};
+      in.kind = ExprInput::kStrided;
+      in.offset = v.layout.offset;
+      in.strides[0] = row ? v.layout.strides[0] : v.layout.strides[1];
+      in.strides[1] = row ? 0 : v.layout.strides[0];
+    } else if (transposed) {
+      throw RuntimeFailure{"column program operand without a dense value"};
     } else if (v.kind == Value::kDense) {
       in.kind = ExprInput::kStrided;
       in.offset = v.layout.offset;
@@ -833,12 +1137,13 @@ struct topos_hip_program {
     RowProgram p;
     p.rank = g.rank;
     for (int d = 0; d < g.rank; ++d) p.shape[d] = g.shape[d];
+    p.transposed_outputs = g.transposed;
     std::vector<int> storage_of;
     std::map<int64_t, int> input_of;
     std::map<int64_t, RowRef> ref_of;
     auto ref = [&](int64_t o) -> RowRef {
       if (group_of[o] == id) return ref_of.at(o);
-      return RowRef{RowRef::kInput, row_input(p, storage_of, input_of, o)};
+      return RowRef{RowRef::kInput, row_input(p, storage_of, input_of, o, g.transposed)};
     };
     int zero_input = -1;
     for (int64_t m : g.members) {
@@ -920,8 +1225,8 @@ struct topos_hip_program {
     for (const RowNode &rn : p.nodes)
       folds += rn.kind == RowNode::kSum ? 1 : (rn.kind == RowNode::kLogSumExp || rn.kind == RowNode::kLogSoftmax) ? 2 : 0;
     std::ostringstream what;
-    what << "rows [";
-    for (int d = 0; d < p.rank; ++d) what << (d ? "," : "") << p.shape[d];
+    what << (g.transposed ? "columns [" : "rows [");
+    for (int d = 0; d < p.rank; ++d) what << (d ? "," : "") << p.shape[g.transposed ? p.rank - 1 - d : d];
     what << "] " << p.inputs.size() << " inputs, " << p.nodes.size() << " nodes, " << folds << " folds, "
          << p.full_outputs.size() << "+" << p.row_outputs.size() << " outputs";
     add_launch(what.str(), real(storage_of), writes,
@@ -941,10 +1246,27 @@ struct topos_hip_program {
     }
     int64_t row_shape[kMaxRank];
     for (int d = 0; d + 1 < p.rank; ++d) row_shape[d] = p.shape[d];
-    for (auto &kv : full_out) values[kv.first] = dense_value(full_storage[kv.second], contiguous(p.rank, p.shape));
+    // A transposed program writes its [R, C] nodes row-major.
+    Layout full_layout = contiguous(p.rank, p.shape);
+    if (g.transposed) {
+      const int64_t node_shape[2] = {p.shape[1], p.shape[0]};
+      full_layout = contiguous(2, node_shape);
+    }
+    for (auto &kv : full_out) values[kv.first] = dense_value(full_storage[kv.second], full_layout);
     for (auto &kv : row_out) values[kv.first] = dense_value(row_storage[kv.second], contiguous(p.rank - 1, row_shape));
     for (int64_t b : broadcast_views) {
       const Value &a = values[nodes[b].operands[0]];
+      if (g.transposed) {
+        Layout l;
+        l.rank = 2;
+        l.offset = a.layout.offset;
+        l.shape[0] = columns;
+        l.shape[1] = rows;
+        l.strides[0] = 0;
+        l.strides[1] = a.layout.strides[0];
+        values[b] = view_of(a, l);
+        continue;
+      }
       Layout l;
       l.rank = p.rank;
       l.offset = a.layout.offset;
@@ -1314,6 +1636,7 @@ struct topos_hip_program {
       return dense_value(out, contiguous(n.rank, n.shape));
     }
     if (v.kind != Value::kDense) throw RuntimeFailure{"materialising a value without storage"};
+    if (v.reshape_pending) throw RuntimeFailure{"materialising a pending reshape"};
     Expr e;
     e.rank = n.rank;
     for (int d = 0; d < n.rank; ++d) e.shape[d] = n.shape[d];
@@ -1439,6 +1762,21 @@ struct topos_hip_program {
   }
 
   // Makes node i's value usable as a strided dense operand.
+  // Node i, a reshape of a value laid out as `from`, is read only by
+  // narrows, each of which narrow_reshape_view resolves to a view of `from`.
+  bool narrows_view_through(int64_t i, const Layout &from) const {
+    if (readable[i] || consumers[i].empty()) return false;
+    const topos_hip_node &x = nodes[i];
+    for (int c : consumers[i]) {
+      const topos_hip_node &y = nodes[c];
+      Layout l;
+      if (y.op != TOPOS_HIP_OP_NARROW ||
+          !narrow_reshape_view(from, x.rank, x.shape, (int)y.params[0], y.params[1], y.params[2], l))
+        return false;
+    }
+    return true;
+  }
+
   const Value &dense_operand(int64_t i) {
     if (values[i].kind == Value::kSelection || values[i].split_inner > 0) values[i] = materialize(i);
     return values[i];
@@ -1528,6 +1866,12 @@ struct topos_hip_program {
         return;
       }
       case TOPOS_HIP_OP_TRANSPOSE: {
+        if (values[x.operands[0]].kind == Value::kWindow) {
+          out = values[x.operands[0]];
+          out.window_transposed = !out.window_transposed;
+          out.layout = contiguous(x.rank, x.shape);
+          return;
+        }
         const Value &a = dense_operand(x.operands[0]);
         Layout l = a.layout;
         if (l.rank == 2) {
@@ -1559,9 +1903,19 @@ struct topos_hip_program {
         return;
       }
       case TOPOS_HIP_OP_NARROW: {
+        const int axis = (int)x.params[0];
+        if (values[x.operands[0]].reshape_pending) {
+          const Value &a = values[x.operands[0]];
+          const topos_hip_node &r = nodes[x.operands[0]];
+          Layout l;
+          if (!narrow_reshape_view(a.layout, r.rank, r.shape, axis, x.params[1], x.params[2], l))
+            throw RuntimeFailure{"a narrow of a pending reshape is no view"};
+          out = view_of(a, l);
+          out.reshape_pending = false;
+          return;
+        }
         const Value &a = dense_operand(x.operands[0]);
         Layout l = a.layout;
-        const int axis = (int)x.params[0];
         l.shape[axis] = x.params[2];
         l.offset += x.params[1] * l.strides[axis];
         out = view_of(a, l);
@@ -1621,6 +1975,13 @@ struct topos_hip_program {
           return;
         }
         if (retarget_product(x.operands[0], i, out)) return;
+        // Read only by narrows that are each a view of the operand (the lanes
+        // of a max-pool window): no copy, the narrows view the operand.
+        if (narrows_view_through(i, a.layout)) {
+          out = a;
+          out.reshape_pending = true;
+          return;
+        }
         // Not a view (layout.rs reshape answers None): the interpreter copies
         // the elements out in logical order.
         Value copied = materialize(x.operands[0]);
@@ -1918,6 +2279,10 @@ struct topos_hip_program {
   }
 
   void plan_matmul(int64_t i) {
+    if (values[nodes[i].operands[0]].kind == Value::kWindow) {
+      plan_window_matmul(i);
+      return;
+    }
     if (read_transposed(i)) {
       plan_transposed_matmul(i);
       return;
@@ -2474,10 +2839,15 @@ struct topos_hip_program {
     deduplicate();
     mark_wanted();
     form_row_groups();
+    form_window_products();
     values.assign(nodes.size(), Value());
     mfma_product.assign(nodes.size(), false);
     for (int64_t i = 0; i < (int64_t)nodes.size(); ++i) {
-      if (!wanted[i] || alias_of[i] >= 0) continue;
+      if (!wanted[i] || alias_of[i] >= 0 || window_interior[i]) continue;
+      if (window_roots.count(i)) {
+        values[i] = window_value(i);
+        continue;
+      }
       const int group = group_of[i];
       if (group >= 0) {
         if (i == row_groups[group].members.back()) plan_row_group(group);

@@ -38,9 +38,10 @@ def test_manifest_answers_without_a_device():
     assert (fidelity.value, precisions.value) == (n.ENVELOPE, n.PRECISION_F32)
     assert n.lib.topos_hip_coverage(n.FORMULA_MAP, ctypes.byref(fidelity), ctypes.byref(precisions)) == 1
     assert (fidelity.value, precisions.value) == (n.BIT_IDENTICAL, n.PRECISION_F32)
-    for formula in (n.FORMULA_WINDOW_PRODUCT, n.FORMULA_REDUCE_WINDOW, n.FORMULA_BATCH_NORM_TRAINING,
-                    n.FORMULA_BATCH_NORM_INFERENCE):
-        assert n.lib.topos_hip_coverage(formula, None, None) == 0
+    for formula in (n.FORMULA_WINDOW_PRODUCT, n.FORMULA_REDUCE_WINDOW, n.FORMULA_BATCH_NORM_TRAINING):
+        assert n.lib.topos_hip_coverage(formula, ctypes.byref(fidelity), ctypes.byref(precisions)) == 1
+        assert (fidelity.value, precisions.value) == (n.BIT_IDENTICAL, n.PRECISION_F32)
+    assert n.lib.topos_hip_coverage(n.FORMULA_BATCH_NORM_INFERENCE, None, None) == 0
 
 
 def test_coverage_matches_the_integration_table():

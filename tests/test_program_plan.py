@@ -280,3 +280,46 @@ print("Powf" in d, p.info["launches"])
 ''')
     ok, launches = out.split()
     assert ok == "True" and int(launches) >= 1, out
+
+
+def test_composed_formulas_plan_their_dedicated_forms():
+    """The reference pattern bench's three composed formulas
+    (benches/pattern.rs; src/backend/formula.rs:30-37): conv2d's im2col chain
+    becomes one window product with no pad or copy launch (WindowProduct);
+    max_pool's lanes are read through window views, one launch
+    (ReduceWindow); BatchNorm's statistics, normalisation and affine map are
+    one column program (BatchNormTraining). The coverage cells say so."""
+    out = run(r'''
+import ctypes
+for numerics in (n.EXACT, n.FAST):
+    tape = t.Tape()
+    x = tape.input((64, 16, 14, 14)); w = tape.parameter((32, 16, 3, 3)); b = tape.parameter((32,))
+    conv = DeviceProgram(tape, [t.conv2d(x, w, b, 1, 1)], numerics=numerics).describe
+    tape = t.Tape()
+    pool = DeviceProgram(tape, [t.max_pool(tape.input((64, 32, 28, 28)), 2, 2)], numerics=numerics)
+    tape = t.Tape()
+    x = tape.input((256, 512)); s = tape.parameter((512,)); h = tape.parameter((512,))
+    o, mean, var = t.batch_norm(x, s, h, tape.leaf(t.Constant((), 1e-5)))
+    norm = DeviceProgram(tape, [o, mean, var], numerics=numerics)
+    print("gemm window patches" in conv, "pad [" not in conv, "copy [64,14,14" not in conv,
+          pool.info["launches"], norm.info["launches"], "columns [256,512]" in norm.describe)
+fidelity, precisions = ctypes.c_int(), ctypes.c_uint()
+for formula in (n.lib.topos_hip_coverage(2, ctypes.byref(fidelity), ctypes.byref(precisions)),
+                n.lib.topos_hip_coverage(3, ctypes.byref(fidelity), ctypes.byref(precisions)),
+                n.lib.topos_hip_coverage(4, ctypes.byref(fidelity), ctypes.byref(precisions))):
+    print(formula, fidelity.value, precisions.value)
+''')
+    lines = out.splitlines()
+    assert lines[0] == lines[1] == "True True True 1 1 True", out
+    assert lines[2:] == ["1 0 1"] * 3, out
+
+
+def test_max_pool_lanes_in_a_training_step_read_the_source():
+    """In a training step the pooled lanes also feed maximum's gradient rules:
+    every lane is still a view of the window source, so no copy is planned."""
+    out = run(r'''
+w = workloads.cnn(batch=8)
+d = DeviceProgram(w.tape, w.roots).describe
+print("copy [8,8,14,14,2,2]" in d, "copy [8,16,7,7,2,2]" in d, d.count("gemm window"))
+''')
+    assert out.split() == ["False", "False", "4"], out
