@@ -143,12 +143,14 @@ int topos_hip_coverage(int formula, int *fidelity, unsigned *precisions) {
   // from the posture it is handed, and the envelope is the weaker guarantee
   // the cell may promise. Map is bit-identical: every operation matches the
   // host libm on all 2^32 inputs. Three composed formulas are elected onto
-  // device programs, each bit-identical in both postures (the composed
+  // device programs, each bit-identical under Exact (the composed
   // recording's bits, as src/backend/fused.rs:18-50 declares for the
-  // reference's own fused kernels): WindowProduct as window products that
-  // gather the patch matrix, ReduceWindow as lanes viewed from the source in
-  // one launch, BatchNormTraining as one column program. BatchNormInference
-  // stays absent, as in the reference.
+  // reference's own fused kernels, whose products take the envelope under
+  // Fast through the gemm seam): WindowProduct as window products that
+  // gather the patch matrix (under Fast a kernel gradient with few outputs
+  // runs in ranges of whole images), ReduceWindow as lanes viewed from the
+  // source in one launch, BatchNormTraining as one column program.
+  // BatchNormInference stays absent, as in the reference.
   switch (formula) {
     case TOPOS_HIP_FORMULA_GEMM:
       if (fidelity) *fidelity = TOPOS_HIP_ENVELOPE;

@@ -172,20 +172,56 @@ void launch_gemm_exact(const float *a, int64_t a_rs, int64_t a_cs, const float *
 // strided windows of a rank-4 [batch, channels, height, width] source read
 // through any strides; +0 where a window leaves the source (the padding).
 // The patch matrix of src/payload/tensor.rs:1475-1544.
+// Division of a 32-bit index below 2^31 by a fixed divisor d >= 1 as a
+// multiply and a shift: with l = ceil(log2 d) and magic = ceil(2^(32+l) / d),
+// floor(i * magic / 2^(32+l)) = floor(i / d), since the magic's excess over
+// 2^(32+l) / d adds less than i / 2^(32+l) < 2^-(l+1) <= 1/(2d) to a quotient
+// whose fraction is at most (d - 1) / d. (i * magic < 2^31 * 2^33 fits 64
+// bits.)
+struct Divisor {
+  uint64_t magic = 1ull << 32;
+  uint32_t shift = 32;
+  static Divisor of(uint32_t d) {
+    Divisor v;
+    uint32_t l = 0;
+    while ((1ull << l) < d) ++l;
+    v.shift = 32 + l;  // l <= 31 for d <= 2^31
+    v.magic = ((1ull << v.shift) - 1) / d + 1;
+    return v;
+  }
+  __host__ __device__ uint32_t divide(uint32_t i) const { return (uint32_t)(((uint64_t)i * magic) >> shift); }
+};
+
 struct WindowShape {
   int64_t offset = 0;
   int64_t s_batch = 0, s_channel = 0, s_height = 0, s_width = 0;
   int32_t channels = 0, height = 0, width = 0;
   int32_t kernel_height = 0, kernel_width = 0, out_height = 0, out_width = 0, stride = 1, padding = 0;
+  // Set by launch_window_product from the extents above.
+  Divisor by_out_width, by_out_height, by_kernel_width, by_kernel_height;
 };
 // WindowProduct (src/payload/tensorial.rs:112-122, elected by
 // src/engine/pattern/window.rs:58-150): patches . b ([m, k] . [k, n], m the
 // patch rows) or, transposed, patches^T . b ([m, k] with m the patch columns
 // and k the patch rows: the kernel gradient), bit-identical to
-// gemm::multiply over the materialised patches.
+// gemm::multiply over the materialised patches. With `splits` > 1 (the
+// transposed form only, window_splits' choice, and a workspace of splits * m
+// * n floats) the patch rows are cut at image boundaries into that many
+// ranges, each range's chain is exact, and the partials are added in range
+// order: deterministic, within the Fast envelope, not bit-identical.
 void launch_window_product(const float *source, const WindowShape &w, bool transposed, const float *b, int64_t b_rs,
                            int64_t b_cs, int64_t m, int64_t k, int64_t n, float *c, int64_t ldc,
-                           hipStream_t stream);
+                           hipStream_t stream, float *workspace = nullptr, int splits = 1);
+// The ranges a Fast kernel gradient (patches^T . b, m patch columns, n
+// filters, k patch rows over `images` images) is cut into: 1 when its
+// outputs fill the chip or its chains are short, else the largest divisor of
+// `images` up to 16 that leaves each range at least 512 rows.
+int window_splits(int64_t m, int64_t n, int64_t k, int64_t images);
+// gemm_mfma.hip: c[i][j] = ((p_0 + p_1) + p_2) + ... over `splits`
+// contiguous [m][n] partials (c's rows ldc apart), m * n % 4 == 0 or n % 4 ==
+// 0, m * n < 2^33.
+void launch_split_reduce(const float *partials, int splits, int64_t m, int64_t n, float *c, int64_t ldc,
+                         hipStream_t stream);
 // gemm_mfma.hip: fp32 MFMA product within the stated envelope. Returns false
 // when the stride pattern is outside its loaders (caller falls back).
 // With a workspace of at least mfma_splits(m, n, k, count) * count * m * n

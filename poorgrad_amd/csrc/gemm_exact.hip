@@ -33,18 +33,26 @@ enum { kGeneric = 0, kInnerUnit = 1, kOuterUnit = 2, kWindowRows = 3, kWindowCol
 // Element (row, col) of the patch matrix: row = (image, out_y, out_x),
 // col = (channel, kernel_y, kernel_x), the source element under that window
 // position or +0 in the padding (zero_like of an f32 element, as the padded
-// copy holds).
+// copy holds), or +0 when `valid` is false (a slab's overhang). The load is
+// unconditional, from the view's first element when the position reads
+// nothing, and the value is selected afterwards: loads under branches made
+// the compiler wait for each earlier load before the next (the branch's +0
+// and the load share a register). The caller launches no window kernel over
+// an empty source, so the first element exists.
 __device__ __forceinline__ float window_element(const float *__restrict__ src, const WindowShape &w, uint32_t row,
-                                                uint32_t col) {
-  const uint32_t x = row % (uint32_t)w.out_width, t = row / (uint32_t)w.out_width;
-  const uint32_t y = t % (uint32_t)w.out_height, image = t / (uint32_t)w.out_height;
-  const uint32_t kx = col % (uint32_t)w.kernel_width, u = col / (uint32_t)w.kernel_width;
-  const uint32_t ky = u % (uint32_t)w.kernel_height, channel = u / (uint32_t)w.kernel_height;
+                                                uint32_t col, bool valid) {
+  const uint32_t t = w.by_out_width.divide(row), x = row - t * (uint32_t)w.out_width;
+  const uint32_t image = w.by_out_height.divide(t), y = t - image * (uint32_t)w.out_height;
+  const uint32_t u = w.by_kernel_width.divide(col), kx = col - u * (uint32_t)w.kernel_width;
+  const uint32_t channel = w.by_kernel_height.divide(u), ky = u - channel * (uint32_t)w.kernel_height;
   const int32_t hy = (int32_t)(y * (uint32_t)w.stride + ky) - w.padding;
   const int32_t wx = (int32_t)(x * (uint32_t)w.stride + kx) - w.padding;
-  if (hy < 0 || hy >= w.height || wx < 0 || wx >= w.width) return 0.0f;
-  return src[w.offset + (int64_t)image * w.s_batch + (int64_t)channel * w.s_channel + (int64_t)hy * w.s_height +
-             (int64_t)wx * w.s_width];
+  const bool inside = valid && (uint32_t)hy < (uint32_t)w.height && (uint32_t)wx < (uint32_t)w.width;
+  const int64_t at = inside ? (int64_t)image * w.s_batch + (int64_t)channel * w.s_channel +
+                                  (int64_t)hy * w.s_height + (int64_t)wx * w.s_width
+                            : 0;
+  const float v = src[w.offset + at];
+  return inside ? v : 0.0f;
 }
 
 // One kTileK x E slab of an operand (outer index o0.., inner k0..) in a
@@ -68,10 +76,9 @@ struct Stage {
       const int o = kMode == kWindowRows ? flat % E : flat / kTileK;
       const int kk = kMode == kWindowRows ? flat / E : flat % kTileK;
       const int64_t go = o0 + o, gk = k0 + kk;
-      v[e] = 0.0f;
-      if (go < outer_extent && gk < k)
-        v[e] = kMode == kWindowRows ? window_element(p, w, (uint32_t)go, (uint32_t)gk)
-                                    : window_element(p, w, (uint32_t)gk, (uint32_t)go);
+      const bool valid = go < outer_extent && gk < k;
+      v[e] = kMode == kWindowRows ? window_element(p, w, (uint32_t)go, (uint32_t)gk, valid)
+                                  : window_element(p, w, (uint32_t)gk, (uint32_t)go, valid);
     }
   }
 
@@ -299,9 +306,9 @@ __global__ __launch_bounds__(kThreads) void gemm_exact_small_kernel(
       coords(e, kLeftUnitInner, o, kk);
       const int64_t gm = m0 + o, gk = k0 + kk;
       if constexpr (kLeftWindow == kWindowRows)
-        va[e] = (gm < m && gk < k) ? window_element(a, w, (uint32_t)gm, (uint32_t)gk) : 0.0f;
+        va[e] = window_element(a, w, (uint32_t)gm, (uint32_t)gk, gm < m && gk < k);
       else if constexpr (kLeftWindow == kWindowCols)
-        va[e] = (gm < m && gk < k) ? window_element(a, w, (uint32_t)gk, (uint32_t)gm) : 0.0f;
+        va[e] = window_element(a, w, (uint32_t)gk, (uint32_t)gm, gm < m && gk < k);
       else
         va[e] = (gm < m && gk < k) ? a[gm * a_rs + gk * a_cs] : 0.0f;
       coords(e, kRightUnitInner, o, kk);
@@ -334,6 +341,173 @@ __global__ __launch_bounds__(kThreads) void gemm_exact_small_kernel(
   }
   const int64_t row = m0 + ti, col = n0 + tj;
   if (row < m && col < n) c[row * ldc + col] = acc;
+}
+
+// A convolution's kernel gradient with few outputs (patches^T . b: m patch
+// columns by n filters over k patch rows; the MNIST stages' [9, 8] over
+// 50176 rows): one output per lane, up to 16x16 outputs a workgroup, each lane's
+// chain over ascending patch rows staged 256 deep. The workgroup is eight
+// waves: four chain waves (one output a lane) and four producer waves that
+// gather the next slab into the other of two LDS buffers while the chain
+// waves walk the current one, so the gather's address arithmetic does not
+// sit in the chain waves' instruction stream. Producer lane p gathers patch
+// row k0 + p for the tile's 16 columns: the row's (image, y, x) is divided
+// out once a slab, each column's (channel, ky, kx) once a launch. The chain
+// reads 32 terms as sixteen 16-byte LDS reads issued together (rows padded
+// by four floats, so the 16 right-hand rows a wave reads fall in distinct
+// banks). Batch z (the Fast posture's ranges of whole images) offsets the
+// source, b and c.
+constexpr int kDeep = 16;
+constexpr int kDeepK = 256;
+
+__global__ __launch_bounds__(2 * kThreads) void window_deep_kernel(const float *__restrict__ src,
+                                                                   const WindowShape w, const float *__restrict__ b,
+                                                                   int64_t b_rs, int64_t b_cs, int64_t m, int64_t k,
+                                                                   int64_t n, float *__restrict__ c, int64_t ldc,
+                                                                   int64_t a_bs, int64_t b_bs, int64_t c_bs) {
+  static_assert(kDeepK == kThreads && kDeep * kDeep == kThreads, "one patch row a lane, one output a lane");
+  __shared__ __attribute__((aligned(16))) float left[2][kDeep][kDeepK + 4];
+  __shared__ __attribute__((aligned(16))) float right[2][kDeep][kDeepK + 4];
+  src += w.offset + (int64_t)blockIdx.z * a_bs;
+  b += (int64_t)blockIdx.z * b_bs;
+  c += (int64_t)blockIdx.z * c_bs;
+  const int64_t m0 = (int64_t)blockIdx.y * kDeep, n0 = (int64_t)blockIdx.x * kDeep;
+  const bool producer = threadIdx.x >= kThreads;
+  const int t = threadIdx.x & (kThreads - 1), tj = t % kDeep;
+  // Chain lanes hold the tile's outputs densely (row-major over its mt x nt
+  // outputs), so only the waves that own outputs read the LDS slabs: the
+  // chain waves are bound by the LDS bytes they read.
+  const int mt = m - m0 < kDeep ? (int)(m - m0) : kDeep, nt = n - n0 < kDeep ? (int)(n - n0) : kDeep;
+  const bool owner = t < mt * nt;
+  const int out_i = owner ? t / nt : 0, out_j = owner ? t % nt : 0;
+  const bool walks = (t & ~63) < mt * nt;  // the wave owns at least one output
+  constexpr int32_t kOutside = -(1 << 30);  // a window offset that no in-range sum reaches
+
+  // ---- producers: the gather ----
+  // Values of rows past k, of columns past m and of filters past n are never
+  // read by a stored output's chain, so their addresses are only clamped in
+  // range; the padding's +0 is selected. The tile's columns (patch columns
+  // m0 + e, clamped to m - 1): source offset and kernel position.
+  int32_t col_ky[kDeep], col_kx[kDeep];
+  int64_t col_off[kDeep];
+  // Two register sets: a slab's loads are issued two slabs before its
+  // deposit (each slab's rows of b come from HBM once; one slab of lead did
+  // not cover their latency).
+  float va0[kDeep], vb0[kDeep], va1[kDeep], vb1[kDeep];
+  const float *b_lane = b;  // b's element (row t / 16, filter n0 + tj, clamped)
+  if (producer) {
+#pragma unroll
+    for (int e = 0; e < kDeep; ++e) {
+      const uint32_t o = (uint32_t)(m0 + e < m ? m0 + e : m - 1);
+      const uint32_t u = w.by_kernel_width.divide(o), kx = o - u * (uint32_t)w.kernel_width;
+      const uint32_t channel = w.by_kernel_height.divide(u), ky = u - channel * (uint32_t)w.kernel_height;
+      col_ky[e] = (int32_t)ky;
+      col_kx[e] = (int32_t)kx;
+      col_off[e] = (int64_t)channel * w.s_channel + (int64_t)ky * w.s_height + (int64_t)kx * w.s_width;
+    }
+    b_lane = b + (n0 + tj < n ? n0 + tj : n - 1) * b_cs;
+  }
+  auto fetch = [&](float (&va)[kDeep], float (&vb)[kDeep], int64_t k0) {
+    const int64_t r = k0 + t < k ? k0 + t : k - 1;
+    const uint32_t q = w.by_out_width.divide((uint32_t)r), x = (uint32_t)r - q * (uint32_t)w.out_width;
+    const uint32_t image = w.by_out_height.divide(q), y = q - image * (uint32_t)w.out_height;
+    const int32_t y0 = (int32_t)(y * (uint32_t)w.stride) - w.padding;
+    const int32_t x0 = (int32_t)(x * (uint32_t)w.stride) - w.padding;
+    const int64_t base = (int64_t)image * w.s_batch + (int64_t)y0 * w.s_height + (int64_t)x0 * w.s_width;
+    const bool whole = k0 + kDeepK <= k;
+    // Unconditional loads (clamped), values selected afterwards: see
+    // window_element.
+#pragma unroll
+    for (int e = 0; e < kDeep; ++e) {
+      const int32_t hy = y0 + col_ky[e], wx = x0 + col_kx[e];
+      const bool inside = (uint32_t)hy < (uint32_t)w.height && (uint32_t)wx < (uint32_t)w.width;
+      const float a_value = src[inside ? base + col_off[e] : 0];
+      va[e] = inside ? a_value : 0.0f;
+      const int64_t gk = k0 + e * kDeep + t / kDeep;
+      vb[e] = b_lane[(whole || gk < k ? gk : k - 1) * b_rs];
+    }
+  };
+  auto deposit = [&](const float (&va)[kDeep], const float (&vb)[kDeep], int buffer) {
+#pragma unroll
+    for (int e = 0; e < kDeep; ++e) {
+      left[buffer][e][t] = va[e];
+      right[buffer][tj][e * kDeep + t / kDeep] = vb[e];
+    }
+  };
+
+  // ---- chain waves: the ordered sum ----
+  float acc = 0.0f;
+  auto chain = [&](int64_t k0, int buffer) {
+    const int steps = (k - k0) < kDeepK ? (int)(k - k0) : kDeepK;
+    const float *lrow = left[buffer][out_i], *rrow = right[buffer][out_j];
+    int s = 0;
+    if (k0 == 0) {
+      acc = __fmul_rn(lrow[0], rrow[0]);  // the seed: the first term itself (gemm.rs:151-160)
+      for (s = 1; s < 4 && s < steps; ++s) acc = __fadd_rn(acc, __fmul_rn(lrow[s], rrow[s]));
+    }
+    const int whole = steps & ~3;
+    // Blocks of 32 terms: all sixteen 16-byte LDS reads issued before the
+    // block's chain, so the LDS latency is met once a block, not once every
+    // four terms.
+    for (; s + 32 <= whole; s += 32) {
+      float4 l[8], r[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        l[q] = *reinterpret_cast<const float4 *>(lrow + s + 4 * q);
+        r[q] = *reinterpret_cast<const float4 *>(rrow + s + 4 * q);
+      }
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        acc = __fadd_rn(acc, __fmul_rn(l[q].x, r[q].x));
+        acc = __fadd_rn(acc, __fmul_rn(l[q].y, r[q].y));
+        acc = __fadd_rn(acc, __fmul_rn(l[q].z, r[q].z));
+        acc = __fadd_rn(acc, __fmul_rn(l[q].w, r[q].w));
+      }
+    }
+    for (; s < whole; s += 4) {
+      const float4 l = *reinterpret_cast<const float4 *>(lrow + s);
+      const float4 r = *reinterpret_cast<const float4 *>(rrow + s);
+      acc = __fadd_rn(acc, __fmul_rn(l.x, r.x));
+      acc = __fadd_rn(acc, __fmul_rn(l.y, r.y));
+      acc = __fadd_rn(acc, __fmul_rn(l.z, r.z));
+      acc = __fadd_rn(acc, __fmul_rn(l.w, r.w));
+    }
+    for (; s < steps; ++s) acc = __fadd_rn(acc, __fmul_rn(lrow[s], rrow[s]));
+  };
+
+  // Slab s is walked from buffer s % 2 while the producers deposit slab
+  // s + 1 (register set (s + 1) % 2, loaded since slab s - 2) into the other
+  // buffer and issue slab s + 3's loads into the set just emptied; one
+  // barrier a slab. The loop body is written twice, for even and odd s.
+  if (producer) {
+    fetch(va0, vb0, 0);
+    deposit(va0, vb0, 0);
+    if (kDeepK < k) fetch(va1, vb1, kDeepK);
+    if (2 * kDeepK < k) fetch(va0, vb0, 2 * kDeepK);
+  }
+  __syncthreads();
+  for (int64_t k0 = 0; k0 < k; k0 += 2 * kDeepK) {
+    if (producer) {
+      if (k0 + kDeepK < k) {
+        deposit(va1, vb1, 1);
+        if (k0 + 3 * kDeepK < k) fetch(va1, vb1, k0 + 3 * kDeepK);
+      }
+    } else if (walks) {
+      chain(k0, 0);
+    }
+    __syncthreads();
+    if (k0 + kDeepK >= k) break;
+    if (producer) {
+      if (k0 + 2 * kDeepK < k) {
+        deposit(va0, vb0, 0);
+        if (k0 + 4 * kDeepK < k) fetch(va0, vb0, k0 + 4 * kDeepK);
+      }
+    } else if (walks) {
+      chain(k0 + kDeepK, 1);
+    }
+    __syncthreads();
+  }
+  if (!producer && owner) c[(m0 + out_i) * ldc + n0 + out_j] = acc;
 }
 
 }  // namespace
@@ -450,18 +624,62 @@ void launch_gemm_exact(const float *a, int64_t a_rs, int64_t a_cs, const float *
   enqueue_exact(kGeneric, WindowShape(), a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, stream, batch);
 }
 
-void launch_window_product(const float *source, const WindowShape &w, bool transposed, const float *b, int64_t b_rs,
-                           int64_t b_cs, int64_t m, int64_t k, int64_t n, float *c, int64_t ldc,
-                           hipStream_t stream) {
+int window_splits(int64_t m, int64_t n, int64_t k, int64_t images) {
+  // Enough 16x16 output tiles to fill the chip, or partials the reduction
+  // cannot take in quads: one range.
+  if (((m + kDeep - 1) / kDeep) * ((n + kDeep - 1) / kDeep) >= 256 || images < 2) return 1;
+  if ((m * n) % 4 != 0 && n % 4 != 0) return 1;
+  int best = 1;
+  for (int s = 2; s <= 16; ++s)
+    if (images % s == 0 && k / s >= 512) best = s;
+  return best;
+}
+
+void launch_window_product(const float *source, const WindowShape &shape, bool transposed, const float *b,
+                           int64_t b_rs, int64_t b_cs, int64_t m, int64_t k, int64_t n, float *c, int64_t ldc,
+                           hipStream_t stream, float *workspace, int splits) {
   // The patch matrix is [batch * out_height * out_width, channels *
   // kernel_height * kernel_width]; its indices are taken in 32 bits.
   const int64_t rows = transposed ? k : m, columns = transposed ? m : k;
-  const int64_t positions = (int64_t)w.out_height * w.out_width;
-  if (positions <= 0 || rows % positions != 0 || columns != (int64_t)w.channels * w.kernel_height * w.kernel_width ||
-      rows > 0x7fffffff || columns > 0x7fffffff)
+  const int64_t positions = (int64_t)shape.out_height * shape.out_width;
+  if (shape.out_height < 1 || shape.out_width < 1 || shape.kernel_height < 1 || shape.kernel_width < 1 ||
+      rows % positions != 0 ||
+      columns != (int64_t)shape.channels * shape.kernel_height * shape.kernel_width || rows > 0x7fffffff ||
+      columns > 0x7fffffff)
     throw Unsupported{"window product: extents outside the patch matrix"};
-  enqueue_exact(transposed ? kWindowCols : kWindowRows, w, source, 0, 0, b, b_rs, b_cs, m, k, n, c, ldc, stream,
-                Batch());
+  if (m == 0 || n == 0) return;
+  if (rows == 0 || columns == 0) {
+    // An empty source: every output is the empty sum, +0 (the exact kernel
+    // with k = 0 reads nothing and writes +0).
+    launch_gemm_exact(c, 0, 0, c, 0, 0, m, 0, n, c, ldc, stream);
+    return;
+  }
+  WindowShape w = shape;
+  w.by_out_width = Divisor::of((uint32_t)w.out_width);
+  w.by_out_height = Divisor::of((uint32_t)w.out_height);
+  w.by_kernel_width = Divisor::of((uint32_t)w.kernel_width);
+  w.by_kernel_height = Divisor::of((uint32_t)w.kernel_height);
+  const int64_t images = rows / positions;
+  if (splits > 1 && (!transposed || workspace == nullptr || images % splits != 0 || splits > 16 ||
+                     ((m * n) % 4 != 0 && n % 4 != 0)))
+    throw Unsupported{"window product: ranges outside what the split form takes"};
+  const int64_t tiles = ((m + 63) / 64) * ((n + 63) / 64);
+  if (!transposed || (splits <= 1 && tiles >= 256)) {
+    enqueue_exact(transposed ? kWindowCols : kWindowRows, w, source, 0, 0, b, b_rs, b_cs, m, k, n, c, ldc, stream,
+                  Batch());
+    return;
+  }
+  const int z = splits > 1 ? splits : 1;
+  const int64_t range = k / z;  // patch rows of each range: whole images
+  const int64_t grid_m = (m + kDeep - 1) / kDeep, grid_n = (n + kDeep - 1) / kDeep;
+  if (grid_m > 65535 || grid_n > 0x7fffffff) throw Unsupported{"window product: too many output tiles"};
+  const dim3 grid((unsigned)grid_n, (unsigned)grid_m, (unsigned)z);
+  float *target = z > 1 ? workspace : c;
+  const int64_t target_ld = z > 1 ? n : ldc;
+  window_deep_kernel<<<grid, 2 * kThreads, 0, stream>>>(source, w, b, b_rs, b_cs, m, range, n, target, target_ld,
+                                                     range / positions * w.s_batch, range * b_rs, m * n);
+  check_launch("window_deep_kernel launch");
+  if (z > 1) launch_split_reduce(workspace, z, m, n, c, ldc, stream);
 }
 
 }  // namespace topos_hip

@@ -802,6 +802,28 @@ __global__ __launch_bounds__(256) void split_reduce_flat_kernel(const float4 *__
 
 }  // namespace
 
+void launch_split_reduce(const float *partials, int splits, int64_t m, int64_t n, float *c, int64_t ldc,
+                         hipStream_t stream) {
+  const int64_t quads = m * n / 4;
+  const bool flat = ldc == n && (m * n) % 4 == 0;
+  if (splits < 1 || splits > 16 || m < 0 || n < 0 || (!flat && n % 4 != 0) || quads >= (int64_t(1) << 32) ||
+      reinterpret_cast<uintptr_t>(partials) % 16 != 0)
+    throw Unsupported{"split reduce: partials outside what the reduction takes"};
+  if (quads == 0) return;
+  int64_t blocks = (quads + 255) / 256;
+  if (blocks > 256 * 32) blocks = 256 * 32;
+  if (flat) {
+    split_reduce_flat_kernel<<<(unsigned)blocks, 256, 0, stream>>>(
+        reinterpret_cast<const float4 *>(partials), splits, (uint32_t)quads, (uint32_t)n, c, nullptr, 0, 0,
+        reinterpret_cast<uintptr_t>(c) % 16 == 0);
+  } else {
+    split_reduce_kernel<<<(unsigned)blocks, 256, 0, stream>>>(
+        reinterpret_cast<const float4 *>(partials), splits, (uint32_t)quads, (uint32_t)m, (uint32_t)(n / 4), c, ldc,
+        0, nullptr, 0, 0, reinterpret_cast<uintptr_t>(c) % 16 == 0 && ldc % 4 == 0);
+  }
+  check_launch("split_reduce_kernel launch");
+}
+
 int mfma_splits(int64_t m, int64_t n, int64_t k, int64_t batches) {
   // A full chip holds per_cu workgroups on each of the 256 CUs; a product
   // with fewer tiles is split along k until it reaches that, each split at

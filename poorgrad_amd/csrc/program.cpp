@@ -889,9 +889,10 @@ struct topos_hip_program {
     return v;
   }
 
-  // A product whose left operand is a patch matrix: the exact window kernel
-  // in both postures (bit-identical to the product over the materialised
-  // patches, so within the Fast envelope too).
+  // A product whose left operand is a patch matrix: exact window kernels
+  // (bit-identical to the product over the materialised patches). Under Fast
+  // a kernel gradient with few outputs cuts its patch rows into ranges of
+  // whole images, each an exact chain, added in range order (the envelope).
   void plan_window_matmul(int64_t i) {
     const topos_hip_node &x = nodes[i];
     const int64_t m = x.shape[0], n = x.shape[1], k = nodes[x.operands[0]].shape[1];
@@ -903,15 +904,25 @@ struct topos_hip_program {
     const WindowShape w = a.window;
     const bool transposed = a.window_transposed;
     const int64_t a_offset = 0, b_offset = b.layout.offset;
+    const int64_t positions = (int64_t)w.out_height * w.out_width;
+    int splits = 1;
+    int workspace = -1;
+    if (numerics == TOPOS_HIP_FAST && transposed && positions > 0 && k % positions == 0) {
+      splits = window_splits(m, n, k, k / positions);
+      if (splits > 1) workspace = arena_storage((int64_t)splits * m * n * 4);
+    }
     std::ostringstream what;
     what << "gemm window " << (transposed ? "patches^T" : "patches") << " (" << m << "," << n << "," << k << ") kernel "
          << w.kernel_height << "x" << w.kernel_width << " stride " << w.stride << " pad " << w.padding << " b[" << brs
          << "," << bcs << "]";
-    add_launch(what.str(), {a.storage, b.storage}, {out}, [this, a, b, w, transposed, out, m, n, k, brs, bcs,
-                                                           a_offset, b_offset](const Exec &ex) {
+    if (splits > 1) what << " in " << splits << " ranges";
+    std::vector<int> writes = {out};
+    if (workspace >= 0) writes.push_back(workspace);
+    add_launch(what.str(), {a.storage, b.storage}, writes, [this, a, b, w, transposed, out, m, n, k, brs, bcs,
+                                                            a_offset, b_offset, splits, workspace](const Exec &ex) {
       launch_window_product((const float *)base(a.storage) + a_offset, w, transposed,
                             (const float *)base(b.storage) + b_offset, brs, bcs, m, k, n, (float *)base(out), n,
-                            ex.stream);
+                            ex.stream, workspace >= 0 ? (float *)base(workspace) : nullptr, splits);
     });
     launches.back().flops = 2.0 * (double)m * n * k;
     const double source = (double)(w.channels) * w.height * w.width * (double)(transposed ? k : m) /
