@@ -614,20 +614,26 @@ __global__ __launch_bounds__(BM / WM * BN, BM == 256 ? 4 : 3) void gemm_dma_kern
   store_block<WM, kT>(acc, c, ldc, m, n, m0, n0, wm, wn, lane, bias, bias_cs, bias_mode);
 }
 
-// The tile shape for an m x n product (over `batches`): 128x64 or 64x128
-// when one output extent is at most 64; 256x128 (eight waves, less operand
-// traffic per flop than 128x128) when its tiles fill whole rounds of two
-// workgroups per CU, or at least one and a half such rounds (measured on
-// MI355X: the [8192, 3072] products gain, [8192, 2304] loses); else 128x128.
-// `per_cu` is how many of its workgroups a CU holds at once.
+// The tile shape for an m x n product over k (and `batches`): 128x64 or
+// 64x128 when one output extent is at most 64; 256x128 (eight waves, less
+// operand traffic per flop than 128x128) when its tiles fill whole rounds of
+// two workgroups per CU, or at least one and a half such rounds (measured on
+// MI355X: the [8192, 3072] products gain, [8192, 2304] loses); 64x128 when k
+// is at most 1024 and those tiles fill whole rounds of three workgroups per
+// CU (measured in the GPT-2 step: the [8192, 768] products over k = 768 took
+// 95 us against 106 on 128x128 tiles in two ranges, [8192, 2304] over 768
+// 262 against 269); else 128x128. `per_cu` is how many of its workgroups a
+// CU holds at once.
 struct TileShape {
   int bm, bn, per_cu;
 };
-TileShape tile_shape(int64_t m, int64_t n, int64_t batches) {
+TileShape tile_shape(int64_t m, int64_t n, int64_t k, int64_t batches) {
   if (n <= 64 && m > 64) return {128, 64, 3};
   if (m <= 64 && n > 64) return {64, 128, 3};
   const int64_t wide = ((m + 255) / 256) * ((n + 127) / 128) * batches;
   if (wide >= 768 || (wide >= 512 && wide % 512 == 0)) return {256, 128, 2};
+  const int64_t thin = ((m + 63) / 64) * ((n + 127) / 128) * batches;
+  if (k <= 1024 && thin >= 768 && thin % 768 == 0) return {64, 128, 3};
   return {128, 128, 3};
 }
 
@@ -830,7 +836,7 @@ int mfma_splits(int64_t m, int64_t n, int64_t k, int64_t batches) {
   // least 256 deep (64 below k = 1024), and deep products are split further
   // (up to 2048 workgroups while each split stays 512 deep): measured on
   // MI355X, the partial products' extra traffic costs less than idle CUs.
-  const TileShape shape = tile_shape(m, n, batches);
+  const TileShape shape = tile_shape(m, n, k, batches);
   const int64_t tiles = ((m + shape.bm - 1) / shape.bm) * ((n + shape.bn - 1) / shape.bn) * batches;
   const int64_t full = 256 * shape.per_cu;
   if (tiles >= full) {
@@ -859,6 +865,11 @@ int mfma_splits(int64_t m, int64_t n, int64_t k, int64_t batches) {
   // 512-cube has 16 tiles, and eight 64-deep ranges ran it at 9.4-11 TFLOP/s
   // against 6.3-7.5 for two 256-deep ones.
   if (k < 128) return 1;
+  // Unless every CU already holds a workgroup and k is shallow: the [1024,
+  // 4096] products over k = 1024 (256 tiles of 128x128) ran at 98 TFLOP/s
+  // unsplit against 86 in three ranges, the partials' traffic outweighing the
+  // added occupancy.
+  if (tiles >= 256 && k <= 1024) return 1;
   int64_t splits = std::min<int64_t>((full + tiles - 1) / tiles, k / (k < 1024 ? 64 : 256));
   while (splits * 2 * tiles <= 2048 && k / (splits * 2) >= 512) splits *= 2;
   splits = std::min<int64_t>(splits, 16);
@@ -898,7 +909,7 @@ bool launch_gemm_mfma(const float *a, int64_t a_rs, int64_t a_cs, const float *b
   // 16-byte loads need a unit stride along the axis the lanes step on (any
   // 4-byte alignment serves).
   const bool vector = (lk ? a_cs == 1 : a_rs == 1) && (rk ? b_rs == 1 : b_cs == 1);
-  const TileShape shape = tile_shape(m, n, batch.count);
+  const TileShape shape = tile_shape(m, n, k, batch.count);
   const int64_t gm = (m + shape.bm - 1) / shape.bm;
   const int64_t gn = (n + shape.bn - 1) / shape.bn;
   if (gm * gn > 0x7fffffff || batch.count > 65535 || batch.count < 1) throw Unsupported{"mfma gemm: grid too large"};
