@@ -167,11 +167,6 @@ void launch_gemm_exact(const float *a, int64_t a_rs, int64_t a_cs, const float *
                        int64_t b_cs, int64_t m, int64_t k, int64_t n, float *c, int64_t ldc,
                        hipStream_t stream, const Batch &batch = Batch());
 
-// The im2col matrix of a convolution, never materialised: row r = (image,
-// out_y, out_x), column q = (channel, kernel_y, kernel_x) of the padded,
-// strided windows of a rank-4 [batch, channels, height, width] source read
-// through any strides; +0 where a window leaves the source (the padding).
-// The patch matrix of src/payload/tensor.rs:1475-1544.
 // Division of a 32-bit index below 2^31 by a fixed divisor d >= 1 as a
 // multiply and a shift: with l = ceil(log2 d) and magic = ceil(2^(32+l) / d),
 // floor(i * magic / 2^(32+l)) = floor(i / d), since the magic's excess over
@@ -192,6 +187,11 @@ struct Divisor {
   __host__ __device__ uint32_t divide(uint32_t i) const { return (uint32_t)(((uint64_t)i * magic) >> shift); }
 };
 
+// The im2col matrix of a convolution, never materialised: row r = (image,
+// out_y, out_x), column q = (channel, kernel_y, kernel_x) of the padded,
+// strided windows of a rank-4 [batch, channels, height, width] source read
+// through any strides; +0 where a window leaves the source (the padding).
+// The patch matrix of src/payload/tensor.rs:1475-1544.
 struct WindowShape {
   int64_t offset = 0;
   int64_t s_batch = 0, s_channel = 0, s_height = 0, s_width = 0;
@@ -250,9 +250,14 @@ void append_engine_backward(std::vector<topos_hip_node> &nodes, std::vector<topo
 
 // gemm_bf16.hip: bf16 products (operands and product as bf16 bit patterns).
 bool bf16_mfma_serves(int64_t a_rs, int64_t a_cs, int64_t b_rs, int64_t b_cs);
+// With splits > 1 (bf16_splits' choice), `partials` holds splits * m * n
+// floats: k is cut into that many ranges, each range's f32 sums written
+// there, then added in range order and rounded once (the envelope, then the
+// same single rounding).
+int bf16_splits(int64_t m, int64_t n, int64_t k);
 void launch_gemm_bf16_mfma(const uint16_t *a, int64_t a_rs, int64_t a_cs, const uint16_t *b, int64_t b_rs,
                            int64_t b_cs, int64_t m, int64_t k, int64_t n, uint16_t *c, int64_t ldc,
-                           hipStream_t stream);
+                           hipStream_t stream, float *partials = nullptr, int splits = 1);
 // Widens an [outer, inner] bf16 view into a dense f32 [outer][inner] buffer.
 void launch_widen_bf16(const uint16_t *in, int64_t outer, int64_t inner, int64_t outer_stride, int64_t inner_stride,
                        float *out, hipStream_t stream);

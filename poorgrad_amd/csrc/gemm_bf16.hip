@@ -99,54 +99,59 @@ struct Bf16Slab<true, kVector> {
   }
 };
 
-// Outer-contiguous operand: a thread takes two neighbouring outer elements
-// over eight k rows (eight 4-byte loads, consecutive threads on consecutive
-// pairs: coalesced) and writes them as two 16-byte LDS rows; thread t takes
-// pair t % 64, k octet t / 64.
+// Outer-contiguous operand: a thread takes four neighbouring outer elements
+// over four k rows (four 8-byte loads, consecutive threads on consecutive
+// quads: 256 contiguous bytes a k row), transposes them in registers and
+// writes four 8-byte LDS pieces, one per outer element; thread t takes outer
+// quad t % 32, k quad t / 32.
 template <bool kVector>
 struct Bf16Slab<false, kVector> {
-  uint32_t w[8];
+  uint2 w[4];
 
   __device__ void fetch(const uint16_t *__restrict__ p, int64_t outer_stride, int64_t k_stride, int64_t outer_extent,
                         int64_t k, int64_t o0, int64_t k0) {
     const int t = threadIdx.x;
-    const int64_t go = o0 + 2 * (t % 64), gk = k0 + 8 * (t / 64);
+    const int64_t go = o0 + 4 * (t % 32), gk = k0 + 4 * (t / 32);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < 4; ++i) {
       const int64_t kk = gk + i;
-      if (kVector && go + 1 < outer_extent && kk < k) {
-        w[i] = *reinterpret_cast<const uint32_t *>(p + kk * k_stride + go);
+      if (kVector && go + 3 < outer_extent && kk < k) {
+        w[i] = *reinterpret_cast<const uint2 *>(p + kk * k_stride + go);
       } else {
-        const uint32_t lo = (go < outer_extent && kk < k) ? p[kk * k_stride + go * outer_stride] : 0u;
-        const uint32_t hi = (go + 1 < outer_extent && kk < k) ? p[kk * k_stride + (go + 1) * outer_stride] : 0u;
-        w[i] = lo | (hi << 16);
+        uint32_t h[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          h[q] = (go + q < outer_extent && kk < k) ? p[kk * k_stride + (go + q) * outer_stride] : 0u;
+        w[i] = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
       }
     }
   }
 
   __device__ void deposit(uint16_t (*lds)[kBK + kRowPad]) const {
     const int t = threadIdx.x;
-    const int o = 2 * (t % 64), q = t / 64;
-    uint4 lo, hi;
-    lo.x = (w[0] & 0xffffu) | (w[1] << 16);
-    lo.y = (w[2] & 0xffffu) | (w[3] << 16);
-    lo.z = (w[4] & 0xffffu) | (w[5] << 16);
-    lo.w = (w[6] & 0xffffu) | (w[7] << 16);
-    hi.x = (w[0] >> 16) | (w[1] & 0xffff0000u);
-    hi.y = (w[2] >> 16) | (w[3] & 0xffff0000u);
-    hi.z = (w[4] >> 16) | (w[5] & 0xffff0000u);
-    hi.w = (w[6] >> 16) | (w[7] & 0xffff0000u);
-    *reinterpret_cast<uint4 *>(&lds[o][8 * q]) = lo;
-    *reinterpret_cast<uint4 *>(&lds[o + 1][8 * q]) = hi;
+    const int o = 4 * (t % 32), kq = t / 32;
+    // Outer element j of k row i is half (j % 2) of word (j / 2) of w[i].
+    const uint2 r0 = make_uint2((w[0].x & 0xffffu) | (w[1].x << 16), (w[2].x & 0xffffu) | (w[3].x << 16));
+    const uint2 r1 = make_uint2((w[0].x >> 16) | (w[1].x & 0xffff0000u), (w[2].x >> 16) | (w[3].x & 0xffff0000u));
+    const uint2 r2 = make_uint2((w[0].y & 0xffffu) | (w[1].y << 16), (w[2].y & 0xffffu) | (w[3].y << 16));
+    const uint2 r3 = make_uint2((w[0].y >> 16) | (w[1].y & 0xffff0000u), (w[2].y >> 16) | (w[3].y & 0xffff0000u));
+    *reinterpret_cast<uint2 *>(&lds[o][4 * kq]) = r0;
+    *reinterpret_cast<uint2 *>(&lds[o + 1][4 * kq]) = r1;
+    *reinterpret_cast<uint2 *>(&lds[o + 2][4 * kq]) = r2;
+    *reinterpret_cast<uint2 *>(&lds[o + 3][4 * kq]) = r3;
   }
 };
 
+// With `partials` set, range z = blockIdx.z of k ([z * split_len, ..)) is
+// multiplied and its f32 sums written unrounded to partials + z * m * n
+// (rows n apart); reduce_bf16_kernel adds the ranges and rounds once.
 template <bool kLeftInnerK, bool kRightInnerK, bool kVector>
 __global__ __launch_bounds__(256) void gemm_bf16_mfma_kernel(const uint16_t *__restrict__ a, int64_t a_rs,
                                                              int64_t a_cs, const uint16_t *__restrict__ b,
                                                              int64_t b_rs, int64_t b_cs, int64_t m, int64_t k,
                                                              int64_t n, uint16_t *__restrict__ c, int64_t ldc,
-                                                             int grid_m, int grid_n) {
+                                                             int grid_m, int grid_n, float *__restrict__ partials,
+                                                             int64_t split_len) {
   __shared__ __attribute__((aligned(16))) uint16_t lds_a[2][128][kBK + kRowPad];
   __shared__ __attribute__((aligned(16))) uint16_t lds_b[2][128][kBK + kRowPad];
   // Groups of eight tile rows walk the columns together (operand panels
@@ -171,17 +176,19 @@ __global__ __launch_bounds__(256) void gemm_bf16_mfma_kernel(const uint16_t *__r
 
   Bf16Slab<kLeftInnerK, kVector> sa;
   Bf16Slab<kRightInnerK, kVector> sb;
-  const int slabs = (int)((k + kBK - 1) / kBK);
-  sa.fetch(a, a_rs, a_cs, m, k, m0, 0);
-  sb.fetch(b, b_cs, b_rs, n, k, n0, 0);
+  const int64_t k_begin = partials ? (int64_t)blockIdx.z * split_len : 0;
+  const int64_t k_end = partials ? min(k, k_begin + split_len) : k;
+  const int slabs = (int)((k_end - k_begin + kBK - 1) / kBK);
+  sa.fetch(a, a_rs, a_cs, m, k_end, m0, k_begin);
+  sb.fetch(b, b_cs, b_rs, n, k_end, n0, k_begin);
   sa.deposit(lds_a[0]);
   sb.deposit(lds_b[0]);
   __syncthreads();
   for (int s = 0; s < slabs; ++s) {
     const int buf = s & 1;
     if (s + 1 < slabs) {
-      sa.fetch(a, a_rs, a_cs, m, k, m0, (int64_t)(s + 1) * kBK);
-      sb.fetch(b, b_cs, b_rs, n, k, n0, (int64_t)(s + 1) * kBK);
+      sa.fetch(a, a_rs, a_cs, m, k_end, m0, k_begin + (int64_t)(s + 1) * kBK);
+      sb.fetch(b, b_cs, b_rs, n, k_end, n0, k_begin + (int64_t)(s + 1) * kBK);
     }
 #pragma unroll
     for (int ks = 0; ks < kBK / 16; ++ks) {
@@ -213,20 +220,37 @@ __global__ __launch_bounds__(256) void gemm_bf16_mfma_kernel(const uint16_t *__r
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int64_t row = m0 + wm + 32 * i + 8 * (r / 4) + 4 * half + (r % 4);
-        if (row < m) c[row * ldc + col] = bf16_of(acc[i][j][r]);
+        if (row >= m) continue;
+        if (partials)
+          partials[(int64_t)blockIdx.z * m * n + row * n + col] = acc[i][j][r];
+        else
+          c[row * ldc + col] = bf16_of(acc[i][j][r]);
       }
     }
+}
+
+// The ranges' f32 sums added in range order, then rounded once to bf16.
+__global__ __launch_bounds__(256) void reduce_bf16_kernel(const float *__restrict__ partials, int splits, int64_t m,
+                                                          int64_t n, uint16_t *__restrict__ c, int64_t ldc) {
+  const int64_t total = m * n;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    float acc = partials[i];
+    for (int z = 1; z < splits; ++z) acc = acc + partials[(int64_t)z * total + i];
+    const int64_t r = i / n, col = i - r * n;
+    c[r * ldc + col] = bf16_of(acc);
+  }
 }
 
 template <bool kL, bool kR>
 void dispatch_bf16(bool vector, dim3 grid, hipStream_t stream, const uint16_t *a, int64_t a_rs, int64_t a_cs,
                    const uint16_t *b, int64_t b_rs, int64_t b_cs, int64_t m, int64_t k, int64_t n, uint16_t *c,
-                   int64_t ldc, int gm, int gn) {
+                   int64_t ldc, int gm, int gn, float *partials, int64_t split_len) {
   if (vector)
-    gemm_bf16_mfma_kernel<kL, kR, true><<<grid, 256, 0, stream>>>(a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, gm, gn);
+    gemm_bf16_mfma_kernel<kL, kR, true><<<grid, 256, 0, stream>>>(a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, gm, gn,
+                                                                 partials, split_len);
   else
     gemm_bf16_mfma_kernel<kL, kR, false><<<grid, 256, 0, stream>>>(a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, gm,
-                                                                  gn);
+                                                                  gn, partials, split_len);
 }
 
 unsigned blocks_for(int64_t count) {
@@ -240,30 +264,55 @@ bool bf16_mfma_serves(int64_t a_rs, int64_t a_cs, int64_t b_rs, int64_t b_cs) {
   return (a_cs == 1 || a_rs == 1) && (b_rs == 1 || b_cs == 1);
 }
 
+int bf16_splits(int64_t m, int64_t n, int64_t k) {
+  // Products with fewer 128x128 tiles than four per CU split k into ranges
+  // of at least 512 (at most 16 of them) until they have that many
+  // workgroups: the [3072, 768] weight gradient over k = 8192 (144 tiles)
+  // went from 44 TFLOP/s unsplit to 184 in four ranges and 212 in eight.
+  const int64_t tiles = ((m + 127) / 128) * ((n + 127) / 128);
+  int64_t s = 1;
+  while (s < 16 && tiles * s < 1024 && k / (2 * s) >= 512) s *= 2;
+  return (int)s;
+}
+
 void launch_gemm_bf16_mfma(const uint16_t *a, int64_t a_rs, int64_t a_cs, const uint16_t *b, int64_t b_rs,
                            int64_t b_cs, int64_t m, int64_t k, int64_t n, uint16_t *c, int64_t ldc,
-                           hipStream_t stream) {
+                           hipStream_t stream, float *partials, int splits) {
   const bool lk = a_cs == 1, rk = b_rs == 1;
-  // Vector loads: 16 bytes along a k-contiguous operand's rows, 4 bytes along
+  // Vector loads: 16 bytes along a k-contiguous operand's rows, 8 bytes along
   // an outer-contiguous operand's k rows; every row start aligned to them.
   const int64_t a_step = lk ? a_rs : a_cs, b_step = rk ? b_cs : b_rs;
-  const int a_align = lk ? 8 : 2, b_align = rk ? 8 : 2;  // in elements
+  const int a_align = lk ? 8 : 4, b_align = rk ? 8 : 4;  // in elements
   const bool vector = reinterpret_cast<uintptr_t>(a) % (2 * a_align) == 0 &&
                       reinterpret_cast<uintptr_t>(b) % (2 * b_align) == 0 && a_step % a_align == 0 &&
                       b_step % b_align == 0;
   const int64_t gm = (m + 127) / 128, gn = (n + 127) / 128;
   if (gm * gn > 0x7fffffff) throw Unsupported{"bf16 gemm: grid too large"};
-  const dim3 grid((unsigned)(gm * gn));
+  if (splits < 1 || splits > 16 || (splits > 1 && !partials)) throw Unsupported{"bf16 gemm: split without partials"};
+  int64_t split_len = k;
+  if (splits > 1) {
+    split_len = ((k + splits - 1) / splits + kBK - 1) / kBK * kBK;
+    splits = (int)((k + split_len - 1) / split_len);
+  }
+  float *target = splits > 1 ? partials : nullptr;
+  const dim3 grid((unsigned)(gm * gn), 1, (unsigned)splits);
   if (lk && rk)
-    dispatch_bf16<true, true>(vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, (int)gm, (int)gn);
+    dispatch_bf16<true, true>(vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, (int)gm, (int)gn,
+                              target, split_len);
   else if (lk)
-    dispatch_bf16<true, false>(vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, (int)gm, (int)gn);
+    dispatch_bf16<true, false>(vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, (int)gm, (int)gn,
+                               target, split_len);
   else if (rk)
-    dispatch_bf16<false, true>(vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, (int)gm, (int)gn);
+    dispatch_bf16<false, true>(vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, (int)gm, (int)gn,
+                               target, split_len);
   else
     dispatch_bf16<false, false>(vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, (int)gm,
-                                (int)gn);
+                                (int)gn, target, split_len);
   check_launch("gemm_bf16_mfma_kernel launch");
+  if (splits > 1) {
+    reduce_bf16_kernel<<<blocks_for(m * n), 256, 0, stream>>>(partials, splits, m, n, c, ldc);
+    check_launch("reduce_bf16_kernel launch");
+  }
 }
 
 void launch_widen_bf16(const uint16_t *in, int64_t outer, int64_t inner, int64_t outer_stride, int64_t inner_stride,

@@ -4,7 +4,9 @@ rounding): bit-identical under Exact; under Fast (bf16 matrix cores, f32
 accumulation) within |c - exact| <= 1e-5 * sum_k |a_ik b_kj| before the
 rounding, so within that plus one bf16 spacing of the rounded exact
 result. Shapes and stride forms as the f32 grid (forward, both transposed
-operands, a narrowed window, and rows not 16-byte aligned)."""
+operands, a narrowed window, and rows not 16-byte aligned), and products
+with few tiles over deep k, which Fast cuts into k ranges (f32 partials
+added in range order, one rounding)."""
 import numpy as np
 import pytest
 import torch
@@ -15,7 +17,9 @@ from tests.conftest import banner
 pytestmark = pytest.mark.gpu
 
 SHAPES = [(2, 3, 4), (5, 8, 13), (16, 16, 16), (63, 64, 65), (100, 127, 3), (129, 257, 131), (256, 384, 512),
-          (1024, 1024, 1024), (777, 1000, 515)]
+          (1024, 1024, 1024), (777, 1000, 515),
+          # few tiles over deep k: under Fast, k in 8 ranges and in 4 ragged ones
+          (128, 4096, 192), (300, 2600, 260)]
 FORMS = ["contiguous", "a_transposed", "b_transposed", "narrowed"]
 
 
