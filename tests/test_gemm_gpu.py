@@ -93,7 +93,11 @@ def test_negative_zero_seed_survives_on_device(hip):
 
 @pytest.mark.parametrize("m, k, n", [(1024, 1024, 4096), (512, 512, 512), (4096, 4096, 4096), (8192, 3072, 768),
                                      (768, 8192, 768), (768, 4096, 20001),
-                                     (1025, 1027, 1029), (1000, 512, 1020), (300, 64, 260)])
+                                     (1025, 1027, 1029), (1000, 512, 1020), (300, 64, 260),
+                                     # fast tile choices: 64x128 tiles filling whole rounds (k <= 1024),
+                                     # unsplit with a tile per CU, three k ranges
+                                     (8192, 768, 768), (8192, 768, 2304), (4096, 2048, 2048),
+                                     (2048, 4096, 2048)])
 @pytest.mark.parametrize("product", ["forward", "a_transposed", "b_transposed"])
 def test_sweep_shapes_sampled_rows(hip, m, k, n, product):
     """The GEMM-sweep products at full size (forward A.B, then A^T.G and
