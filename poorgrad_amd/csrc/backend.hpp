@@ -303,6 +303,7 @@ struct AdamTable {
   float *first[kAdamTensors];
   float *second[kAdamTensors];
   int64_t start[kAdamTensors + 1];
+  int64_t quad_start[kAdamTensors + 1];  // filled by launch_adamw_multi
   int32_t decayed[kAdamTensors];
   int32_t count;
 };

@@ -288,13 +288,24 @@ Generated make(const std::string &source) {
   return g;
 }
 
+// An input the launch reads each element of once (no repeated axis). Its
+// 16-byte loads carry the nontemporal hint, so they do not displace what the
+// last-level cache holds for the next launch (this launch's own output among
+// it). Measured on MI355X, a copy over [16384, 4096] and a read of its output:
+// 114 against 135 us with plain loads.
+bool read_once(const Expr &e, const ExprInput &in) {
+  for (int d = 0; d < e.rank; ++d)
+    if (e.shape[d] > 1 && in.strides[d] == 0) return false;
+  return true;
+}
+
 // Emits in<i>_<lanes[j]> (j < 4): the expression inputs at the four points of
 // a quad (coordinates `c`, the innermost coordinate c[inner] the quad's first,
 // a multiple of four in an innermost extent that is one). Unit-stride inputs
 // take one 16-byte load.
 void emit_quad_inputs(std::ostringstream &s, const Expr &e, const std::vector<std::string> &c,
                       const std::string &tag, const std::vector<std::string> &lanes, const std::string &indent,
-                      const std::vector<bool> *only = nullptr, bool declare = true) {
+                      const std::vector<bool> *only = nullptr, bool declare = true, bool streaming = false) {
   // declare = false: assign to registers the caller declared (zeroed).
   const std::string cf = declare ? "const float " : "";
   const int inner = e.rank - 1;
@@ -332,8 +343,12 @@ void emit_quad_inputs(std::ostringstream &s, const Expr &e, const std::vector<st
         s << indent << "  " << v(0) << " = " << p << "[" << a << "]; " << v(1) << " = " << v(0) << "; " << v(2)
           << " = " << v(0) << "; " << v(3) << " = " << v(0) << ";\n";
       } else if (vector_input(e, in)) {
-        s << indent << "  const topos_f4 w = *(const topos_f4*)(" << p << " + " << a << "); " << v(0) << " = w.x; "
-          << v(1) << " = w.y; " << v(2) << " = w.z; " << v(3) << " = w.w;\n";
+        if (streaming && read_once(e, in))
+          s << indent << "  const topos_f4 w = __builtin_nontemporal_load((const topos_f4*)(" << p << " + " << a
+            << ")); ";
+        else
+          s << indent << "  const topos_f4 w = *(const topos_f4*)(" << p << " + " << a << "); ";
+        s << v(0) << " = w.x; " << v(1) << " = w.y; " << v(2) << " = w.z; " << v(3) << " = w.w;\n";
       } else {
         for (int j = 0; j < 4; ++j)
           s << indent << "  " << v(j) << " = " << p << "[" << a << " + " << ll(j * in.strides[inner]) << "];\n";
@@ -467,7 +482,7 @@ Generated generate_chain(const Expr &e) {
       std::vector<std::string> c;
       if (e.rank > 1) emit_coordinates(s, e.rank - 1, e.shape, "row" + U_, tag, c);
       c.push_back("lc" + U_);
-      emit_quad_inputs(s, e, c, tag, lanes_u, "    ");
+      emit_quad_inputs(s, e, c, tag, lanes_u, "    ", nullptr, true, true);
     }
     emit_steps(s, e, all_lanes);
     for (int u = 0; u < U; ++u) {
@@ -516,7 +531,7 @@ Generated generate_chain(const Expr &e) {
       s << "      const long long base_" << tag << " = block + (" << 256 * u << " + threadIdx.x) * 4;\n";
       std::vector<std::string> c;
       emit_coordinates(s, e.rank, e.shape, "base_" + tag, tag, c);
-      emit_quad_inputs(s, e, c, tag, lanes_u, "      ");
+      emit_quad_inputs(s, e, c, tag, lanes_u, "      ", nullptr, true, true);
     }
     emit_steps(s, e, all_lanes);
     for (int u = 0; u < U; ++u) {
@@ -533,7 +548,7 @@ Generated generate_chain(const Expr &e) {
     s << "        if (base >= " << ll(volume) << ") break;\n";
     std::vector<std::string> c;
     emit_coordinates(s, e.rank, e.shape, "base", "q", c);
-    emit_quad_inputs(s, e, c, "q", lanes, "        ");
+    emit_quad_inputs(s, e, c, "q", lanes, "        ", nullptr, true, true);
     emit_steps(s, e, lanes);
     for (size_t o = 0; o < e.outputs.size(); ++o) {
       s << "        *(topos_f4*)(q" << o << " + base) = topos_f4{";
@@ -571,7 +586,7 @@ void launch_generated_chain(const Generated &g, const Expr &e, const void *const
   const int64_t per_block = quads || odd_rows ? 1024LL * chain_unroll(e) : 1024;
   int64_t blocks = (e.volume() + per_block - 1) / per_block;
   if (blocks < 1) blocks = 1;
-  if (blocks > 256 * 16) blocks = 256 * 16;
+  if (blocks > 256 * 64) blocks = 256 * 64;
   launch(g, (unsigned)blocks, arguments, stream);
 }
 
@@ -1356,7 +1371,7 @@ Generated generate_row_resident(const RowProgram &p, const RowLayout &l, const R
     if (p.rank > 1) emit_coordinates(s, p.rank - 1, p.shape, "g_r" + I, "r" + I, c);
     c.push_back("col" + I);
     if (V == 4) {
-      emit_quad_inputs(s, m.e, c, "r" + I, lanes, "    ", &loaded, false);
+      emit_quad_inputs(s, m.e, c, "r" + I, lanes, "    ", &loaded, false, true);
     } else {
       for (size_t k = 0; k < p.inputs.size(); ++k)
         if (loaded[k]) s << "    " << ref(-(int)k - 1, lanes[0]) << " = " << scalar_value(m.e, (int)k, c) << ";\n";
@@ -1519,7 +1534,7 @@ Generated generate_row_streaming(const RowProgram &p, const RowLayout &l, const 
       c.push_back("col");
       const std::vector<std::string> lanes = lanes_of(i);
       if (V == 4) {
-        emit_quad_inputs(s, m.e, c, "s" + I, lanes, ind + "    ", &loaded, false);
+        emit_quad_inputs(s, m.e, c, "s" + I, lanes, ind + "    ", &loaded, false, true);
       } else {
         for (size_t k = 0; k < p.inputs.size(); ++k)
           if (loaded[k]) s << ind << "    " << ref(-(int)k - 1, lanes[0]) << " = " << scalar_value(m.e, (int)k, c) << ";\n";

@@ -707,6 +707,15 @@ void dispatch_dma(bool lk, bool rk, bool vector_out, dim3 grid, hipStream_t stre
 #undef TOPOS_DMA_ARGS
 }
 
+// A 16-byte load with the nontemporal hint: the partials are read once, and
+// the hint leaves the last-level cache to the reduced output, which the next
+// launch reads.
+__device__ __forceinline__ float4 load_once(const float4 *p) {
+  typedef float f4v __attribute__((ext_vector_type(4)));
+  const f4v w = __builtin_nontemporal_load(reinterpret_cast<const f4v *>(p));
+  return make_float4(w.x, w.y, w.z, w.w);
+}
+
 // The fixed-order sum of `splits` partial products (each [count][m][n],
 // contiguous) into c: partial 0 seeds, then 1, 2, ... are added in order, so
 // the result is the same on every run. Four consecutive elements per lane:
@@ -723,7 +732,7 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float4 *__restr
     float4 v[kMax];
 #pragma unroll
     for (int s = 0; s < kMax; ++s)
-      if (s < splits) v[s] = partials[(size_t)s * split_quads + e];
+      if (s < splits) v[s] = load_once(partials + (size_t)s * split_quads + e);
     float4 acc = v[0];
 #pragma unroll
     for (int s = 1; s < kMax; ++s)
@@ -775,7 +784,7 @@ __global__ __launch_bounds__(256) void split_reduce_flat_kernel(const float4 *__
     float4 v[kMax];
 #pragma unroll
     for (int s = 0; s < kMax; ++s)
-      if (s < splits) v[s] = partials[(size_t)s * split_quads + e];
+      if (s < splits) v[s] = load_once(partials + (size_t)s * split_quads + e);
     float4 acc = v[0];
 #pragma unroll
     for (int s = 1; s < kMax; ++s)

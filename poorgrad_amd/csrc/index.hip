@@ -221,24 +221,34 @@ __global__ __launch_bounds__(256) void sgd_kernel(float *__restrict__ parameter,
 }
 
 // One element of AdamW::step (src/neural/adam.rs:62-171), in the optimizer's
-// operation order.
+// operation order: the new moments m, v and parameter p from the gradient g,
+// the old moments m0, v0 and the current parameter.
+__device__ __forceinline__ void adamw_value(float g, float m0, float v0, float current, float beta1, float beta2,
+                                            float first_share, float second_share, float first_correction,
+                                            float second_correction, float epsilon, float rate, float decay,
+                                            int decayed, float &m, float &v, float &p) {
+  m = m0 * beta1 + g * first_share;
+  const float squared = g * g;
+  v = v0 * beta2 + squared * second_share;
+  const float corrected_first = m / first_correction;
+  const float corrected_second = v / second_correction;
+  const float direction = corrected_first / (__builtin_sqrtf(corrected_second) + epsilon);
+  const float stepped = current - direction * rate;
+  p = decayed ? stepped - (current * decay) * rate : stepped;
+}
+
+// The same element through the buffers.
 __device__ __forceinline__ void adamw_element(float *__restrict__ parameter, const float *__restrict__ gradient,
                                               float *__restrict__ first, float *__restrict__ second, int64_t i,
                                               float beta1, float beta2, float first_share, float second_share,
                                               float first_correction, float second_correction, float epsilon,
                                               float rate, float decay, int decayed) {
-  const float g = gradient[i];
-  const float m = first[i] * beta1 + g * first_share;
-  const float squared = g * g;
-  const float v = second[i] * beta2 + squared * second_share;
+  float m, v, p;
+  adamw_value(gradient[i], first[i], second[i], parameter[i], beta1, beta2, first_share, second_share,
+              first_correction, second_correction, epsilon, rate, decay, decayed, m, v, p);
   first[i] = m;
   second[i] = v;
-  const float corrected_first = m / first_correction;
-  const float corrected_second = v / second_correction;
-  const float direction = corrected_first / (__builtin_sqrtf(corrected_second) + epsilon);
-  const float current = parameter[i];
-  const float stepped = current - direction * rate;
-  parameter[i] = decayed ? stepped - (current * decay) * rate : stepped;
+  parameter[i] = p;
 }
 
 __global__ __launch_bounds__(256) void adamw_kernel(float *__restrict__ parameter, const float *__restrict__ gradient,
@@ -252,25 +262,59 @@ __global__ __launch_bounds__(256) void adamw_kernel(float *__restrict__ paramete
                   second_correction, epsilon, rate, decay, decayed);
 }
 
-// Many parameters in one launch: the elements of the table's tensors laid
-// end to end (tensor j owns [start[j], start[j + 1])), each lane finding its
-// tensor by binary search over the starts. The table travels as the kernel's
-// argument, so the launch needs no device memory of its own.
+// Many parameters in one launch: the table's tensors laid end to end in
+// quads (tensor j owns quads [quad_start[j], quad_start[j + 1]), its last quad
+// possibly short), each lane finding its tensor by binary search over the quad
+// starts. A whole quad whose four buffers are 16-byte aligned moves in 16-byte
+// loads and stores (the gradient's with the nontemporal hint: it is read once),
+// any other quad element by element; both apply adamw_value per element, so
+// the bits are the single-parameter kernel's. The table travels as the
+// kernel's argument, so the launch needs no device memory of its own.
 __global__ __launch_bounds__(256) void adamw_multi_kernel(AdamTable table, float beta1, float beta2,
                                                           float first_share, float second_share,
                                                           float first_correction, float second_correction,
                                                           float epsilon, float rate, float decay) {
-  const int64_t total = table.start[table.count];
-  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (int64_t)gridDim.x * blockDim.x) {
+  typedef float f4v __attribute__((ext_vector_type(4)));
+  const int64_t total = table.quad_start[table.count];
+  for (int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; q < total; q += (int64_t)gridDim.x * blockDim.x) {
     int lo = 0, hi = table.count - 1;
     while (lo < hi) {
       const int mid = (lo + hi + 1) / 2;
-      if (table.start[mid] <= e) lo = mid;
+      if (table.quad_start[mid] <= q) lo = mid;
       else hi = mid - 1;
     }
-    adamw_element(table.parameter[lo], table.gradient[lo], table.first[lo], table.second[lo], e - table.start[lo],
-                  beta1, beta2, first_share, second_share, first_correction, second_correction, epsilon, rate, decay,
-                  table.decayed[lo]);
+    const int64_t first = (q - table.quad_start[lo]) * 4;
+    const int64_t n = table.start[lo + 1] - table.start[lo];
+    float *parameter = table.parameter[lo];
+    const float *gradient = table.gradient[lo];
+    float *m1 = table.first[lo];
+    float *m2 = table.second[lo];
+    const int decayed = table.decayed[lo];
+    const bool aligned = ((reinterpret_cast<uintptr_t>(parameter + first) | reinterpret_cast<uintptr_t>(gradient + first) |
+                           reinterpret_cast<uintptr_t>(m1 + first) | reinterpret_cast<uintptr_t>(m2 + first)) & 15) == 0;
+    if (first + 4 <= n && aligned) {
+      const f4v g = __builtin_nontemporal_load(reinterpret_cast<const f4v *>(gradient + first));
+      const f4v a = *reinterpret_cast<const f4v *>(m1 + first);
+      const f4v b = *reinterpret_cast<const f4v *>(m2 + first);
+      const f4v c = *reinterpret_cast<const f4v *>(parameter + first);
+      f4v m, v, p;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float me, ve, pe;
+        adamw_value(g[e], a[e], b[e], c[e], beta1, beta2, first_share, second_share, first_correction,
+                    second_correction, epsilon, rate, decay, decayed, me, ve, pe);
+        m[e] = me;
+        v[e] = ve;
+        p[e] = pe;
+      }
+      *reinterpret_cast<f4v *>(m1 + first) = m;
+      *reinterpret_cast<f4v *>(m2 + first) = v;
+      *reinterpret_cast<f4v *>(parameter + first) = p;
+    } else {
+      for (int64_t i = first; i < first + 4 && i < n; ++i)
+        adamw_element(parameter, gradient, m1, m2, i, beta1, beta2, first_share, second_share, first_correction,
+                      second_correction, epsilon, rate, decay, decayed);
+    }
   }
 }
 
@@ -317,10 +361,15 @@ void launch_sgd(float *parameter, const float *gradient, int64_t count, float ra
 void launch_adamw_multi(const AdamTable &table, float beta1, float beta2, float first_share, float second_share,
                         float first_correction, float second_correction, float epsilon, float rate, float decay,
                         hipStream_t stream) {
-  const int64_t total = table.start[table.count];
-  if (table.count <= 0 || total <= 0) return;
-  adamw_multi_kernel<<<blocks_for(total), 256, 0, stream>>>(table, beta1, beta2, first_share, second_share,
-                                                            first_correction, second_correction, epsilon, rate, decay);
+  if (table.count <= 0 || table.start[table.count] <= 0) return;
+  AdamTable quads = table;
+  quads.quad_start[0] = 0;
+  for (int j = 0; j < table.count; ++j)
+    quads.quad_start[j + 1] = quads.quad_start[j] + (table.start[j + 1] - table.start[j] + 3) / 4;
+  int64_t blocks = (quads.quad_start[table.count] + 255) / 256;
+  if (blocks > 256 * 64) blocks = 256 * 64;
+  adamw_multi_kernel<<<(unsigned)blocks, 256, 0, stream>>>(quads, beta1, beta2, first_share, second_share,
+                                                           first_correction, second_correction, epsilon, rate, decay);
   check_launch("adamw_multi_kernel launch");
 }
 

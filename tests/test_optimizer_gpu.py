@@ -15,18 +15,32 @@ from tests.gpu_util import assert_bitwise
 pytestmark = pytest.mark.gpu
 
 
-def test_multi_tensor_adamw_equals_single_tensor_steps(hip):
+@pytest.mark.parametrize("offset", [0, 1, 2])
+def test_multi_tensor_adamw_equals_single_tensor_steps(hip, offset):
+    """offset 0: 16-byte aligned buffers (whole quads move in 16-byte loads
+    and stores); 1 and 2: every buffer, or only the gradients, start one
+    float into an allocation (the element-by-element path)."""
     import torch
 
-    banner("adamw multi-tensor vs single-tensor")
+    banner(f"adamw multi-tensor vs single-tensor offset={offset}")
     rng = np.random.default_rng(3)
     sizes = [0, 1, 5, 768, 1000, 100003, 2304 * 768] + [int(s) for s in rng.integers(1, 5000, 60)]
     make = lambda s: torch.from_numpy(rng.standard_normal(s).astype(np.float32)).cuda()
+
+    def placed(t, shift):
+        if not shift:
+            return t
+        buffer = torch.empty(t.numel() + 1, device="cuda")
+        view = buffer[1:]
+        view.copy_(t)
+        return view
+
     params = [make(s) for s in sizes]
-    grads = [make(s) for s in sizes]
+    grads = [placed(make(s), offset > 0) for s in sizes]
     decayed = [i % 3 != 0 for i in range(len(sizes))]
     single = [(p.clone(), torch.zeros_like(p), torch.zeros_like(p)) for p in params]
-    multi = [(p.clone(), torch.zeros_like(p), torch.zeros_like(p)) for p in params]
+    multi = [tuple(placed(x, offset == 1) for x in (p.clone(), torch.zeros_like(p), torch.zeros_like(p)))
+             for p in params]
     f = np.float32
     beta1, beta2, eps, decay, rate = f(0.9), f(0.999), f(1e-8), f(0.01), 3e-4
     p1 = p2 = f(1)
