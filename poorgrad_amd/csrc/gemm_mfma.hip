@@ -644,11 +644,12 @@ __global__ __launch_bounds__(BM / WM * BN, BM == 256 ? 4 : 3) void gemm_dma_kern
 // operand traffic per flop than 128x128) when its tiles fill whole rounds of
 // two workgroups per CU, or at least one and a half such rounds (measured on
 // MI355X: the [8192, 3072] products gain, [8192, 2304] loses); 64x128 when k
-// is at most 1024 and those tiles fill whole rounds of three workgroups per
+// is at most 4096 and those tiles fill whole rounds of three workgroups per
 // CU (measured in the GPT-2 step: the [8192, 768] products over k = 768 took
 // 95 us against 106 on 128x128 tiles in two ranges, [8192, 2304] over 768
-// 262 against 269); else 128x128. `per_cu` is how many of its workgroups a
-// CU holds at once.
+// 262 against 269; [8192, 768] over 3072 ran at 127 TFLOP/s unsplit against
+// 121 on 128x128 tiles in two ranges); else 128x128. `per_cu` is how many of
+// its workgroups a CU holds at once.
 struct TileShape {
   int bm, bn, per_cu;
 };
@@ -658,7 +659,7 @@ TileShape tile_shape(int64_t m, int64_t n, int64_t k, int64_t batches) {
   const int64_t wide = ((m + 255) / 256) * ((n + 127) / 128) * batches;
   if (wide >= 768 || (wide >= 512 && wide % 512 == 0)) return {256, 128, 2};
   const int64_t thin = ((m + 63) / 64) * ((n + 127) / 128) * batches;
-  if (k <= 1024 && thin >= 768 && thin % 768 == 0) return {64, 128, 3};
+  if (k <= 4096 && thin >= 768 && thin % 768 == 0) return {64, 128, 3};
   return {128, 128, 3};
 }
 
@@ -913,10 +914,25 @@ int mfma_splits(int64_t m, int64_t n, int64_t k, int64_t batches) {
     while (s * 2 * tiles <= 2048 && k / (s * 2) >= 8192) s *= 2;
     return (int)std::min<int64_t>(s, 16);
   }
-  int64_t splits = std::min<int64_t>((full + tiles - 1) / tiles, k / (k < 1024 ? 64 : 256));
-  while (splits * 2 * tiles <= 2048 && k / (splits * 2) >= 512) splits *= 2;
-  splits = std::min<int64_t>(splits, 16);
-  return (int)std::max<int64_t>(splits, 1);
+  // Fewer tiles than CUs: the split that minimises the busiest CU's work,
+  // ceil(tiles * s / 256) workgroups of k / s each (a CU's matrix cores serve
+  // its workgroups in turn), plus the partials' s + 1 passes over the output.
+  // Measured on MI355X: [768, 768] over 8192 (36 tiles) ran at 79 TFLOP/s in
+  // 16 ranges and 90 in 6 (8: 66); [1024, 1024] over 4096 (64 tiles) at 86
+  // in 12 and 98 in 4; [768, 3072] over 8192 (144 tiles) at 117 in 16 and
+  // 95 in 4.
+  const double slab_s = 2.0 * shape.bm * shape.bn * kTileK / (157.3e12 / 256);
+  const double partial_bytes = 4.0 * (double)batches * (double)m * (double)n;
+  auto cost = [&](int64_t s) {
+    const int64_t per_cu = (tiles * s + 255) / 256;
+    const int64_t slabs = ((k + s - 1) / s + kTileK - 1) / kTileK;
+    const double partials = s > 1 ? (double)(s + 1) * partial_bytes / 5e12 : 0.0;
+    return (double)per_cu * (double)slabs * slab_s + partials;
+  };
+  int64_t best = 1;
+  for (int64_t s = 2; s <= 16 && k / s >= (k < 1024 ? 64 : 256); ++s)
+    if (cost(s) < cost(best)) best = s;
+  return (int)best;
 }
 
 int64_t mfma_split_floats(int64_t m, int64_t n, int64_t k, const Batch &batch, int64_t ldc) {
