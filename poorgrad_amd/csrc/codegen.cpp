@@ -288,12 +288,17 @@ Generated make(const std::string &source) {
   return g;
 }
 
-// An input the launch reads each element of once (no repeated axis). Its
-// 16-byte loads carry the nontemporal hint, so they do not displace what the
-// last-level cache holds for the next launch (this launch's own output among
-// it). Measured on MI355X, a copy over [16384, 4096] and a read of its output:
-// 114 against 135 us with plain loads.
+// An input the launch reads each element of once (no repeated axis), over
+// at least 16 MB. Its 16-byte loads carry the nontemporal hint, so they do not
+// displace what the last-level cache holds for the next launch (this
+// launch's own output among it). Measured on MI355X, a copy over
+// [16384, 4096] and a read of its output: 114 against 135 us with plain
+// loads. Smaller operands keep plain loads: a program over a few megabytes
+// finds them in the caches from launch to launch, which the hint would give
+// up (in an A/B on one MI355X the GPT-2 step ran 73.6 ms with this bound
+// against 73.7 with the hint on every read-once input).
 bool read_once(const Expr &e, const ExprInput &in) {
+  if (e.volume() < (int64_t(1) << 22)) return false;
   for (int d = 0; d < e.rank; ++d)
     if (e.shape[d] > 1 && in.strides[d] == 0) return false;
   return true;
