@@ -1,4 +1,5 @@
-// Fast-posture GEMM on the fp32 matrix cores (v_mfma_f32_32x32x2_f32).
+// Fast-posture GEMM on the fp32 matrix cores: v_mfma_f32_16x16x4_f32 on the
+// LDS-DMA kernel, v_mfma_f32_32x32x2_f32 on the register-staged one.
 //
 // Envelope fidelity: the k-sum is blocked and reassociated by the matrix core,
 // so results are compared against the exact product within
@@ -6,18 +7,17 @@
 // inputs give the same bits on every run: no atomics, and a split along k is
 // reduced in a fixed order).
 //
-// Shape: a BM x BN output tile per workgroup of 64 * (BM / 64) * (BN / 64)
-// lanes, each wave owning a 64x64 block (2x2 MFMA blocks of 32x32). Tiles are
-// 256x128 (eight waves) for products with enough tiles, 128x128, or 128x64 /
-// 64x128 when one output extent is at most 64 (the attention products with a
-// 64-wide head), so no half-empty tiles are launched. k is staged 16 deep through LDS, double-buffered: the next slab's
-// global loads are in flight while the current slab feeds the matrix cores.
-// LDS holds both operands k-major ([k][outer]) so an MFMA fragment is one
-// 32-lane b32 read; rows are padded by 20 floats (276, 148 or 84: 20 mod 64
-// banks), which measured fastest for both the fragment reads and the
-// transposing stores of k-contiguous operands. A tile wholly inside the
-// operands takes a branch-free load path (one uniform test per slab); only
-// edge tiles pay per-element bounds checks.
+// Shape: a BM x BN output tile per workgroup, each wave owning a 64x64 block
+// (32x64 on the thin tiles). Tiles are 256x128 (eight waves) for products
+// with enough tiles, 128x128, or 128x64 / 64x128 when one output extent is at
+// most 64 (the attention products with a 64-wide head) or when those tiles
+// fill whole rounds, so no half-empty tiles are launched. The LDS-DMA kernel
+// stages k 16 deep in three LDS stages written by global_load_lds_dwordx4;
+// the register-staged kernel (operands without a unit stride, and the 128x64
+// tiles) double-buffers slabs through registers into [k][outer] LDS rows
+// padded by 20 floats. A tile wholly inside the operands takes a branch-free
+// load path (one uniform test per slab); only edge tiles pay per-element
+// bounds checks.
 // The forward product and both transposed backward products (A^T G with A
 // m-contiguous, G B^T with B k-contiguous; src/function/matmul.rs:76-91) are
 // served by the same kernel through the operand-orientation template flags, so
@@ -295,12 +295,12 @@ __global__ __launch_bounds__(BM / WM * BN, BM == 256 && kVector ? 4 : 1) void ge
 // address each lane loads:
 //  * k-contiguous operand: 16 rows x 16 k per KB; the k-quad q of local row
 //    r sits at position 4r + (q ^ swz(r)) (conflict-free 16-byte fragment
-//    reads for 32 or 64 banks). A fragment read gives a lane four k values;
-//    MFMA t of a k-group of 8 then takes k = t from lanes 0-31 and k = 4 + t
-//    from lanes 32-63 (the other operand is read in the same k order).
+//    reads for 32 or 64 banks). A fragment read gives a lane the four k
+//    values of one quad; the 16x16x4 MFMAs then take k = 4g + t from the
+//    lanes of group g (the other operand is read in the same k order).
 //  * outer-contiguous operand: k-rows of O floats; quad j of row kk sits at
-//    quad position j ^ (kk & 4 ? 8 : 0) (rows kk and kk + 4, read by the two
-//    half-waves together, land on different banks).
+//    quad position j ^ (kk & 4 ? 8 : 0) (rows kk and kk + 4, read by
+//    neighbouring lane groups together, land on different banks).
 // Rows or columns past the operand's edge load a clamped in-range address;
 // they only feed outputs that are not stored.
 __device__ __forceinline__ int dma_swizzle(int r) { return ((r >> 1) ^ (r >> 2)) & 3; }
@@ -411,103 +411,6 @@ __device__ __forceinline__ void dma_barrier() {
   TOPOS_COMPILER_FENCE();
   __builtin_amdgcn_s_barrier();
   TOPOS_COMPILER_FENCE();
-}
-
-// One slab's fragment reads and matrix-core products for a wave's WM x 64
-// block (the k order described above).
-template <int BM, int BN, int WM, bool kLeftInnerK, bool kRightInnerK, bool kT>
-__device__ __forceinline__ void dma_mfma_slab(const float *sa, const float *sb, int wm, int wn, int half, int l32,
-                                              floatx16 (&acc)[WM / 32][2]) {
-  constexpr int WI = WM / 32;
-#pragma unroll
-  for (int g = 0; g < 2; ++g) {  // k groups of 8
-    float av[WI][4], bv[2][4];
-#pragma unroll
-    for (int i = 0; i < WI; ++i) {
-      const int row = wm + 32 * i + l32;
-      if (kLeftInnerK) {
-        const int q = 2 * g + half;
-        const float4 v = *reinterpret_cast<const float4 *>(
-            sa + 256 * (row >> 4) + 4 * (4 * (row & 15) + (q ^ dma_swizzle(row & 15))));
-        av[i][0] = v.x;
-        av[i][1] = v.y;
-        av[i][2] = v.z;
-        av[i][3] = v.w;
-      } else {
-#pragma unroll
-        for (int t = 0; t < 4; ++t) av[i][t] = sa[dma_outer_index<BM>(8 * g + 4 * half + t, row)];
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int col = wn + 32 * j + l32;
-      if (kRightInnerK) {
-        const int q = 2 * g + half;
-        const float4 v = *reinterpret_cast<const float4 *>(
-            sb + 256 * (col >> 4) + 4 * (4 * (col & 15) + (q ^ dma_swizzle(col & 15))));
-        bv[j][0] = v.x;
-        bv[j][1] = v.y;
-        bv[j][2] = v.z;
-        bv[j][3] = v.w;
-      } else {
-#pragma unroll
-        for (int t = 0; t < 4; ++t) bv[j][t] = sb[dma_outer_index<BN>(8 * g + 4 * half + t, col)];
-      }
-    }
-    // kT: the products go in as B^T A^T, so each 32x32 block accumulates
-    // transposed: a lane holds one output row and runs of four consecutive
-    // columns (16-byte stores in the epilogue). Otherwise a lane holds one
-    // column, and a store instruction writes two whole 128-byte row
-    // segments (the layout for outputs whose rows are not 16-byte aligned).
-#pragma unroll
-    for (int t = 0; t < 4; ++t)
-#pragma unroll
-      for (int i = 0; i < WI; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-          acc[i][j] = kT ? __builtin_amdgcn_mfma_f32_32x32x2f32(bv[j][t], av[i][t], acc[i][j], 0, 0, 0)
-                         : __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][t], bv[j][t], acc[i][j], 0, 0, 0);
-  }
-}
-
-// The epilogue of an interior tile through LDS (transposed accumulator
-// blocks of 64-row waves): each half of a wave's 64x64 block (32 rows) goes
-// into the wave's own LDS region, then every store instruction writes four
-// whole 256-byte row segments (16 lanes a row, 16 bytes a lane) instead of
-// 32-byte pieces of 32 rows. `stage` holds 32 x 68 floats for this wave.
-__device__ __forceinline__ void store_block_staged(const floatx16 (&acc)[2][2], float *__restrict__ c, int64_t ldc,
-                                                   int64_t m0, int64_t n0, int wm, int wn, int lane,
-                                                   const float *__restrict__ bias, int64_t bias_cs, int bias_mode,
-                                                   float *stage) {
-  constexpr int kStride = 68;
-  const int h = lane / 32, r = lane % 32;
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int col = 32 * j + 8 * g + 4 * h;
-        float v[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          v[e] = acc[i][j][4 * g + e];
-          if (bias_mode != 0) {
-            const float add = bias[(n0 + wn + col + e) * bias_cs];
-            v[e] = bias_mode == 1 ? v[e] + add : add + v[e];
-          }
-        }
-        *reinterpret_cast<float4 *>(stage + r * kStride + col) = make_float4(v[0], v[1], v[2], v[3]);
-      }
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // this wave's LDS writes done (lgkmcnt(0))
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const int row = 4 * q + lane / 16, col = 4 * (lane % 16);
-      const float4 v = *reinterpret_cast<const float4 *>(stage + row * kStride + col);
-      *reinterpret_cast<float4 *>(c + (m0 + wm + 32 * i + row) * ldc + n0 + wn + col) = v;
-    }
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // the reads are done before the next half overwrites
-  }
 }
 
 // One slab's fragment reads and 16x16x4 matrix-core products for a wave's
