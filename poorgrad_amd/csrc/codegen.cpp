@@ -595,6 +595,99 @@ void launch_generated_chain(const Generated &g, const Expr &e, const void *const
   launch(g, (unsigned)blocks, arguments, stream);
 }
 
+// ---- transposing copy ----
+
+namespace {
+
+// The axis u < rank - 1 along which the single strided input of a pure copy
+// has unit stride while the innermost axis does not, with both extents whole
+// 64-element tiles; -1 when the copy does not have that form.
+int transpose_axis(const Expr &e) {
+  if (e.rank < 2 || e.rank > kMaxRank || e.inputs.size() != 1 || !e.steps.empty() || e.outputs.size() != 1 ||
+      e.outputs[0] != -1)
+    return -1;
+  const ExprInput &in = e.inputs[0];
+  const int inner = e.rank - 1;
+  if (in.kind != ExprInput::kStrided || in.strides[inner] == 1 || e.shape[inner] % 64 != 0) return -1;
+  for (int d = 0; d < inner; ++d)
+    if (in.strides[d] == 1 && e.shape[d] % 64 == 0) return d;
+  return -1;
+}
+
+}  // namespace
+
+bool transposing_copy(const Expr &e) { return transpose_axis(e) >= 0; }
+
+// A copy of a transposed view into a contiguous output (the key gradient of
+// attention read through its head permutation): the chain would read the
+// input four bytes at a time, 4 KB apart. Each workgroup instead moves one
+// 64 x 64 tile of (inner axis, u) through LDS: 16-byte loads along u, where
+// the input is contiguous, and 16-byte stores along the output's inner axis.
+// Every other axis indexes whole tiles.
+Generated generate_transpose_copy(const Expr &e) {
+  const int u = transpose_axis(e);
+  if (u < 0) throw InvalidArgument{"transposing copy: not a transposed view"};
+  const ExprInput &in = e.inputs[0];
+  const int inner = e.rank - 1;
+  int64_t out_stride[kMaxRank];
+  out_stride[inner] = 1;
+  for (int d = inner - 1; d >= 0; --d) out_stride[d] = out_stride[d + 1] * e.shape[d + 1];
+  // Tile grid: inner tiles fastest, then u tiles, then the other axes.
+  std::vector<int> others;
+  for (int d = 0; d < inner; ++d)
+    if (d != u) others.push_back(d);
+  const int64_t ni = e.shape[inner] / 64, nu = e.shape[u] / 64;
+  std::ostringstream s;
+  s << preamble();
+  s << "extern \"C\" __global__ __launch_bounds__(256) void topos_gen(const float* __restrict__ p0, "
+       "float* __restrict__ q0) {\n";
+  s << "  __shared__ float tile[64][65];\n";
+  s << "  long long b = blockIdx.x;\n";
+  s << "  const long long ti = b % " << ll(ni) << ";\n  b /= " << ll(ni) << ";\n";
+  s << "  const long long tu = b % " << ll(nu) << ";\n  b /= " << ll(nu) << ";\n";
+  std::string base_in = ll(in.offset), base_out = "0LL";
+  {
+    // The other axes' coordinates: b over their extents, the last fastest.
+    s << "  long long b0 = b;\n";
+    for (int j = (int)others.size() - 1; j >= 0; --j) {
+      const int d = others[j];
+      const std::string name = "o" + std::to_string(j);
+      s << "  const long long " << name << " = b0 % " << ll(e.shape[d]) << ";\n  b0 /= " << ll(e.shape[d]) << ";\n";
+      base_in += " + " + name + " * " + ll(in.strides[d]);
+      base_out += " + " + name + " * " + ll(out_stride[d]);
+    }
+  }
+  base_in += " + tu * 64LL + ti * " + ll(64 * in.strides[inner]);
+  base_out += " + tu * " + ll(64 * out_stride[u]) + " + ti * 64LL";
+  s << "  const long long bi = " << base_in << ";\n";
+  s << "  const long long bo = " << base_out << ";\n";
+  s << "  const int t = threadIdx.x, q = t % 16;\n";
+  s << "  #pragma unroll\n";
+  s << "  for (int r = 0; r < 4; ++r) {\n";
+  s << "    const int j = 16 * r + t / 16;\n";
+  s << "    const topos_f4 v = *(const topos_f4*)(p0 + bi + (long long)j * " << ll(in.strides[inner]) << " + 4 * q);\n";
+  s << "    tile[j][4 * q] = v.x; tile[j][4 * q + 1] = v.y; tile[j][4 * q + 2] = v.z; tile[j][4 * q + 3] = v.w;\n";
+  s << "  }\n";
+  s << "  __syncthreads();\n";
+  s << "  #pragma unroll\n";
+  s << "  for (int r = 0; r < 4; ++r) {\n";
+  s << "    const int v_ = 16 * r + t / 16;\n";
+  s << "    *(topos_f4*)(q0 + bo + (long long)v_ * " << ll(out_stride[u]) << " + 4 * q) = "
+       "topos_f4{tile[4 * q][v_], tile[4 * q + 1][v_], tile[4 * q + 2][v_], tile[4 * q + 3][v_]};\n";
+  s << "  }\n";
+  s << "}\n";
+  return make(s.str());
+}
+
+void launch_transpose_copy(const Generated &g, const Expr &e, const void *input, float *output, hipStream_t stream) {
+  const int64_t tiles = e.volume() / (64 * 64);
+  if (tiles < 1 || tiles > 0x7fffffff) throw Unsupported{"transposing copy: tile count out of range"};
+  const void *p = input;
+  float *q = output;
+  std::vector<void *> arguments = {&p, &q};
+  launch(g, (unsigned)tiles, arguments, stream);
+}
+
 // ---- fold ----
 
 namespace {

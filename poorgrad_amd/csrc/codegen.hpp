@@ -89,6 +89,14 @@ Generated generate_chain(const Expr &e);
 void launch_generated_chain(const Generated &g, const Expr &e, const void *const *inputs,
                             float *const *outputs, hipStream_t stream);
 
+// A pure copy of one strided input whose innermost axis has a non-unit
+// stride while another axis has unit stride, both extents multiples of 64:
+// generate_transpose_copy moves it in 64 x 64 tiles through LDS. The output
+// receives volume() contiguous floats.
+bool transposing_copy(const Expr &e);
+Generated generate_transpose_copy(const Expr &e);
+void launch_transpose_copy(const Generated &g, const Expr &e, const void *input, float *output, hipStream_t stream);
+
 // Fold along `axis`: the output is the expression's shape without that axis,
 // contiguous.
 Generated generate_fold(const Expr &e, int axis, FoldKind kind);

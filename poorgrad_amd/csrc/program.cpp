@@ -1676,6 +1676,17 @@ struct topos_hip_program {
     e.inputs.push_back(in);
     e.outputs.push_back(-1);
     const int out = arena_storage(e.volume() * 4);
+    if (transposing_copy(e)) {
+      Generated g = generate_transpose_copy(e);
+      pending.push_back(g);
+      add_launch("copy (tiles) " + describe_expr(e), real(storage_of), {out},
+                 [this, e, g, storage_of, out](const Exec &x) {
+                   auto p = pointers_for(storage_of);
+                   launch_transpose_copy(g, e, p[0], (float *)base(out), x.stream);
+                 });
+      account(e, (double)e.volume());
+      return dense_value(out, contiguous(n.rank, n.shape));
+    }
     Generated g = generate_chain(e);
     pending.push_back(g);
     add_launch("copy " + describe_expr(e), real(storage_of), {out}, [this, e, g, storage_of, out](const Exec &x) {

@@ -55,6 +55,42 @@ def test_small_gpt2_train_step_exact_is_bit_identical(hip, layers, heads):
         assert_bitwise(got[r.id], want[r.id], f"gpt2 node {r.id} {r.shape}")
 
 
+@pytest.mark.parametrize("shape", [(2, 3, 64, 128), (1, 2, 128, 64), (3, 1, 64, 192)])
+def test_transposed_view_copied_in_tiles_is_exact(hip, shape):
+    """A reshape of a permuted view whose innermost axis steps through the
+    input while another axis is contiguous (the key gradient of attention
+    read through the head permutation) is copied in 64 x 64 LDS tiles: the
+    same bits as the transposition itself, in both postures."""
+    B, H, D, T = shape
+    banner(f"program tiled transposing copy {shape}")
+    rng = np.random.default_rng(61)
+    tape = t.Tape()
+    x = tape.input((B, H, D, T))
+    y = x.permute((0, 3, 1, 2)).reshape((B * T, H * D))
+    dense = {x.node.slot: rng.standard_normal((B, H, D, T)).astype(np.float32)}
+    want = np.ascontiguousarray(dense[x.node.slot].transpose(0, 3, 1, 2)).reshape(B * T, H * D)
+    for posture in (hip.EXACT, hip.FAST):
+        got, program = run_device(tape, [y], [], dense, numerics=posture)
+        assert "copy (tiles)" in program.describe, program.describe
+        assert_bitwise(got[y.id], want, f"copy {shape}")
+
+
+def test_gpt2_with_tiled_head_copies_fast_within_envelope(hip):
+    """Context and head width multiples of 64: under Fast the key gradient,
+    read through the head permutation, is copied in 64 x 64 LDS tiles (the
+    plan names it `copy (tiles)`). Loss and gradients within the envelope."""
+    banner("program gpt2 tiled head copies fast")
+    w = workloads.gpt2(batch=2, context=64, vocab=61, width=128, heads=2, layers=1, positions=64)
+    want, got, program = check_workload(w, hip.FAST, hip)
+    assert "copy (tiles)" in program.describe
+    loss_exact, loss_fast = want[w.loss.id].item(), got[w.loss.id].item()
+    assert abs(loss_fast - loss_exact) <= 1e-4 * max(abs(loss_exact), 1.0)
+    for r in w.gradients:
+        g, e = got[r.id].astype(np.float64), want[r.id].astype(np.float64)
+        scale = max(np.abs(e).max(), 1e-3)
+        assert np.abs(g - e).max() <= 1e-3 * scale, f"gradient {r.id} {r.shape}"
+
+
 def test_small_gpt2_fast_within_envelope(hip):
     banner("program gpt2 small fast")
     w = workloads.gpt2(batch=2, context=32, vocab=61, width=64, heads=4, layers=2, positions=32)

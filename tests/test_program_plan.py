@@ -323,3 +323,17 @@ d = DeviceProgram(w.tape, w.roots).describe
 print("copy [8,8,14,14,2,2]" in d, "copy [8,16,7,7,2,2]" in d, d.count("gemm window"))
 ''')
     assert out.split() == ["False", "False", "4"], out
+
+
+def test_a_transposed_view_is_copied_in_tiles():
+    # The key gradient of attention, (q^T dS)^T read through the head
+    # permutation: a copy whose innermost axis steps 4 KB through its input
+    # while another axis is contiguous, moved in 64 x 64 tiles through LDS
+    # (the tile kernel compiles for gfx950 with the rest).
+    out = run(r'''
+w = workloads.gpt2(batch=2, context=64, vocab=61, width=128, heads=2, layers=1, positions=64)
+p = DeviceProgram(w.tape, w.roots, numerics=n.FAST)
+print(p.describe)
+''')
+    assert "copy (tiles) [2,64,2,64]" in out, out
+    assert "copy [2,64,2,64]" not in out, out
