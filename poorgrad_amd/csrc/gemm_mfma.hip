@@ -711,9 +711,11 @@ TileShape tile_shape(int64_t m, int64_t n, int64_t k, int64_t batches) {
   const int64_t wide = ((m + 255) / 256) * ((n + 127) / 128) * batches;
   // (Not when the rows would pad a 256-row tile by more than an eighth: the
   // Llama key gradient, 32 x [128, 2048] over 2048, ran at 66 TFLOP/s on
-  // half-empty 256x128 tiles.)
+  // half-empty 256x128 tiles. Nor for k of at most 128, whose tiles are
+  // mostly epilogue: the attention scores on 128x128 tiles took the GPT-2
+  // step from 73.3 to 72.8 ms in a same-box A/B.)
   const bool rows_fill = ((m + 255) / 256 * 256 - m) * 8 <= m;
-  if (rows_fill && (wide >= 768 || (wide >= 512 && wide % 512 == 0))) return {256, 128, 2};
+  if (rows_fill && k > 128 && (wide >= 768 || (wide >= 512 && wide % 512 == 0))) return {256, 128, 2};
   const int64_t thin = ((m + 63) / 64) * ((n + 127) / 128) * batches;
   if (k <= 4096 && thin >= 768 && thin % 768 == 0) return {64, 128, 3};
   return {128, 128, 3};
