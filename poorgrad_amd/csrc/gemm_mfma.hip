@@ -712,8 +712,9 @@ TileShape tile_shape(int64_t m, int64_t n, int64_t k, int64_t batches) {
   // (Not when the rows would pad a 256-row tile by more than an eighth: the
   // Llama key gradient, 32 x [128, 2048] over 2048, ran at 66 TFLOP/s on
   // half-empty 256x128 tiles. Nor for k of at most 128, whose tiles are
-  // mostly epilogue: the attention scores on 128x128 tiles took the GPT-2
-  // step from 73.3 to 72.8 ms in a same-box A/B.)
+  // mostly epilogue: the attention scores, on the 64x128 tiles below, took
+  // the GPT-2 step from 73.3 to 72.8 ms in a same-box A/B; 128x128 tiles
+  // for them measured the same on GPT-2 and 0.3 ms slower on Llama.)
   const bool rows_fill = ((m + 255) / 256 * 256 - m) * 8 <= m;
   if (rows_fill && k > 128 && (wide >= 768 || (wide >= 512 && wide % 512 == 0))) return {256, 128, 2};
   const int64_t thin = ((m + 63) / 64) * ((n + 127) / 128) * batches;
@@ -1059,7 +1060,8 @@ bool launch_gemm_mfma(const float *a, int64_t a_rs, int64_t a_cs, const float *b
   // 16-byte operand access (the DMA loads need 4-byte alignment only); an
   // outer-contiguous operand needs an outer extent of at least 4 (its clamped
   // edge quads). The 128x64 tile (the attention products with a 64-wide right
-  // operand) measured faster on the register-staged kernel.
+  // operand) measured faster on the register-staged kernel with 32x32x2
+  // blocks, and the same with 16x16x4 blocks (GPT-2 step, same-box A/B).
   const bool dma = vector && (lk || m >= 4) && (rk || n >= 4);
   // 16-byte output stores: every batch's and split's base and every row
   // start 16-byte aligned.

@@ -15,7 +15,7 @@ from tests.gpu_util import assert_bitwise, to_device
 pytestmark = pytest.mark.gpu
 
 SHAPES = [(2, 3, 4), (5, 8, 13), (16, 16, 16), (63, 64, 65), (100, 127, 3), (128, 100, 64), (2, 64, 128),
-          (129, 257, 131), (256, 384, 512)]
+          (129, 257, 131), (256, 384, 512), (257, 131, 61)]
 FORMS = ["contiguous", "a_transposed", "b_transposed", "both_transposed", "narrowed", "broadcast"]
 
 
@@ -97,7 +97,9 @@ def test_negative_zero_seed_survives_on_device(hip):
                                      # fast tile choices: 64x128 tiles filling whole rounds (k <= 1024),
                                      # unsplit with a tile per CU, three k ranges
                                      (8192, 768, 768), (8192, 768, 2304), (4096, 2048, 2048),
-                                     (2048, 4096, 2048)])
+                                     (2048, 4096, 2048),
+                                     # 128x64 tiles (an output 64 or fewer wide), whole and ragged
+                                     (1024, 1024, 64), (1000, 300, 62)])
 @pytest.mark.parametrize("product", ["forward", "a_transposed", "b_transposed"])
 def test_sweep_shapes_sampled_rows(hip, m, k, n, product):
     """The GEMM-sweep products at full size (forward A.B, then A^T.G and
