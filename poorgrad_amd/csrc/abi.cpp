@@ -284,14 +284,16 @@ int topos_hip_gemm_bf16_device(const uint16_t *a, int64_t a_row_stride, int64_t 
       return;
     }
     if (numerics == TOPOS_HIP_FAST && bf16_mfma_serves(a_row_stride, a_col_stride, b_row_stride, b_col_stride)) {
-      const int splits = bf16_splits(m, n, k);
-      if (splits > 1)
-        context.with_workspace(splits * m * n, s, [&](float *w) {
-          launch_gemm_bf16_mfma(a, a_row_stride, a_col_stride, b, b_row_stride, b_col_stride, m, k, n, product, ldc,
-                                s, w, splits);
+      const int64_t floats =
+          bf16_fast_workspace_floats(a, a_row_stride, a_col_stride, b, b_row_stride, b_col_stride, m, k, n);
+      if (floats > 0)
+        context.with_workspace(floats, s, [&](float *w) {
+          launch_gemm_bf16_fast(a, a_row_stride, a_col_stride, b, b_row_stride, b_col_stride, m, k, n, product, ldc,
+                                s, w);
         });
       else
-        launch_gemm_bf16_mfma(a, a_row_stride, a_col_stride, b, b_row_stride, b_col_stride, m, k, n, product, ldc, s);
+        launch_gemm_bf16_fast(a, a_row_stride, a_col_stride, b, b_row_stride, b_col_stride, m, k, n, product, ldc, s,
+                              nullptr);
       return;
     }
     // The exact contract step by step: widen both operands, the bit-identical

@@ -250,14 +250,16 @@ void append_engine_backward(std::vector<topos_hip_node> &nodes, std::vector<topo
 
 // gemm_bf16.hip: bf16 products (operands and product as bf16 bit patterns).
 bool bf16_mfma_serves(int64_t a_rs, int64_t a_cs, int64_t b_rs, int64_t b_cs);
-// With splits > 1 (bf16_splits' choice), `partials` holds splits * m * n
-// floats: k is cut into that many ranges, each range's f32 sums written
-// there, then added in range order and rounded once (the envelope, then the
-// same single rounding).
-int bf16_splits(int64_t m, int64_t n, int64_t k);
-void launch_gemm_bf16_mfma(const uint16_t *a, int64_t a_rs, int64_t a_cs, const uint16_t *b, int64_t b_rs,
+// The fast product's workspace, in floats (256-byte aligned): operands the
+// matrix-core kernel cannot read in place (not k-contiguous, or rows not
+// 4-byte aligned) packed into k-contiguous rows, and, for products with few
+// tiles, the f32 sums of each k range (added in range order, then rounded
+// once: the envelope, then the same single rounding).
+int64_t bf16_fast_workspace_floats(const uint16_t *a, int64_t a_rs, int64_t a_cs, const uint16_t *b, int64_t b_rs,
+                                   int64_t b_cs, int64_t m, int64_t k, int64_t n);
+void launch_gemm_bf16_fast(const uint16_t *a, int64_t a_rs, int64_t a_cs, const uint16_t *b, int64_t b_rs,
                            int64_t b_cs, int64_t m, int64_t k, int64_t n, uint16_t *c, int64_t ldc,
-                           hipStream_t stream, float *partials = nullptr, int splits = 1);
+                           hipStream_t stream, float *workspace);
 // Widens an [outer, inner] bf16 view into a dense f32 [outer][inner] buffer.
 void launch_widen_bf16(const uint16_t *in, int64_t outer, int64_t inner, int64_t outer_stride, int64_t inner_stride,
                        float *out, hipStream_t stream);

@@ -10,12 +10,15 @@
 // order: the envelope, then the same single rounding.
 #pragma clang fp contract(off)
 #include "backend.hpp"
+#include "lds_dma.hpp"
 
 namespace topos_hip {
 namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+using namespace lds_dma;
 
 // Bf16::from_f32: round to nearest with ties to even by adding the rounding
 // bias to the bits (the carry runs into the exponent, so overflow reaches
@@ -49,184 +52,299 @@ __global__ __launch_bounds__(256) void narrow_kernel(const float *__restrict__ i
   }
 }
 
-// The matrix-core kernel: 128x128 output tiles of four waves, each wave a
-// 64x64 block of 2x2 MFMA blocks (32x32, k = 16 a product). k is staged 32
-// deep through LDS, double-buffered, each operand stored [outer][k] so a
-// lane's MFMA operand (eight consecutive k of one row or column) is one
-// 16-byte LDS read: lane l takes row (column) l % 32 and k = 8 (l / 32) ..
-// 8 (l / 32) + 7 of each 16-deep step, for both operands alike.
-// kLeftInnerK / kRightInnerK: the operand's k axis has unit stride (else its
-// outer axis has). kVector: 16-byte global loads (every row start 16-byte
-// aligned along the unit-stride axis); otherwise element loads.
-constexpr int kBK = 32;
-constexpr int kRowPad = 8;  // LDS row of 40 bf16 (80 bytes): 16-byte aligned, banks spread
+// The matrix-core kernel: BM x BN output tiles (256x256 of sixteen waves,
+// 256x128 of eight, or 128x128 of four), each wave a 64x64 block of 4x4
+// 16x16 accumulator blocks fed by v_mfma_f32_16x16x32_bf16. k is staged 32
+// deep in P LDS stages written by global_load_lds_dwordx4 (slab s + P - 1 in
+// flight while slab s feeds the matrix cores; one wait and one barrier per
+// slab). Both operands are
+// k-contiguous here: a 32-deep bf16 row is 64 bytes, the f32 products'
+// 16-deep row, so the slab layout is theirs (16 rows a KB, the 16-byte
+// octets of k swizzled by row). Lane l reads octet g = l / 16 of row (or
+// column) l % 16, eight consecutive k, one 16-byte LDS read, and the MFMA
+// takes them for both operands alike, so the k order inside an MFMA is the
+// same for A and B. Operands that are not k-contiguous, or whose rows are not
+// 4-byte aligned, are first packed into k-contiguous rows (pack kernels
+// below). Rows past an operand's edge load a clamped in-range row and feed
+// only outputs that are not stored; a slab crossing k_end goes through
+// registers with zeros past it.
+constexpr int kSlabK = 32;  // bf16 k per slab: 64-byte rows
 
-template <bool kInnerK, bool kVector>
-struct Bf16Slab;
-
-// k-contiguous operand: 128 rows x 32 k = 512 chunks of eight bf16 (one
-// 16-byte load and one 16-byte LDS store each), two a thread; chunk c is
-// row c / 4, k octet c % 4.
-template <bool kVector>
-struct Bf16Slab<true, kVector> {
-  uint4 v[2];
-
-  __device__ void fetch(const uint16_t *__restrict__ p, int64_t outer_stride, int64_t k_stride, int64_t outer_extent,
-                        int64_t k, int64_t o0, int64_t k0) {
+// One slab of a k-contiguous operand (outer extent O, rows outer_stride
+// apart) into `lds`: O / 16 wave-wide DMA loads, spread over the W waves.
+template <int O, int W>
+__device__ __forceinline__ void bf16_dma_slab(const uint16_t *__restrict__ p, int64_t outer_stride,
+                                              int64_t outer_extent, int64_t o0, int64_t k0, float *lds, int wave,
+                                              int lane) {
+  constexpr int kChunks = O / 16;  // 1 KB per wave-wide load
+  static_assert(kChunks % W == 0, "whole chunks per wave");
 #pragma unroll
-    for (int e = 0; e < 2; ++e) {
-      const int c = threadIdx.x + 256 * e;
-      const int64_t go = o0 + c / 4, gk = k0 + 8 * (c % 4);
-      if (kVector && go < outer_extent && gk + 7 < k) {
-        v[e] = *reinterpret_cast<const uint4 *>(p + go * outer_stride + gk);
-      } else {
-        uint16_t h[8];
-#pragma unroll
-        for (int q = 0; q < 8; ++q)
-          h[q] = (go < outer_extent && gk + q < k) ? p[go * outer_stride + (gk + q) * k_stride] : (uint16_t)0;
-        v[e] = make_uint4((uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16),
-                          (uint32_t)h[4] | ((uint32_t)h[5] << 16), (uint32_t)h[6] | ((uint32_t)h[7] << 16));
-      }
-    }
+  for (int i = 0; i < kChunks / W; ++i) {
+    const int c = wave + W * i;
+    const int r = lane >> 2;
+    const int q = (lane & 3) ^ dma_swizzle(r);
+    const int64_t row = min(o0 + 16 * c + r, outer_extent - 1);
+    TOPOS_COMPILER_FENCE();
+    dma_load16(p + row * outer_stride + (k0 + 8 * q), lds_byte_address(lds) + 1024 * c);
+    TOPOS_COMPILER_FENCE();
   }
+}
 
-  __device__ void deposit(uint16_t (*lds)[kBK + kRowPad]) const {
+// The same slab through registers with zeros past k_end (the k tail).
+template <int O, int W>
+__device__ __forceinline__ void bf16_guarded_slab(const uint16_t *__restrict__ p, int64_t outer_stride,
+                                                  int64_t outer_extent, int64_t k_end, int64_t o0, int64_t k0,
+                                                  float *lds, int wave, int lane) {
+  constexpr int kChunks = O / 16;
 #pragma unroll
-    for (int e = 0; e < 2; ++e) {
-      const int c = threadIdx.x + 256 * e;
-      *reinterpret_cast<uint4 *>(&lds[c / 4][8 * (c % 4)]) = v[e];
+  for (int i = 0; i < kChunks / W; ++i) {
+    const int c = wave + W * i;
+    const int r = lane >> 2;
+    const int q = (lane & 3) ^ dma_swizzle(r);
+    const uint16_t *row = p + min(o0 + 16 * c + r, outer_extent - 1) * outer_stride;
+    uint32_t w[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int64_t kk = k0 + 8 * q + 2 * e;
+      const uint32_t lo = kk < k_end ? row[kk] : 0u;
+      const uint32_t hi = kk + 1 < k_end ? row[kk + 1] : 0u;
+      w[e] = lo | (hi << 16);
     }
+    *reinterpret_cast<uint4 *>(lds + c * 256 + 4 * lane) = make_uint4(w[0], w[1], w[2], w[3]);
   }
-};
+}
 
-// Outer-contiguous operand: a thread takes four neighbouring outer elements
-// over four k rows (four 8-byte loads, consecutive threads on consecutive
-// quads: 256 contiguous bytes a k row), transposes them in registers and
-// writes four 8-byte LDS pieces, one per outer element; thread t takes outer
-// quad t % 32, k quad t / 32.
-template <bool kVector>
-struct Bf16Slab<false, kVector> {
-  uint2 w[4];
+// One slab's fragment reads and matrix-core products for a wave's 64x64
+// block. kT: the products go in as B^T A^T, so a lane holds one output row
+// (16i + l % 16) and four consecutive columns (16j + 4g + {0..3}); otherwise
+// a lane holds one column (16j + l % 16) and rows 16i + 4g + r.
+template <bool kT>
+__device__ __forceinline__ void bf16_mfma_slab(const float *sa, const float *sb, int wm, int wn, int lane,
+                                               floatx4 (&acc)[4][4]) {
+  const int l16 = lane % 16, g = lane / 16;
+  const int at = 4 * (4 * l16 + (g ^ dma_swizzle(l16)));  // within a 16-row KB
+  bf16x8 av[4], bv[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) av[i] = *reinterpret_cast<const bf16x8 *>(sa + 256 * ((wm >> 4) + i) + at);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) bv[j] = *reinterpret_cast<const bf16x8 *>(sb + 256 * ((wn >> 4) + j) + at);
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      acc[i][j] = kT ? __builtin_amdgcn_mfma_f32_16x16x32_bf16(bv[j], av[i], acc[i][j], 0, 0, 0)
+                     : __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[i], bv[j], acc[i][j], 0, 0, 0);
+}
 
-  __device__ void fetch(const uint16_t *__restrict__ p, int64_t outer_stride, int64_t k_stride, int64_t outer_extent,
-                        int64_t k, int64_t o0, int64_t k0) {
-    const int t = threadIdx.x;
-    const int64_t go = o0 + 4 * (t % 32), gk = k0 + 4 * (t / 32);
+// Waits until the next slab has landed, with `ahead` slabs issued after it
+// (uniform, at most A): vmcnt(ahead * kIssue).
+template <int kIssue, int A>
+__device__ __forceinline__ void wait_for_next(int ahead) {
+  if constexpr (A > 0) {
+    if (ahead >= A) {
+      dma_wait<A * kIssue>();
+      return;
+    }
+    wait_for_next<kIssue, A - 1>(ahead);
+  } else {
+    dma_wait<0>();
+  }
+}
+
+// Output element stores: rounded once to bf16 into c (rows ldc apart), or
+// the f32 sums of k range z into partials + z * m * n (rows n apart).
+// kT: four consecutive columns a lane, one 8-byte (bf16) or 16-byte (f32)
+// store when they are inside the output.
+template <bool kT, bool kPartials>
+__device__ __forceinline__ void bf16_store(const floatx4 (&acc)[4][4], uint16_t *__restrict__ c, int64_t ldc,
+                                           float *__restrict__ partials, int64_t m, int64_t n, int64_t m0,
+                                           int64_t n0, int wm, int wn, int lane) {
+  const int l16 = lane % 16, g = lane / 16;
+  if (kT) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int64_t kk = gk + i;
-      if (kVector && go + 3 < outer_extent && kk < k) {
-        w[i] = *reinterpret_cast<const uint2 *>(p + kk * k_stride + go);
-      } else {
-        uint32_t h[4];
+      const int64_t row = m0 + wm + 16 * i + l16;
+      if (row >= m) continue;
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-          h[q] = (go + q < outer_extent && kk < k) ? p[kk * k_stride + (go + q) * outer_stride] : 0u;
-        w[i] = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+      for (int j = 0; j < 4; ++j) {
+        const int64_t col = n0 + wn + 16 * j + 4 * g;
+        if (kPartials) {
+          float *out = partials + row * n + col;
+          if (col + 3 < n) {
+            *reinterpret_cast<float4 *>(out) = make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (col + e < n) out[e] = acc[i][j][e];
+          }
+        } else {
+          uint16_t *out = c + row * ldc + col;
+          if (col + 3 < n) {
+            *reinterpret_cast<uint2 *>(out) =
+                make_uint2((uint32_t)bf16_of(acc[i][j][0]) | ((uint32_t)bf16_of(acc[i][j][1]) << 16),
+                           (uint32_t)bf16_of(acc[i][j][2]) | ((uint32_t)bf16_of(acc[i][j][3]) << 16));
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (col + e < n) out[e] = bf16_of(acc[i][j][e]);
+          }
+        }
       }
     }
+    return;
   }
-
-  __device__ void deposit(uint16_t (*lds)[kBK + kRowPad]) const {
-    const int t = threadIdx.x;
-    const int o = 4 * (t % 32), kq = t / 32;
-    // Outer element j of k row i is half (j % 2) of word (j / 2) of w[i].
-    const uint2 r0 = make_uint2((w[0].x & 0xffffu) | (w[1].x << 16), (w[2].x & 0xffffu) | (w[3].x << 16));
-    const uint2 r1 = make_uint2((w[0].x >> 16) | (w[1].x & 0xffff0000u), (w[2].x >> 16) | (w[3].x & 0xffff0000u));
-    const uint2 r2 = make_uint2((w[0].y & 0xffffu) | (w[1].y << 16), (w[2].y & 0xffffu) | (w[3].y << 16));
-    const uint2 r3 = make_uint2((w[0].y >> 16) | (w[1].y & 0xffff0000u), (w[2].y >> 16) | (w[3].y & 0xffff0000u));
-    *reinterpret_cast<uint2 *>(&lds[o][4 * kq]) = r0;
-    *reinterpret_cast<uint2 *>(&lds[o + 1][4 * kq]) = r1;
-    *reinterpret_cast<uint2 *>(&lds[o + 2][4 * kq]) = r2;
-    *reinterpret_cast<uint2 *>(&lds[o + 3][4 * kq]) = r3;
-  }
-};
-
-// With `partials` set, range z = blockIdx.z of k ([z * split_len, ..)) is
-// multiplied and its f32 sums written unrounded to partials + z * m * n
-// (rows n apart); reduce_bf16_kernel adds the ranges and rounds once.
-template <bool kLeftInnerK, bool kRightInnerK, bool kVector>
-__global__ __launch_bounds__(256) void gemm_bf16_mfma_kernel(const uint16_t *__restrict__ a, int64_t a_rs,
-                                                             int64_t a_cs, const uint16_t *__restrict__ b,
-                                                             int64_t b_rs, int64_t b_cs, int64_t m, int64_t k,
-                                                             int64_t n, uint16_t *__restrict__ c, int64_t ldc,
-                                                             int grid_m, int grid_n, float *__restrict__ partials,
-                                                             int64_t split_len) {
-  __shared__ __attribute__((aligned(16))) uint16_t lds_a[2][128][kBK + kRowPad];
-  __shared__ __attribute__((aligned(16))) uint16_t lds_b[2][128][kBK + kRowPad];
-  // Groups of eight tile rows walk the columns together (operand panels
-  // reused from L2).
-  const int pid = blockIdx.x;
-  const int in_group = 8 * grid_n;
-  const int first_m = (pid / in_group) * 8;
-  const int group_rows = min(grid_m - first_m, 8);
-  const int64_t m0 = (int64_t)(first_m + (pid % in_group) % group_rows) * 128;
-  const int64_t n0 = (int64_t)((pid % in_group) / group_rows) * 128;
-  const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
-  const int wm = (wave / 2) * 64, wn = (wave % 2) * 64;
-  const int half = lane / 32, l32 = lane % 32;
-
-  floatx16 acc[2][2];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-
-  Bf16Slab<kLeftInnerK, kVector> sa;
-  Bf16Slab<kRightInnerK, kVector> sb;
-  const int64_t k_begin = partials ? (int64_t)blockIdx.z * split_len : 0;
-  const int64_t k_end = partials ? min(k, k_begin + split_len) : k;
-  const int slabs = (int)((k_end - k_begin + kBK - 1) / kBK);
-  sa.fetch(a, a_rs, a_cs, m, k_end, m0, k_begin);
-  sb.fetch(b, b_cs, b_rs, n, k_end, n0, k_begin);
-  sa.deposit(lds_a[0]);
-  sb.deposit(lds_b[0]);
-  __syncthreads();
-  for (int s = 0; s < slabs; ++s) {
-    const int buf = s & 1;
-    if (s + 1 < slabs) {
-      sa.fetch(a, a_rs, a_cs, m, k_end, m0, k_begin + (int64_t)(s + 1) * kBK);
-      sb.fetch(b, b_cs, b_rs, n, k_end, n0, k_begin + (int64_t)(s + 1) * kBK);
-    }
-#pragma unroll
-    for (int ks = 0; ks < kBK / 16; ++ks) {
-      bf16x8 af[2], bfr[2];
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        af[i] = *reinterpret_cast<const bf16x8 *>(&lds_a[buf][wm + 32 * i + l32][16 * ks + 8 * half]);
-        bfr[i] = *reinterpret_cast<const bf16x8 *>(&lds_b[buf][wn + 32 * i + l32][16 * ks + 8 * half]);
-      }
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
-    }
-    if (s + 1 < slabs) {
-      sa.deposit(lds_a[buf ^ 1]);
-      sb.deposit(lds_b[buf ^ 1]);
-    }
-    __syncthreads();
-  }
-  // Accumulator element r of block (i, j): row 8 (r / 4) + 4 (lane / 32) +
-  // r % 4 and column lane % 32 of the block.
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int64_t col = n0 + wn + 32 * j + l32;
+    for (int j = 0; j < 4; ++j) {
+      const int64_t col = n0 + wn + 16 * j + l16;
       if (col >= n) continue;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int64_t row = m0 + wm + 32 * i + 8 * (r / 4) + 4 * half + (r % 4);
+      for (int r = 0; r < 4; ++r) {
+        const int64_t row = m0 + wm + 16 * i + 4 * g + r;
         if (row >= m) continue;
-        if (partials)
-          partials[(int64_t)blockIdx.z * m * n + row * n + col] = acc[i][j][r];
+        if (kPartials)
+          partials[row * n + col] = acc[i][j][r];
         else
           c[row * ldc + col] = bf16_of(acc[i][j][r]);
       }
     }
+}
+
+// Workgroups of one kernel shape that fit a CU's 160 KB of LDS, and the
+// waves each SIMD then holds (the register budget: 512 / that many).
+constexpr int bf16_lds_bytes(int bm, int bn, int p) { return p * (bm + bn) * kSlabK * 2; }
+constexpr int bf16_waves_per_simd(int bm, int bn, int p) {
+  return (163840 / bf16_lds_bytes(bm, bn, p)) * (bm / 64) * (bn / 64) / 4;
+}
+
+// a: [m][k] rows a_rs apart, b: [n][k] rows b_cs apart (B^T's rows), both
+// k-contiguous with 4-byte aligned rows. P stages: slab s + P - 1 is issued
+// while slab s feeds the matrix cores. With kPartials, range z = blockIdx.z
+// of k ([z * split_len, ..)) writes its f32 sums to partials.
+template <int BM, int BN, int P, bool kT, bool kPartials>
+__global__ __launch_bounds__(BM * BN / 64, bf16_waves_per_simd(BM, BN, P)) void gemm_bf16_dma_kernel(
+    const uint16_t *__restrict__ a, int64_t a_rs, const uint16_t *__restrict__ b, int64_t b_cs, int64_t m,
+    int64_t k, int64_t n, uint16_t *__restrict__ c, int64_t ldc, float *__restrict__ partials, int grid_m,
+    int grid_n, int64_t split_len) {
+  constexpr int WN = BN / 64;
+  constexpr int W = BM / 64 * WN;                            // waves, one 64x64 block each
+  constexpr int SA = BM * kSlabK / 2, SB = BN * kSlabK / 2;  // 4-byte words per stage
+  constexpr int kIssue = (BM / 16 + BN / 16) / W;           // DMA loads per wave per slab
+  static_assert((BM / 16) % W == 0 && (BN / 16) % W == 0, "whole chunks per wave");
+  static_assert(P >= 2 && (P - 2) * kIssue < 16, "slabs in flight within the vmcnt field");
+  __shared__ __attribute__((aligned(1024))) float lds[P * (SA + SB)];
+
+  const int64_t k_begin = kPartials ? (int64_t)blockIdx.z * split_len : 0;
+  const int64_t k_end = kPartials ? min(k, k_begin + split_len) : k;
+  if (kPartials) partials += (int64_t)blockIdx.z * m * n;
+
+  // Consecutive workgroups go to different XCDs: renumber so each XCD takes
+  // a contiguous run of tiles, then groups of eight tile rows walk the
+  // columns together (operand panels reused from that XCD's L2).
+  const int blocks = grid_m * grid_n;
+  int pid = blockIdx.x;
+  if (blocks % 8 == 0) pid = (pid % 8) * (blocks / 8) + pid / 8;
+  const int in_group = 8 * grid_n;
+  const int first_m = (pid / in_group) * 8;
+  const int group_rows = min(grid_m - first_m, 8);
+  const int64_t m0 = (int64_t)(first_m + (pid % in_group) % group_rows) * BM;
+  const int64_t n0 = (int64_t)((pid % in_group) / group_rows) * BN;
+
+  const int lane = threadIdx.x % 64;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+  const int wm = (wave / WN) * 64, wn = (wave % WN) * 64;
+
+  floatx4 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[i][j][r] = 0.0f;
+
+  auto issue = [&](int s) {
+    float *stage = lds + (s % P) * (SA + SB);
+    const int64_t k0 = k_begin + (int64_t)s * kSlabK;
+    if (k0 + kSlabK > k_end) {
+      bf16_guarded_slab<BM, W>(a, a_rs, m, k_end, m0, k0, stage, wave, lane);
+      bf16_guarded_slab<BN, W>(b, b_cs, n, k_end, n0, k0, stage + SA, wave, lane);
+    } else {
+      bf16_dma_slab<BM, W>(a, a_rs, m, m0, k0, stage, wave, lane);
+      bf16_dma_slab<BN, W>(b, b_cs, n, n0, k0, stage + SA, wave, lane);
+    }
+  };
+  const int slabs = (int)((k_end - k_begin + kSlabK - 1) / kSlabK);
+  for (int s = 0; s < P - 1 && s < slabs; ++s) issue(s);
+  wait_for_next<kIssue, P - 2>(min(P - 2, slabs - 1));
+  dma_barrier();
+  for (int s = 0; s < slabs; ++s) {
+    // Stage (s + P - 1) % P held slab s - 1, which every wave finished
+    // before the last barrier.
+    if (s + P - 1 < slabs) issue(s + P - 1);
+    const float *sa = lds + (s % P) * (SA + SB);
+    bf16_mfma_slab<kT>(sa, sa + SA, wm, wn, lane, acc);
+    if (s + 1 < slabs) {
+      wait_for_next<kIssue, P - 2>(min(P - 2, slabs - 2 - s));
+      dma_barrier();
+    }
+  }
+  bf16_store<kT, kPartials>(acc, c, ldc, partials, m, n, m0, n0, wm, wn, lane);
+}
+
+// Packs an operand view into k-contiguous rows: element (o, kk), at
+// p[o * outer_stride + kk * k_stride], goes to q[o * kp + kk]. An
+// outer-contiguous view (outer_stride 1) is transposed through 64 x 64 LDS
+// tiles: 8-byte loads along the input's rows, 8-byte stores along the
+// output's (kVector: those accesses aligned); any other view is gathered
+// element by element, consecutive lanes along k.
+template <bool kVector>
+__global__ __launch_bounds__(256) void pack_transpose_kernel(const uint16_t *__restrict__ p, int64_t outer,
+                                                             int64_t kdim, int64_t k_stride,
+                                                             uint16_t *__restrict__ q, int64_t kp, int tiles_o) {
+  __shared__ uint16_t tile[64][64 + 4];  // [kk][o]
+  const int t = threadIdx.x;
+  const int64_t o0 = (int64_t)(blockIdx.x % tiles_o) * 64, k0 = (int64_t)(blockIdx.x / tiles_o) * 64;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int kk = t / 16 + 16 * e, o = 4 * (t % 16);
+    const uint16_t *src = p + (k0 + kk) * k_stride + o0 + o;
+    uint16_t v[4];
+    if (kVector && k0 + kk < kdim && o0 + o + 3 < outer) {
+      const uint2 w = *reinterpret_cast<const uint2 *>(src);
+      v[0] = (uint16_t)w.x, v[1] = (uint16_t)(w.x >> 16), v[2] = (uint16_t)w.y, v[3] = (uint16_t)(w.y >> 16);
+    } else {
+#pragma unroll
+      for (int x = 0; x < 4; ++x) v[x] = (k0 + kk < kdim && o0 + o + x < outer) ? src[x] : (uint16_t)0;
+    }
+#pragma unroll
+    for (int x = 0; x < 4; ++x) tile[kk][o + x] = v[x];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int o = t / 16 + 16 * e, kk = 4 * (t % 16);
+    if (o0 + o >= outer) continue;
+    uint16_t *dst = q + (o0 + o) * kp + k0 + kk;
+    if (kVector && k0 + kk + 3 < kdim) {
+      *reinterpret_cast<uint2 *>(dst) = make_uint2((uint32_t)tile[kk][o] | ((uint32_t)tile[kk + 1][o] << 16),
+                                                   (uint32_t)tile[kk + 2][o] | ((uint32_t)tile[kk + 3][o] << 16));
+    } else {
+#pragma unroll
+      for (int x = 0; x < 4; ++x)
+        if (k0 + kk + x < kdim) dst[x] = tile[kk + x][o];
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void pack_gather_kernel(const uint16_t *__restrict__ p, int64_t outer,
+                                                          int64_t kdim, int64_t outer_stride, int64_t k_stride,
+                                                          uint16_t *__restrict__ q, int64_t kp) {
+  const int64_t count = outer * kdim;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t o = i / kdim, kk = i - o * kdim;
+    q[o * kp + kk] = p[o * outer_stride + kk * k_stride];
+  }
 }
 
 // The ranges' f32 sums added in range order, then rounded once to bf16.
@@ -241,21 +359,138 @@ __global__ __launch_bounds__(256) void reduce_bf16_kernel(const float *__restric
   }
 }
 
-template <bool kL, bool kR>
-void dispatch_bf16(bool vector, dim3 grid, hipStream_t stream, const uint16_t *a, int64_t a_rs, int64_t a_cs,
-                   const uint16_t *b, int64_t b_rs, int64_t b_cs, int64_t m, int64_t k, int64_t n, uint16_t *c,
-                   int64_t ldc, int gm, int gn, float *partials, int64_t split_len) {
-  if (vector)
-    gemm_bf16_mfma_kernel<kL, kR, true><<<grid, 256, 0, stream>>>(a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, gm, gn,
-                                                                 partials, split_len);
-  else
-    gemm_bf16_mfma_kernel<kL, kR, false><<<grid, 256, 0, stream>>>(a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, gm,
-                                                                  gn, partials, split_len);
-}
-
 unsigned blocks_for(int64_t count) {
   const int64_t blocks = (count + 255) / 256;
   return (unsigned)std::min<int64_t>(std::max<int64_t>(blocks, 1), 256 * 64);
+}
+
+int64_t whole_words(int64_t halves) { return (halves + 127) / 128 * 64; }  // 4-byte words, 256-byte multiples
+
+// An operand the DMA kernel reads in place: k-contiguous, every row start
+// 4-byte aligned (the DMA's 16-byte loads need no more).
+bool dma_ready(const uint16_t *p, int64_t outer_stride, int64_t k_stride, int64_t outer) {
+  return k_stride == 1 && reinterpret_cast<uintptr_t>(p) % 4 == 0 && (outer_stride % 2 == 0 || outer == 1);
+}
+
+struct Bf16Plan {
+  bool pack_a = false, pack_b = false;
+  int64_t kp = 0;  // packed row length: k rounded up to 8 (16-byte rows)
+  int bm = 128, bn = 128;  // tile
+  int stages = 3;          // LDS stages (slabs in flight: stages - 1)
+  int splits = 1;
+  int64_t split_len = 0;
+  int64_t a_words = 0, b_words = 0, partial_words = 0;  // workspace pieces
+};
+
+Bf16Plan bf16_plan(const uint16_t *a, int64_t a_rs, int64_t a_cs, const uint16_t *b, int64_t b_rs, int64_t b_cs,
+                   int64_t m, int64_t k, int64_t n) {
+  Bf16Plan plan;
+  plan.pack_a = !dma_ready(a, a_rs, a_cs, m);
+  plan.pack_b = !dma_ready(b, b_cs, b_rs, n);
+  plan.kp = (k + 7) / 8 * 8;
+  if (plan.pack_a) plan.a_words = whole_words(m * plan.kp);
+  if (plan.pack_b) plan.b_words = whole_words(n * plan.kp);
+  // Tile shapes, from a sweep of every shape, stage count and split over the
+  // GEMM sweep's products on MI355X: 256x256 tiles (sixteen waves, one
+  // workgroup a CU, four stages) when they fill whole rounds without padding
+  // either extent by more than an eighth (4096^3: 954-1093 TFLOP/s against
+  // 818-928 on 256x128); 256x128 (two a CU, three stages) when those fill a
+  // round ([8192, 3072] over 768: 643 against 570 on 256x256, which leaves
+  // half a round); else 128x128 (two a CU, four stages: three measured 1-2%
+  // slower).
+  auto fills = [](int64_t extent, int64_t tile) { return ((extent + tile - 1) / tile * tile - extent) * 8 <= extent; };
+  const int64_t big = ((m + 255) / 256) * ((n + 255) / 256);
+  if (fills(m, 256) && fills(n, 256) && k >= 1024 && (big % 256 == 0 || big >= 1024)) {
+    plan.bm = 256, plan.bn = 256, plan.stages = 4;
+  } else if (fills(m, 256) && ((m + 255) / 256) * ((n + 127) / 128) >= 512) {
+    plan.bm = 256, plan.bn = 128, plan.stages = 3;
+  } else {
+    plan.bm = 128, plan.bn = 128, plan.stages = 4;
+  }
+  // Only products with fewer tiles than CUs split k, into at most four
+  // ranges (at most two workgroups a CU), each at least 512 deep (128 below
+  // k = 2048). The bf16 matrix cores finish a range quickly, so the partials'
+  // extra pass costs more than it does for f32: [8192, 768] over 3072 (384
+  // tiles) ran at 575 TFLOP/s unsplit against 453 in two ranges, [1024, 1024]
+  // over 4096 (64 tiles) at 262 in four against 233 in eight.
+  const int64_t tiles = ((m + plan.bm - 1) / plan.bm) * ((n + plan.bn - 1) / plan.bn);
+  const int64_t shortest = k < 2048 ? 128 : 512;
+  int64_t s = 1;
+  if (tiles < 256)
+    while (s < 4 && tiles * (s + 1) <= 512 && k / (s + 1) >= shortest) ++s;
+  plan.split_len = k;
+  if (s > 1) {
+    plan.split_len = ((k + s - 1) / s + kSlabK - 1) / kSlabK * kSlabK;
+    s = (k + plan.split_len - 1) / plan.split_len;
+  }
+  plan.splits = (int)s;
+  if (plan.splits > 1) plan.partial_words = plan.splits * m * n;
+  return plan;
+}
+
+// Packs the [outer, kdim] view (element (o, kk) at p[o * os + kk * ks]) into
+// q's k-contiguous rows of kp.
+void pack_rows(const uint16_t *p, int64_t outer, int64_t kdim, int64_t os, int64_t ks, uint16_t *q, int64_t kp,
+               hipStream_t stream) {
+  if (os == 1) {
+    const int64_t tiles_o = (outer + 63) / 64, tiles_k = (kdim + 63) / 64;
+    if (tiles_o * tiles_k > 0x7fffffff) throw Unsupported{"bf16 gemm: operand too large to pack"};
+    const bool vector = reinterpret_cast<uintptr_t>(p) % 8 == 0 && ks % 4 == 0;
+    const dim3 grid((unsigned)(tiles_o * tiles_k));
+    if (vector)
+      pack_transpose_kernel<true><<<grid, 256, 0, stream>>>(p, outer, kdim, ks, q, kp, (int)tiles_o);
+    else
+      pack_transpose_kernel<false><<<grid, 256, 0, stream>>>(p, outer, kdim, ks, q, kp, (int)tiles_o);
+    check_launch("pack_transpose_kernel launch");
+  } else {
+    pack_gather_kernel<<<blocks_for(outer * kdim), 256, 0, stream>>>(p, outer, kdim, os, ks, q, kp);
+    check_launch("pack_gather_kernel launch");
+  }
+}
+
+template <int BM, int BN, int P>
+void dispatch_bf16(bool vector_out, dim3 grid, hipStream_t stream, const uint16_t *a, int64_t a_row,
+                   const uint16_t *b, int64_t b_row, int64_t m, int64_t k, int64_t n, uint16_t *c, int64_t ldc,
+                   float *partials, int gm, int gn, int64_t split_len) {
+  constexpr int T = BM * BN / 64;
+#define TOPOS_BF16_LAUNCH(kT, kP) \
+  gemm_bf16_dma_kernel<BM, BN, P, kT, kP><<<grid, T, 0, stream>>>(a, a_row, b, b_row, m, k, n, c, ldc, partials, gm, gn, split_len)
+  if (partials && vector_out)
+    TOPOS_BF16_LAUNCH(true, true);
+  else if (partials)
+    TOPOS_BF16_LAUNCH(false, true);
+  else if (vector_out)
+    TOPOS_BF16_LAUNCH(true, false);
+  else
+    TOPOS_BF16_LAUNCH(false, false);
+#undef TOPOS_BF16_LAUNCH
+}
+
+// The kernel shapes the planner chooses from: (tile rows, tile columns,
+// stages).
+#define TOPOS_BF16_SHAPES(X) X(256, 256, 4) X(256, 128, 3) X(128, 128, 4)
+
+void launch_bf16_plan(const Bf16Plan &plan, const uint16_t *a_in, int64_t a_row, const uint16_t *b_in, int64_t b_row,
+                      int64_t m, int64_t k, int64_t n, uint16_t *c, int64_t ldc, float *partials, hipStream_t stream) {
+  const int64_t gm = (m + plan.bm - 1) / plan.bm, gn = (n + plan.bn - 1) / plan.bn;
+  if (gm * gn > 0x7fffffff) throw Unsupported{"bf16 gemm: grid too large"};
+  const dim3 grid((unsigned)(gm * gn), 1, (unsigned)plan.splits);
+  const bool vector_out = partials ? n % 4 == 0 : ldc % 4 == 0 && reinterpret_cast<uintptr_t>(c) % 8 == 0;
+  bool launched = false;
+#define TOPOS_BF16_SHAPE(BM, BN, P)                                                                               \
+  if (!launched && plan.bm == BM && plan.bn == BN && plan.stages == P) {                                          \
+    dispatch_bf16<BM, BN, P>(vector_out, grid, stream, a_in, a_row, b_in, b_row, m, k, n, c, ldc, partials, (int)gm, \
+                             (int)gn, plan.split_len);                                                            \
+    launched = true;                                                                                              \
+  }
+  TOPOS_BF16_SHAPES(TOPOS_BF16_SHAPE)
+#undef TOPOS_BF16_SHAPE
+  if (!launched) throw Unsupported{"bf16 gemm: no kernel for the planned tile"};
+  check_launch("gemm_bf16_dma_kernel launch");
+  if (partials) {
+    reduce_bf16_kernel<<<blocks_for(m * n), 256, 0, stream>>>(partials, plan.splits, m, n, c, ldc);
+    check_launch("reduce_bf16_kernel launch");
+  }
 }
 
 }  // namespace
@@ -264,55 +499,33 @@ bool bf16_mfma_serves(int64_t a_rs, int64_t a_cs, int64_t b_rs, int64_t b_cs) {
   return (a_cs == 1 || a_rs == 1) && (b_rs == 1 || b_cs == 1);
 }
 
-int bf16_splits(int64_t m, int64_t n, int64_t k) {
-  // Products with fewer 128x128 tiles than four per CU split k into ranges
-  // of at least 512 (at most 16 of them) until they have that many
-  // workgroups: the [3072, 768] weight gradient over k = 8192 (144 tiles)
-  // went from 44 TFLOP/s unsplit to 184 in four ranges and 212 in eight.
-  const int64_t tiles = ((m + 127) / 128) * ((n + 127) / 128);
-  int64_t s = 1;
-  while (s < 16 && tiles * s < 1024 && k / (2 * s) >= 512) s *= 2;
-  return (int)s;
+int64_t bf16_fast_workspace_floats(const uint16_t *a, int64_t a_rs, int64_t a_cs, const uint16_t *b, int64_t b_rs,
+                                   int64_t b_cs, int64_t m, int64_t k, int64_t n) {
+  const Bf16Plan plan = bf16_plan(a, a_rs, a_cs, b, b_rs, b_cs, m, k, n);
+  return plan.a_words + plan.b_words + plan.partial_words;
 }
 
-void launch_gemm_bf16_mfma(const uint16_t *a, int64_t a_rs, int64_t a_cs, const uint16_t *b, int64_t b_rs,
+void launch_gemm_bf16_fast(const uint16_t *a, int64_t a_rs, int64_t a_cs, const uint16_t *b, int64_t b_rs,
                            int64_t b_cs, int64_t m, int64_t k, int64_t n, uint16_t *c, int64_t ldc,
-                           hipStream_t stream, float *partials, int splits) {
-  const bool lk = a_cs == 1, rk = b_rs == 1;
-  // Vector loads: 16 bytes along a k-contiguous operand's rows, 8 bytes along
-  // an outer-contiguous operand's k rows; every row start aligned to them.
-  const int64_t a_step = lk ? a_rs : a_cs, b_step = rk ? b_cs : b_rs;
-  const int a_align = lk ? 8 : 4, b_align = rk ? 8 : 4;  // in elements
-  const bool vector = reinterpret_cast<uintptr_t>(a) % (2 * a_align) == 0 &&
-                      reinterpret_cast<uintptr_t>(b) % (2 * b_align) == 0 && a_step % a_align == 0 &&
-                      b_step % b_align == 0;
-  const int64_t gm = (m + 127) / 128, gn = (n + 127) / 128;
-  if (gm * gn > 0x7fffffff) throw Unsupported{"bf16 gemm: grid too large"};
-  if (splits < 1 || splits > 16 || (splits > 1 && !partials)) throw Unsupported{"bf16 gemm: split without partials"};
-  int64_t split_len = k;
-  if (splits > 1) {
-    split_len = ((k + splits - 1) / splits + kBK - 1) / kBK * kBK;
-    splits = (int)((k + split_len - 1) / split_len);
+                           hipStream_t stream, float *workspace) {
+  const Bf16Plan plan = bf16_plan(a, a_rs, a_cs, b, b_rs, b_cs, m, k, n);
+  if (plan.a_words + plan.b_words + plan.partial_words > 0 &&
+      (!workspace || reinterpret_cast<uintptr_t>(workspace) % 256 != 0))
+    throw Unsupported{"bf16 gemm: workspace missing or misaligned"};
+  const uint16_t *a_in = a, *b_in = b;
+  int64_t a_row = a_rs, b_row = b_cs;
+  if (plan.pack_a) {
+    uint16_t *q = reinterpret_cast<uint16_t *>(workspace);
+    pack_rows(a, m, k, a_rs, a_cs, q, plan.kp, stream);
+    a_in = q, a_row = plan.kp;
   }
-  float *target = splits > 1 ? partials : nullptr;
-  const dim3 grid((unsigned)(gm * gn), 1, (unsigned)splits);
-  if (lk && rk)
-    dispatch_bf16<true, true>(vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, (int)gm, (int)gn,
-                              target, split_len);
-  else if (lk)
-    dispatch_bf16<true, false>(vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, (int)gm, (int)gn,
-                               target, split_len);
-  else if (rk)
-    dispatch_bf16<false, true>(vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, (int)gm, (int)gn,
-                               target, split_len);
-  else
-    dispatch_bf16<false, false>(vector, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, c, ldc, (int)gm,
-                                (int)gn, target, split_len);
-  check_launch("gemm_bf16_mfma_kernel launch");
-  if (splits > 1) {
-    reduce_bf16_kernel<<<blocks_for(m * n), 256, 0, stream>>>(partials, splits, m, n, c, ldc);
-    check_launch("reduce_bf16_kernel launch");
+  if (plan.pack_b) {
+    uint16_t *q = reinterpret_cast<uint16_t *>(workspace + plan.a_words);
+    pack_rows(b, n, k, b_cs, b_rs, q, plan.kp, stream);
+    b_in = q, b_row = plan.kp;
   }
+  float *partials = plan.splits > 1 ? workspace + plan.a_words + plan.b_words : nullptr;
+  launch_bf16_plan(plan, a_in, a_row, b_in, b_row, m, k, n, c, ldc, partials, stream);
 }
 
 void launch_widen_bf16(const uint16_t *in, int64_t outer, int64_t inner, int64_t outer_stride, int64_t inner_stride,

@@ -25,9 +25,12 @@
 #include <algorithm>
 
 #include "backend.hpp"
+#include "lds_dma.hpp"
 
 namespace topos_hip {
 namespace {
+
+using namespace lds_dma;
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
@@ -303,30 +306,9 @@ __global__ __launch_bounds__(BM / WM * BN, BM == 256 && kVector ? 4 : 1) void ge
 //    neighbouring lane groups together, land on different banks).
 // Rows or columns past the operand's edge load a clamped in-range address;
 // they only feed outputs that are not stored.
-__device__ __forceinline__ int dma_swizzle(int r) { return ((r >> 1) ^ (r >> 2)) & 3; }
-
 template <int O>
 __device__ __forceinline__ int dma_outer_index(int kk, int o) {
   return kk * O + (((o >> 2) ^ ((kk & 4) ? 8 : 0)) << 2) + (o & 3);
-}
-
-#define TOPOS_COMPILER_FENCE() __atomic_signal_fence(__ATOMIC_SEQ_CST)
-
-// One wave-wide global_load_lds_dwordx4: each lane's 16 bytes at `src` land
-// in LDS at `lds` + 16 * lane (M0 holds the wave's LDS byte address). Issued
-// as inline assembly: the compiler's wait insertion treats a DMA issued
-// through the builtin as a pending LDS write that every later LDS read must
-// wait for, which put a vmcnt(0) before each slab's fragment reads and so
-// waited for the slab two ahead as well; the kernel orders its DMA itself
-// (dma_wait, then a barrier).
-__device__ __forceinline__ void dma_load16(const float *src, uint32_t lds_byte) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds_byte)
-               : "memory", "m0");
-}
-
-// The LDS byte address of an LDS location.
-__device__ __forceinline__ uint32_t lds_byte_address(const float *p) {
-  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) float *)p;
 }
 
 // One slab (16 deep) of an operand with outer extent O into `lds`.
@@ -392,25 +374,6 @@ __device__ __forceinline__ void guarded_slab(const float *__restrict__ p, int64_
     }
     *reinterpret_cast<float4 *>(lds + c * 256 + 4 * lane) = make_float4(v[0], v[1], v[2], v[3]);
   }
-}
-
-// Waits until at most N of this lane's vector-memory operations are
-// outstanding and its LDS operations are done (s_waitcnt vmcnt(N)
-// lgkmcnt(0); expcnt left at its maximum).
-template <int N>
-__device__ __forceinline__ void dma_wait() {
-  static_assert(N < 16, "vmcnt field");
-  TOPOS_COMPILER_FENCE();
-  __builtin_amdgcn_s_waitcnt(0x070 | N);
-  TOPOS_COMPILER_FENCE();
-}
-
-// A barrier without the workgroup fence of __syncthreads(), which would also
-// wait for the DMA loads kept in flight across it.
-__device__ __forceinline__ void dma_barrier() {
-  TOPOS_COMPILER_FENCE();
-  __builtin_amdgcn_s_barrier();
-  TOPOS_COMPILER_FENCE();
 }
 
 // One slab's fragment reads and 16x16x4 matrix-core products for a wave's

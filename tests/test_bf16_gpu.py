@@ -113,3 +113,23 @@ def test_bf16_narrow_slices_of_wide_buffers(hip, a_transposed):
     w = oracle.bf16_widen(want).astype(np.float64)
     bound = 1e-5 * (np.abs(wa) @ np.abs(wb)) + np.abs(w) * 2.0**-7 + 1e-38
     assert (np.abs(oracle.bf16_widen(fast).astype(np.float64) - w) <= bound).all()
+
+
+@pytest.mark.parametrize("m, k, n", [(4096, 4096, 4096), (8192, 768, 3072), (3072, 8192, 768)])
+@pytest.mark.parametrize("form", ["contiguous", "a_transposed", "b_transposed"])
+def test_bf16_fast_full_size_sampled_rows(hip, m, k, n, form):
+    """The bench's bf16 products at full size under Fast (256x256 tiles for
+    4096^3, 256x128 for [8192, 3072], k ranges for [3072, 768] over 8192),
+    each operand form, checked on a sample of output rows against the oracle
+    within the envelope plus one bf16 spacing, and repeated bit for bit."""
+    banner(f"bf16 fast full size {m}x{k}x{n} {form}")
+    a, b, a_view, b_view = _operands(m, k, n, form, seed=11)
+    fast = _device(a_view, b_view, m, k, n, hip.FAST)
+    assert np.array_equal(_device(a_view, b_view, m, k, n, hip.FAST), fast), "fast bf16 products repeat bit for bit"
+    wb = oracle.bf16_widen(b).astype(np.float64)
+    for r in sorted({0, 1, m // 3, m // 2 + 1, m - 2, m - 1}):
+        want = oracle.gemm_bf16(a[r:r + 1], (k, 1), b, (n, 1), 1, k, n)[0]
+        w = oracle.bf16_widen(want).astype(np.float64)
+        wa = oracle.bf16_widen(a[r:r + 1]).astype(np.float64)
+        bound = 1e-5 * (np.abs(wa) @ np.abs(wb))[0] + np.abs(w) * 2.0**-7 + 1e-38
+        assert (np.abs(oracle.bf16_widen(fast[r]).astype(np.float64) - w) <= bound).all(), f"row {r}"
