@@ -12,6 +12,8 @@
 #include "backend.hpp"
 #include "lds_dma.hpp"
 
+#include <type_traits>
+
 namespace topos_hip {
 namespace {
 
@@ -278,7 +280,33 @@ __global__ __launch_bounds__(BM * BN / 64, bf16_waves_per_simd(BM, BN, P)) void 
   for (int s = 0; s < P - 1 && s < slabs; ++s) issue(s);
   wait_for_next<kIssue, P - 2>(min(P - 2, slabs - 1));
   dma_barrier();
-  for (int s = 0; s < slabs; ++s) {
+  // P slabs a trip while every slab issued in it is a whole DMA slab: the
+  // stages are compile-time offsets and a slab has no branch of its own.
+  // The last slabs take the general loop below.
+  int s = 0;
+  {
+    auto steady = [&](auto stage_index) {
+      constexpr int st = decltype(stage_index)::value;  // s % P
+      const int64_t k0 = k_begin + (int64_t)(s + P - 1) * kSlabK;
+      float *stage = lds + ((st + P - 1) % P) * (SA + SB);
+      bf16_dma_slab<BM, W>(a, a_rs, m, m0, k0, stage, wave, lane);
+      bf16_dma_slab<BN, W>(b, b_cs, n, n0, k0, stage + SA, wave, lane);
+      const float *sa = lds + st * (SA + SB);
+      bf16_mfma_slab<kT>(sa, sa + SA, wm, wn, lane, acc);
+      dma_wait<(P - 2) * kIssue>();
+      dma_barrier();
+      ++s;
+    };
+    const int whole = (int)((k_end - k_begin) / kSlabK);  // slabs without a k tail
+    while (s + 2 * P - 1 <= whole) {
+      steady(std::integral_constant<int, 0>{});
+      steady(std::integral_constant<int, 1>{});
+      if constexpr (P > 2) steady(std::integral_constant<int, 2 % P>{});
+      if constexpr (P > 3) steady(std::integral_constant<int, 3 % P>{});
+      static_assert(P <= 4, "unrolled to four stages");
+    }
+  }
+  for (; s < slabs; ++s) {
     // Stage (s + P - 1) % P held slab s - 1, which every wave finished
     // before the last barrier.
     if (s + P - 1 < slabs) issue(s + P - 1);
@@ -295,43 +323,41 @@ __global__ __launch_bounds__(BM * BN / 64, bf16_waves_per_simd(BM, BN, P)) void 
 // Packs an operand view into k-contiguous rows: element (o, kk), at
 // p[o * outer_stride + kk * k_stride], goes to q[o * kp + kk]. An
 // outer-contiguous view (outer_stride 1) is transposed through 64 x 64 LDS
-// tiles: 8-byte loads along the input's rows, 8-byte stores along the
+// tiles: 16-byte loads along the input's rows, 16-byte stores along the
 // output's (kVector: those accesses aligned); any other view is gathered
 // element by element, consecutive lanes along k.
 template <bool kVector>
 __global__ __launch_bounds__(256) void pack_transpose_kernel(const uint16_t *__restrict__ p, int64_t outer,
                                                              int64_t kdim, int64_t k_stride,
                                                              uint16_t *__restrict__ q, int64_t kp, int tiles_o) {
-  __shared__ uint16_t tile[64][64 + 4];  // [kk][o]
+  __shared__ __attribute__((aligned(16))) uint16_t tile[64][64 + 8];  // [kk][o], 144-byte rows
   const int t = threadIdx.x;
   const int64_t o0 = (int64_t)(blockIdx.x % tiles_o) * 64, k0 = (int64_t)(blockIdx.x / tiles_o) * 64;
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int kk = t / 16 + 16 * e, o = 4 * (t % 16);
+  for (int e = 0; e < 2; ++e) {
+    const int kk = t / 8 + 32 * e, o = 8 * (t % 8);
     const uint16_t *src = p + (k0 + kk) * k_stride + o0 + o;
-    uint16_t v[4];
-    if (kVector && k0 + kk < kdim && o0 + o + 3 < outer) {
-      const uint2 w = *reinterpret_cast<const uint2 *>(src);
-      v[0] = (uint16_t)w.x, v[1] = (uint16_t)(w.x >> 16), v[2] = (uint16_t)w.y, v[3] = (uint16_t)(w.y >> 16);
+    if (kVector && k0 + kk < kdim && o0 + o + 7 < outer) {
+      *reinterpret_cast<uint4 *>(&tile[kk][o]) = *reinterpret_cast<const uint4 *>(src);
     } else {
 #pragma unroll
-      for (int x = 0; x < 4; ++x) v[x] = (k0 + kk < kdim && o0 + o + x < outer) ? src[x] : (uint16_t)0;
+      for (int x = 0; x < 8; ++x) tile[kk][o + x] = (k0 + kk < kdim && o0 + o + x < outer) ? src[x] : (uint16_t)0;
     }
-#pragma unroll
-    for (int x = 0; x < 4; ++x) tile[kk][o + x] = v[x];
   }
   __syncthreads();
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int o = t / 16 + 16 * e, kk = 4 * (t % 16);
+  for (int e = 0; e < 2; ++e) {
+    const int o = t / 8 + 32 * e, kk = 8 * (t % 8);
     if (o0 + o >= outer) continue;
     uint16_t *dst = q + (o0 + o) * kp + k0 + kk;
-    if (kVector && k0 + kk + 3 < kdim) {
-      *reinterpret_cast<uint2 *>(dst) = make_uint2((uint32_t)tile[kk][o] | ((uint32_t)tile[kk + 1][o] << 16),
-                                                   (uint32_t)tile[kk + 2][o] | ((uint32_t)tile[kk + 3][o] << 16));
+    uint32_t w[4];
+#pragma unroll
+    for (int x = 0; x < 4; ++x) w[x] = (uint32_t)tile[kk + 2 * x][o] | ((uint32_t)tile[kk + 2 * x + 1][o] << 16);
+    if (kVector && k0 + kk + 7 < kdim) {
+      *reinterpret_cast<uint4 *>(dst) = make_uint4(w[0], w[1], w[2], w[3]);
     } else {
 #pragma unroll
-      for (int x = 0; x < 4; ++x)
+      for (int x = 0; x < 8; ++x)
         if (k0 + kk + x < kdim) dst[x] = tile[kk + x][o];
     }
   }
@@ -435,7 +461,7 @@ void pack_rows(const uint16_t *p, int64_t outer, int64_t kdim, int64_t os, int64
   if (os == 1) {
     const int64_t tiles_o = (outer + 63) / 64, tiles_k = (kdim + 63) / 64;
     if (tiles_o * tiles_k > 0x7fffffff) throw Unsupported{"bf16 gemm: operand too large to pack"};
-    const bool vector = reinterpret_cast<uintptr_t>(p) % 8 == 0 && ks % 4 == 0;
+    const bool vector = reinterpret_cast<uintptr_t>(p) % 16 == 0 && ks % 8 == 0;
     const dim3 grid((unsigned)(tiles_o * tiles_k));
     if (vector)
       pack_transpose_kernel<true><<<grid, 256, 0, stream>>>(p, outer, kdim, ks, q, kp, (int)tiles_o);
