@@ -5,7 +5,7 @@
 //
 // Exact posture: the widened operands go through the bit-identical f32
 // kernel (gemm::multiply's seed and ascending k), then round: bit-identical.
-// Fast posture: gfx950's bf16 matrix cores (v_mfma_f32_32x32x16_bf16),
+// Fast posture: gfx950's bf16 matrix cores (v_mfma_f32_16x16x32_bf16),
 // which multiply bf16 pairs exactly and accumulate in f32 in their own
 // order: the envelope, then the same single rounding.
 #pragma clang fp contract(off)
