@@ -644,7 +644,7 @@ __global__ __launch_bounds__(BM / WM * BN, BM == 256 ? 4 : 3) void gemm_dma_kern
   // Interior tiles of 64-row waves store through LDS in whole row segments
   // (measured on the attention-scores product, which writes 402 MB for 12.9
   // GFLOP: 198 -> 172 us).
-  if constexpr (kT && WM == 64) {
+  if constexpr (kT && WM == 64 && (BM / WM) * (BN / 64) * 32 * 68 <= 3 * (SA + SB)) {
     if (m0 + BM <= m && n0 + BN <= n) {
       dma_barrier();  // every wave's last fragment reads are done before LDS is reused
       store_block_staged16(acc, c, ldc, m0, n0, wm, wn, lane, bias, bias_cs, bias_mode, lds + wave * 32 * 68);
@@ -655,7 +655,8 @@ __global__ __launch_bounds__(BM / WM * BN, BM == 256 ? 4 : 3) void gemm_dma_kern
 }
 
 // The tile shape for an m x n product over k (and `batches`): 128x64 or
-// 64x128 when one output extent is at most 64; 256x128 (eight waves, less
+// 64x128 when one output extent is at most 64; 256x256 (sixteen waves, LDS-DMA
+// operands only, never split) for four rounds or more of such tiles; 256x128 (eight waves, less
 // operand traffic per flop than 128x128) when its tiles fill whole rounds of
 // two workgroups per CU, or at least one and a half such rounds (measured on
 // MI355X: the [8192, 3072] products gain, [8192, 2304] loses); 64x128 when k
@@ -679,6 +680,14 @@ TileShape tile_shape(int64_t m, int64_t n, int64_t k, int64_t batches) {
   // the GPT-2 step from 73.3 to 72.8 ms in a same-box A/B; 128x128 tiles
   // for them measured the same on GPT-2 and 0.3 ms slower on Llama.)
   const bool rows_fill = ((m + 255) / 256 * 256 - m) * 8 <= m;
+  // 256x256 tiles (sixteen waves, one workgroup a CU: half the operand
+  // traffic per product of 256x128) for products of at least four full
+  // rounds of them, unsplit: the GPT-2 vocabulary head, [8192, 50257] over
+  // 768, went from 5.06 to 4.78 ms inside the step; [50257, 768] over 8192
+  // (591 such tiles) ran 5.5-6.8 ms against 5.1 on 256x128 tiles.
+  const bool cols_fill = ((n + 255) / 256 * 256 - n) * 8 <= n;
+  if (rows_fill && cols_fill && k > 128 && ((m + 255) / 256) * ((n + 255) / 256) * batches >= 1024)
+    return {256, 256, 1};
   if (rows_fill && k > 128 && (wide >= 768 || (wide >= 512 && wide % 512 == 0))) return {256, 128, 2};
   const int64_t thin = ((m + 63) / 64) * ((n + 127) / 128) * batches;
   if (k <= 4096 && thin >= 768 && thin % 768 == 0) return {64, 128, 3};
@@ -894,6 +903,7 @@ int mfma_splits(int64_t m, int64_t n, int64_t k, int64_t batches) {
   // (up to 2048 workgroups while each split stays 512 deep): measured on
   // MI355X, the partial products' extra traffic costs less than idle CUs.
   const TileShape shape = tile_shape(m, n, k, batches);
+  if (shape.bn == 256) return 1;  // four rounds or more of whole tiles
   const int64_t tiles = ((m + shape.bm - 1) / shape.bm) * ((n + shape.bn - 1) / shape.bn) * batches;
   const int64_t full = 256 * shape.per_cu;
   if (tiles >= full) {
@@ -990,7 +1000,9 @@ bool launch_gemm_mfma(const float *a, int64_t a_rs, int64_t a_cs, const float *b
   // 16-byte loads need a unit stride along the axis the lanes step on (any
   // 4-byte alignment serves).
   const bool vector = (lk ? a_cs == 1 : a_rs == 1) && (rk ? b_rs == 1 : b_cs == 1);
-  const TileShape shape = tile_shape(m, n, k, batch.count);
+  TileShape shape = tile_shape(m, n, k, batch.count);
+  // The 256x256 tiles exist on the LDS-DMA kernel only (unsplit either way).
+  if (shape.bn == 256 && !(vector && (lk || m >= 4) && (rk || n >= 4))) shape = {256, 128, 2};
   const int64_t gm = (m + shape.bm - 1) / shape.bm;
   const int64_t gn = (n + shape.bn - 1) / shape.bn;
   if (gm * gn > 0x7fffffff || batch.count > 65535 || batch.count < 1) throw Unsupported{"mfma gemm: grid too large"};
@@ -1031,7 +1043,9 @@ bool launch_gemm_mfma(const float *a, int64_t a_rs, int64_t a_cs, const float *b
   const bool vector_out = target_ld % 4 == 0 && reinterpret_cast<uintptr_t>(target) % 16 == 0 &&
                           (batch.count == 1 || (target_bs % 4 == 0 && target_bs2 % 4 == 0)) &&
                           (splits == 1 || split_stride % 4 == 0);
-  if (dma && shape.bm == 256)
+  if (dma && shape.bn == 256)
+    dispatch_dma<256, 256>(lk, rk, vector_out, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, target, target_ld, (int)gm, (int)gn, batch, target_bs, target_bs2, split_len, split_stride, epilogue, gemm_mode);
+  else if (dma && shape.bm == 256)
     dispatch_dma<256, 128>(lk, rk, vector_out, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, target, target_ld, (int)gm, (int)gn, batch, target_bs, target_bs2, split_len, split_stride, epilogue, gemm_mode);
   else if (dma && shape.bm == 64)
     dispatch_dma<64, 128>(lk, rk, vector_out, grid, stream, a, a_rs, a_cs, b, b_rs, b_cs, m, k, n, target, target_ld, (int)gm, (int)gn, batch, target_bs, target_bs2, split_len, split_stride, epilogue, gemm_mode);

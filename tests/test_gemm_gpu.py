@@ -99,7 +99,9 @@ def test_negative_zero_seed_survives_on_device(hip):
                                      (8192, 768, 768), (8192, 768, 2304), (4096, 2048, 2048),
                                      (2048, 4096, 2048),
                                      # 128x64 tiles (an output 64 or fewer wide), whole and ragged
-                                     (1024, 1024, 64), (1000, 300, 62)])
+                                     (1024, 1024, 64), (1000, 300, 62),
+                                     # 256x256 tiles (four rounds or more), whole and a ragged vocabulary
+                                     (8192, 256, 8192), (2048, 192, 50257)])
 @pytest.mark.parametrize("product", ["forward", "a_transposed", "b_transposed"])
 def test_sweep_shapes_sampled_rows(hip, m, k, n, product):
     """The GEMM-sweep products at full size (forward A.B, then A^T.G and
