@@ -932,17 +932,18 @@ int mfma_splits(int64_t m, int64_t n, int64_t k, int64_t batches) {
   // 512-cube has 16 tiles, and eight 64-deep ranges ran it at 9.4-11 TFLOP/s
   // against 6.3-7.5 for two 256-deep ones.
   if (k < 128) return 1;
-  // Every CU already holds a workgroup: split only as far as one round of
-  // full slots, into ranges at least 1024 deep, and further only for very
-  // deep products (ranges of 8192 or more, up to 2048 workgroups: the
-  // vocabulary products). Measured on MI355X: the [1024, 4096] products over
-  // k = 1024 (256 tiles of 128x128) ran at 98 TFLOP/s unsplit against 86 in
-  // three ranges; [4096, 2048] over 2048 (512 tiles) 121 unsplit against 108
-  // in four; [2048, 2048] over 4096 (256 tiles) 118 in three ranges against
-  // 113 in six.
+  // Every CU already holds a workgroup: split only as far as two workgroups
+  // a CU, into ranges at least 1024 deep, and further only for very deep
+  // products (ranges of 8192 or more, up to 2048 workgroups: the vocabulary
+  // products). Measured on MI355X: the [1024, 4096] products over k = 1024
+  // (256 tiles of 128x128) ran at 98 TFLOP/s unsplit against 86 in three
+  // ranges; [4096, 2048] over 2048 (512 tiles) 121 unsplit against 108 in
+  // four; [2048, 2048] over 4096 (256 tiles) 118 in three ranges against 113
+  // in six, and in the Llama step its 32 launches took 8.71 ms in two ranges
+  // against 8.98 in three.
   if (tiles >= 256) {
     int64_t s = 1;
-    while ((s + 1) * tiles <= full && k / (s + 1) >= 1024) ++s;
+    while ((s + 1) * tiles <= 512 && k / (s + 1) >= 1024) ++s;
     while (s * 2 * tiles <= 2048 && k / (s * 2) >= 8192) s *= 2;
     return (int)std::min<int64_t>(s, 16);
   }

@@ -95,7 +95,7 @@ def test_negative_zero_seed_survives_on_device(hip):
                                      (768, 8192, 768), (768, 4096, 20001),
                                      (1025, 1027, 1029), (1000, 512, 1020), (300, 64, 260),
                                      # fast tile choices: 64x128 tiles filling whole rounds (k <= 1024),
-                                     # unsplit with a tile per CU, three k ranges
+                                     # unsplit with a tile per CU, two k ranges
                                      (8192, 768, 768), (8192, 768, 2304), (4096, 2048, 2048),
                                      (2048, 4096, 2048),
                                      # 128x64 tiles (an output 64 or fewer wide), whole and ragged
