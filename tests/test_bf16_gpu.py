@@ -19,7 +19,9 @@ pytestmark = pytest.mark.gpu
 SHAPES = [(2, 3, 4), (5, 8, 13), (16, 16, 16), (63, 64, 65), (100, 127, 3), (129, 257, 131), (256, 384, 512),
           (1024, 1024, 1024), (777, 1000, 515),
           # few tiles over deep k: under Fast, k in 8 ranges and in 4 ragged ones
-          (128, 4096, 192), (300, 2600, 260)]
+          (128, 4096, 192), (300, 2600, 260),
+          # a single output row or column, and k = 1 (operands of outer extent 1, packs of one k)
+          (1, 77, 300), (300, 77, 1), (70, 1, 90)]
 FORMS = ["contiguous", "a_transposed", "b_transposed", "narrowed"]
 
 
