@@ -2816,7 +2816,8 @@ struct topos_hip_program {
   // Short dead-end branches run on a side stream, overlapping the main
   // chain: a launch whose downstream is at most kSideDepth launches, all of
   // them side launches themselves (a parameter gradient's product or fold
-  // and the zero-seeded accumulation behind it). A side launch waits for the
+  // and the zero-seeded accumulation behind it), except trailing ones fed
+  // only by the main stream. A side launch waits for the
   // event of its latest main-stream producer; the run ends with the main
   // stream waiting for the side stream. Every storage a side launch touches
   // is kept to the end of the run, so no later main launch reuses its memory
@@ -2841,6 +2842,30 @@ struct topos_hip_program {
       }
       downstream[q] = std::min(below, 1 << 20);
       launches[q].side = side && below <= kSideDepth;
+    }
+    // Side launches that cannot start before the main stream's last launch
+    // ends (they read its output, or a launch moved here) and read nothing
+    // a side launch writes run on the main stream instead: it is idle by
+    // then, while the side stream still works through the branches queued
+    // before them (in the GPT-2 step, layer 0's LayerNorm gradient and the
+    // embedding scatters behind its weight gradient). A launch that reads a
+    // side launch's output stays on the side stream, which orders it.
+    int last_main = -1;
+    for (size_t l = 0; l < count; ++l)
+      if (!launches[l].side) last_main = (int)l;
+    if (last_main >= 0) {
+      std::vector<bool> at_end(count, false);
+      at_end[last_main] = true;
+      for (size_t l = (size_t)last_main + 1; l < count; ++l) {
+        bool from_main = true, after_end = false;
+        for (int s : launches[l].reads) {
+          const int p = producer[s];
+          if (p < 0 || p == (int)l) continue;
+          if (launches[p].side) from_main = false;
+          if (at_end[p]) after_end = true;
+        }
+        if (from_main && after_end) launches[l].side = false, at_end[l] = true;
+      }
     }
     for (size_t l = 0; l < count; ++l) {
       Launch &launch = launches[l];
