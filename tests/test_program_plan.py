@@ -337,3 +337,20 @@ print(p.describe)
 ''')
     assert "copy (tiles) [2,64,2,64]" in out, out
     assert "copy [2,64,2,64]" not in out, out
+
+
+def test_trailing_branches_fed_by_the_main_stream_run_on_it():
+    """Side branches that cannot start before the main stream's last launch
+    ends and read no side output run on the main stream (the GPT-2 step's
+    embedding scatters); the tied embedding's final accumulation, which reads
+    the head's side-stream weight gradient, stays on the side stream."""
+    out = run(r'''
+w = workloads.gpt2(batch=2, context=16, vocab=37, width=32, heads=4, layers=2, positions=24)
+p = DeviceProgram(w.tape, w.roots, numerics=n.FAST)
+for line in p.describe.splitlines()[1:]:
+    print(line)
+''')
+    lines = out.splitlines()
+    scatters = [line for line in lines if ": scatter " in line]
+    assert len(scatters) == 2 and not any("[side]" in line for line in scatters), out
+    assert "[side]" in lines[-1] and "chain Add [37,32]" in lines[-1], out
