@@ -643,7 +643,8 @@ __global__ __launch_bounds__(BM / WM * BN, BM == 256 ? 4 : 3) void gemm_dma_kern
 
   // Interior tiles of 64-row waves store through LDS in whole row segments
   // (measured on the attention-scores product, which writes 402 MB for 12.9
-  // GFLOP: 198 -> 172 us).
+  // GFLOP: 198 -> 172 us), where every wave's 32 x 68 stage fits the tile's
+  // three slab stages (not the sixteen waves of a 256x256 tile).
   if constexpr (kT && WM == 64 && (BM / WM) * (BN / 64) * 32 * 68 <= 3 * (SA + SB)) {
     if (m0 + BM <= m && n0 + BN <= n) {
       dma_barrier();  // every wave's last fragment reads are done before LDS is reused
